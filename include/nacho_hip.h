@@ -1,0 +1,182 @@
+/*
+ * nacho_hip.h — C ABI of the MI355X (gfx950) backend for nacho's GPU target.
+ *
+ * Every declared GPU kernel of the reference gets one extern "C" entry point here.  The
+ * reference binds `namespace <k> { Z_tensor_format <k>_gpu_i32_f32(a, b, num_blocks,
+ * threads_per_block); }` (entry point printed at src/backend/stitch_and_generate.cpp:299-301,
+ * called from the wrapper written by src/backend/generate_bindings.cpp:288-314).  These
+ * functions replace those generated entry points: same operands, same meaning of every
+ * field, same launch-geometry arguments, plus an explicit stream and an optional allocator.
+ *
+ * Tensor descriptors are plain C structs whose field order is the reference's generated
+ * tensor struct (src/backend/tensor.cpp:13-61: dimension sizes first, then the level arrays
+ * in level order, then `values`, then `nnz`).  Index arrays are int32, values float32, all
+ * pointers are device pointers except where stated.
+ *
+ * Return value of every entry point: 0 on success, a positive hipError_t value when a HIP
+ * call failed, or one of the negative NACHO_ERR_* codes.  On failure every scratch buffer is
+ * released and the result descriptor is left zeroed.  nacho_error_string() names a code.
+ *
+ * Ownership: operands are borrowed and never written.  Result buffers are allocated by
+ * `alloc` (or by the library's stream-ordered pool when `alloc` is NULL, in which case the
+ * caller releases them with nacho_free()).  A result array of length 0 is a NULL pointer.
+ *
+ * Input contract (the reference's, made explicit): pos[0] == 0, pos non-decreasing,
+ * pos[rows] == length of the coordinate array, coordinates strictly increasing within
+ * each fibre (sorted, no duplicates), COO/COO3 coordinates sorted lexicographically and
+ * distinct.  nacho_validate_*() check this on the device when asked.
+ */
+#ifndef NACHO_HIP_H
+#define NACHO_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- error codes ------------------------------------------------------------------- */
+#define NACHO_OK 0
+#define NACHO_ERR_INVALID_ARGUMENT (-1) /* null pointer, negative size, shape mismatch   */
+#define NACHO_ERR_INDEX_OVERFLOW (-2)   /* result or work count does not fit int32        */
+#define NACHO_ERR_OUT_OF_MEMORY (-3)    /* the allocator returned NULL                    */
+#define NACHO_ERR_MALFORMED_INPUT (-4)  /* validation found unsorted/duplicate/bad pos    */
+#define NACHO_ERR_NO_DEVICE (-5)        /* no HIP device visible                          */
+#define NACHO_ERR_INTERNAL (-6)         /* a kernel's bounded wait expired (library bug)  */
+
+/* ---- tensor descriptors (field order = the reference's generated structs) ---------- */
+
+/* CSR, format {i: Dense, j: Compressed_unique} named "CSR" (compiler.cpp:21-24).
+ * Reference struct: {dim_i_size, dim_j_size, dim_j_offsets, dim_j_length, dim_j_indices,
+ * values, nnz} (tensor.cpp:13-61). */
+typedef struct nacho_csr {
+    int32_t dim_i_size;     /* rows                                              */
+    int32_t dim_j_size;     /* columns                                           */
+    int32_t *dim_j_offsets; /* pos, dim_i_size + 1 entries                       */
+    int32_t dim_j_length;   /* number of stored coordinates                      */
+    int32_t *dim_j_indices; /* crd, dim_j_length entries                         */
+    float *values;          /* dim_j_length entries                              */
+    int32_t nnz;            /* == dim_j_length                                   */
+} nacho_csr;
+
+/* CSR whose offsets are 64-bit: the SpGEMM result, whose length can exceed 2^31.  Same
+ * field order as nacho_csr; no counterpart in the reference, which is int32-only
+ * (index_t = int32_t, stitch_and_generate.cpp:235). */
+typedef struct nacho_csr64 {
+    int32_t dim_i_size;
+    int32_t dim_j_size;
+    int64_t *dim_j_offsets; /* dim_i_size + 1 entries */
+    int64_t dim_j_length;
+    int32_t *dim_j_indices;
+    float *values;
+    int64_t nnz;
+} nacho_csr64;
+
+/* COO, format {i: Compressed_non_unique, j: Singleton_unique} named "COO"
+ * (compiler.cpp:50-53), lowered to one merged level (Compile.cpp:66-154).  Reference struct:
+ * {dim_i_size, dim_j_size, dim_i_length, dim_i_indices, dim_j_length, dim_j_indices, values,
+ * nnz}. */
+typedef struct nacho_coo {
+    int32_t dim_i_size;
+    int32_t dim_j_size;
+    int32_t dim_i_length;
+    int32_t *dim_i_indices;
+    int32_t dim_j_length;
+    int32_t *dim_j_indices;
+    float *values;
+    int32_t nnz;
+} nacho_coo;
+
+/* COO3, format {i: Compressed_non_unique, j: Singleton_non_unique, k: Singleton_unique}
+ * named "COO3" (compiler.cpp:60-64). */
+typedef struct nacho_coo3 {
+    int32_t dim_i_size;
+    int32_t dim_j_size;
+    int32_t dim_k_size;
+    int32_t dim_i_length;
+    int32_t *dim_i_indices;
+    int32_t dim_j_length;
+    int32_t *dim_j_indices;
+    int32_t dim_k_length;
+    int32_t *dim_k_indices;
+    float *values;
+    int32_t nnz;
+} nacho_coo3;
+
+/* CSF3, format {i, j, k: Compressed_unique} named "CSF3" (compiler.cpp:44-48).  The
+ * outermost compressed level has no offsets (tensor.cpp:36-39). */
+typedef struct nacho_csf3 {
+    int32_t dim_i_size;
+    int32_t dim_j_size;
+    int32_t dim_k_size;
+    int32_t dim_i_length;
+    int32_t *dim_i_indices; /* dim_i_length entries       */
+    int32_t *dim_j_offsets; /* dim_i_length + 1 entries   */
+    int32_t dim_j_length;
+    int32_t *dim_j_indices; /* dim_j_length entries       */
+    int32_t *dim_k_offsets; /* dim_j_length + 1 entries   */
+    int32_t dim_k_length;
+    int32_t *dim_k_indices; /* dim_k_length entries       */
+    float *values;          /* dim_k_length entries       */
+    int32_t nnz;
+} nacho_csf3;
+
+/* ---- allocation ------------------------------------------------------------------- */
+
+/* Caller-supplied device allocator, used for results and scratch.  `allocate` returns NULL
+ * on failure.  `stream` is the hipStream_t the call runs on.  Replaces the generated code's
+ * cudaMallocAsync/cudaFreeAsync on stream 0 (stitch_and_generate_gpu.cpp:187-196) and the
+ * Python deleter of runtime/nacho_nb.h:50-58. */
+typedef struct nacho_allocator {
+    void *ctx;
+    void *(*allocate)(void *ctx, size_t bytes, void *stream);
+    void (*release)(void *ctx, void *ptr, void *stream);
+} nacho_allocator;
+
+/* Release a buffer that an entry point allocated with the default allocator (alloc == NULL).
+ * Stream-ordered on `stream`.  Replaces cudaFreeWrapper (runtime/cuda_utils/cuda_utils.cu:7-11). */
+int nacho_free(void *ptr, void *stream);
+
+/* ---- entry points ------------------------------------------------------------------
+ * `num_blocks` / `threads_per_block` are the reference's launch arguments
+ * (generate_bindings.cpp:292-325, default 256/256).  They are accepted and validated
+ * (both > 0) but advisory: the gfx950 kernels pick their own tiles.
+ * `stream` is a hipStream_t (NULL = the null stream, as the reference's `stream = 0`). */
+
+/* Z = a + b over CSR (union; explicit zeros kept).  Replaces csr_add::csr_add_gpu_i32_f32
+ * (kernel declared at compiler.cpp:112). */
+int nacho_gpu_csr_add_f32(const nacho_csr *a, const nacho_csr *b, nacho_csr *z,
+                          int32_t num_blocks, int32_t threads_per_block, void *stream,
+                          const nacho_allocator *alloc);
+
+/* Z = a * b elementwise over CSR (intersection).  Replaces csr_mul::csr_mul_gpu_i32_f32
+ * (compiler.cpp:116), including its empty-result early exit
+ * (stitch_and_generate.cpp:168-220): an empty product returns zeroed offsets and NULL
+ * coordinate/value arrays. */
+int nacho_gpu_csr_mul_f32(const nacho_csr *a, const nacho_csr *b, nacho_csr *z,
+                          int32_t num_blocks, int32_t threads_per_block, void *stream,
+                          const nacho_allocator *alloc);
+
+/* ---- diagnostics ------------------------------------------------------------------ */
+
+/* Static string naming an error code (HIP codes use hipGetErrorString). */
+const char *nacho_error_string(int code);
+
+/* Library version string. */
+const char *nacho_version(void);
+
+/* When enabled (nonzero), every entry point brackets its dominant kernel with HIP events
+ * on its stream, and nacho_last_kernel_ms() returns that kernel's duration for the most
+ * recent call on this host thread (0 when disabled). */
+void nacho_set_kernel_timing(int enable);
+float nacho_last_kernel_ms(void);
+
+/* Name of the kernel nacho_last_kernel_ms() timed in the last call on this thread. */
+const char *nacho_last_kernel_name(void);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* NACHO_HIP_H */

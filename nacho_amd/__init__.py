@@ -1,0 +1,24 @@
+"""nacho_amd — MI355X (gfx950) backend for nacho's GPU target.
+
+Python surface of the reference (`import nacho`; python/nacho/__init__.py) for the GPU
+target: the tensor classes, the `gpu_<kernel>_f32` entry points and the converters.  Every
+entry point runs hand-written HIP kernels from libnacho_hip.so through its C ABI
+(include/nacho_hip.h); nothing here computes on the CPU.
+"""
+
+from .convert import to_coo, to_coo3, to_csf3, to_csr  # noqa: F401
+from .ops import (  # noqa: F401
+    gpu_coo3d_add_f32,
+    gpu_coo_add_f32,
+    gpu_coo_mul_f32,
+    gpu_csf_add_f32,
+    gpu_csr_add_f32,
+    gpu_csr_mul_f32,
+    gpu_spgemm64_f32,
+    gpu_spgemm_f32,
+    last_kernel_ms,
+    set_kernel_timing,
+)
+from .tensors import COO3_gpu, COO_gpu, CSF3_gpu, CSR64_gpu, CSR_gpu  # noqa: F401
+
+__version__ = "0.1.0"

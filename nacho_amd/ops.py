@@ -1,0 +1,207 @@
+"""`gpu_<kernel>_f32` entry points with the reference's Python signatures.
+
+The reference's generated wrapper (src/backend/generate_bindings.cpp:288-327) unwraps each
+operand class into the kernel's tensor struct, calls `<k>::<k>_gpu_i32_f32(operands...,
+num_blocks, threads_per_block)` and adopts the returned buffers.  These functions do the
+same through the C ABI of libnacho_hip.so: borrow operand buffers, call the entry point on
+torch's current stream, adopt the result buffers.  There is no CPU fallback: a missing
+library raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _device, _lib
+from .tensors import COO3_gpu, COO_gpu, CSF3_gpu, CSR64_gpu, CSR_gpu
+
+_I32, _I64, _F32 = torch.int32, torch.int64, torch.float32
+
+
+def _p(t: torch.Tensor):
+    return ctypes.c_void_p(_device.ptr(t))
+
+
+def _same_device(*tensors):
+    device = tensors[0].device
+    for t in tensors[1:]:
+        if t.device != device:
+            raise ValueError(f"operands on different devices: {device} and {t.device}")
+    return device
+
+
+# ---- descriptor conversion -----------------------------------------------------------
+
+def _csr_desc(t: CSR_gpu) -> _lib.CsrDesc:
+    rows, cols = (int(x) for x in t.shape)
+    if t.dim_j_offsets.numel() != rows + 1:
+        raise ValueError(f"CSR_gpu: dim_j_offsets has {t.dim_j_offsets.numel()} entries, "
+                         f"expected rows + 1 = {rows + 1}")
+    n = t.dim_j_indices.numel()
+    if t.values.numel() != n:
+        raise ValueError("CSR_gpu: dim_j_indices and values differ in length")
+    return _lib.CsrDesc(rows, cols, _p(t.dim_j_offsets), n, _p(t.dim_j_indices), _p(t.values), n)
+
+
+def _coo_desc(t: COO_gpu) -> _lib.CooDesc:
+    rows, cols = (int(x) for x in t.shape)
+    n = t.values.numel()
+    if t.dim_i_indices.numel() != n or t.dim_j_indices.numel() != n:
+        raise ValueError("COO_gpu: coordinate and value arrays differ in length")
+    return _lib.CooDesc(rows, cols, n, _p(t.dim_i_indices), n, _p(t.dim_j_indices),
+                        _p(t.values), n)
+
+
+def _coo3_desc(t: COO3_gpu) -> _lib.Coo3Desc:
+    si, sj, sk = (int(x) for x in t.shape)
+    n = t.values.numel()
+    if any(x.numel() != n for x in (t.dim_i_indices, t.dim_j_indices, t.dim_k_indices)):
+        raise ValueError("COO3_gpu: coordinate and value arrays differ in length")
+    return _lib.Coo3Desc(si, sj, sk, n, _p(t.dim_i_indices), n, _p(t.dim_j_indices), n,
+                         _p(t.dim_k_indices), _p(t.values), n)
+
+
+def _csf3_desc(t: CSF3_gpu) -> _lib.Csf3Desc:
+    si, sj, sk = (int(x) for x in t.shape)
+    ni, nj, nk = t.dim_i_indices.numel(), t.dim_j_indices.numel(), t.dim_k_indices.numel()
+    if t.dim_j_offsets.numel() != ni + 1 or t.dim_k_offsets.numel() != nj + 1:
+        raise ValueError("CSF3_gpu: offsets arrays must have parent length + 1 entries")
+    if t.values.numel() != nk:
+        raise ValueError("CSF3_gpu: dim_k_indices and values differ in length")
+    return _lib.Csf3Desc(si, sj, sk, ni, _p(t.dim_i_indices), _p(t.dim_j_offsets), nj,
+                         _p(t.dim_j_indices), _p(t.dim_k_offsets), nk, _p(t.dim_k_indices),
+                         _p(t.values), nk)
+
+
+# ---- result adoption -----------------------------------------------------------------
+
+def _adopt_csr(z: _lib.CsrDesc, device, stream) -> CSR_gpu:
+    rows, n = z.dim_i_size, z.dim_j_length
+    return CSR_gpu(_device.adopt(z.dim_j_offsets, rows + 1, _I32, device, stream),
+                   _device.adopt(z.dim_j_indices, n, _I32, device, stream),
+                   _device.adopt(z.values, n, _F32, device, stream),
+                   [z.dim_i_size, z.dim_j_size])
+
+
+def _adopt_csr64(z: _lib.Csr64Desc, device, stream) -> CSR64_gpu:
+    rows, n = z.dim_i_size, z.dim_j_length
+    return CSR64_gpu(_device.adopt(z.dim_j_offsets, rows + 1, _I64, device, stream),
+                     _device.adopt(z.dim_j_indices, n, _I32, device, stream),
+                     _device.adopt(z.values, n, _F32, device, stream),
+                     [z.dim_i_size, z.dim_j_size])
+
+
+def _adopt_coo(z: _lib.CooDesc, device, stream) -> COO_gpu:
+    n = z.nnz
+    return COO_gpu(_device.adopt(z.dim_i_indices, n, _I32, device, stream),
+                   _device.adopt(z.dim_j_indices, n, _I32, device, stream),
+                   _device.adopt(z.values, n, _F32, device, stream),
+                   [z.dim_i_size, z.dim_j_size])
+
+
+def _adopt_coo3(z: _lib.Coo3Desc, device, stream) -> COO3_gpu:
+    n = z.nnz
+    return COO3_gpu(_device.adopt(z.dim_i_indices, n, _I32, device, stream),
+                    _device.adopt(z.dim_j_indices, n, _I32, device, stream),
+                    _device.adopt(z.dim_k_indices, n, _I32, device, stream),
+                    _device.adopt(z.values, n, _F32, device, stream),
+                    [z.dim_i_size, z.dim_j_size, z.dim_k_size])
+
+
+def _adopt_csf3(z: _lib.Csf3Desc, device, stream) -> CSF3_gpu:
+    ni, nj, nk = z.dim_i_length, z.dim_j_length, z.dim_k_length
+    return CSF3_gpu(_device.adopt(z.dim_i_indices, ni, _I32, device, stream),
+                    _device.adopt(z.dim_j_offsets, ni + 1, _I32, device, stream),
+                    _device.adopt(z.dim_j_indices, nj, _I32, device, stream),
+                    _device.adopt(z.dim_k_offsets, nj + 1, _I32, device, stream),
+                    _device.adopt(z.dim_k_indices, nk, _I32, device, stream),
+                    _device.adopt(z.values, nk, _F32, device, stream),
+                    [z.dim_i_size, z.dim_j_size, z.dim_k_size])
+
+
+# ---- generic call --------------------------------------------------------------------
+
+def _call(entry, a, b, cls, desc_fn, result_desc, adopt_fn, num_blocks, threads_per_block):
+    for name, t in (("a", a), ("b", b)):
+        if not isinstance(t, cls):
+            raise TypeError(f"{entry}: operand {name} must be {cls.__name__}, "
+                            f"got {type(t).__name__}")
+    device = _same_device(a, b)
+    lib = _lib.load()
+    fn = getattr(lib, entry, None)
+    if fn is None:
+        raise RuntimeError(f"{entry} is not exported by {_lib.LIBRARY_PATH.name}")
+    da, db = desc_fn(a), desc_fn(b)
+    z = result_desc()
+    with torch.cuda.device(device):
+        stream = _device.current_stream(device)
+        rc = fn(ctypes.byref(da), ctypes.byref(db), ctypes.byref(z), int(num_blocks),
+                int(threads_per_block), ctypes.c_void_p(stream), None)
+        _lib.check(rc, entry)
+        return adopt_fn(z, device, stream)
+
+
+def gpu_csr_add_f32(a: CSR_gpu, b: CSR_gpu, num_blocks: int = 256,
+                    threads_per_block: int = 256) -> CSR_gpu:
+    """Z = a + b (sorted union per row; explicit zeros kept).  compiler.cpp:112."""
+    return _call("nacho_gpu_csr_add_f32", a, b, CSR_gpu, _csr_desc, _lib.CsrDesc, _adopt_csr,
+                 num_blocks, threads_per_block)
+
+
+def gpu_csr_mul_f32(a: CSR_gpu, b: CSR_gpu, num_blocks: int = 256,
+                    threads_per_block: int = 256) -> CSR_gpu:
+    """Z = a * b elementwise (sorted intersection per row).  compiler.cpp:116."""
+    return _call("nacho_gpu_csr_mul_f32", a, b, CSR_gpu, _csr_desc, _lib.CsrDesc, _adopt_csr,
+                 num_blocks, threads_per_block)
+
+
+def gpu_coo_add_f32(a: COO_gpu, b: COO_gpu, num_blocks: int = 256,
+                    threads_per_block: int = 256) -> COO_gpu:
+    """Z = a + b over COO (union of (i, j)).  compiler.cpp:118."""
+    return _call("nacho_gpu_coo_add_f32", a, b, COO_gpu, _coo_desc, _lib.CooDesc, _adopt_coo,
+                 num_blocks, threads_per_block)
+
+
+def gpu_coo_mul_f32(a: COO_gpu, b: COO_gpu, num_blocks: int = 256,
+                    threads_per_block: int = 256) -> COO_gpu:
+    """Z = a * b over COO (intersection of (i, j)).  compiler.cpp:120."""
+    return _call("nacho_gpu_coo_mul_f32", a, b, COO_gpu, _coo_desc, _lib.CooDesc, _adopt_coo,
+                 num_blocks, threads_per_block)
+
+
+def gpu_coo3d_add_f32(a: COO3_gpu, b: COO3_gpu, num_blocks: int = 256,
+                      threads_per_block: int = 256) -> COO3_gpu:
+    """Z = a + b over COO3 (union of (i, j, k)).  compiler.cpp:138."""
+    return _call("nacho_gpu_coo3d_add_f32", a, b, COO3_gpu, _coo3_desc, _lib.Coo3Desc,
+                 _adopt_coo3, num_blocks, threads_per_block)
+
+
+def gpu_csf_add_f32(a: CSF3_gpu, b: CSF3_gpu, num_blocks: int = 256,
+                    threads_per_block: int = 256) -> CSF3_gpu:
+    """Z = a + b over CSF3 (union at every level).  compiler.cpp:135."""
+    return _call("nacho_gpu_csf_add_f32", a, b, CSF3_gpu, _csf3_desc, _lib.Csf3Desc,
+                 _adopt_csf3, num_blocks, threads_per_block)
+
+
+def gpu_spgemm_f32(a: CSR_gpu, b: CSR_gpu, num_blocks: int = 256,
+                   threads_per_block: int = 256) -> CSR_gpu:
+    """Z_ik = sum_j a_ij b_jk (ESC SpGEMM), int32 result.  compiler.cpp:145-148."""
+    return _call("nacho_gpu_spgemm_f32", a, b, CSR_gpu, _csr_desc, _lib.CsrDesc, _adopt_csr,
+                 num_blocks, threads_per_block)
+
+
+def gpu_spgemm64_f32(a: CSR_gpu, b: CSR_gpu, num_blocks: int = 256,
+                     threads_per_block: int = 256) -> CSR64_gpu:
+    """The same product with int64 result offsets, for results beyond 2^31 entries."""
+    return _call("nacho_gpu_spgemm64_f32", a, b, CSR_gpu, _csr_desc, _lib.Csr64Desc,
+                 _adopt_csr64, num_blocks, threads_per_block)
+
+
+def set_kernel_timing(enable: bool) -> None:
+    _lib.load().nacho_set_kernel_timing(1 if enable else 0)
+
+
+def last_kernel_ms() -> float:
+    return float(_lib.load().nacho_last_kernel_ms())

@@ -1,0 +1,775 @@
+/*
+ * nacho_oracle.c — CPU restatement of the reference's kernels, used ONLY as a checker.
+ *
+ * TEST INFRASTRUCTURE.  Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+ * leg may load this library; the product (nacho_amd) never links or calls it.
+ *
+ * What is restated (own code, following the reference's generated CPU target):
+ *   - csr_union / csr_intersect: the CPU entry point of csr_add / csr_mul.  One merge-path
+ *     partition per hardware thread (stitch_and_generate_cpu.cpp:26-31, 138-154), then a
+ *     count pass, a serial exclusive scan over threads (156-215), result allocation with
+ *     pos[0] zeroed (stitch_and_generate.cpp:438-527) and a write pass.  The partition is the
+ *     reference's: count = t * per_thread_work with per_thread_work = total_work / T + 1 and
+ *     total_work = nnzA + nnzB (stitch_and_generate.cpp:90-112); boundary threads take
+ *     (0, -1, -1) / (rows, nnzA-1, nnzB-1) (partition.cpp:143-267, base_lowerer.cpp:79-110);
+ *     otherwise a binary search over rows on the work functions (partition.cpp:586-811,
+ *     tensor.cpp:162-440) followed by the balanced merge-path search inside the row
+ *     (partition.cpp:813-993).  Positions stored are "last consumed" (pos - 1).  The compute
+ *     pass walks rows start_i..end_i and merges with the union / intersection lattice
+ *     (compute.cpp:25-149, 619-1388): coordinates ascending, a+b / a*b where both exist,
+ *     copies otherwise (union only), explicit zeros kept, pos[i+1] written for every row a
+ *     thread finishes.
+ *   - coo_union / coo_intersect / coo3_union: the merged-coordinate lowering of COO
+ *     (Compile.cpp:66-154, tensor.cpp:447-577): the same pipeline over one level whose
+ *     coordinates are tuples compared lexicographically.
+ *   - csf3_union: the three-level union lattice (for i in A_i ∪ B_i, for j in A_ij ∪ B_ij,
+ *     for k in A_ijk ∪ B_ijk), emitted in lexicographic order; a fibre is appended to a level
+ *     when the loop body below it runs.  Serial restatement of the lattice; the reference's
+ *     nested partitioning (partition.cpp:286-461) only splits this work among threads.
+ *   - spgemm: the reference has no CPU SpGEMM (compiler.cpp:145-148 is GPU-only).  This is
+ *     the ESC semantics of its GPU path (stitch_and_generate_gpu.cpp:14-138, 257-366) run
+ *     row-parallel on the CPU: per row, expand a_ij * b_jk, sort by k, and sum runs.
+ *     Products are f32 (one IEEE multiply, as the reference), sums accumulate in f64 in
+ *     ascending (j) order and are rounded to f32 once.
+ */
+#include <pthread.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#include <unistd.h>
+
+#define ORC_OK 0
+#define ORC_ENOMEM (-3)
+#define ORC_EOVERFLOW (-2)
+
+/* ---------------------------------------------------------------------------------- */
+/* thread pool: run fn(t, arg) for t in [0, n) on n threads                              */
+
+typedef void (*task_fn)(int t, void *arg);
+typedef struct {
+    task_fn fn;
+    void *arg;
+    int t;
+} task;
+
+static void *task_main(void *p) {
+    task *k = (task *)p;
+    k->fn(k->t, k->arg);
+    return NULL;
+}
+
+static void parallel_for(int n, task_fn fn, void *arg) {
+    if (n <= 1) {
+        if (n == 1) fn(0, arg);
+        return;
+    }
+    pthread_t *th = (pthread_t *)malloc(sizeof(pthread_t) * (size_t)n);
+    task *ks = (task *)malloc(sizeof(task) * (size_t)n);
+    int started = 0;
+    for (int t = 1; t < n; ++t) {
+        ks[t].fn = fn;
+        ks[t].arg = arg;
+        ks[t].t = t;
+        if (pthread_create(&th[t], NULL, task_main, &ks[t]) == 0) {
+            ++started;
+        } else {
+            fn(t, arg); /* could not spawn: run inline */
+            th[t] = 0;
+        }
+    }
+    fn(0, arg);
+    for (int t = 1; t < n; ++t)
+        if (th[t]) pthread_join(th[t], NULL);
+    (void)started;
+    free(th);
+    free(ks);
+}
+
+int oracle_default_threads(void) {
+    long n = sysconf(_SC_NPROCESSORS_ONLN);
+    return n > 0 ? (int)n : 1;
+}
+
+void oracle_free(void *p) { free(p); }
+
+/* ---------------------------------------------------------------------------------- */
+/* CSR union / intersection                                                            */
+
+typedef struct {
+    /* operands */
+    int rows;
+    const int32_t *pa, *ca, *pb, *cb;
+    const float *va, *vb;
+    int nnz_a, nnz_b;
+    int intersect;
+    /* partition */
+    int nthreads;
+    long per_thread_work, total_work;
+    int *part_i, *part_a, *part_b; /* last-consumed positions */
+    long *count;                   /* per-thread output counts, then exclusive offsets */
+    /* result */
+    int32_t *pz, *cz;
+    float *vz;
+} csr_job;
+
+/* Work of rows [0, i) in one operand: the reference's work_ij_<t>_dim_i(t, i - 1) =
+ * pos[i] - pos[0] (tensor.cpp:162-440). */
+static long csr_work_rows(const int32_t *pos, int i) { return (long)pos[i] - pos[0]; }
+
+static void csr_partition(csr_job *J, int t) {
+    const long count = (long)t * J->per_thread_work;
+    if (count == 0) {
+        J->part_i[t] = 0;
+        J->part_a[t] = -1;
+        J->part_b[t] = -1;
+        return;
+    }
+    if (J->total_work <= count) {
+        J->part_i[t] = J->rows;
+        J->part_a[t] = J->nnz_a - 1;
+        J->part_b[t] = J->nnz_b - 1;
+        return;
+    }
+    /* Row search over the dense i level (not the last loop): mid = start + (end-start+1)/2,
+     * work of the rows before mid; keep the largest row whose preceding work < count. */
+    long rem = count;
+    int start = -1, end = J->rows - 1, i = 0;
+    for (;;) {
+        const int mid = start + (end - start + 1) / 2;
+        const long work = csr_work_rows(J->pa, mid) + csr_work_rows(J->pb, mid);
+        if (end <= start) {
+            i = mid;
+            rem -= work;
+            break;
+        }
+        if (work < rem) {
+            start = mid;
+        } else {
+            end = mid - 1;
+        }
+    }
+    /* Balanced merge-path inside row i over last-consumed positions. */
+    const int t1s = J->pa[i] - 1, t1e = J->pa[i + 1] - 1;
+    const int t2s = J->pb[i] - 1, t2e = J->pb[i + 1] - 1;
+    const int32_t *A = J->ca, *B = J->cb;
+    int sj = t1s, ej = t1e;
+    int t1 = sj + (ej - sj + 1) / 2;
+    int t2 = t2s + (int)(rem - (t1 - t1s));
+    while (sj < ej) {
+        t1 = sj + (ej - sj + 1) / 2;
+        t2 = t2s + (int)(rem - (t1 - t1s));
+        if (t2s <= t2 && t2 <= t2e) {
+            if (t2s < t2 && t1 + 1 <= t1e && A[t1 + 1] < B[t2]) {
+                sj = t1 + 1;
+            } else if (t1s < t1 && t2 + 1 <= t2e && B[t2 + 1] < A[t1]) {
+                ej = t1 - 1;
+            } else {
+                sj = t1;
+                ej = t1;
+            }
+        } else if (t2e < t2) {
+            sj = t1 + 1;
+        } else {
+            ej = t1 - 1;
+        }
+    }
+    t1 = sj + (ej - sj + 1) / 2;
+    t2 = t2s + (int)(rem - (t1 - t1s));
+    /* keep an equal pair in one partition */
+    if (t2s < t2 && t1 + 1 <= t1e && A[t1 + 1] == B[t2]) {
+        t1 += 1;
+    } else if (t1s < t1 && t2 + 1 <= t2e && B[t2 + 1] == A[t1]) {
+        t2 += 1;
+    }
+    J->part_i[t] = i;
+    J->part_a[t] = t1;
+    J->part_b[t] = t2;
+}
+
+static void csr_partition_task(int t, void *arg) { csr_partition((csr_job *)arg, t); }
+
+/* Walk thread t's share.  write == 0: count outputs.  write == 1: emit them at offset. */
+static long csr_walk(csr_job *J, int t, int write) {
+    const int T = J->nthreads;
+    const int start_i = J->part_i[t];
+    const int end_i = t < T - 1 ? J->part_i[t + 1] : J->rows;
+    const int start_a = J->part_a[t] + 1, start_b = J->part_b[t] + 1;
+    const int end_a = t < T - 1 ? J->part_a[t + 1] : J->nnz_a - 1; /* inclusive */
+    const int end_b = t < T - 1 ? J->part_b[t + 1] : J->nnz_b - 1;
+    long off = write ? J->count[t] : 0;
+    const long off0 = off;
+    for (int it = start_i; it <= end_i; ++it) {
+        if (it == J->rows) break;
+        int ia = (it == start_i) ? start_a : J->pa[it];
+        int ib = (it == start_i) ? start_b : J->pb[it];
+        const int sa = (it == end_i) ? end_a : J->pa[it + 1] - 1;
+        const int sb = (it == end_i) ? end_b : J->pb[it + 1] - 1;
+        while (ia <= sa && ib <= sb) {
+            const int32_t aj = J->ca[ia], bj = J->cb[ib];
+            const int32_t j = bj < aj ? bj : aj;
+            if (j == aj && j == bj) {
+                if (write) {
+                    J->cz[off] = j;
+                    J->vz[off] = J->intersect ? J->va[ia] * J->vb[ib] : J->va[ia] + J->vb[ib];
+                }
+                ++off;
+            } else if (!J->intersect && j == aj) {
+                if (write) {
+                    J->cz[off] = j;
+                    J->vz[off] = J->va[ia];
+                }
+                ++off;
+            } else if (!J->intersect && j == bj) {
+                if (write) {
+                    J->cz[off] = j;
+                    J->vz[off] = J->vb[ib];
+                }
+                ++off;
+            }
+            ia += (aj == j);
+            ib += (bj == j);
+        }
+        if (!J->intersect) {
+            for (; ia <= sa; ++ia) {
+                if (write) {
+                    J->cz[off] = J->ca[ia];
+                    J->vz[off] = J->va[ia];
+                }
+                ++off;
+            }
+            for (; ib <= sb; ++ib) {
+                if (write) {
+                    J->cz[off] = J->cb[ib];
+                    J->vz[off] = J->vb[ib];
+                }
+                ++off;
+            }
+        }
+        if (write && it < end_i) J->pz[it + 1] = (int32_t)off;
+    }
+    return off - off0;
+}
+
+static void csr_count_task(int t, void *arg) {
+    csr_job *J = (csr_job *)arg;
+    J->count[t] = csr_walk(J, t, 0);
+}
+
+static void csr_write_task(int t, void *arg) { (void)csr_walk((csr_job *)arg, t, 1); }
+
+/* Z = A (+|*) B over CSR.  Outputs are malloc'd (free with oracle_free).  Returns 0 or an
+ * error code.  nthreads <= 0 means one per online CPU. */
+int oracle_csr_binary(int intersect, int rows, const int32_t *pa, const int32_t *ca,
+                      const float *va, int nnz_a, const int32_t *pb, const int32_t *cb,
+                      const float *vb, int nnz_b, int nthreads, int32_t **out_pos,
+                      int32_t **out_crd, float **out_val, int *out_nnz) {
+    csr_job J;
+    memset(&J, 0, sizeof(J));
+    J.rows = rows;
+    J.pa = pa;
+    J.ca = ca;
+    J.va = va;
+    J.pb = pb;
+    J.cb = cb;
+    J.vb = vb;
+    J.nnz_a = nnz_a;
+    J.nnz_b = nnz_b;
+    J.intersect = intersect;
+    J.nthreads = nthreads > 0 ? nthreads : oracle_default_threads();
+    J.total_work = (long)nnz_a + nnz_b;
+    J.per_thread_work = J.total_work / J.nthreads + 1;
+    const int T = J.nthreads;
+    J.part_i = (int *)malloc(sizeof(int) * (size_t)T);
+    J.part_a = (int *)malloc(sizeof(int) * (size_t)T);
+    J.part_b = (int *)malloc(sizeof(int) * (size_t)T);
+    J.count = (long *)malloc(sizeof(long) * (size_t)T);
+    if (!J.part_i || !J.part_a || !J.part_b || !J.count) goto oom;
+
+    parallel_for(T, csr_partition_task, &J);
+    parallel_for(T, csr_count_task, &J);
+    long total = 0;
+    for (int t = 0; t < T; ++t) { /* serial exclusive scan over threads */
+        const long c = J.count[t];
+        J.count[t] = total;
+        total += c;
+    }
+    if (total > 0x7fffffffL) {
+        free(J.part_i);
+        free(J.part_a);
+        free(J.part_b);
+        free(J.count);
+        return ORC_EOVERFLOW;
+    }
+    J.pz = (int32_t *)malloc(sizeof(int32_t) * ((size_t)rows + 1));
+    J.cz = (int32_t *)malloc(sizeof(int32_t) * (size_t)(total > 0 ? total : 1));
+    J.vz = (float *)malloc(sizeof(float) * (size_t)(total > 0 ? total : 1));
+    if (!J.pz || !J.cz || !J.vz) goto oom;
+    if (total == 0) { /* empty result: zeroed offsets (stitch_and_generate.cpp:168-220) */
+        memset(J.pz, 0, sizeof(int32_t) * ((size_t)rows + 1));
+    }
+    J.pz[0] = 0;
+    if (total > 0) parallel_for(T, csr_write_task, &J);
+    free(J.part_i);
+    free(J.part_a);
+    free(J.part_b);
+    free(J.count);
+    *out_pos = J.pz;
+    *out_crd = J.cz;
+    *out_val = J.vz;
+    *out_nnz = (int)total;
+    return ORC_OK;
+oom:
+    free(J.part_i);
+    free(J.part_a);
+    free(J.part_b);
+    free(J.count);
+    free(J.pz);
+    free(J.cz);
+    free(J.vz);
+    return ORC_ENOMEM;
+}
+
+/* ---------------------------------------------------------------------------------- */
+/* COO (merged coordinate) union / intersection over 2- or 3-tuples                      */
+
+typedef struct {
+    int arity; /* 2 or 3 */
+    const int32_t *a[3], *b[3];
+    const float *va, *vb;
+    int nnz_a, nnz_b;
+    int intersect;
+    int nthreads;
+    long per_thread_work, total_work;
+    int *part_a, *part_b;
+    long *count;
+    int32_t *z[3];
+    float *vz;
+} coo_job;
+
+/* lexicographic compare of A[x] and B[y] */
+static int coo_cmp(const coo_job *J, int x, int y) {
+    for (int d = 0; d < J->arity; ++d) {
+        const int32_t p = J->a[d][x], q = J->b[d][y];
+        if (p != q) return p < q ? -1 : 1;
+    }
+    return 0;
+}
+
+static void coo_partition(coo_job *J, int t) {
+    const long count = (long)t * J->per_thread_work;
+    if (count == 0) {
+        J->part_a[t] = -1;
+        J->part_b[t] = -1;
+        return;
+    }
+    if (J->total_work <= count) {
+        J->part_a[t] = J->nnz_a - 1;
+        J->part_b[t] = J->nnz_b - 1;
+        return;
+    }
+    const long rem = count;
+    const int t1s = -1, t1e = J->nnz_a - 1, t2s = -1, t2e = J->nnz_b - 1;
+    int sj = t1s, ej = t1e;
+    int t1 = sj + (ej - sj + 1) / 2;
+    int t2 = t2s + (int)(rem - (t1 - t1s));
+    while (sj < ej) {
+        t1 = sj + (ej - sj + 1) / 2;
+        t2 = t2s + (int)(rem - (t1 - t1s));
+        if (t2s <= t2 && t2 <= t2e) {
+            if (t2s < t2 && t1 + 1 <= t1e && coo_cmp(J, t1 + 1, t2) < 0) {
+                sj = t1 + 1;
+            } else if (t1s < t1 && t2 + 1 <= t2e && coo_cmp(J, t1, t2 + 1) > 0) {
+                ej = t1 - 1;
+            } else {
+                sj = t1;
+                ej = t1;
+            }
+        } else if (t2e < t2) {
+            sj = t1 + 1;
+        } else {
+            ej = t1 - 1;
+        }
+    }
+    t1 = sj + (ej - sj + 1) / 2;
+    t2 = t2s + (int)(rem - (t1 - t1s));
+    if (t2s < t2 && t1 + 1 <= t1e && coo_cmp(J, t1 + 1, t2) == 0) {
+        t1 += 1;
+    } else if (t1s < t1 && t2 + 1 <= t2e && coo_cmp(J, t1, t2 + 1) == 0) {
+        t2 += 1;
+    }
+    J->part_a[t] = t1;
+    J->part_b[t] = t2;
+}
+
+static void coo_partition_task(int t, void *arg) { coo_partition((coo_job *)arg, t); }
+
+static void coo_emit(coo_job *J, long off, const int32_t *const *src, int idx, float v) {
+    for (int d = 0; d < J->arity; ++d) J->z[d][off] = src[d][idx];
+    J->vz[off] = v;
+}
+
+static long coo_walk(coo_job *J, int t, int write) {
+    const int T = J->nthreads;
+    int ia = J->part_a[t] + 1, ib = J->part_b[t] + 1;
+    const int sa = t < T - 1 ? J->part_a[t + 1] : J->nnz_a - 1;
+    const int sb = t < T - 1 ? J->part_b[t + 1] : J->nnz_b - 1;
+    long off = write ? J->count[t] : 0;
+    const long off0 = off;
+    while (ia <= sa && ib <= sb) {
+        const int c = coo_cmp(J, ia, ib);
+        if (c == 0) {
+            if (write)
+                coo_emit(J, off, J->a, ia,
+                         J->intersect ? J->va[ia] * J->vb[ib] : J->va[ia] + J->vb[ib]);
+            ++off;
+            ++ia;
+            ++ib;
+        } else if (c < 0) {
+            if (!J->intersect) {
+                if (write) coo_emit(J, off, J->a, ia, J->va[ia]);
+                ++off;
+            }
+            ++ia;
+        } else {
+            if (!J->intersect) {
+                if (write) coo_emit(J, off, J->b, ib, J->vb[ib]);
+                ++off;
+            }
+            ++ib;
+        }
+    }
+    if (!J->intersect) {
+        for (; ia <= sa; ++ia) {
+            if (write) coo_emit(J, off, J->a, ia, J->va[ia]);
+            ++off;
+        }
+        for (; ib <= sb; ++ib) {
+            if (write) coo_emit(J, off, J->b, ib, J->vb[ib]);
+            ++off;
+        }
+    }
+    return off - off0;
+}
+
+static void coo_count_task(int t, void *arg) {
+    coo_job *J = (coo_job *)arg;
+    J->count[t] = coo_walk(J, t, 0);
+}
+
+static void coo_write_task(int t, void *arg) { (void)coo_walk((coo_job *)arg, t, 1); }
+
+/* Z = A (+|*) B over COO tuples of `arity` (2 or 3) coordinates.  a_crd/b_crd hold `arity`
+ * coordinate arrays; out_crd receives `arity` malloc'd arrays. */
+int oracle_coo_binary(int intersect, int arity, const int32_t *const *a_crd, const float *va,
+                      int nnz_a, const int32_t *const *b_crd, const float *vb, int nnz_b,
+                      int nthreads, int32_t **out_crd, float **out_val, int *out_nnz) {
+    coo_job J;
+    memset(&J, 0, sizeof(J));
+    if (arity < 1 || arity > 3) return -1;
+    J.arity = arity;
+    for (int d = 0; d < arity; ++d) {
+        J.a[d] = a_crd[d];
+        J.b[d] = b_crd[d];
+    }
+    J.va = va;
+    J.vb = vb;
+    J.nnz_a = nnz_a;
+    J.nnz_b = nnz_b;
+    J.intersect = intersect;
+    J.nthreads = nthreads > 0 ? nthreads : oracle_default_threads();
+    J.total_work = (long)nnz_a + nnz_b;
+    J.per_thread_work = J.total_work / J.nthreads + 1;
+    const int T = J.nthreads;
+    J.part_a = (int *)malloc(sizeof(int) * (size_t)T);
+    J.part_b = (int *)malloc(sizeof(int) * (size_t)T);
+    J.count = (long *)malloc(sizeof(long) * (size_t)T);
+    if (!J.part_a || !J.part_b || !J.count) goto oom;
+    parallel_for(T, coo_partition_task, &J);
+    parallel_for(T, coo_count_task, &J);
+    long total = 0;
+    for (int t = 0; t < T; ++t) {
+        const long c = J.count[t];
+        J.count[t] = total;
+        total += c;
+    }
+    for (int d = 0; d < arity; ++d) {
+        J.z[d] = (int32_t *)malloc(sizeof(int32_t) * (size_t)(total > 0 ? total : 1));
+        if (!J.z[d]) goto oom;
+    }
+    J.vz = (float *)malloc(sizeof(float) * (size_t)(total > 0 ? total : 1));
+    if (!J.vz) goto oom;
+    if (total > 0) parallel_for(T, coo_write_task, &J);
+    free(J.part_a);
+    free(J.part_b);
+    free(J.count);
+    for (int d = 0; d < arity; ++d) out_crd[d] = J.z[d];
+    *out_val = J.vz;
+    *out_nnz = (int)total;
+    return ORC_OK;
+oom:
+    free(J.part_a);
+    free(J.part_b);
+    free(J.count);
+    for (int d = 0; d < 3; ++d) free(J.z[d]);
+    free(J.vz);
+    return ORC_ENOMEM;
+}
+
+/* ---------------------------------------------------------------------------------- */
+/* CSF3 union                                                                            */
+
+typedef struct {
+    int32_t *ci, *pj, *cj, *pk, *ck;
+    float *v;
+    long ni, nj, nk;
+} csf_out;
+
+/* Append the union of k-fibres A[ka0,ka1) and B[kb0,kb1); returns entries appended. */
+static long csf_k_union(csf_out *o, const int32_t *ak, const float *av, int ka0, int ka1,
+                        const int32_t *bk, const float *bv, int kb0, int kb1) {
+    long n0 = o->nk;
+    int x = ka0, y = kb0;
+    while (x < ka1 && y < kb1) {
+        if (ak[x] == bk[y]) {
+            o->ck[o->nk] = ak[x];
+            o->v[o->nk++] = av[x++] + bv[y++];
+        } else if (ak[x] < bk[y]) {
+            o->ck[o->nk] = ak[x];
+            o->v[o->nk++] = av[x++];
+        } else {
+            o->ck[o->nk] = bk[y];
+            o->v[o->nk++] = bv[y++];
+        }
+    }
+    for (; x < ka1; ++x) {
+        o->ck[o->nk] = ak[x];
+        o->v[o->nk++] = av[x];
+    }
+    for (; y < kb1; ++y) {
+        o->ck[o->nk] = bk[y];
+        o->v[o->nk++] = bv[y];
+    }
+    return o->nk - n0;
+}
+
+/* Z = A + B over CSF3.  Inputs: (crd_i[ni], pos_j[ni+1], crd_j[nj], pos_k[nj+1], crd_k[nk],
+ * val[nk]) per operand.  Output arrays are malloc'd with capacity ni_a+ni_b etc. */
+int oracle_csf3_union(const int32_t *a_ci, int a_ni, const int32_t *a_pj, const int32_t *a_cj,
+                      int a_nj, const int32_t *a_pk, const int32_t *a_ck, const float *a_v,
+                      int a_nk, const int32_t *b_ci, int b_ni, const int32_t *b_pj,
+                      const int32_t *b_cj, int b_nj, const int32_t *b_pk, const int32_t *b_ck,
+                      const float *b_v, int b_nk, int32_t **o_ci, int32_t **o_pj,
+                      int32_t **o_cj, int32_t **o_pk, int32_t **o_ck, float **o_v, int *o_ni,
+                      int *o_nj, int *o_nk) {
+    csf_out o;
+    memset(&o, 0, sizeof(o));
+    const size_t ci_cap = (size_t)a_ni + b_ni + 1, cj_cap = (size_t)a_nj + b_nj + 1,
+                 ck_cap = (size_t)a_nk + b_nk + 1;
+    o.ci = (int32_t *)malloc(sizeof(int32_t) * ci_cap);
+    o.pj = (int32_t *)malloc(sizeof(int32_t) * (ci_cap + 1));
+    o.cj = (int32_t *)malloc(sizeof(int32_t) * cj_cap);
+    o.pk = (int32_t *)malloc(sizeof(int32_t) * (cj_cap + 1));
+    o.ck = (int32_t *)malloc(sizeof(int32_t) * ck_cap);
+    o.v = (float *)malloc(sizeof(float) * ck_cap);
+    if (!o.ci || !o.pj || !o.cj || !o.pk || !o.ck || !o.v) {
+        free(o.ci);
+        free(o.pj);
+        free(o.cj);
+        free(o.pk);
+        free(o.ck);
+        free(o.v);
+        return ORC_ENOMEM;
+    }
+    o.pj[0] = 0;
+    o.pk[0] = 0;
+    int ia = 0, ib = 0;
+    while (ia < a_ni || ib < b_ni) {
+        int i;
+        int ha = ia < a_ni, hb = ib < b_ni;
+        if (ha && hb) {
+            i = a_ci[ia] < b_ci[ib] ? a_ci[ia] : b_ci[ib];
+            ha = a_ci[ia] == i;
+            hb = b_ci[ib] == i;
+        } else {
+            i = ha ? a_ci[ia] : b_ci[ib];
+        }
+        /* j-level union inside fibre i */
+        int ja = ha ? a_pj[ia] : 0, jae = ha ? a_pj[ia + 1] : 0;
+        int jb = hb ? b_pj[ib] : 0, jbe = hb ? b_pj[ib + 1] : 0;
+        const long nj0 = o.nj;
+        while (ja < jae || jb < jbe) {
+            int j;
+            int ga = ja < jae, gb = jb < jbe;
+            if (ga && gb) {
+                j = a_cj[ja] < b_cj[jb] ? a_cj[ja] : b_cj[jb];
+                ga = a_cj[ja] == j;
+                gb = b_cj[jb] == j;
+            } else {
+                j = ga ? a_cj[ja] : b_cj[jb];
+            }
+            csf_k_union(&o, a_ck, a_v, ga ? a_pk[ja] : 0, ga ? a_pk[ja + 1] : 0, b_ck, b_v,
+                        gb ? b_pk[jb] : 0, gb ? b_pk[jb + 1] : 0);
+            o.cj[o.nj++] = j;
+            o.pk[o.nj] = (int32_t)o.nk;
+            ja += ga;
+            jb += gb;
+        }
+        (void)nj0;
+        o.ci[o.ni++] = i;
+        o.pj[o.ni] = (int32_t)o.nj;
+        ia += ha;
+        ib += hb;
+    }
+    *o_ci = o.ci;
+    *o_pj = o.pj;
+    *o_cj = o.cj;
+    *o_pk = o.pk;
+    *o_ck = o.ck;
+    *o_v = o.v;
+    *o_ni = (int)o.ni;
+    *o_nj = (int)o.nj;
+    *o_nk = (int)o.nk;
+    return ORC_OK;
+}
+
+/* ---------------------------------------------------------------------------------- */
+/* SpGEMM (ESC semantics, row-parallel)                                                  */
+
+typedef struct {
+    int rows, cols;
+    const int32_t *pa, *ca, *pb, *cb;
+    const float *va, *vb;
+    int nthreads;
+    int64_t *row_nnz; /* symbolic: distinct k per row, then exclusive offsets */
+    int64_t *pz;
+    int32_t *cz;
+    float *vz;
+    int64_t rows_per_chunk;
+    int phase;
+} sp_job;
+
+/* Per-thread dense accumulator over k (an SPA): the row's distinct columns are the keys of
+ * the expanded products; emitting them in ascending k order is the sort + compress. */
+typedef struct {
+    double *acc;
+    int32_t *mark; /* row id + 1 that last touched k */
+    int32_t *keys;
+} spa;
+
+static int cmp_i32(const void *x, const void *y) {
+    const int32_t p = *(const int32_t *)x, q = *(const int32_t *)y;
+    return (p > q) - (p < q);
+}
+
+static void sp_row_range(sp_job *J, int t, int *r0, int *r1) {
+    const long per = (J->rows + J->nthreads - 1) / J->nthreads;
+    long s = (long)t * per, e = s + per;
+    if (s > J->rows) s = J->rows;
+    if (e > J->rows) e = J->rows;
+    *r0 = (int)s;
+    *r1 = (int)e;
+}
+
+static void sp_task(int t, void *arg) {
+    sp_job *J = (sp_job *)arg;
+    int r0, r1;
+    sp_row_range(J, t, &r0, &r1);
+    if (r0 >= r1) return;
+    spa s;
+    s.acc = (double *)calloc((size_t)J->cols + 1, sizeof(double));
+    s.mark = (int32_t *)calloc((size_t)J->cols + 1, sizeof(int32_t));
+    s.keys = (int32_t *)malloc(sizeof(int32_t) * ((size_t)J->cols + 1));
+    if (!s.acc || !s.mark || !s.keys) {
+        free(s.acc);
+        free(s.mark);
+        free(s.keys);
+        for (int r = r0; r < r1; ++r) J->row_nnz[r] = -1;
+        return;
+    }
+    for (int r = r0; r < r1; ++r) {
+        int nkeys = 0;
+        for (int p = J->pa[r]; p < J->pa[r + 1]; ++p) {
+            const int j = J->ca[p];
+            const float a = J->va[p];
+            for (int q = J->pb[j]; q < J->pb[j + 1]; ++q) {
+                const int k = J->cb[q];
+                if (s.mark[k] != r + 1) {
+                    s.mark[k] = r + 1;
+                    s.acc[k] = 0.0;
+                    s.keys[nkeys++] = k;
+                }
+                if (J->phase == 1) s.acc[k] += (double)(a * J->vb[q]); /* f32 product */
+            }
+        }
+        if (J->phase == 0) {
+            J->row_nnz[r] = nkeys;
+            continue;
+        }
+        qsort(s.keys, (size_t)nkeys, sizeof(int32_t), cmp_i32);
+        int64_t off = J->pz[r];
+        for (int x = 0; x < nkeys; ++x) {
+            J->cz[off] = s.keys[x];
+            J->vz[off] = (float)s.acc[s.keys[x]];
+            ++off;
+        }
+    }
+    free(s.acc);
+    free(s.mark);
+    free(s.keys);
+}
+
+/* Z = A B (rows x cols result).  Offsets are int64.  Returns 0 or error. */
+int oracle_spgemm(int rows, int inner, int cols, const int32_t *pa, const int32_t *ca,
+                  const float *va, const int32_t *pb, const int32_t *cb, const float *vb,
+                  int nthreads, int64_t **out_pos, int32_t **out_crd, float **out_val,
+                  int64_t *out_nnz) {
+    (void)inner;
+    sp_job J;
+    memset(&J, 0, sizeof(J));
+    J.rows = rows;
+    J.cols = cols;
+    J.pa = pa;
+    J.ca = ca;
+    J.va = va;
+    J.pb = pb;
+    J.cb = cb;
+    J.vb = vb;
+    J.nthreads = nthreads > 0 ? nthreads : oracle_default_threads();
+    J.row_nnz = (int64_t *)malloc(sizeof(int64_t) * ((size_t)rows + 1));
+    J.pz = (int64_t *)malloc(sizeof(int64_t) * ((size_t)rows + 1));
+    if (!J.row_nnz || !J.pz) {
+        free(J.row_nnz);
+        free(J.pz);
+        return ORC_ENOMEM;
+    }
+    J.phase = 0; /* symbolic */
+    parallel_for(J.nthreads, sp_task, &J);
+    int64_t total = 0;
+    for (int r = 0; r < rows; ++r) {
+        if (J.row_nnz[r] < 0) {
+            free(J.row_nnz);
+            free(J.pz);
+            return ORC_ENOMEM;
+        }
+        J.pz[r] = total;
+        total += J.row_nnz[r];
+    }
+    J.pz[rows] = total;
+    J.cz = (int32_t *)malloc(sizeof(int32_t) * (size_t)(total > 0 ? total : 1));
+    J.vz = (float *)malloc(sizeof(float) * (size_t)(total > 0 ? total : 1));
+    if (!J.cz || !J.vz) {
+        free(J.row_nnz);
+        free(J.pz);
+        free(J.cz);
+        free(J.vz);
+        return ORC_ENOMEM;
+    }
+    J.phase = 1; /* numeric */
+    parallel_for(J.nthreads, sp_task, &J);
+    free(J.row_nnz);
+    *out_pos = J.pz;
+    *out_crd = J.cz;
+    *out_val = J.vz;
+    *out_nnz = total;
+    return ORC_OK;
+}

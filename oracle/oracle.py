@@ -1,0 +1,288 @@
+"""CPU oracle for the nacho GPU path — TEST INFRASTRUCTURE, never the product.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this module, and
+only as the checker.  Two independent kinds of reference live here:
+
+1. `port_*`: ctypes bindings to nacho_oracle.c, the C restatement of the reference's
+   generated CPU pipeline (per-thread merge-path partition, count, serial scan, write).
+   Each function's file:line anchors are in nacho_oracle.c.
+2. `closed_*`: numpy closed forms of the same results, derived from the mathematics only
+   (sorted union / intersection of coordinate keys, lexsort + run-length reduce), used to
+   pin (1) — a mistake in the partitioning, lattice or scan of (1) fails against (2).
+
+Parity status of each function (how it is pinned) is recorded in the test modules and in
+the repository's design notes: csr/coo/coo3/csf union and intersection are pinned by the
+closed forms, by scipy, by brute force on tiny inputs and by the reference's own smoke
+cases (tests/smoke.py semantics); spgemm is pinned by a float64 scipy product.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+ORACLE_DIR = Path(__file__).resolve().parent
+LIBRARY = ORACLE_DIR / "liboracle.so"
+
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_i64p = ctypes.POINTER(ctypes.c_int64)
+_f32p = ctypes.POINTER(ctypes.c_float)
+
+_lib = None
+
+
+def build() -> Path:
+    """Compile nacho_oracle.c with gcc (always rebuilds)."""
+    subprocess.run(["make", "-B", "-s", "-C", str(ORACLE_DIR), "liboracle.so"], check=True)
+    return LIBRARY
+
+
+def load() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIBRARY.exists():
+            build()
+        lib = ctypes.CDLL(str(LIBRARY))
+        lib.oracle_free.argtypes = [ctypes.c_void_p]
+        lib.oracle_free.restype = None
+        lib.oracle_default_threads.restype = ctypes.c_int
+        lib.oracle_csr_binary.restype = ctypes.c_int
+        lib.oracle_csr_binary.argtypes = [
+            ctypes.c_int, ctypes.c_int, _i32p, _i32p, _f32p, ctypes.c_int, _i32p, _i32p, _f32p,
+            ctypes.c_int, ctypes.c_int, ctypes.POINTER(_i32p), ctypes.POINTER(_i32p),
+            ctypes.POINTER(_f32p), ctypes.POINTER(ctypes.c_int)]
+        lib.oracle_coo_binary.restype = ctypes.c_int
+        lib.oracle_coo_binary.argtypes = [
+            ctypes.c_int, ctypes.c_int, ctypes.POINTER(_i32p), _f32p, ctypes.c_int,
+            ctypes.POINTER(_i32p), _f32p, ctypes.c_int, ctypes.c_int, ctypes.POINTER(_i32p),
+            ctypes.POINTER(_f32p), ctypes.POINTER(ctypes.c_int)]
+        lib.oracle_csf3_union.restype = ctypes.c_int
+        lib.oracle_csf3_union.argtypes = (
+            [_i32p, ctypes.c_int, _i32p, _i32p, ctypes.c_int, _i32p, _i32p, _f32p, ctypes.c_int]
+            * 2 + [ctypes.POINTER(_i32p)] * 5 + [ctypes.POINTER(_f32p)]
+            + [ctypes.POINTER(ctypes.c_int)] * 3)
+        lib.oracle_spgemm.restype = ctypes.c_int
+        lib.oracle_spgemm.argtypes = [
+            ctypes.c_int, ctypes.c_int, ctypes.c_int, _i32p, _i32p, _f32p, _i32p, _i32p, _f32p,
+            ctypes.c_int, ctypes.POINTER(_i64p), ctypes.POINTER(_i32p), ctypes.POINTER(_f32p),
+            ctypes.POINTER(ctypes.c_int64)]
+        _lib = lib
+    return _lib
+
+
+def _as(arr, dtype):
+    a = np.ascontiguousarray(arr, dtype=dtype)
+    if a.size == 0:  # never hand C a null pointer for an empty array
+        a = np.zeros(1, dtype=dtype)
+    return a
+
+
+def _ptr(a, ctype):
+    return a.ctypes.data_as(ctypes.POINTER(ctype))
+
+
+def _take(ptr, n, dtype):
+    """Copy n elements from a malloc'd C array into numpy, then free it."""
+    lib = load()
+    out = np.ctypeslib.as_array(ptr, shape=(max(n, 1),))[:n].astype(dtype, copy=True)
+    lib.oracle_free(ctypes.cast(ptr, ctypes.c_void_p))
+    return out
+
+
+def threads() -> int:
+    return int(load().oracle_default_threads())
+
+
+# ---- (1) C restatement of the reference pipeline --------------------------------------
+
+def port_csr_binary(op, rows, pa, ca, va, pb, cb, vb, nthreads=0, timing=None):
+    """op in {"add", "mul"}: returns (pos int32, crd int32, val float32).  If `timing` is a
+    dict, timing["seconds"] receives the duration of the C call alone."""
+    import time
+
+    lib = load()
+    keep = [_as(pa, np.int32), _as(ca, np.int32), _as(va, np.float32),
+            _as(pb, np.int32), _as(cb, np.int32), _as(vb, np.float32)]
+    opos, ocrd, oval, onnz = _i32p(), _i32p(), _f32p(), ctypes.c_int()
+    t0 = time.perf_counter()
+    rc = lib.oracle_csr_binary(
+        1 if op == "mul" else 0, int(rows),
+        _ptr(keep[0], ctypes.c_int32), _ptr(keep[1], ctypes.c_int32),
+        _ptr(keep[2], ctypes.c_float), int(len(ca)),
+        _ptr(keep[3], ctypes.c_int32), _ptr(keep[4], ctypes.c_int32),
+        _ptr(keep[5], ctypes.c_float), int(len(cb)), int(nthreads),
+        ctypes.byref(opos), ctypes.byref(ocrd), ctypes.byref(oval), ctypes.byref(onnz))
+    if timing is not None:
+        timing["seconds"] = time.perf_counter() - t0
+    if rc != 0:
+        raise RuntimeError(f"oracle_csr_binary failed ({rc})")
+    n = onnz.value
+    return (_take(opos, rows + 1, np.int32), _take(ocrd, n, np.int32),
+            _take(oval, n, np.float32))
+
+
+def port_coo_binary(op, a_crd, va, b_crd, vb, nthreads=0):
+    """a_crd / b_crd: tuple of 2 or 3 int arrays (lexicographically sorted, distinct)."""
+    lib = load()
+    arity = len(a_crd)
+    a = [_as(x, np.int32) for x in a_crd]
+    b = [_as(x, np.int32) for x in b_crd]
+    fa, fb = _as(va, np.float32), _as(vb, np.float32)
+    arr_t = _i32p * 3
+    ap = arr_t(*[_ptr(x, ctypes.c_int32) for x in a] + [None] * (3 - arity))
+    bp = arr_t(*[_ptr(x, ctypes.c_int32) for x in b] + [None] * (3 - arity))
+    out = arr_t()
+    oval, onnz = _f32p(), ctypes.c_int()
+    rc = lib.oracle_coo_binary(1 if op == "mul" else 0, arity, ap, _ptr(fa, ctypes.c_float),
+                               int(len(va)), bp, _ptr(fb, ctypes.c_float), int(len(vb)),
+                               int(nthreads), out, ctypes.byref(oval), ctypes.byref(onnz))
+    if rc != 0:
+        raise RuntimeError(f"oracle_coo_binary failed ({rc})")
+    n = onnz.value
+    crd = tuple(_take(out[d], n, np.int32) for d in range(arity))
+    return crd, _take(oval, n, np.float32)
+
+
+def port_csf3_union(a_levels, a_val, b_levels, b_val):
+    """levels = (crd_i, pos_j, crd_j, pos_k, crd_k).  Returns (levels, val)."""
+    lib = load()
+
+    def prep(levels, val):
+        ci, pj, cj, pk, ck = (_as(x, np.int32) for x in levels)
+        v = _as(val, np.float32)
+        return (ci, len(levels[0]), pj, cj, len(levels[2]), pk, ck, v, len(levels[4]))
+
+    pa, pb = prep(a_levels, a_val), prep(b_levels, b_val)
+
+    def args(p):
+        ci, ni, pj, cj, nj, pk, ck, v, nk = p
+        return [_ptr(ci, ctypes.c_int32), ni, _ptr(pj, ctypes.c_int32), _ptr(cj, ctypes.c_int32),
+                nj, _ptr(pk, ctypes.c_int32), _ptr(ck, ctypes.c_int32), _ptr(v, ctypes.c_float),
+                nk]
+
+    outs = [_i32p() for _ in range(5)]
+    oval = _f32p()
+    ns = [ctypes.c_int() for _ in range(3)]
+    rc = lib.oracle_csf3_union(*args(pa), *args(pb), *[ctypes.byref(o) for o in outs],
+                               ctypes.byref(oval), *[ctypes.byref(n) for n in ns])
+    if rc != 0:
+        raise RuntimeError(f"oracle_csf3_union failed ({rc})")
+    ni, nj, nk = (n.value for n in ns)
+    levels = (_take(outs[0], ni, np.int32), _take(outs[1], ni + 1, np.int32),
+              _take(outs[2], nj, np.int32), _take(outs[3], nj + 1, np.int32),
+              _take(outs[4], nk, np.int32))
+    return levels, _take(oval, nk, np.float32)
+
+
+def port_spgemm(rows, inner, cols, pa, ca, va, pb, cb, vb, nthreads=0):
+    """ESC semantics on the CPU: returns (pos int64, crd int32, val float32)."""
+    lib = load()
+    keep = [_as(pa, np.int32), _as(ca, np.int32), _as(va, np.float32),
+            _as(pb, np.int32), _as(cb, np.int32), _as(vb, np.float32)]
+    opos, ocrd, oval, onnz = _i64p(), _i32p(), _f32p(), ctypes.c_int64()
+    rc = lib.oracle_spgemm(int(rows), int(inner), int(cols),
+                           _ptr(keep[0], ctypes.c_int32), _ptr(keep[1], ctypes.c_int32),
+                           _ptr(keep[2], ctypes.c_float), _ptr(keep[3], ctypes.c_int32),
+                           _ptr(keep[4], ctypes.c_int32), _ptr(keep[5], ctypes.c_float),
+                           int(nthreads), ctypes.byref(opos), ctypes.byref(ocrd),
+                           ctypes.byref(oval), ctypes.byref(onnz))
+    if rc != 0:
+        raise RuntimeError(f"oracle_spgemm failed ({rc})")
+    n = onnz.value
+    return (_take(opos, rows + 1, np.int64), _take(ocrd, n, np.int32),
+            _take(oval, n, np.float32))
+
+
+# ---- (2) closed forms from the mathematics --------------------------------------------
+
+def _rows_of(pos):
+    pos = np.asarray(pos, dtype=np.int64)
+    return np.repeat(np.arange(len(pos) - 1, dtype=np.int64), np.diff(pos))
+
+
+def _lookup(src_keys, src_vals, keys):
+    """(present mask, value where present) of sorted `keys` in sorted `src_keys`."""
+    if len(src_keys) == 0:
+        return np.zeros(len(keys), bool), np.zeros(len(keys), np.float32)
+    idx = np.searchsorted(src_keys, keys)
+    idx_c = np.minimum(idx, len(src_keys) - 1)
+    hit = (idx < len(src_keys)) & (src_keys[idx_c] == keys)
+    return hit, np.where(hit, src_vals[idx_c], np.float32(0)).astype(np.float32)
+
+
+def _combine_keys(op, ka, va, kb, vb):
+    """Sorted result keys and f32 values of the union (add) / intersection (mul)."""
+    va = np.asarray(va, np.float32)
+    vb = np.asarray(vb, np.float32)
+    keys = np.union1d(ka, kb) if op == "add" else np.intersect1d(ka, kb, assume_unique=True)
+    hit_a, xa = _lookup(ka, va, keys)
+    hit_b, xb = _lookup(kb, vb, keys)
+    both = hit_a & hit_b
+    if op == "add":
+        val = np.where(both, xa + xb, np.where(hit_a, xa, xb))  # one f32 add or a copy
+    else:
+        val = xa * xb  # one f32 multiply
+    return keys, val.astype(np.float32)
+
+
+def closed_csr_binary(op, rows, cols, pa, ca, va, pb, cb, vb):
+    """Union (add) or intersection (mul) of the (row, col) key sets; values by one f32 op.
+    Explicit zeros are kept (no pruning)."""
+    width = int(cols) + 1
+    ka = _rows_of(pa) * width + np.asarray(ca, np.int64)
+    kb = _rows_of(pb) * width + np.asarray(cb, np.int64)
+    keys, val = _combine_keys(op, ka, va, kb, vb)
+    r = keys // width
+    crd = (keys % width).astype(np.int32)
+    pos = np.zeros(int(rows) + 1, np.int64)
+    np.add.at(pos, r + 1, 1)
+    return np.cumsum(pos).astype(np.int32), crd, val
+
+
+def _tuple_keys(crd, shape):
+    k = np.zeros(len(crd[0]), dtype=np.int64)
+    for c, n in zip(crd, shape):
+        k = k * (int(n) + 1) + np.asarray(c, np.int64)
+    return k
+
+
+def closed_coo_binary(op, shape, a_crd, va, b_crd, vb):
+    """Union / intersection of coordinate tuples (keys packed in int64; shape must allow)."""
+    bits = sum(int(np.ceil(np.log2(int(n) + 2))) for n in shape)
+    if bits > 62:
+        raise ValueError("shape too large for packed keys")
+    keys, val = _combine_keys(op, _tuple_keys(a_crd, shape), va, _tuple_keys(b_crd, shape), vb)
+    crd = []
+    rest = keys.copy()
+    for n in reversed(shape):
+        crd.append((rest % (int(n) + 1)).astype(np.int32))
+        rest //= (int(n) + 1)
+    return tuple(reversed(crd)), val
+
+
+def closed_spgemm_f64(rows, inner, cols, pa, ca, va, pb, cb, vb):
+    """C = A B in float64 from f32 products (scipy), structure without pruning."""
+    import scipy.sparse as sp
+
+    a = sp.csr_matrix((np.asarray(va, np.float64), np.asarray(ca), np.asarray(pa)),
+                      shape=(rows, inner))
+    b = sp.csr_matrix((np.asarray(vb, np.float64), np.asarray(cb), np.asarray(pb)),
+                      shape=(inner, cols))
+    # pattern product (ones) gives the exact structure even where values cancel
+    pat = (sp.csr_matrix((np.ones(len(ca)), np.asarray(ca), np.asarray(pa)), shape=(rows, inner))
+           @ sp.csr_matrix((np.ones(len(cb)), np.asarray(cb), np.asarray(pb)),
+                           shape=(inner, cols)))
+    pat.sort_indices()
+    c = (a @ b).tocsr()
+    c.sort_indices()
+    # align values onto the pattern (cancellation can drop entries from c)
+    vals = np.zeros(pat.nnz, np.float64)
+    pr = _rows_of(pat.indptr)
+    cr = _rows_of(c.indptr)
+    kp = pr * (cols + 1) + pat.indices
+    kc = cr * (cols + 1) + c.indices
+    vals[np.searchsorted(kp, kc)] = c.data
+    return pat.indptr.astype(np.int64), pat.indices.astype(np.int32), vals

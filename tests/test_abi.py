@@ -1,0 +1,101 @@
+"""The C ABI library loads and exports every function include/nacho_hip.h declares.
+
+Runs on the CPU: only argument-validation paths are called (they return before any HIP
+call), no kernels.
+"""
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+REPO = Path(__file__).resolve().parent.parent
+HEADER = REPO / "include" / "nacho_hip.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(nacho_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from nacho_amd import _lib
+
+    return _lib.load()
+
+
+def test_header_declares_entry_points():
+    names = declared_functions()
+    assert "nacho_gpu_csr_add_f32" in names and "nacho_gpu_csr_mul_f32" in names
+    assert "nacho_free" in names and "nacho_error_string" in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    from nacho_amd import _lib
+
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIBRARY_PATH)],
+                         capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (nacho_\w+)", out))
+    missing = [n for n in declared_functions() if n not in exported]
+    assert not missing, f"declared but not exported: {missing}"
+    for name in declared_functions():
+        assert getattr(lib, name) is not None
+
+
+def test_python_bindings_cover_every_gpu_entry_point():
+    from nacho_amd import _lib
+
+    gpu = [n for n in declared_functions() if n.startswith("nacho_gpu_")]
+    assert set(gpu) <= set(_lib.ENTRY_POINTS), set(gpu) - set(_lib.ENTRY_POINTS)
+
+
+def test_error_strings(lib):
+    from nacho_amd import _lib
+
+    assert _lib.error_string(0) == "success"
+    assert "invalid" in _lib.error_string(-1)
+    assert "int32" in _lib.error_string(-2)
+    assert lib.nacho_version().decode().startswith("nacho-mi355x")
+
+
+def test_invalid_arguments_rejected_without_a_device(lib):
+    from nacho_amd import _lib
+
+    z = _lib.CsrDesc()
+    good = _lib.CsrDesc(4, 4, ctypes.c_void_p(0x1000), 0, None, None, 0)
+    fn = lib.nacho_gpu_csr_add_f32
+    # null operand
+    assert fn(None, ctypes.byref(good), ctypes.byref(z), 256, 256, None, None) == -1
+    # null result
+    assert fn(ctypes.byref(good), ctypes.byref(good), None, 256, 256, None, None) == -1
+    # bad launch hints (the reference's num_blocks / threads_per_block)
+    assert fn(ctypes.byref(good), ctypes.byref(good), ctypes.byref(z), 0, 256, None, None) == -1
+    assert fn(ctypes.byref(good), ctypes.byref(good), ctypes.byref(z), 256, -1, None, None) == -1
+    # shape mismatch
+    other = _lib.CsrDesc(5, 4, ctypes.c_void_p(0x1000), 0, None, None, 0)
+    assert fn(ctypes.byref(good), ctypes.byref(other), ctypes.byref(z), 256, 256, None,
+              None) == -1
+    # missing crd with a positive length
+    bad = _lib.CsrDesc(4, 4, ctypes.c_void_p(0x1000), 3, None, None, 3)
+    assert lib.nacho_gpu_csr_mul_f32(ctypes.byref(bad), ctypes.byref(good), ctypes.byref(z),
+                                     256, 256, None, None) == -1
+    # int32 overflow of the work count is refused before any allocation
+    huge = _lib.CsrDesc(2**31 - 2, 4, ctypes.c_void_p(0x1000), 2**30, ctypes.c_void_p(0x2000),
+                        ctypes.c_void_p(0x3000), 2**30)
+    assert fn(ctypes.byref(huge), ctypes.byref(huge), ctypes.byref(z), 256, 256, None,
+              None) == -2
+    assert z.dim_j_offsets is None and z.nnz == 0
+
+
+def test_struct_layouts_match_the_header():
+    """ctypes mirrors of the descriptors have the C layout (offsets of pointer fields)."""
+    from nacho_amd import _lib
+
+    assert _lib.CsrDesc.dim_j_offsets.offset == 8
+    assert _lib.CsrDesc.dim_j_indices.offset == 24
+    assert ctypes.sizeof(_lib.CsrDesc) == 48
+    assert ctypes.sizeof(_lib.Csr64Desc) == 48
