@@ -158,6 +158,24 @@ int nacho_gpu_csr_mul_f32(const nacho_csr *a, const nacho_csr *b, nacho_csr *z,
                           int32_t num_blocks, int32_t threads_per_block, void *stream,
                           const nacho_allocator *alloc);
 
+/* Z = a + b over COO (union of (i, j) tuples).  Replaces coo_add::coo_add_gpu_i32_f32
+ * (compiler.cpp:118). */
+int nacho_gpu_coo_add_f32(const nacho_coo *a, const nacho_coo *b, nacho_coo *z,
+                          int32_t num_blocks, int32_t threads_per_block, void *stream,
+                          const nacho_allocator *alloc);
+
+/* Z = a * b over COO (intersection of (i, j) tuples).  Replaces coo_mul::coo_mul_gpu_i32_f32
+ * (compiler.cpp:120). */
+int nacho_gpu_coo_mul_f32(const nacho_coo *a, const nacho_coo *b, nacho_coo *z,
+                          int32_t num_blocks, int32_t threads_per_block, void *stream,
+                          const nacho_allocator *alloc);
+
+/* Z = a + b over COO3 (union of (i, j, k) tuples).  Replaces
+ * coo3d_add::coo3d_add_gpu_i32_f32 (compiler.cpp:138). */
+int nacho_gpu_coo3d_add_f32(const nacho_coo3 *a, const nacho_coo3 *b, nacho_coo3 *z,
+                            int32_t num_blocks, int32_t threads_per_block, void *stream,
+                            const nacho_allocator *alloc);
+
 /* ---- diagnostics ------------------------------------------------------------------ */
 
 /* Static string naming an error code (HIP codes use hipGetErrorString). */

@@ -13,6 +13,7 @@ from __future__ import annotations
 import ctypes
 
 import torch
+import torch.utils.dlpack
 
 from . import _lib
 
@@ -130,8 +131,6 @@ def adopt(ptr: int | None, count: int, dtype: torch.dtype, device: torch.device,
                     raise
                 tensor = None
         if tensor is None:
-            import torch.utils.dlpack  # noqa: F401
-
             tensor = _adopt_dlpack(owner, device)
             _ROUTE = "dlpack"
     if tensor.data_ptr() != ptr or tensor.numel() != count or tensor.dtype != dtype:
