@@ -18,8 +18,8 @@
  * released and the result descriptor is left zeroed.  nacho_error_string() names a code.
  *
  * Ownership: operands are borrowed and never written.  Result buffers are allocated by
- * `alloc` (or by the library's stream-ordered pool when `alloc` is NULL, in which case the
- * caller releases them with nacho_free()).  A result array of length 0 is a NULL pointer.
+ * `alloc` (or by the library's caching device allocator when `alloc` is NULL, in which case
+ * the caller releases them with nacho_free()).  A result array of length 0 is a NULL pointer.
  *
  * Input contract (the reference's, made explicit): pos[0] == 0, pos non-decreasing,
  * pos[rows] == length of the coordinate array, coordinates strictly increasing within
@@ -137,6 +137,10 @@ typedef struct nacho_allocator {
 /* Release a buffer that an entry point allocated with the default allocator (alloc == NULL).
  * Stream-ordered on `stream`.  Replaces cudaFreeWrapper (runtime/cuda_utils/cuda_utils.cu:7-11). */
 int nacho_free(void *ptr, void *stream);
+
+/* The default allocator keeps freed buffers cached for reuse by later calls (per size class,
+ * stream-ordered).  This returns every cached, unused buffer to the driver. */
+int nacho_release_cached_memory(void);
 
 /* ---- entry points ------------------------------------------------------------------
  * `num_blocks` / `threads_per_block` are the reference's launch arguments

@@ -131,6 +131,8 @@ def load() -> ctypes.CDLL:
                        ctypes.POINTER(Allocator)]
     lib.nacho_free.restype = ctypes.c_int
     lib.nacho_free.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    lib.nacho_release_cached_memory.restype = ctypes.c_int
+    lib.nacho_release_cached_memory.argtypes = []
     lib.nacho_error_string.restype = ctypes.c_char_p
     lib.nacho_error_string.argtypes = [ctypes.c_int]
     lib.nacho_version.restype = ctypes.c_char_p

@@ -41,7 +41,7 @@ namespace csr {
 enum class Op { Union, Intersect };
 
 constexpr int kBlock = 256;
-constexpr int kItemsPerLane = 8;
+constexpr int kItemsPerLane = 15;  // odd: lanes' LDS walks spread over banks
 constexpr int kTile = kBlock * kItemsPerLane;
 
 // Per-call info words in scratch, cleared by the partition kernel:
@@ -108,199 +108,266 @@ __global__ __launch_bounds__(256) void csr_partition_kernel(
     split_b[t] = b;
 }
 
-template <Op OP>
+// Tile inputs staged in LDS: A's crd/val range then B's, and one packed word per row of the
+// tile: (max(posA[r], a0) - a0) | (max(posB[r], b0) - b0) << 16.
+struct TileSplit {
+    int r0, a0, b0, r1, a1, b1;
+};
+
+__device__ __forceinline__ TileSplit load_split(const int *__restrict__ split_r,
+                                                const int *__restrict__ split_a,
+                                                const int *__restrict__ split_b, int tile) {
+    return TileSplit{split_r[tile], split_a[tile], split_b[tile],
+                     split_r[tile + 1], split_a[tile + 1], split_b[tile + 1]};
+}
+
+// Registers of one lane's share of a tile's staged inputs (prefetched one tile ahead).
+template <int LOADS>
+struct Staged {
+    int crd[LOADS];
+    float val[LOADS];
+    unsigned row[LOADS];
+};
+
+template <bool VALUES, int LOADS>
+__device__ __forceinline__ void fetch_tile(Staged<LOADS> &st, const TileSplit &sp,
+                                           const int *__restrict__ pa, const int *__restrict__ ca,
+                                           const float *__restrict__ va,
+                                           const int *__restrict__ pb, const int *__restrict__ cb,
+                                           const float *__restrict__ vb, int tid) {
+    const int na = sp.a1 - sp.a0, nab = na + (sp.b1 - sp.b0), nr = sp.r1 - sp.r0 + 1;
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+        const int k = tid + j * kBlock;
+        if (k < na) {
+            st.crd[j] = ca[sp.a0 + k];
+            if (VALUES) st.val[j] = va[sp.a0 + k];
+        } else if (k < nab) {
+            st.crd[j] = cb[sp.b0 + k - na];
+            if (VALUES) st.val[j] = vb[sp.b0 + k - na];
+        }
+        if (k < nr) {
+            const unsigned ra = static_cast<unsigned>(max(pa[sp.r0 + k], sp.a0) - sp.a0);
+            const unsigned rb = static_cast<unsigned>(max(pb[sp.r0 + k], sp.b0) - sp.b0);
+            st.row[j] = ra | (rb << 16);
+        }
+    }
+}
+
+template <bool VALUES, int LOADS>
+__device__ __forceinline__ void stage_tile(const Staged<LOADS> &st, const TileSplit &sp,
+                                           int *s_crd, float *s_val, unsigned *s_row, int tid) {
+    const int nab = (sp.a1 - sp.a0) + (sp.b1 - sp.b0), nr = sp.r1 - sp.r0 + 1;
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+        const int k = tid + j * kBlock;
+        if (k < nab) {
+            s_crd[k] = st.crd[j];
+            if (VALUES) s_val[k] = st.val[j];
+        }
+        if (k < nr) s_row[k] = st.row[j];
+    }
+}
+
+// Persistent merge kernel.  Each workgroup takes tiles in ticket order; while it computes
+// tile T it already holds the inputs of its next tile N in registers and the split of the
+// tile after that, so global-memory latency overlaps computation.
+//
+// Inside a tile, lane t owns the items [tile_lo + t*IPT, tile_lo + (t+1)*IPT) of the
+// merged sequence (lane 0 starts at the tile's own split, the last lane ends at the next
+// tile's), found by a merge-path search in LDS.  It walks exactly those items in a fixed,
+// unrolled number of steps: take A's head (ties: A first), take B's head, or consume the
+// row-end item.  An equal A/B pair is combined when its A entry is taken (the B head is
+// peeked) and the B entry is skipped when its turn comes, so a pair may straddle two
+// lanes.  Outputs stay in registers with a validity mask until their global offset is known.
+template <Op OP, int IPT>
 __global__ __launch_bounds__(kBlock) void csr_merge_tile_kernel(
     const int *__restrict__ pa, const int *__restrict__ ca, const float *__restrict__ va,
     const int *__restrict__ pb, const int *__restrict__ cb, const float *__restrict__ vb,
-    int total, const int *__restrict__ split_r, const int *__restrict__ split_a,
+    int num_tiles, const int *__restrict__ split_r, const int *__restrict__ split_a,
     const int *__restrict__ split_b, unsigned long long *__restrict__ status,
     unsigned *__restrict__ info, int rows, int *__restrict__ pc, int *__restrict__ cc,
     float *__restrict__ vc) {
-    constexpr int kCap = kTile + 2;
-    constexpr int kLoads = kItemsPerLane + 1;  // ceil(kCap / kBlock)
-    static_assert(kLoads * kBlock >= kCap, "staging loop too short");
+    constexpr int kTileItems = kBlock * IPT;
+    constexpr int kCap = kTileItems + 2;
+    constexpr int kLoads = (kCap + kBlock - 1) / kBlock;
+    constexpr int kSteps = IPT + 1;
+    constexpr int kMax = INT_MAX;  // sentinel head: row exhausted
+    static_assert(kCap < 65536, "row offsets are packed in 16 bits");
+    static_assert(kSteps <= 32, "masks are 32-bit");
 
-    __shared__ int s_crd[kCap];  // A's range then B's range
+    __shared__ int s_crd[kCap];
     __shared__ float s_val[kCap];
-    __shared__ int s_pa[kCap];  // pos entries of rows r0..r1
-    __shared__ int s_pb[kCap];
-    __shared__ int s_oc[kCap];  // staged output
-    __shared__ float s_ov[kCap];
-    __shared__ int s_sr[kBlock + 1], s_sa[kBlock + 1], s_sb[kBlock + 1];
+    __shared__ unsigned s_row[kCap];
     __shared__ int s_wave[kBlock / dev::kWave];
-    __shared__ int s_tile, s_base;
+    __shared__ int s_next, s_base;
 
     const int tid = threadIdx.x;
-    if (tid == 0) s_tile = static_cast<int>(atomicAdd(&info[kInfoTicket], 1u));
+    if (tid == 0) s_next = static_cast<int>(atomicAdd(&info[kInfoTicket], 1u));
     __syncthreads();
-    const int tile = s_tile;
-
-    const int r0 = split_r[tile], a0 = split_a[tile], b0 = split_b[tile];
-    const int r1 = split_r[tile + 1], a1 = split_a[tile + 1], b1 = split_b[tile + 1];
-    const int na = a1 - a0, nb = b1 - b0, nab = na + nb, nr = r1 - r0 + 1;
-    const int tile_lo = tile * kTile;
-    const int tile_hi = min(tile_lo + kTile, total);
-
-    // Stage crd/val of A[a0,a1) ++ B[b0,b1) and pos[r0..r1] of both; loads first, then LDS
-    // stores, so every load of a lane is in flight at once.
-    {
-        int rc[kLoads];
-        float rv[kLoads];
-        int rpa[kLoads], rpb[kLoads];
-#pragma unroll
-        for (int j = 0; j < kLoads; ++j) {
-            const int k = tid + j * kBlock;
-            if (k < na) {
-                rc[j] = ca[a0 + k];
-                rv[j] = va[a0 + k];
-            } else if (k < nab) {
-                rc[j] = cb[b0 + k - na];
-                rv[j] = vb[b0 + k - na];
-            }
-            if (k < nr) {
-                rpa[j] = pa[r0 + k];
-                rpb[j] = pb[r0 + k];
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < kLoads; ++j) {
-            const int k = tid + j * kBlock;
-            if (k < nab) {
-                s_crd[k] = rc[j];
-                s_val[k] = rv[j];
-            }
-            if (k < nr) {
-                s_pa[k] = rpa[j];
-                s_pb[k] = rpb[j];
-            }
-        }
-    }
+    int cur = s_next;
+    if (cur >= num_tiles) return;
+    TileSplit sp = load_split(split_r, split_a, split_b, cur);
+    Staged<kLoads> st;
+    fetch_tile<true, kLoads>(st, sp, pa, ca, va, pb, cb, vb, tid);
+    __syncthreads();  // every lane has read s_next
+    stage_tile<true, kLoads>(st, sp, s_crd, s_val, s_row, tid);
+    if (tid == 0) s_next = static_cast<int>(atomicAdd(&info[kInfoTicket], 1u));
     __syncthreads();
+    int nxt = s_next;
+    TileSplit nsp = sp;
+    if (nxt < num_tiles) nsp = load_split(split_r, split_a, split_b, nxt);
 
-    auto A = [&](int x) { return s_crd[x - a0]; };
-    auto B = [&](int y) { return s_crd[na + y - b0]; };
+    while (true) {
+        // Prefetch the next tile's inputs and take the ticket after it.
+        if (nxt < num_tiles) fetch_tile<true, kLoads>(st, nsp, pa, ca, va, pb, cb, vb, tid);
+        unsigned ticket2 = 0;
+        if (tid == 0) ticket2 = atomicAdd(&info[kInfoTicket], 1u);
 
-    // This lane's starting split: diagonal tile_lo + tid*IPT, found in LDS.
-    {
-        const int g = tile_lo + tid * kItemsPerLane;
-        int r, a, b;
-        if (tid == 0) {
-            r = r0;
-            a = a0;
-            b = b0;
-        } else if (g >= tile_hi) {
-            r = r1;
-            a = a1;
-            b = b1;
-        } else {
+        const int r0 = sp.r0, a0 = sp.a0, b0 = sp.b0, r1 = sp.r1, a1 = sp.a1, b1 = sp.b1;
+        const int na = a1 - a0, nr = r1 - r0 + 1;
+        const int tile_lo = cur * kTileItems;
+        const int tile_start = a0 + b0 + r0;  // item index of the tile's first item
+        const int tile_end = a1 + b1 + r1;    // one past its last item
+        auto A = [&](int x) { return s_crd[x - a0]; };
+        auto B = [&](int y) { return s_crd[na + y - b0]; };
+        auto row_a = [&](int k) { return a0 + static_cast<int>(s_row[k] & 0xffffu); };
+        auto row_b = [&](int k) { return b0 + static_cast<int>(s_row[k] >> 16); };
+
+        // This lane's first item and its split (r, a, b).
+        const int g_lo = tid == 0 ? tile_start : tile_lo + tid * IPT;
+        const int g_hi = min(tile_lo + (tid + 1) * IPT, tile_end);
+        const int steps = tid == kBlock - 1 ? tile_end - g_lo : g_hi - g_lo;
+        int k = 0, a = a0, b = b0;
+        if (tid > 0 && g_lo < tile_end) {
             int lo = 0, hi = nr - 1;
             while (lo < hi) {
                 const int mid = (lo + hi + 1) >> 1;
-                if (s_pa[mid] + s_pb[mid] + r0 + mid <= g) {
+                if (row_a(mid) + row_b(mid) + r0 + mid <= g_lo) {
                     lo = mid;
                 } else {
                     hi = mid - 1;
                 }
             }
-            const int k = lo;
-            r = r0 + k;
-            const int aS = max(s_pa[k], a0), bS = max(s_pb[k], b0);
-            const int aE = (k < nr - 1) ? s_pa[k + 1] : a1;
-            const int bE = (k < nr - 1) ? s_pb[k + 1] : b1;
-            merge_split(A, B, aS, aE, bS, bE, g - r, a, b);
-        }
-        s_sr[tid] = r;
-        s_sa[tid] = a;
-        s_sb[tid] = b;
-        if (tid == 0) {
-            s_sr[kBlock] = r1;
-            s_sa[kBlock] = a1;
-            s_sb[kBlock] = b1;
-        }
-    }
-    __syncthreads();
-
-    const int rs = s_sr[tid], as = s_sa[tid], bs = s_sb[tid];
-    const int re = s_sr[tid + 1], ae = s_sa[tid + 1], be = s_sb[tid + 1];
-
-    // Walk this lane's share: merge each row's A and B runs, then its row-end item, up to the
-    // next lane's split.  `emit(crd, ia, ib)` gets absolute positions (-1 = absent);
-    // `row_end(r)` fires when row r's end item is consumed.
-    auto walk = [&](auto emit, auto row_end) {
-        int r = rs, a = as, b = bs;
-        while (true) {
-            const int k = r - r0;
-            const bool last = r >= re;
-            const int aEnd = last ? ae : s_pa[k + 1];
-            const int bEnd = last ? be : s_pb[k + 1];
-            while (a < aEnd && b < bEnd) {
-                const int x = A(a), y = B(b);
-                if (x < y) {
-                    if (OP == Op::Union) emit(x, a, -1);
-                    ++a;
-                } else if (y < x) {
-                    if (OP == Op::Union) emit(y, -1, b);
-                    ++b;
+            k = lo;
+            const int aS = row_a(k), bS = row_b(k);
+            const int aE = k < nr - 1 ? row_a(k + 1) : a1;
+            const int bE = k < nr - 1 ? row_b(k + 1) : b1;
+            const int D = g_lo - (r0 + k);
+            int slo = max(aS, D - bE), shi = min(aE, D - bS);
+            while (slo < shi) {
+                const int mid = (slo + shi) >> 1;
+                if (A(mid) <= B(D - 1 - mid)) {
+                    slo = mid + 1;
                 } else {
-                    emit(x, a, b);
-                    ++a;
-                    ++b;
+                    shi = mid;
                 }
             }
-            if (OP == Op::Union) {
-                for (; a < aEnd; ++a) emit(A(a), a, -1);
-                for (; b < bEnd; ++b) emit(B(b), -1, b);
-            }
-            if (last) break;
-            row_end(r);
-            ++r;
-            a = aEnd;
-            b = bEnd;
+            a = slo;
+            b = D - slo;
         }
-    };
+        const int rs = r0 + k;  // first row this lane touches
+        int aE = k < nr - 1 ? row_a(k + 1) : a1;
+        int bE = k < nr - 1 ? row_b(k + 1) : b1;
+        int last_a = a > row_a(k) ? A(a - 1) : -1;  // previous A of this row inside the tile
+        int xa = a < aE ? A(a) : kMax;
+        int xb = b < bE ? B(b) : kMax;
 
-    int count = 0;
-    walk([&](int, int, int) { ++count; }, [&](int) {});
-
-    int tile_total = 0;
-    const int offset = dev::block_exclusive_sum<kBlock>(count, s_wave, tile_total);
-    if (tid < dev::kWave) {
-        const uint32_t base =
-            dev::lookback_exclusive(status, tile, static_cast<uint32_t>(tile_total),
-                                    &info[kInfoError]);
-        if (tid == 0) s_base = static_cast<int>(base);
-    }
-    __syncthreads();
-    const int base = s_base;
-    if (tile == 0 && tid == 0) pc[0] = 0;
-
-    int o = offset;
-    walk(
-        [&](int x, int ia, int ib) {
-            float v;
-            if (ia >= 0 && ib >= 0) {
-                const float p = s_val[ia - a0], q = s_val[na + ib - b0];
-                v = (OP == Op::Union) ? (p + q) : (p * q);
-            } else {
-                v = (ia >= 0) ? s_val[ia - a0] : s_val[na + ib - b0];
-            }
-            s_oc[o] = x;
-            s_ov[o] = v;
-            ++o;
-        },
-        [&](int r) {
-            pc[r + 1] = base + o;
-            if (r + 1 == rows) info[kInfoLength] = static_cast<unsigned>(base + o);
-        });
-    __syncthreads();
-
+        int out_crd[kSteps];
+        float out_val[kSteps];
+        unsigned valid = 0, row_ends = 0;
 #pragma unroll
-    for (int j = 0; j < kLoads; ++j) {
-        const int k = tid + j * kBlock;
-        if (k < tile_total) {
-            cc[base + k] = s_oc[k];
-            vc[base + k] = s_ov[k];
+        for (int s = 0; s < kSteps; ++s) {
+            out_crd[s] = 0;
+            out_val[s] = 0.0f;
+            if (s < steps) {
+                if (xa != kMax || xb != kMax) {
+                    if (xa <= xb) {  // take A
+                        const bool pair = (xa == xb);
+                        float v = 0.0f;
+                        if (OP == Op::Union) {
+                            v = s_val[a - a0];
+                            if (pair) v = v + s_val[na + b - b0];
+                        } else if (pair) {
+                            v = s_val[a - a0] * s_val[na + b - b0];
+                        }
+                        out_crd[s] = xa;
+                        out_val[s] = v;
+                        if (OP == Op::Union || pair) valid |= 1u << s;
+                        last_a = xa;
+                        ++a;
+                        xa = a < aE ? A(a) : kMax;
+                    } else {  // take B; skipped when it was combined with the previous A
+                        if (OP == Op::Union && last_a != xb) {
+                            out_crd[s] = xb;
+                            out_val[s] = s_val[na + b - b0];
+                            valid |= 1u << s;
+                        }
+                        ++b;
+                        xb = b < bE ? B(b) : kMax;
+                    }
+                } else {  // row end
+                    row_ends |= 1u << s;
+                    ++k;
+                    aE = k < nr - 1 ? row_a(k + 1) : a1;
+                    bE = k < nr - 1 ? row_b(k + 1) : b1;
+                    last_a = -1;
+                    xa = a < aE ? A(a) : kMax;
+                    xb = b < bE ? B(b) : kMax;
+                }
+            }
         }
+
+        const int count = __popc(valid);
+        int tile_total = 0;
+        if (tid == 0) s_next = static_cast<int>(ticket2);
+        const int offset = dev::block_exclusive_sum<kBlock>(count, s_wave, tile_total);
+        if (tid < dev::kWave) {
+            const uint32_t base = dev::lookback_exclusive(
+                status, cur, static_cast<uint32_t>(tile_total), &info[kInfoError]);
+            if (tid == 0) s_base = static_cast<int>(base);
+        }
+        __syncthreads();
+        const int base = s_base;
+        const int nxt2 = s_next;
+        TileSplit nsp2 = nsp;
+        if (nxt2 < num_tiles) nsp2 = load_split(split_r, split_a, split_b, nxt2);
+        if (cur == 0 && tid == 0) pc[0] = 0;
+
+        // Row ends: pos[r+1] = global offset of the first output after row r.  Outputs are
+        // staged in LDS (the inputs are no longer read) for coalesced stores.
+#pragma unroll
+        for (int s = 0; s < kSteps; ++s) {
+            const unsigned below = (1u << s) - 1u;
+            if (row_ends & (1u << s)) {
+                const int r = rs + __popc(row_ends & below);
+                const int at = base + offset + __popc(valid & below);
+                pc[r + 1] = at;
+                if (r + 1 == rows) info[kInfoLength] = static_cast<unsigned>(at);
+            }
+            if (valid & (1u << s)) {
+                const int o = offset + __popc(valid & below);
+                s_crd[o] = out_crd[s];
+                s_val[o] = out_val[s];
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < kLoads; ++j) {
+            const int o = tid + j * kBlock;
+            if (o < tile_total) {
+                cc[base + o] = s_crd[o];
+                vc[base + o] = s_val[o];
+            }
+        }
+        if (nxt >= num_tiles) break;
+        __syncthreads();  // staged outputs consumed
+        stage_tile<true, kLoads>(st, nsp, s_crd, s_val, s_row, tid);
+        __syncthreads();
+        cur = nxt;
+        sp = nsp;
+        nxt = nxt2;
+        nsp = nsp2;
     }
 }
 
@@ -348,11 +415,14 @@ int csr_binary(const nacho_csr *a, const nacho_csr *b, nacho_csr *z, int32_t num
         a->dim_j_offsets, a->dim_j_indices, b->dim_j_offsets, b->dim_j_indices, rows,
         static_cast<int>(total), num_tiles, split_r, split_a, split_b, status, info);
     NACHO_TRY_HIP(hipGetLastError());
+    auto kernel = csr_merge_tile_kernel<OP, kItemsPerLane>;
+    int resident = 0;
+    NACHO_TRY(resident_grid(reinterpret_cast<const void *>(kernel), kBlock, &resident));
+    const int grid = num_tiles < resident ? num_tiles : resident;
     NACHO_TRY(call.timer_start(kernel_name));
-    csr_merge_tile_kernel<OP><<<num_tiles, kBlock, 0, s>>>(
-        a->dim_j_offsets, a->dim_j_indices, a->values, b->dim_j_offsets, b->dim_j_indices,
-        b->values, static_cast<int>(total), split_r, split_a, split_b, status, info, rows, pc, cc,
-        vc);
+    kernel<<<grid, kBlock, 0, s>>>(a->dim_j_offsets, a->dim_j_indices, a->values,
+                                   b->dim_j_offsets, b->dim_j_indices, b->values, num_tiles,
+                                   split_r, split_a, split_b, status, info, rows, pc, cc, vc);
     NACHO_TRY_HIP(hipGetLastError());
     NACHO_TRY(call.timer_stop());
 

@@ -5,65 +5,99 @@
 #include <atomic>
 #include <cstdint>
 #include <cstring>
+#include <map>
 #include <mutex>
+#include <unordered_map>
+#include <utility>
+#include <vector>
 
 namespace nacho {
 namespace {
 
-// Devices whose default memory pool has been told to keep freed memory cached.  Without it
-// the pool returns memory to the driver at every synchronisation and each call pays for
-// fresh mappings.
-std::mutex g_pool_mutex;
-uint64_t g_pool_ready_mask = 0;
-int g_pool_supported[64];
+// ---- caching device allocator --------------------------------------------------------
+// Result and scratch buffers are recycled instead of going back to the driver: every call
+// of an entry point allocates a handful of buffers, and driver allocation (or the
+// stream-ordered pool) costs tens of microseconds each.  Blocks are binned by size class
+// (powers of two split into 4 sub-classes, minimum 512 B).  A block freed on stream S is
+// reused immediately by a later allocation on S (stream order makes that safe); before a
+// block is reused on another stream, S is synchronised.  When the
+// driver runs out of memory the cache is emptied (after a device synchronise) and the
+// allocation retried.
+struct Block {
+    void *ptr;
+    size_t size;  // rounded size class
+    int device;
+    hipStream_t stream;  // stream of the last use (allocation or free)
+};
 
-int prepare_pool(int device, bool *supported) {
-    std::lock_guard<std::mutex> lock(g_pool_mutex);
-    if (device < 0 || device >= 64) {
-        *supported = false;
-        return NACHO_OK;
+std::mutex g_cache_mutex;
+std::unordered_map<void *, Block> g_live;              // allocated blocks by pointer
+std::map<std::pair<int, size_t>, std::vector<Block>> g_free;  // (device, size) -> free
+
+size_t size_class(size_t bytes) {
+    if (bytes <= 512) return 512;
+    size_t p = 1;
+    while (p < bytes) p <<= 1;
+    const size_t quarter = p >> 3;  // p/2 .. p in 4 steps of p/8
+    size_t c = p >> 1;
+    while (c < bytes) c += quarter;
+    return c;
+}
+
+void release_cached_blocks_locked() {
+    (void)hipDeviceSynchronize();
+    for (auto &bin : g_free) {
+        for (Block &b : bin.second) (void)hipFree(b.ptr);
     }
-    if (!(g_pool_ready_mask & (1ull << device))) {
-        int has_pools = 0;
-        NACHO_TRY_HIP(hipDeviceGetAttribute(&has_pools, hipDeviceAttributeMemoryPoolsSupported,
-                                            device));
-        if (has_pools) {
-            hipMemPool_t pool;
-            NACHO_TRY_HIP(hipDeviceGetDefaultMemPool(&pool, device));
-            uint64_t keep = UINT64_MAX;
-            NACHO_TRY_HIP(hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep));
-        }
-        g_pool_supported[device] = has_pools;
-        g_pool_ready_mask |= (1ull << device);
-    }
-    *supported = g_pool_supported[device] != 0;
-    return NACHO_OK;
+    g_free.clear();
 }
 
 void *default_allocate(size_t bytes, hipStream_t stream) {
     int device = 0;
     if (hipGetDevice(&device) != hipSuccess) return nullptr;
-    bool pools = false;
-    if (prepare_pool(device, &pools) != NACHO_OK) return nullptr;
-    void *ptr = nullptr;
-    hipError_t err = pools ? hipMallocAsync(&ptr, bytes, stream) : hipMalloc(&ptr, bytes);
-    if (err != hipSuccess) {
-        (void)hipGetLastError();  // clear the sticky-free error so later calls are unaffected
-        return nullptr;
+    const size_t size = size_class(bytes);
+    std::lock_guard<std::mutex> lock(g_cache_mutex);
+    auto it = g_free.find({device, size});
+    if (it != g_free.end() && !it->second.empty()) {
+        std::vector<Block> &bin = it->second;
+        size_t pick = bin.size() - 1;
+        for (size_t i = bin.size(); i-- > 0;) {
+            if (bin[i].stream == stream) {
+                pick = i;
+                break;
+            }
+        }
+        Block b = bin[pick];
+        bin.erase(bin.begin() + static_cast<std::ptrdiff_t>(pick));
+        if (b.stream != stream) (void)hipStreamSynchronize(b.stream);
+        b.stream = stream;
+        g_live[b.ptr] = b;
+        return b.ptr;
     }
+    void *ptr = nullptr;
+    hipError_t err = hipMalloc(&ptr, size);
+    if (err != hipSuccess) {
+        (void)hipGetLastError();
+        release_cached_blocks_locked();
+        err = hipMalloc(&ptr, size);
+        if (err != hipSuccess) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+    }
+    g_live[ptr] = Block{ptr, size, device, stream};
     return ptr;
 }
 
 void default_release(void *ptr, hipStream_t stream) {
     if (!ptr) return;
-    int device = 0;
-    bool pools = false;
-    if (hipGetDevice(&device) == hipSuccess && prepare_pool(device, &pools) == NACHO_OK && pools) {
-        (void)hipFreeAsync(ptr, stream);
-    } else {
-        (void)hipStreamSynchronize(stream);
-        (void)hipFree(ptr);
-    }
+    std::lock_guard<std::mutex> lock(g_cache_mutex);
+    auto it = g_live.find(ptr);
+    if (it == g_live.end()) return;  // not ours: ignore rather than corrupt the cache
+    Block b = it->second;
+    g_live.erase(it);
+    b.stream = stream;
+    g_free[{b.device, b.size}].push_back(b);
 }
 
 // Kernel timing state (per host thread).
@@ -167,12 +201,38 @@ int Call::timer_stop() {
     return NACHO_OK;
 }
 
+int resident_grid(const void *kernel, int block, int *grid) {
+    static std::mutex mutex;
+    static std::map<std::pair<const void *, int>, int> cache;
+    int device = 0;
+    NACHO_TRY_HIP(hipGetDevice(&device));
+    std::lock_guard<std::mutex> lock(mutex);
+    auto it = cache.find({kernel, device});
+    if (it != cache.end()) {
+        *grid = it->second;
+        return NACHO_OK;
+    }
+    int per_cu = 0, cus = 0;
+    NACHO_TRY_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, 0));
+    NACHO_TRY_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
+    const int g = (per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+    cache[{kernel, device}] = g;
+    *grid = g;
+    return NACHO_OK;
+}
+
 }  // namespace nacho
 
 extern "C" {
 
 int nacho_free(void *ptr, void *stream) {
     nacho::default_release(ptr, static_cast<hipStream_t>(stream));
+    return NACHO_OK;
+}
+
+int nacho_release_cached_memory(void) {
+    std::lock_guard<std::mutex> lock(nacho::g_cache_mutex);
+    nacho::release_cached_blocks_locked();
     return NACHO_OK;
 }
 

@@ -91,4 +91,8 @@ inline int check_launch_hints(int32_t num_blocks, int32_t threads_per_block) {
 
 inline unsigned ceil_div(size_t a, size_t b) { return static_cast<unsigned>((a + b - 1) / b); }
 
+// Number of workgroups of `kernel` (block size `block`, static LDS only) that the current
+// device holds resident at once: the grid of a persistent kernel.  Cached per kernel/device.
+int resident_grid(const void *kernel, int block, int *grid);
+
 }  // namespace nacho

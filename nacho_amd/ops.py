@@ -79,46 +79,46 @@ def _csf3_desc(t: CSF3_gpu) -> _lib.Csf3Desc:
 
 def _adopt_csr(z: _lib.CsrDesc, device, stream) -> CSR_gpu:
     rows, n = z.dim_i_size, z.dim_j_length
-    return CSR_gpu(_device.adopt(z.dim_j_offsets, rows + 1, _I32, device, stream),
-                   _device.adopt(z.dim_j_indices, n, _I32, device, stream),
-                   _device.adopt(z.values, n, _F32, device, stream),
-                   [z.dim_i_size, z.dim_j_size])
+    return CSR_gpu._trusted((_device.adopt(z.dim_j_offsets, rows + 1, _I32, device, stream),
+                             _device.adopt(z.dim_j_indices, n, _I32, device, stream),
+                             _device.adopt(z.values, n, _F32, device, stream)),
+                            [z.dim_i_size, z.dim_j_size], device)
 
 
 def _adopt_csr64(z: _lib.Csr64Desc, device, stream) -> CSR64_gpu:
     rows, n = z.dim_i_size, z.dim_j_length
-    return CSR64_gpu(_device.adopt(z.dim_j_offsets, rows + 1, _I64, device, stream),
-                     _device.adopt(z.dim_j_indices, n, _I32, device, stream),
-                     _device.adopt(z.values, n, _F32, device, stream),
-                     [z.dim_i_size, z.dim_j_size])
+    return CSR64_gpu._trusted((_device.adopt(z.dim_j_offsets, rows + 1, _I64, device, stream),
+                               _device.adopt(z.dim_j_indices, n, _I32, device, stream),
+                               _device.adopt(z.values, n, _F32, device, stream)),
+                              [z.dim_i_size, z.dim_j_size], device)
 
 
 def _adopt_coo(z: _lib.CooDesc, device, stream) -> COO_gpu:
     n = z.nnz
-    return COO_gpu(_device.adopt(z.dim_i_indices, n, _I32, device, stream),
-                   _device.adopt(z.dim_j_indices, n, _I32, device, stream),
-                   _device.adopt(z.values, n, _F32, device, stream),
-                   [z.dim_i_size, z.dim_j_size])
+    return COO_gpu._trusted((_device.adopt(z.dim_i_indices, n, _I32, device, stream),
+                             _device.adopt(z.dim_j_indices, n, _I32, device, stream),
+                             _device.adopt(z.values, n, _F32, device, stream)),
+                            [z.dim_i_size, z.dim_j_size], device)
 
 
 def _adopt_coo3(z: _lib.Coo3Desc, device, stream) -> COO3_gpu:
     n = z.nnz
-    return COO3_gpu(_device.adopt(z.dim_i_indices, n, _I32, device, stream),
-                    _device.adopt(z.dim_j_indices, n, _I32, device, stream),
-                    _device.adopt(z.dim_k_indices, n, _I32, device, stream),
-                    _device.adopt(z.values, n, _F32, device, stream),
-                    [z.dim_i_size, z.dim_j_size, z.dim_k_size])
+    return COO3_gpu._trusted((_device.adopt(z.dim_i_indices, n, _I32, device, stream),
+                              _device.adopt(z.dim_j_indices, n, _I32, device, stream),
+                              _device.adopt(z.dim_k_indices, n, _I32, device, stream),
+                              _device.adopt(z.values, n, _F32, device, stream)),
+                             [z.dim_i_size, z.dim_j_size, z.dim_k_size], device)
 
 
 def _adopt_csf3(z: _lib.Csf3Desc, device, stream) -> CSF3_gpu:
     ni, nj, nk = z.dim_i_length, z.dim_j_length, z.dim_k_length
-    return CSF3_gpu(_device.adopt(z.dim_i_indices, ni, _I32, device, stream),
-                    _device.adopt(z.dim_j_offsets, ni + 1, _I32, device, stream),
-                    _device.adopt(z.dim_j_indices, nj, _I32, device, stream),
-                    _device.adopt(z.dim_k_offsets, nj + 1, _I32, device, stream),
-                    _device.adopt(z.dim_k_indices, nk, _I32, device, stream),
-                    _device.adopt(z.values, nk, _F32, device, stream),
-                    [z.dim_i_size, z.dim_j_size, z.dim_k_size])
+    return CSF3_gpu._trusted((_device.adopt(z.dim_i_indices, ni, _I32, device, stream),
+                              _device.adopt(z.dim_j_offsets, ni + 1, _I32, device, stream),
+                              _device.adopt(z.dim_j_indices, nj, _I32, device, stream),
+                              _device.adopt(z.dim_k_offsets, nj + 1, _I32, device, stream),
+                              _device.adopt(z.dim_k_indices, nk, _I32, device, stream),
+                              _device.adopt(z.values, nk, _F32, device, stream)),
+                             [z.dim_i_size, z.dim_j_size, z.dim_k_size], device)
 
 
 # ---- generic call --------------------------------------------------------------------

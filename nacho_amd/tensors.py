@@ -56,6 +56,16 @@ class _GpuTensor:
         object.__setattr__(self, "_shape", _shape(shape, self._rank, cls))
         object.__setattr__(self, "_device", device)
 
+    @classmethod
+    def _trusted(cls, buffers, shape_list, device):
+        """Build from buffers the library just produced (already checked): no validation."""
+        obj = object.__new__(cls)
+        for (name, _), buf in zip(cls._fields, buffers):
+            object.__setattr__(obj, "_" + name, buf)
+        object.__setattr__(obj, "_shape", torch.tensor(shape_list, dtype=_I32))
+        object.__setattr__(obj, "_device", device)
+        return obj
+
     @property
     def shape(self) -> torch.Tensor:
         return self._shape

@@ -23,9 +23,11 @@
  *     (Compile.cpp:66-154, tensor.cpp:447-577): the same pipeline over one level whose
  *     coordinates are tuples compared lexicographically.
  *   - csf3_union: the three-level union lattice (for i in A_i ∪ B_i, for j in A_ij ∪ B_ij,
- *     for k in A_ijk ∪ B_ijk), emitted in lexicographic order; a fibre is appended to a level
- *     when the loop body below it runs.  Serial restatement of the lattice; the reference's
- *     nested partitioning (partition.cpp:286-461) only splits this work among threads.
+ *     for k in A_ijk ∪ B_ijk), emitted in lexicographic order; every coordinate of each
+ *     level's union is appended, and its child range is the union below it (never empty for
+ *     operands without empty fibres, which is what to_csf3 builds).  Serial restatement of
+ *     the lattice; the reference's nested partitioning (partition.cpp:286-461) only splits
+ *     this work among threads.
  *   - spgemm: the reference has no CPU SpGEMM (compiler.cpp:145-148 is GPU-only).  This is
  *     the ESC semantics of its GPU path (stitch_and_generate_gpu.cpp:14-138, 257-366) run
  *     row-parallel on the CPU: per row, expand a_ij * b_jk, sort by k, and sum runs.
