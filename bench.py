@@ -12,8 +12,9 @@ still resident in the 256 MB Infinity Cache.
 
 Prints ONE JSON line:
   value            whole-job throughput: algorithmic bytes per step / wall time per step
-  roofline         dominant kernel (csr_merge_tile_kernel): algorithmic bytes per launch /
-                   its average duration from HIP events on the launch stream, vs 8 TB/s;
+  roofline         the call's device pipeline (partition, count and write kernels, bracketed
+                   by HIP events on the launch stream): algorithmic bytes per call / its
+                   average duration, vs 8 TB/s;
                    `traffic` = measured HBM bytes per launch (rocprofv3 FETCH_SIZE +
                    WRITE_SIZE, calibrated on a copy kernel) when profiles/ holds them
   cpu_baseline     the C restatement of the reference's CPU kernel (oracle/) on this host's
@@ -39,10 +40,12 @@ PEAK_HBM_GBS = 8000.0
 ROTATE = 4  # independent operand copies cycled through by the timed steps
 
 WORKLOADS = {
-    "c2": dict(op="add", kernel="csr_merge_tile_kernel<Union>",
+    "c2": dict(op="add", kernel="csr_partition_kernel + csr_count_kernel<Union> + "
+                              "csr_write_kernel<Union> (one call's device pipeline)",
                desc="C2 csr_add f32 2^20x2^20, Zipf(1.6) rows rescaled to mean 16 "
                     "(16.7M nnz each), seeds 1/2"),
-    "c3": dict(op="mul", kernel="csr_merge_tile_kernel<Intersect>",
+    "c3": dict(op="mul", kernel="csr_partition_kernel + csr_count_kernel<Intersect> + "
+                              "csr_write_kernel<Intersect> (one call's device pipeline)",
                desc="C3 csr_mul f32 2^20x2^20, A as C2, B = 50% of A + fresh columns "
                     "(seed 3)"),
 }

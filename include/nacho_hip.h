@@ -180,6 +180,12 @@ int nacho_gpu_coo3d_add_f32(const nacho_coo3 *a, const nacho_coo3 *b, nacho_coo3
                             int32_t num_blocks, int32_t threads_per_block, void *stream,
                             const nacho_allocator *alloc);
 
+/* Z = a + b over CSF3 (union at every level; every coordinate of each level's union is
+ * emitted).  Replaces csf_add::csf_add_gpu_i32_f32 (compiler.cpp:135). */
+int nacho_gpu_csf_add_f32(const nacho_csf3 *a, const nacho_csf3 *b, nacho_csf3 *z,
+                          int32_t num_blocks, int32_t threads_per_block, void *stream,
+                          const nacho_allocator *alloc);
+
 /* ---- diagnostics ------------------------------------------------------------------ */
 
 /* Static string naming an error code (HIP codes use hipGetErrorString). */

@@ -34,6 +34,9 @@ HIP_FLAGS = [
     "-fPIC",
     "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Keep single-lane atomics (tile tickets) plain: the wave-level atomic optimizer consumes
+    # their result right away, which stalls on every load issued before them.
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
     "-Wall",
     "-Wno-unused-function",
     "-Wno-unused-command-line-argument",

@@ -9,13 +9,16 @@
 //   COO3 (i, j, k) -> i << (bj+bk) | j << bk | k  when the three extents fit 64 bits
 //                     (bj, bk = bits of the j and k extents), else a (i<<32|j, k) pair.
 // Coordinates are non-negative int32 below their extents, so key order is tuple order.
-// The work is the merged sequence of both key lists (nnzA + nnzB items).  A partition
-// kernel finds every tile's merge-path split (equal keys never split, as the reference's
-// balancing step, partition.cpp:964-983); one workgroup per tile stages its keys and values
-// in LDS with coalesced loads, splits among lanes in LDS, counts, takes its global offset by
-// decoupled look-back, merges again into LDS and writes the unpacked coordinates and values
-// coalesced.  Values are one IEEE binary32 add / multiply or a copy, as the reference's
-// lattice (compute.cpp:476-491), so results are bit-exact.
+// The work is the merged sequence of both key lists (nnzA + nnzB items), cut into tiles.  A
+// partition kernel finds every tile's merge-path split (equal keys never split, as the
+// reference's balancing step, partition.cpp:964-983).  As for CSR (csr_merge.hip), each
+// workgroup then owns a fixed chunk of tiles: a count kernel stores each chunk's output count
+// and a write kernel starts from the preceding chunks' total.  Inside a tile the keys and
+// values are staged in LDS from registers loaded one tile ahead, lanes split the tile by a
+// merge-path search in LDS and walk their items (equal keys combined at the A step, the B
+// step skipped), and results go through LDS to coalesced stores of the unpacked coordinates.
+// Values are one IEEE binary32 add / multiply or a copy, as the reference's lattice
+// (compute.cpp:476-491), so results are bit-exact.
 #include <hip/hip_runtime.h>
 
 #include <climits>
@@ -32,8 +35,6 @@ enum class Op { Union, Intersect };
 constexpr int kBlock = 256;
 constexpr int kItemsPerLane = 8;
 constexpr int kTile = kBlock * kItemsPerLane;
-constexpr int kInfoWords = 4;
-constexpr int kInfoTicket = 0, kInfoLength = 1, kInfoError = 2;
 
 struct WideKey {
     unsigned long long hi;
@@ -111,12 +112,8 @@ template <typename Codec>
 __global__ __launch_bounds__(256) void coo_partition_kernel(Codec codec, Coords ca, int nnz_a,
                                                             Coords cb, int nnz_b, int num_tiles,
                                                             int *__restrict__ split_a,
-                                                            int *__restrict__ split_b,
-                                                            unsigned long long *__restrict__ status,
-                                                            unsigned *__restrict__ info) {
+                                                            int *__restrict__ split_b) {
     const int t = blockIdx.x * blockDim.x + threadIdx.x;
-    if (t < kInfoWords) info[t] = 0u;
-    if (t < num_tiles) status[t] = 0ull;
     if (t > num_tiles) return;
     const int total = nnz_a + nnz_b;
     const long long d64 = static_cast<long long>(t) * kTile;
@@ -128,146 +125,239 @@ __global__ __launch_bounds__(256) void coo_partition_kernel(Codec codec, Coords 
     split_b[t] = b;
 }
 
-template <Op OP, typename Codec>
-__global__ __launch_bounds__(kBlock) void coo_merge_tile_kernel(
-    Codec codec, Coords ca, const float *__restrict__ va, int nnz_a, Coords cb,
-    const float *__restrict__ vb, int nnz_b, const int *__restrict__ split_a,
-    const int *__restrict__ split_b, unsigned long long *__restrict__ status,
-    unsigned *__restrict__ info, int num_tiles, int *__restrict__ zi, int *__restrict__ zj,
-    int *__restrict__ zk, float *__restrict__ zv) {
-    using Key = typename Codec::Key;
-    constexpr int kCap = kTile + 2;
-    constexpr int kLoads = kItemsPerLane + 1;
-    static_assert(kLoads * kBlock >= kCap, "staging loop too short");
+constexpr int kMaxChunk = 64;
 
-    __shared__ Key s_key[kCap];  // A's range then B's range
-    __shared__ float s_val[kCap];
-    __shared__ Key s_okey[kCap];
-    __shared__ float s_oval[kCap];
-    __shared__ int s_sa[kBlock + 1], s_sb[kBlock + 1];
-    __shared__ int s_wave[kBlock / dev::kWave];
-    __shared__ int s_tile, s_base;
+// Stage the chunk's splits (2 ints per boundary) in LDS once per workgroup.
+__device__ __forceinline__ void stage_splits(int *s_split, const int *__restrict__ split_a,
+                                             const int *__restrict__ split_b, int t0, int t1) {
+    for (int i = threadIdx.x; i <= t1 - t0; i += kBlock) {
+        s_split[2 * i] = split_a[t0 + i];
+        s_split[2 * i + 1] = split_b[t0 + i];
+    }
+}
 
-    const int tid = threadIdx.x;
-    if (tid == 0) s_tile = static_cast<int>(atomicAdd(&info[kInfoTicket], 1u));
-    __syncthreads();
-    const int tile = s_tile;
-    const int a0 = split_a[tile], b0 = split_b[tile];
-    const int a1 = split_a[tile + 1], b1 = split_b[tile + 1];
-    const int na = a1 - a0, nab = na + (b1 - b0);
-    const int total = nnz_a + nnz_b;
-    const int tile_lo = tile * kTile;
-    const int tile_hi = min(tile_lo + kTile, total);
+// One lane's keys/values of a tile, loaded one tile ahead (unconditional, clamped loads).
+template <typename Key, int LOADS>
+struct StagedKeys {
+    Key key[LOADS];
+    int val[LOADS];
+};
 
-    {
-        Key rk[kLoads];
-        float rv[kLoads];
+template <bool VALUES, typename Codec, int LOADS>
+__device__ __forceinline__ void fetch_keys(StagedKeys<typename Codec::Key, LOADS> &st,
+                                           const Codec &codec, const int *s_split, int i,
+                                           Coords ca, const float *__restrict__ va, Coords cb,
+                                           const float *__restrict__ vb, int tid) {
+    const int a0 = s_split[2 * i], b0 = s_split[2 * i + 1];
+    const int na = s_split[2 * i + 2] - a0, nab = na + s_split[2 * i + 3] - b0;
+    if (nab <= 0) return;
+    const int *vai = reinterpret_cast<const int *>(va);
+    const int *vbi = reinterpret_cast<const int *>(vb);
 #pragma unroll
-        for (int j = 0; j < kLoads; ++j) {
-            const int k = tid + j * kBlock;
-            if (k < na) {
-                rk[j] = codec.load(ca, a0 + k);
-                rv[j] = va[a0 + k];
-            } else if (k < nab) {
-                rk[j] = codec.load(cb, b0 + k - na);
-                rv[j] = vb[b0 + k - na];
-            }
-        }
+    for (int j = 0; j < LOADS; ++j) {
+        const int k = min(tid + j * kBlock, nab - 1);
+        const bool in_a = k < na;
+        const int off = in_a ? a0 + k : b0 + (k - na);
+        st.key[j] = codec.load(in_a ? ca : cb, off);
+        if (VALUES) st.val[j] = (in_a ? vai : vbi)[off];
+    }
+}
+
+template <bool VALUES, typename Key, int LOADS>
+__device__ __forceinline__ void stage_keys(const StagedKeys<Key, LOADS> &st, const int *s_split,
+                                           int i, Key *s_key, float *s_val, int tid) {
+    const int nab = s_split[2 * i + 2] - s_split[2 * i] + s_split[2 * i + 3] - s_split[2 * i + 1];
 #pragma unroll
-        for (int j = 0; j < kLoads; ++j) {
-            const int k = tid + j * kBlock;
-            if (k < nab) {
-                s_key[k] = rk[j];
-                s_val[k] = rv[j];
-            }
+    for (int j = 0; j < LOADS; ++j) {
+        const int k = tid + j * kBlock;
+        if (k < nab) {
+            s_key[k] = st.key[j];
+            if (VALUES) s_val[k] = __int_as_float(st.val[j]);
         }
     }
-    __syncthreads();
+}
 
+// Lane walk over a tile of keys (no rows): lane t owns items [t*IPT, (t+1)*IPT) of the
+// tile's merged order; equal keys are combined at the A step and the B step is skipped.
+template <Op OP, bool VALUES, typename Key, int STEPS>
+struct KeyLaneOut {
+    Key key[STEPS];
+    float val[STEPS];
+    unsigned valid;
+};
+
+template <Op OP, bool VALUES, typename Key>
+__device__ __forceinline__ void walk_keys(KeyLaneOut<OP, VALUES, Key, kItemsPerLane + 1> &out,
+                                          const int *s_split, int i, int tile, const Key *s_key,
+                                          const float *s_val, int tid) {
+    constexpr int kSteps = kItemsPerLane + 1;
+    const int a0 = s_split[2 * i], b0 = s_split[2 * i + 1];
+    const int a1 = s_split[2 * i + 2], b1 = s_split[2 * i + 3];
+    const int na = a1 - a0;
     auto A = [&](int x) { return s_key[x - a0]; };
     auto B = [&](int y) { return s_key[na + y - b0]; };
-    {
-        const int g = tile_lo + tid * kItemsPerLane;
-        int a, b;
-        if (tid == 0) {
-            a = a0;
-            b = b0;
-        } else if (g >= tile_hi) {
-            a = a1;
-            b = b1;
-        } else {
-            merge_split(A, B, a0, a1, b0, b1, g, a, b);
-        }
-        s_sa[tid] = a;
-        s_sb[tid] = b;
-        if (tid == 0) {
-            s_sa[kBlock] = a1;
-            s_sb[kBlock] = b1;
-        }
-    }
-    __syncthreads();
-    const int as = s_sa[tid], bs = s_sb[tid], ae = s_sa[tid + 1], be = s_sb[tid + 1];
-
-    auto walk = [&](auto emit) {
-        int a = as, b = bs;
-        while (a < ae && b < be) {
-            const Key x = A(a), y = B(b);
-            if (x < y) {
-                if (OP == Op::Union) emit(x, a, -1);
-                ++a;
-            } else if (y < x) {
-                if (OP == Op::Union) emit(y, -1, b);
-                ++b;
+    const int tile_lo = tile * kTile;
+    const int tile_start = a0 + b0, tile_end = a1 + b1;
+    const int g_lo = tid == 0 ? tile_start : tile_lo + tid * kItemsPerLane;
+    const int steps = tid == kBlock - 1 ? tile_end - g_lo
+                                        : min(tile_lo + (tid + 1) * kItemsPerLane, tile_end) - g_lo;
+    int a = a0, b = b0;
+    if (tid > 0 && g_lo < tile_end) {
+        int slo = max(a0, g_lo - b1), shi = min(a1, g_lo - b0);
+        while (slo < shi) {
+            const int mid = (slo + shi) >> 1;
+            if (A(mid) <= B(g_lo - 1 - mid)) {
+                slo = mid + 1;
             } else {
-                emit(x, a, b);
-                ++a;
-                ++b;
+                shi = mid;
             }
         }
-        if (OP == Op::Union) {
-            for (; a < ae; ++a) emit(A(a), a, -1);
-            for (; b < be; ++b) emit(B(b), -1, b);
-        }
-    };
-
-    int count = 0;
-    walk([&](const Key &, int, int) { ++count; });
-    int tile_total = 0;
-    const int offset = dev::block_exclusive_sum<kBlock>(count, s_wave, tile_total);
-    if (tid < dev::kWave) {
-        const uint32_t base = dev::lookback_exclusive(status, tile, static_cast<uint32_t>(tile_total),
-                                                      &info[kInfoError]);
-        if (tid == 0) s_base = static_cast<int>(base);
+        a = slo;
+        b = g_lo - slo;
     }
-    __syncthreads();
-    const int base = s_base;
-    if (tile == num_tiles - 1 && tid == 0) info[kInfoLength] = static_cast<unsigned>(base + tile_total);
-
-    int o = offset;
-    walk([&](const Key &key, int ia, int ib) {
-        float v;
-        if (ia >= 0 && ib >= 0) {
-            const float p = s_val[ia - a0], q = s_val[na + ib - b0];
-            v = (OP == Op::Union) ? (p + q) : (p * q);
-        } else {
-            v = (ia >= 0) ? s_val[ia - a0] : s_val[na + ib - b0];
-        }
-        s_okey[o] = key;
-        s_oval[o] = v;
-        ++o;
-    });
-    __syncthreads();
-
+    bool has_last = a > a0;
+    Key last_a = has_last ? A(a - 1) : Key{};
+    unsigned valid = 0;
 #pragma unroll
-    for (int j = 0; j < kLoads; ++j) {
-        const int k = tid + j * kBlock;
-        if (k < tile_total) {
-            int ci, cj, ck;
-            codec.unpack(s_okey[k], ci, cj, ck);
-            zi[base + k] = ci;
-            zj[base + k] = cj;
-            if (codec.arity == 3) zk[base + k] = ck;
-            zv[base + k] = s_oval[k];
+    for (int s = 0; s < kSteps; ++s) {
+        out.val[s] = 0.0f;
+        if (s < steps) {
+            const bool a_in = a < a1, b_in = b < b1;
+            // out-of-range heads read a harmless in-bounds slot and are masked by a_in / b_in
+            const Key xa = A(a_in ? a : a0);
+            const Key xb = B(b_in ? b : b0);
+            const bool take_a = a_in && (!b_in || xa <= xb);
+            const bool pair = take_a && b_in && xa == xb;
+            out.key[s] = take_a ? xa : xb;
+            if (VALUES) {
+                const float own = s_val[take_a ? a - a0 : na + b - b0];
+                if (OP == Op::Union) {
+                    out.val[s] = pair ? own + s_val[na + b - b0] : own;
+                } else {
+                    out.val[s] = own * s_val[na + b - b0];
+                }
+            }
+            const bool skip = !take_a && has_last && last_a == xb;
+            const bool emit = (OP == Op::Union) ? !skip : pair;
+            valid |= static_cast<unsigned>(emit) << s;
+            if (take_a) {
+                last_a = xa;
+                has_last = true;
+            }
+            a += take_a;
+            b += !take_a;
+        }
+    }
+    out.valid = valid;
+}
+
+template <Op OP, typename Codec>
+__global__ __launch_bounds__(kBlock) void coo_count_kernel(Codec codec, Coords ca, Coords cb,
+                                                          int num_tiles, int chunk,
+                                                          const int *__restrict__ split_a,
+                                                          const int *__restrict__ split_b,
+                                                          unsigned *__restrict__ chunk_count) {
+    using Key = typename Codec::Key;
+    constexpr int kCap = kTile + 2;
+    constexpr int kLoads = (kCap + kBlock - 1) / kBlock;
+    __shared__ Key s_key[kCap];
+    __shared__ unsigned s_wave[kBlock / dev::kWave];
+    __shared__ int s_split[2 * (kMaxChunk + 1)];
+    const int tid = threadIdx.x;
+    const int t0 = blockIdx.x * chunk, t1 = min(t0 + chunk, num_tiles);
+    if (t0 >= t1) {
+        if (tid == 0) chunk_count[blockIdx.x] = 0u;
+        return;
+    }
+    stage_splits(s_split, split_a, split_b, t0, t1);
+    __syncthreads();
+    StagedKeys<Key, kLoads> st;
+    fetch_keys<false>(st, codec, s_split, 0, ca, nullptr, cb, nullptr, tid);
+    stage_keys<false>(st, s_split, 0, s_key, nullptr, tid);
+    __syncthreads();
+    unsigned total = 0;
+    for (int t = t0; t < t1; ++t) {
+        const int i = t - t0;
+        if (t + 1 < t1) fetch_keys<false>(st, codec, s_split, i + 1, ca, nullptr, cb, nullptr, tid);
+        KeyLaneOut<OP, false, Key, kItemsPerLane + 1> lo;
+        walk_keys<OP, false, Key>(lo, s_split, i, t, s_key, nullptr, tid);
+        unsigned c = dev::wave_sum(static_cast<unsigned>(__popc(lo.valid)));
+        if (dev::lane() == 0) s_wave[tid / dev::kWave] = c;
+        __syncthreads();
+#pragma unroll
+        for (int w = 0; w < kBlock / dev::kWave; ++w) total += s_wave[w];
+        __syncthreads();
+        if (t + 1 < t1) {
+            stage_keys<false>(st, s_split, i + 1, s_key, nullptr, tid);
+            __syncthreads();
+        }
+    }
+    if (tid == 0) chunk_count[blockIdx.x] = total;
+}
+
+template <Op OP, typename Codec>
+__global__ __launch_bounds__(kBlock) void coo_write_kernel(
+    Codec codec, Coords ca, const float *__restrict__ va, Coords cb, const float *__restrict__ vb,
+    int num_tiles, int chunk, const int *__restrict__ split_a, const int *__restrict__ split_b,
+    const unsigned *__restrict__ chunk_count, int *__restrict__ zi, int *__restrict__ zj,
+    int *__restrict__ zk, float *__restrict__ zv, unsigned *__restrict__ length) {
+    using Key = typename Codec::Key;
+    constexpr int kCap = kTile + 2;
+    constexpr int kLoads = (kCap + kBlock - 1) / kBlock;
+    constexpr int kSteps = kItemsPerLane + 1;
+    __shared__ Key s_key[kCap];
+    __shared__ float s_val[kCap];
+    __shared__ int s_wave[kBlock / dev::kWave];
+    __shared__ int s_split[2 * (kMaxChunk + 1)];
+    const int tid = threadIdx.x;
+    const int t0 = blockIdx.x * chunk, t1 = min(t0 + chunk, num_tiles);
+    if (t0 >= t1) return;
+    stage_splits(s_split, split_a, split_b, t0, t1);
+    int before = 0;
+    for (int i = tid; i < static_cast<int>(blockIdx.x); i += kBlock) before += chunk_count[i];
+    int base = 0;
+    (void)dev::block_exclusive_sum<kBlock>(before, s_wave, base);
+
+    StagedKeys<Key, kLoads> st;
+    fetch_keys<true>(st, codec, s_split, 0, ca, va, cb, vb, tid);
+    stage_keys<true>(st, s_split, 0, s_key, s_val, tid);
+    __syncthreads();
+    for (int t = t0; t < t1; ++t) {
+        const int i = t - t0;
+        if (t + 1 < t1) fetch_keys<true>(st, codec, s_split, i + 1, ca, va, cb, vb, tid);
+        KeyLaneOut<OP, true, Key, kSteps> lo;
+        walk_keys<OP, true, Key>(lo, s_split, i, t, s_key, s_val, tid);
+        int tile_total = 0;
+        const int offset =
+            dev::block_exclusive_sum<kBlock>(static_cast<int>(__popc(lo.valid)), s_wave, tile_total);
+        int o = offset;
+#pragma unroll
+        for (int s = 0; s < kSteps; ++s) {
+            if (lo.valid & (1u << s)) {
+                s_key[o] = lo.key[s];
+                s_val[o] = lo.val[s];
+                ++o;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < kLoads; ++j) {
+            const int q = tid + j * kBlock;
+            if (q < tile_total) {
+                int ci, cj, ck;
+                codec.unpack(s_key[q], ci, cj, ck);
+                zi[base + q] = ci;
+                zj[base + q] = cj;
+                if (codec.arity == 3) zk[base + q] = ck;
+                zv[base + q] = s_val[q];
+            }
+        }
+        base += tile_total;
+        if (t == num_tiles - 1 && tid == 0) *length = static_cast<unsigned>(base);
+        __syncthreads();
+        if (t + 1 < t1) {
+            stage_keys<true>(st, s_split, i + 1, s_key, s_val, tid);
+            __syncthreads();
         }
     }
 }
@@ -297,11 +387,8 @@ int coo_binary(int arity, const int32_t extents[3], Coords ca, const float *va, 
     const int num_tiles = total > 0 ? static_cast<int>((total + kTile - 1) / kTile) : 1;
 
     Call call(stream, alloc);
-    unsigned long long *status = nullptr;
     int *splits = nullptr;
-    NACHO_TRY(call.scratch_n(static_cast<size_t>(num_tiles) + kInfoWords / 2, &status));
     NACHO_TRY(call.scratch_n(2 * (static_cast<size_t>(num_tiles) + 1), &splits));
-    unsigned *info = reinterpret_cast<unsigned *>(status + num_tiles);
     int *split_a = splits, *split_b = splits + num_tiles + 1;
 
     int32_t *z[3] = {nullptr, nullptr, nullptr};
@@ -313,17 +400,31 @@ int coo_binary(int arity, const int32_t extents[3], Coords ca, const float *va, 
     const unsigned part_grid = ceil_div(static_cast<size_t>(num_tiles) + 1, 256);
     const int bi = bits_for_extent(extents[0]), bj = bits_for_extent(extents[1]);
     const int bk = arity == 3 ? bits_for_extent(extents[2]) : 0;
+    unsigned *counts = nullptr;
     auto launch = [&](auto codec) -> int {
         using Codec = decltype(codec);
-        coo_partition_kernel<Codec><<<part_grid, 256, 0, s>>>(codec, ca, nnz_a, cb, nnz_b, num_tiles,
-                                                              split_a, split_b, status, info);
-        NACHO_TRY_HIP(hipGetLastError());
+        int resident = 0;
+        NACHO_TRY(resident_grid(reinterpret_cast<const void *>(coo_write_kernel<OP, Codec>),
+                                kBlock, &resident));
+        int chunk = (num_tiles + resident - 1) / resident;
+        if (chunk > kMaxChunk) chunk = kMaxChunk;
+        const int grid = (num_tiles + chunk - 1) / chunk;
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(grid) + 4, &counts));
         NACHO_TRY(call.timer_start(kernel_name));
-        coo_merge_tile_kernel<OP, Codec><<<num_tiles, kBlock, 0, s>>>(
-            codec, ca, va, nnz_a, cb, vb, nnz_b, split_a, split_b, status, info, num_tiles, z[0],
-            z[1], z[2], zv);
+        coo_partition_kernel<Codec><<<part_grid, 256, 0, s>>>(codec, ca, nnz_a, cb, nnz_b, num_tiles,
+                                                              split_a, split_b);
         NACHO_TRY_HIP(hipGetLastError());
-        return call.timer_stop();
+        coo_count_kernel<OP, Codec><<<grid, kBlock, 0, s>>>(codec, ca, cb, num_tiles, chunk, split_a,
+                                                            split_b, counts);
+        NACHO_TRY_HIP(hipGetLastError());
+        coo_write_kernel<OP, Codec><<<grid, kBlock, 0, s>>>(codec, ca, va, cb, vb, num_tiles, chunk,
+                                                            split_a, split_b, counts, z[0], z[1],
+                                                            z[2], zv, counts + grid);
+        NACHO_TRY_HIP(hipGetLastError());
+        NACHO_TRY(call.timer_stop());
+        unsigned len = 0;
+        NACHO_TRY(call.read_back(&len, counts + grid, sizeof(len)));
+        return static_cast<int>(len) < 0 ? NACHO_ERR_INDEX_OVERFLOW : (*out_nnz = static_cast<int32_t>(len), NACHO_OK);
     };
     if (arity == 2) {
         PackedCodec c{2, 32, 0, 0xffffffffull, 0ull};
@@ -336,11 +437,7 @@ int coo_binary(int arity, const int32_t extents[3], Coords ca, const float *va, 
         WideCodec c{3};
         NACHO_TRY(launch(c));
     }
-
-    unsigned words[kInfoWords] = {};
-    NACHO_TRY(call.read_back(words, info, sizeof(words)));
-    if (words[kInfoError] != 0) return NACHO_ERR_INTERNAL;
-    const long long nnz = words[kInfoLength];
+    const long long nnz = *out_nnz;
     if (nnz > cap) return NACHO_ERR_MALFORMED_INPUT;
     if (nnz == 0) {
         for (int d = 0; d < arity; ++d) {

@@ -1,4 +1,5 @@
-// CSR elementwise add (union) and multiply (intersection) for gfx950.
+// CSR elementwise add (union) and multiply (intersection) for gfx950, and the level merge
+// that CSF3 add chains three times.
 //
 // Reference path replaced: the generated partition_ij / precompute_ij / compute_ij kernels
 // of csr_add and csr_mul (src/backend/partition.cpp:59-336, 813-993;
@@ -9,18 +10,24 @@
 //
 //  * Work is the merged sequence of every row's A entries, B entries and one row-end item,
 //    so empty rows and Zipf-heavy rows cost the same per item (the reference counts only
-//    nonzeros, tensor.cpp:308-413).  Item count T = nnzA + nnzB + rows.
+//    nonzeros, tensor.cpp:308-413).  Item count T = nnzA + nnzB + rows, cut into tiles of
+//    kTile items.
 //  * csr_partition_kernel: one thread per tile boundary finds (row, a, b) for diagonal
-//    tile*TILE by a binary search over rows on S(r) = posA[r] + posB[r] + r, then a merge-path
-//    search inside the row.  An A/B pair with equal coordinates is never split across tiles
-//    (the reference's balancing step, partition.cpp:964-983).  The same kernel clears the
-//    look-back status words and the tile ticket, so no memset is needed.
-//  * csr_merge_tile_kernel: one workgroup per tile of BLOCK*IPT items.  It stages the tile's
-//    crd/val ranges of A and B and its rows' pos entries in LDS with coalesced loads, splits
-//    the tile among lanes by the same search in LDS, counts outputs, turns counts into global
-//    offsets with a workgroup scan plus decoupled look-back (single pass, no second read of
-//    crd), merges again writing results into LDS, and stores crd/val with coalesced writes.
-//    Row ends write pos[r+1].
+//    tile*kTile by a binary search over rows on S(r) = posA[r] + posB[r] + r, then a
+//    merge-path search inside the row.  An A/B pair with equal coordinates is never split
+//    across tiles (the reference's balancing step, partition.cpp:964-983).
+//  * csr_count_kernel and csr_write_kernel: each workgroup owns a fixed, contiguous chunk of
+//    tiles.  The count kernel reads only coordinates and row offsets and stores the chunk's
+//    output count; the write kernel starts from the sum of the preceding chunks' counts and
+//    carries a running offset through its tiles.  No workgroup ever waits on another (an
+//    earlier single-pass design with decoupled look-back spent most of its time waiting).
+//  * Inside a tile (both kernels): the tile's crd/val ranges of A and B and a packed word per
+//    row are staged in LDS from registers that were loaded one tile ahead; lane t owns items
+//    [t*IPT, (t+1)*IPT) of the tile, found by a merge-path search in LDS, and walks them in a
+//    fixed, unrolled number of steps (take A's head with ties to A, take B's head, or consume a
+//    row end).  An equal A/B pair is combined when its A entry is taken and its B entry is
+//    skipped when reached, so pairs may straddle lanes.  Outputs stay in registers until the
+//    workgroup scan gives their offsets, then go through LDS to coalesced stores.
 //
 // Emission order and values follow the reference's lattice (compute.cpp:476-491,
 // 1169-1198, 1297-1337): coordinates ascending within a row; union emits a+b where both
@@ -32,6 +39,7 @@
 #include <climits>
 #include <cstdint>
 
+#include "csr_merge.hpp"
 #include "device_utils.hpp"
 #include "runtime.hpp"
 
@@ -44,10 +52,6 @@ constexpr int kBlock = 256;
 constexpr int kItemsPerLane = 15;  // odd: lanes' LDS walks spread over banks
 constexpr int kTile = kBlock * kItemsPerLane;
 
-// Per-call info words in scratch, cleared by the partition kernel:
-// [0] tile ticket, [1] result length, [2] error flag (look-back gave up).
-constexpr int kInfoWords = 4;
-constexpr int kInfoTicket = 0, kInfoLength = 1, kInfoError = 2;
 
 // Merge-path split of the merged order of A[aS, aE) and B[bS, bE) (ties: A first) at the
 // point where `a + b == D`, followed by the pair rule: if the last A taken equals the next B,
@@ -74,11 +78,8 @@ __device__ __forceinline__ void merge_split(ReadA A, ReadB B, int aS, int aE, in
 __global__ __launch_bounds__(256) void csr_partition_kernel(
     const int *__restrict__ pa, const int *__restrict__ ca, const int *__restrict__ pb,
     const int *__restrict__ cb, int rows, int total, int num_tiles, int *__restrict__ split_r,
-    int *__restrict__ split_a, int *__restrict__ split_b, unsigned long long *__restrict__ status,
-    unsigned *__restrict__ info) {
+    int *__restrict__ split_a, int *__restrict__ split_b) {
     const int t = blockIdx.x * blockDim.x + threadIdx.x;
-    if (t < kInfoWords) info[t] = 0u;
-    if (t < num_tiles) status[t] = 0ull;
     if (t > num_tiles) return;
     const long long d64 = static_cast<long long>(t) * kTile;
     const int diag = d64 > total ? total : static_cast<int>(d64);
@@ -108,8 +109,9 @@ __global__ __launch_bounds__(256) void csr_partition_kernel(
     split_b[t] = b;
 }
 
-// Tile inputs staged in LDS: A's crd/val range then B's, and one packed word per row of the
-// tile: (max(posA[r], a0) - a0) | (max(posB[r], b0) - b0) << 16.
+
+// ---- tile staging ----------------------------------------------------------------------
+
 struct TileSplit {
     int r0, a0, b0, r1, a1, b1;
 };
@@ -121,12 +123,36 @@ __device__ __forceinline__ TileSplit load_split(const int *__restrict__ split_r,
                      split_r[tile + 1], split_a[tile + 1], split_b[tile + 1]};
 }
 
-// Registers of one lane's share of a tile's staged inputs (prefetched one tile ahead).
+// The splits of a workgroup's whole chunk, staged in LDS once: reading them from global
+// memory per tile would use scalar loads, whose wait counter is shared with LDS and would
+// stall the next LDS access on a memory round trip.
+constexpr int kMaxChunk = 64;
+
+__device__ __forceinline__ void stage_splits(int *s_split, const int *__restrict__ split_r,
+                                             const int *__restrict__ split_a,
+                                             const int *__restrict__ split_b, int t0, int t1) {
+    const int n = t1 - t0 + 1;
+    for (int i = threadIdx.x; i < n; i += kBlock) {
+        s_split[3 * i] = split_r[t0 + i];
+        s_split[3 * i + 1] = split_a[t0 + i];
+        s_split[3 * i + 2] = split_b[t0 + i];
+    }
+}
+
+__device__ __forceinline__ TileSplit lds_split(const int *s_split, int i) {
+    return TileSplit{s_split[3 * i], s_split[3 * i + 1], s_split[3 * i + 2],
+                     s_split[3 * i + 3], s_split[3 * i + 4], s_split[3 * i + 5]};
+}
+
+// One lane's share of a tile's inputs, loaded one tile ahead.  Loads are issued
+// unconditionally (lanes past the end re-read the last element) and nothing is computed from
+// them until they are stored to LDS, so a whole tile's loads are in flight at once.
 template <int LOADS>
 struct Staged {
     int crd[LOADS];
-    float val[LOADS];
-    unsigned row[LOADS];
+    int val[LOADS];  // float bits
+    int pa[LOADS];
+    int pb[LOADS];
 };
 
 template <bool VALUES, int LOADS>
@@ -136,24 +162,28 @@ __device__ __forceinline__ void fetch_tile(Staged<LOADS> &st, const TileSplit &s
                                            const int *__restrict__ pb, const int *__restrict__ cb,
                                            const float *__restrict__ vb, int tid) {
     const int na = sp.a1 - sp.a0, nab = na + (sp.b1 - sp.b0), nr = sp.r1 - sp.r0 + 1;
+    const int *vai = reinterpret_cast<const int *>(va);
+    const int *vbi = reinterpret_cast<const int *>(vb);
+    if (nab > 0) {  // uniform
+#pragma unroll
+        for (int j = 0; j < LOADS; ++j) {
+            const int k = min(tid + j * kBlock, nab - 1);
+            const bool in_a = k < na;
+            const int off = in_a ? sp.a0 + k : sp.b0 + (k - na);
+            st.crd[j] = (in_a ? ca : cb)[off];
+            if (VALUES) st.val[j] = (in_a ? vai : vbi)[off];
+        }
+    }
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
-        const int k = tid + j * kBlock;
-        if (k < na) {
-            st.crd[j] = ca[sp.a0 + k];
-            if (VALUES) st.val[j] = va[sp.a0 + k];
-        } else if (k < nab) {
-            st.crd[j] = cb[sp.b0 + k - na];
-            if (VALUES) st.val[j] = vb[sp.b0 + k - na];
-        }
-        if (k < nr) {
-            const unsigned ra = static_cast<unsigned>(max(pa[sp.r0 + k], sp.a0) - sp.a0);
-            const unsigned rb = static_cast<unsigned>(max(pb[sp.r0 + k], sp.b0) - sp.b0);
-            st.row[j] = ra | (rb << 16);
-        }
+        const int kr = sp.r0 + min(tid + j * kBlock, nr - 1);
+        st.pa[j] = pa[kr];
+        st.pb[j] = pb[kr];
     }
 }
 
+// LDS layout of a staged tile: s_crd = A's crd range then B's; s_val likewise; s_row[k] =
+// (max(posA[r0+k], a0) - a0) | (max(posB[r0+k], b0) - b0) << 16.
 template <bool VALUES, int LOADS>
 __device__ __forceinline__ void stage_tile(const Staged<LOADS> &st, const TileSplit &sp,
                                            int *s_crd, float *s_val, unsigned *s_row, int tid) {
@@ -163,212 +193,375 @@ __device__ __forceinline__ void stage_tile(const Staged<LOADS> &st, const TileSp
         const int k = tid + j * kBlock;
         if (k < nab) {
             s_crd[k] = st.crd[j];
-            if (VALUES) s_val[k] = st.val[j];
+            if (VALUES) s_val[k] = __int_as_float(st.val[j]);
         }
-        if (k < nr) s_row[k] = st.row[j];
+        if (k < nr) {
+            const unsigned ra = static_cast<unsigned>(max(st.pa[j], sp.a0) - sp.a0);
+            const unsigned rb = static_cast<unsigned>(max(st.pb[j], sp.b0) - sp.b0);
+            s_row[k] = ra | (rb << 16);
+        }
     }
 }
 
-// Persistent merge kernel.  Each workgroup takes tiles in ticket order; while it computes
-// tile T it already holds the inputs of its next tile N in registers and the split of the
-// tile after that, so global-memory latency overlaps computation.
-//
-// Inside a tile, lane t owns the items [tile_lo + t*IPT, tile_lo + (t+1)*IPT) of the
-// merged sequence (lane 0 starts at the tile's own split, the last lane ends at the next
-// tile's), found by a merge-path search in LDS.  It walks exactly those items in a fixed,
-// unrolled number of steps: take A's head (ties: A first), take B's head, or consume the
-// row-end item.  An equal A/B pair is combined when its A entry is taken (the B head is
-// peeked) and the B entry is skipped when its turn comes, so a pair may straddle two
-// lanes.  Outputs stay in registers with a validity mask until their global offset is known.
+// ---- one lane's walk -------------------------------------------------------------------
+
+// Result of walking a lane's items: outputs in registers (step s fills slot s when bit s of
+// `valid` is set), the steps that were row ends, and the first row the lane touched.
+template <int STEPS>
+struct LaneOut {
+    int crd[STEPS];
+    float val[STEPS];
+    unsigned pos[STEPS];  // (a - a0) | (b - b0) << 16 before the step (child pointers)
+    unsigned valid, row_ends;
+    int first_row;
+};
+
+template <Op OP, bool VALUES, bool CHILD, int IPT>
+__device__ __forceinline__ void walk_lane(LaneOut<IPT + 1> &out, const TileSplit &sp, int tile,
+                                          const int *s_crd, const float *s_val,
+                                          const unsigned *s_row, int tid) {
+    constexpr int kSteps = IPT + 1;
+    constexpr int kMax = INT_MAX;  // head sentinel: row exhausted on that side
+    constexpr int kCapIdx = kBlock * IPT + 1;  // last index of the staged arrays
+    const int r0 = sp.r0, a0 = sp.a0, b0 = sp.b0, r1 = sp.r1, a1 = sp.a1, b1 = sp.b1;
+    const int na = a1 - a0, nr = r1 - r0 + 1;
+    auto A = [&](int x) { return s_crd[x - a0]; };
+    auto B = [&](int y) { return s_crd[na + y - b0]; };
+    auto row_a = [&](int k) { return a0 + static_cast<int>(s_row[k] & 0xffffu); };
+    auto row_b = [&](int k) { return b0 + static_cast<int>(s_row[k] >> 16); };
+
+    const int tile_lo = tile * (kBlock * IPT);
+    const int tile_start = a0 + b0 + r0;  // item index of the tile's first item
+    const int tile_end = a1 + b1 + r1;    // one past its last item
+    const int g_lo = tid == 0 ? tile_start : tile_lo + tid * IPT;
+    const int steps = tid == kBlock - 1 ? tile_end - g_lo
+                                        : min(tile_lo + (tid + 1) * IPT, tile_end) - g_lo;
+    int k = 0, a = a0, b = b0;
+    if (tid > 0 && g_lo < tile_end) {
+        int lo = 0, hi = nr - 1;  // row of item g_lo
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (row_a(mid) + row_b(mid) + r0 + mid <= g_lo) {
+                lo = mid;
+            } else {
+                hi = mid - 1;
+            }
+        }
+        k = lo;
+        const int aS = row_a(k), bS = row_b(k);
+        const int aE = k < nr - 1 ? row_a(k + 1) : a1;
+        const int bE = k < nr - 1 ? row_b(k + 1) : b1;
+        const int D = g_lo - (r0 + k);
+        int slo = max(aS, D - bE), shi = min(aE, D - bS);
+        while (slo < shi) {
+            const int mid = (slo + shi) >> 1;
+            if (A(mid) <= B(D - 1 - mid)) {
+                slo = mid + 1;
+            } else {
+                shi = mid;
+            }
+        }
+        a = slo;
+        b = D - slo;
+    }
+    out.first_row = r0 + k;
+    int aE = k < nr - 1 ? row_a(k + 1) : a1;
+    int bE = k < nr - 1 ? row_b(k + 1) : b1;
+    int last_a = a > row_a(k) ? A(a - 1) : -1;  // previous A of this row inside the tile
+    int xa = a < aE ? A(a) : kMax;
+    int xb = b < bE ? B(b) : kMax;
+    unsigned valid = 0, row_ends = 0;
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+        out.crd[s] = 0;
+        out.val[s] = 0.0f;
+        out.pos[s] = 0;
+        if (s < steps) {
+            if (xa == kMax && xb == kMax) {  // row end
+                row_ends |= 1u << s;
+                ++k;
+                aE = k < nr - 1 ? row_a(k + 1) : a1;
+                bE = k < nr - 1 ? row_b(k + 1) : b1;
+                last_a = -1;
+                xa = a < aE ? A(a) : kMax;
+                xb = b < bE ? B(b) : kMax;
+            } else {
+                const bool take_a = xa <= xb;
+                const bool pair = take_a && xa == xb;
+                if (CHILD) out.pos[s] = static_cast<unsigned>(a - a0) | (static_cast<unsigned>(b - b0) << 16);
+                out.crd[s] = take_a ? xa : xb;
+                if (VALUES) {
+                    const float own = s_val[take_a ? a - a0 : na + b - b0];
+                    if (OP == Op::Union) {
+                        out.val[s] = pair ? own + s_val[na + b - b0] : own;
+                    } else {
+                        out.val[s] = own * s_val[na + b - b0];
+                    }
+                }
+                const bool emit = (OP == Op::Union) ? (take_a || last_a != xb) : pair;
+                valid |= static_cast<unsigned>(emit) << s;
+                if (take_a) last_a = xa;
+                a += take_a;
+                b += !take_a;
+                const int np = take_a ? a : b;  // reload the head that advanced
+                const bool in = np < (take_a ? aE : bE);
+                // always read (the index stays inside the staged tile), then mask
+                const int h0 = s_crd[min(take_a ? np - a0 : na + np - b0, kCapIdx)];
+                const int h = in ? h0 : kMax;
+                xa = take_a ? h : xa;
+                xb = take_a ? xb : h;
+            }
+        }
+    }
+    out.valid = valid;
+    out.row_ends = row_ends;
+}
+
+// ---- kernels ---------------------------------------------------------------------------
+
+// Chunk of tiles owned by workgroup w: [w*chunk, min((w+1)*chunk, num_tiles)).
+__device__ __forceinline__ void chunk_range(int num_tiles, int chunk, int &t0, int &t1) {
+    t0 = blockIdx.x * chunk;
+    t1 = min(t0 + chunk, num_tiles);
+}
+
+template <int WAVES, typename T>
+__device__ __forceinline__ T block_sum(T v, T *s_wave) {
+    v = dev::wave_sum(v);
+    if (dev::lane() == 0) s_wave[threadIdx.x / dev::kWave] = v;
+    __syncthreads();
+    T all = 0;
+#pragma unroll
+    for (int i = 0; i < WAVES; ++i) all += s_wave[i];
+    __syncthreads();
+    return all;
+}
+
+// Output count of each chunk (coordinates and row offsets only).
 template <Op OP, int IPT>
-__global__ __launch_bounds__(kBlock) void csr_merge_tile_kernel(
+__global__ __launch_bounds__(kBlock) void csr_count_kernel(
+    const int *__restrict__ pa, const int *__restrict__ ca, const int *__restrict__ pb,
+    const int *__restrict__ cb, int num_tiles, int chunk, const int *__restrict__ split_r,
+    const int *__restrict__ split_a, const int *__restrict__ split_b,
+    unsigned *__restrict__ chunk_count) {
+    constexpr int kCap = kBlock * IPT + 2;
+    constexpr int kLoads = (kCap + kBlock - 1) / kBlock;
+    static_assert(kCap < 65536, "row offsets are packed in 16 bits");
+    __shared__ int s_crd[kCap];
+    __shared__ unsigned s_row[kCap];
+    __shared__ unsigned s_wave[kBlock / dev::kWave];
+    __shared__ int s_split[3 * (kMaxChunk + 1)];
+
+    const int tid = threadIdx.x;
+    int t0, t1;
+    chunk_range(num_tiles, chunk, t0, t1);
+    if (t0 >= t1) {
+        if (tid == 0) chunk_count[blockIdx.x] = 0u;
+        return;
+    }
+    stage_splits(s_split, split_r, split_a, split_b, t0, t1);
+    __syncthreads();
+    TileSplit sp = lds_split(s_split, 0);
+    Staged<kLoads> st;
+    fetch_tile<false, kLoads>(st, sp, pa, ca, nullptr, pb, cb, nullptr, tid);
+    stage_tile<false, kLoads>(st, sp, s_crd, nullptr, s_row, tid);
+    __syncthreads();
+    TileSplit nsp = lds_split(s_split, t0 + 1 < t1 ? 1 : 0);
+    unsigned total = 0;
+    for (int t = t0; t < t1; ++t) {
+        fetch_tile<false, kLoads>(st, nsp, pa, ca, nullptr, pb, cb, nullptr, tid);
+        const TileSplit nsp2 = lds_split(s_split, t + 2 < t1 ? t + 2 - t0 : t + 1 < t1 ? t + 1 - t0 : t - t0);
+        LaneOut<IPT + 1> lo;
+        walk_lane<OP, false, false, IPT>(lo, sp, t, s_crd, nullptr, s_row, tid);
+        total += block_sum<kBlock / dev::kWave>(static_cast<unsigned>(__popc(lo.valid)), s_wave);
+        if (t + 1 < t1) {
+            stage_tile<false, kLoads>(st, nsp, s_crd, nullptr, s_row, tid);
+            __syncthreads();
+        }
+        sp = nsp;
+        nsp = nsp2;
+    }
+    if (tid == 0) chunk_count[blockIdx.x] = total;
+}
+
+// Writes the result: crd/val (VALUES) or crd plus child pointers (CHILD: for output o,
+// child_a[o] = next_a[a] and child_b[o] = next_b[b] at the A/B positions a, b reached before
+// o, so [child[o], child[o+1]) is the operand's child range under o, empty when absent).
+template <Op OP, int IPT, bool VALUES, bool CHILD>
+__global__ __launch_bounds__(kBlock) void csr_write_kernel(
     const int *__restrict__ pa, const int *__restrict__ ca, const float *__restrict__ va,
     const int *__restrict__ pb, const int *__restrict__ cb, const float *__restrict__ vb,
-    int num_tiles, const int *__restrict__ split_r, const int *__restrict__ split_a,
-    const int *__restrict__ split_b, unsigned long long *__restrict__ status,
-    unsigned *__restrict__ info, int rows, int *__restrict__ pc, int *__restrict__ cc,
-    float *__restrict__ vc) {
-    constexpr int kTileItems = kBlock * IPT;
-    constexpr int kCap = kTileItems + 2;
+    int nnz_a, int nnz_b, int num_tiles, int chunk, const int *__restrict__ split_r,
+    const int *__restrict__ split_a, const int *__restrict__ split_b,
+    const unsigned *__restrict__ chunk_count, int rows, int *__restrict__ pc,
+    int *__restrict__ cc, float *__restrict__ vc, const int *__restrict__ next_a,
+    const int *__restrict__ next_b, int *__restrict__ child_a, int *__restrict__ child_b,
+    unsigned *__restrict__ length) {
+    static_assert(!(VALUES && CHILD), "a level carries values or child pointers, not both");
+    constexpr int kCap = kBlock * IPT + 2;
     constexpr int kLoads = (kCap + kBlock - 1) / kBlock;
     constexpr int kSteps = IPT + 1;
-    constexpr int kMax = INT_MAX;  // sentinel head: row exhausted
-    static_assert(kCap < 65536, "row offsets are packed in 16 bits");
-    static_assert(kSteps <= 32, "masks are 32-bit");
-
     __shared__ int s_crd[kCap];
     __shared__ float s_val[kCap];
     __shared__ unsigned s_row[kCap];
     __shared__ int s_wave[kBlock / dev::kWave];
-    __shared__ int s_next, s_base;
+    __shared__ int s_split[3 * (kMaxChunk + 1)];
 
     const int tid = threadIdx.x;
-    if (tid == 0) s_next = static_cast<int>(atomicAdd(&info[kInfoTicket], 1u));
-    __syncthreads();
-    int cur = s_next;
-    if (cur >= num_tiles) return;
-    TileSplit sp = load_split(split_r, split_a, split_b, cur);
+    int t0, t1;
+    chunk_range(num_tiles, chunk, t0, t1);
+    if (t0 >= t1) return;
+    stage_splits(s_split, split_r, split_a, split_b, t0, t1);
+
+    // Offset of this chunk: the counts of every earlier chunk.
+    int before = 0;
+    for (int i = tid; i < static_cast<int>(blockIdx.x); i += kBlock) before += chunk_count[i];
+    int base = 0;
+    {
+        int total = 0;
+        (void)dev::block_exclusive_sum<kBlock>(before, s_wave, total);
+        base = total;
+    }
+    if (blockIdx.x == 0 && tid == 0) pc[0] = 0;
+
+    TileSplit sp = lds_split(s_split, 0);  // (the exclusive sum above ended with a barrier)
     Staged<kLoads> st;
-    fetch_tile<true, kLoads>(st, sp, pa, ca, va, pb, cb, vb, tid);
-    __syncthreads();  // every lane has read s_next
-    stage_tile<true, kLoads>(st, sp, s_crd, s_val, s_row, tid);
-    if (tid == 0) s_next = static_cast<int>(atomicAdd(&info[kInfoTicket], 1u));
+    fetch_tile<VALUES, kLoads>(st, sp, pa, ca, va, pb, cb, vb, tid);
+    stage_tile<VALUES, kLoads>(st, sp, s_crd, s_val, s_row, tid);
     __syncthreads();
-    int nxt = s_next;
-    TileSplit nsp = sp;
-    if (nxt < num_tiles) nsp = load_split(split_r, split_a, split_b, nxt);
+    TileSplit nsp = lds_split(s_split, t0 + 1 < t1 ? 1 : 0);
+    for (int t = t0; t < t1; ++t) {
+        fetch_tile<VALUES, kLoads>(st, nsp, pa, ca, va, pb, cb, vb, tid);
+        const TileSplit nsp2 = lds_split(s_split, t + 2 < t1 ? t + 2 - t0 : t + 1 < t1 ? t + 1 - t0 : t - t0);
+        LaneOut<kSteps> lo;
+        walk_lane<OP, VALUES, CHILD, IPT>(lo, sp, t, s_crd, s_val, s_row, tid);
 
-    while (true) {
-        // Prefetch the next tile's inputs and take the ticket after it.
-        if (nxt < num_tiles) fetch_tile<true, kLoads>(st, nsp, pa, ca, va, pb, cb, vb, tid);
-        unsigned ticket2 = 0;
-        if (tid == 0) ticket2 = atomicAdd(&info[kInfoTicket], 1u);
-
-        const int r0 = sp.r0, a0 = sp.a0, b0 = sp.b0, r1 = sp.r1, a1 = sp.a1, b1 = sp.b1;
-        const int na = a1 - a0, nr = r1 - r0 + 1;
-        const int tile_lo = cur * kTileItems;
-        const int tile_start = a0 + b0 + r0;  // item index of the tile's first item
-        const int tile_end = a1 + b1 + r1;    // one past its last item
-        auto A = [&](int x) { return s_crd[x - a0]; };
-        auto B = [&](int y) { return s_crd[na + y - b0]; };
-        auto row_a = [&](int k) { return a0 + static_cast<int>(s_row[k] & 0xffffu); };
-        auto row_b = [&](int k) { return b0 + static_cast<int>(s_row[k] >> 16); };
-
-        // This lane's first item and its split (r, a, b).
-        const int g_lo = tid == 0 ? tile_start : tile_lo + tid * IPT;
-        const int g_hi = min(tile_lo + (tid + 1) * IPT, tile_end);
-        const int steps = tid == kBlock - 1 ? tile_end - g_lo : g_hi - g_lo;
-        int k = 0, a = a0, b = b0;
-        if (tid > 0 && g_lo < tile_end) {
-            int lo = 0, hi = nr - 1;
-            while (lo < hi) {
-                const int mid = (lo + hi + 1) >> 1;
-                if (row_a(mid) + row_b(mid) + r0 + mid <= g_lo) {
-                    lo = mid;
-                } else {
-                    hi = mid - 1;
-                }
-            }
-            k = lo;
-            const int aS = row_a(k), bS = row_b(k);
-            const int aE = k < nr - 1 ? row_a(k + 1) : a1;
-            const int bE = k < nr - 1 ? row_b(k + 1) : b1;
-            const int D = g_lo - (r0 + k);
-            int slo = max(aS, D - bE), shi = min(aE, D - bS);
-            while (slo < shi) {
-                const int mid = (slo + shi) >> 1;
-                if (A(mid) <= B(D - 1 - mid)) {
-                    slo = mid + 1;
-                } else {
-                    shi = mid;
-                }
-            }
-            a = slo;
-            b = D - slo;
-        }
-        const int rs = r0 + k;  // first row this lane touches
-        int aE = k < nr - 1 ? row_a(k + 1) : a1;
-        int bE = k < nr - 1 ? row_b(k + 1) : b1;
-        int last_a = a > row_a(k) ? A(a - 1) : -1;  // previous A of this row inside the tile
-        int xa = a < aE ? A(a) : kMax;
-        int xb = b < bE ? B(b) : kMax;
-
-        int out_crd[kSteps];
-        float out_val[kSteps];
-        unsigned valid = 0, row_ends = 0;
-#pragma unroll
-        for (int s = 0; s < kSteps; ++s) {
-            out_crd[s] = 0;
-            out_val[s] = 0.0f;
-            if (s < steps) {
-                if (xa != kMax || xb != kMax) {
-                    if (xa <= xb) {  // take A
-                        const bool pair = (xa == xb);
-                        float v = 0.0f;
-                        if (OP == Op::Union) {
-                            v = s_val[a - a0];
-                            if (pair) v = v + s_val[na + b - b0];
-                        } else if (pair) {
-                            v = s_val[a - a0] * s_val[na + b - b0];
-                        }
-                        out_crd[s] = xa;
-                        out_val[s] = v;
-                        if (OP == Op::Union || pair) valid |= 1u << s;
-                        last_a = xa;
-                        ++a;
-                        xa = a < aE ? A(a) : kMax;
-                    } else {  // take B; skipped when it was combined with the previous A
-                        if (OP == Op::Union && last_a != xb) {
-                            out_crd[s] = xb;
-                            out_val[s] = s_val[na + b - b0];
-                            valid |= 1u << s;
-                        }
-                        ++b;
-                        xb = b < bE ? B(b) : kMax;
-                    }
-                } else {  // row end
-                    row_ends |= 1u << s;
-                    ++k;
-                    aE = k < nr - 1 ? row_a(k + 1) : a1;
-                    bE = k < nr - 1 ? row_b(k + 1) : b1;
-                    last_a = -1;
-                    xa = a < aE ? A(a) : kMax;
-                    xb = b < bE ? B(b) : kMax;
-                }
-            }
-        }
-
-        const int count = __popc(valid);
         int tile_total = 0;
-        if (tid == 0) s_next = static_cast<int>(ticket2);
-        const int offset = dev::block_exclusive_sum<kBlock>(count, s_wave, tile_total);
-        if (tid < dev::kWave) {
-            const uint32_t base = dev::lookback_exclusive(
-                status, cur, static_cast<uint32_t>(tile_total), &info[kInfoError]);
-            if (tid == 0) s_base = static_cast<int>(base);
-        }
-        __syncthreads();
-        const int base = s_base;
-        const int nxt2 = s_next;
-        TileSplit nsp2 = nsp;
-        if (nxt2 < num_tiles) nsp2 = load_split(split_r, split_a, split_b, nxt2);
-        if (cur == 0 && tid == 0) pc[0] = 0;
+        const int offset =
+            dev::block_exclusive_sum<kBlock>(static_cast<int>(__popc(lo.valid)), s_wave, tile_total);
+        // (the scan's barriers also mean every lane is done reading this tile's LDS inputs)
 
-        // Row ends: pos[r+1] = global offset of the first output after row r.  Outputs are
-        // staged in LDS (the inputs are no longer read) for coalesced stores.
+        int ca_v[kSteps], cb_v[kSteps];
+        if (CHILD) {
+#pragma unroll
+            for (int s = 0; s < kSteps; ++s) {
+                ca_v[s] = next_a[sp.a0 + static_cast<int>(lo.pos[s] & 0xffffu)];
+                cb_v[s] = next_b[sp.b0 + static_cast<int>(lo.pos[s] >> 16)];
+            }
+        }
+        int o = offset, r = lo.first_row;
 #pragma unroll
         for (int s = 0; s < kSteps; ++s) {
-            const unsigned below = (1u << s) - 1u;
-            if (row_ends & (1u << s)) {
-                const int r = rs + __popc(row_ends & below);
-                const int at = base + offset + __popc(valid & below);
-                pc[r + 1] = at;
-                if (r + 1 == rows) info[kInfoLength] = static_cast<unsigned>(at);
+            if (lo.row_ends & (1u << s)) {
+                pc[r + 1] = base + o;
+                ++r;
             }
-            if (valid & (1u << s)) {
-                const int o = offset + __popc(valid & below);
-                s_crd[o] = out_crd[s];
-                s_val[o] = out_val[s];
+            if (lo.valid & (1u << s)) {
+                s_crd[o] = lo.crd[s];
+                if (VALUES) s_val[o] = lo.val[s];
+                if (CHILD) {
+                    reinterpret_cast<int *>(s_val)[o] = ca_v[s];
+                    reinterpret_cast<int *>(s_row)[o] = cb_v[s];
+                }
+                ++o;
             }
         }
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < kLoads; ++j) {
-            const int o = tid + j * kBlock;
-            if (o < tile_total) {
-                cc[base + o] = s_crd[o];
-                vc[base + o] = s_val[o];
+            const int q = tid + j * kBlock;
+            if (q < tile_total) {
+                cc[base + q] = s_crd[q];
+                if (VALUES) vc[base + q] = s_val[q];
+                if (CHILD) {
+                    child_a[base + q] = reinterpret_cast<const int *>(s_val)[q];
+                    child_b[base + q] = reinterpret_cast<const int *>(s_row)[q];
+                }
             }
         }
-        if (nxt >= num_tiles) break;
+        base += tile_total;
+        if (t == num_tiles - 1 && tid == 0) {
+            *length = static_cast<unsigned>(base);
+            if (CHILD) {
+                child_a[base] = next_a[nnz_a];
+                child_b[base] = next_b[nnz_b];
+            }
+        }
         __syncthreads();  // staged outputs consumed
-        stage_tile<true, kLoads>(st, nsp, s_crd, s_val, s_row, tid);
-        __syncthreads();
-        cur = nxt;
+        if (t + 1 < t1) {
+            stage_tile<VALUES, kLoads>(st, nsp, s_crd, s_val, s_row, tid);
+            __syncthreads();
+        }
         sp = nsp;
-        nxt = nxt2;
         nsp = nsp2;
     }
+}
+
+// ---- host ------------------------------------------------------------------------------
+
+int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
+                const LevelOperand &A, const LevelOperand &B, const LevelResult &Z,
+                long long *out_len, const char *kernel_name) {
+    const long long total = static_cast<long long>(A.len) + B.len + rows;
+    if (total > static_cast<long long>(INT_MAX) - 2 * kTile) return NACHO_ERR_INDEX_OVERFLOW;
+    const int num_tiles = total > 0 ? static_cast<int>((total + kTile - 1) / kTile) : 1;
+
+    int *splits = nullptr;
+    unsigned *counts = nullptr;
+    NACHO_TRY(call.scratch_n(3 * (static_cast<size_t>(num_tiles) + 1), &splits));
+    int *split_r = splits, *split_a = splits + num_tiles + 1, *split_b = splits + 2 * (num_tiles + 1);
+
+    // Grid: as many workgroups as stay resident, each owning a contiguous chunk of tiles.
+    int resident = 0;
+    const void *probe = values ? reinterpret_cast<const void *>(
+                                     csr_write_kernel<Op::Union, kItemsPerLane, true, false>)
+                               : reinterpret_cast<const void *>(
+                                     csr_write_kernel<Op::Union, kItemsPerLane, false, true>);
+    NACHO_TRY(resident_grid(probe, kBlock, &resident));
+    int chunk = (num_tiles + resident - 1) / resident;
+    if (chunk > kMaxChunk) chunk = kMaxChunk;  // more workgroups than resident: still correct
+    const int grid = (num_tiles + chunk - 1) / chunk;
+    NACHO_TRY(call.scratch_n(static_cast<size_t>(grid) + 4, &counts));
+    unsigned *length = counts + grid;
+
+    const hipStream_t s = call.stream();
+    NACHO_TRY(call.timer_start(kernel_name));  // the whole device pipeline of this level
+    csr_partition_kernel<<<ceil_div(static_cast<size_t>(num_tiles) + 1, 256), 256, 0, s>>>(
+        A.pos, A.crd, B.pos, B.crd, rows, static_cast<int>(total), num_tiles, split_r, split_a,
+        split_b);
+    NACHO_TRY_HIP(hipGetLastError());
+    if (intersect) {
+        csr_count_kernel<Op::Intersect, kItemsPerLane><<<grid, kBlock, 0, s>>>(
+            A.pos, A.crd, B.pos, B.crd, num_tiles, chunk, split_r, split_a, split_b, counts);
+    } else {
+        csr_count_kernel<Op::Union, kItemsPerLane><<<grid, kBlock, 0, s>>>(
+            A.pos, A.crd, B.pos, B.crd, num_tiles, chunk, split_r, split_a, split_b, counts);
+    }
+    NACHO_TRY_HIP(hipGetLastError());
+#define NACHO_WRITE_LAUNCH(OPV, VAL, CHD)                                                        \
+    csr_write_kernel<OPV, kItemsPerLane, VAL, CHD><<<grid, kBlock, 0, s>>>(                      \
+        A.pos, A.crd, A.val, B.pos, B.crd, B.val, A.len, B.len, num_tiles, chunk, split_r,      \
+        split_a, split_b, counts, rows, Z.pos, Z.crd, Z.val, A.next, B.next, Z.child_a,         \
+        Z.child_b, length)
+    if (intersect) {
+        if (!values || child) return NACHO_ERR_INVALID_ARGUMENT;
+        NACHO_WRITE_LAUNCH(Op::Intersect, true, false);
+    } else if (values) {
+        if (child) return NACHO_ERR_INVALID_ARGUMENT;
+        NACHO_WRITE_LAUNCH(Op::Union, true, false);
+    } else if (child) {
+        NACHO_WRITE_LAUNCH(Op::Union, false, true);
+    } else {
+        NACHO_WRITE_LAUNCH(Op::Union, false, false);
+    }
+#undef NACHO_WRITE_LAUNCH
+    NACHO_TRY_HIP(hipGetLastError());
+    NACHO_TRY(call.timer_stop());
+
+    unsigned len = 0;
+    if (num_tiles > 0) NACHO_TRY(call.read_back(&len, length, sizeof(len)));
+    *out_len = len;
+    return NACHO_OK;
 }
 
 bool bad_csr(const nacho_csr *t) {
@@ -378,10 +571,9 @@ bool bad_csr(const nacho_csr *t) {
     return false;
 }
 
-template <Op OP>
-int csr_binary(const nacho_csr *a, const nacho_csr *b, nacho_csr *z, int32_t num_blocks,
-               int32_t threads_per_block, void *stream, const nacho_allocator *alloc,
-               const char *kernel_name) {
+int csr_binary(bool intersect, const nacho_csr *a, const nacho_csr *b, nacho_csr *z,
+               int32_t num_blocks, int32_t threads_per_block, void *stream,
+               const nacho_allocator *alloc, const char *kernel_name) {
     if (!z) return NACHO_ERR_INVALID_ARGUMENT;
     *z = nacho_csr{};
     NACHO_TRY(check_launch_hints(num_blocks, threads_per_block));
@@ -391,45 +583,23 @@ int csr_binary(const nacho_csr *a, const nacho_csr *b, nacho_csr *z, int32_t num
     }
     const int rows = a->dim_i_size;
     const long long nnz_a = a->dim_j_length, nnz_b = b->dim_j_length;
-    const long long total = nnz_a + nnz_b + rows;
-    if (total > static_cast<long long>(INT_MAX) - 2 * kTile) return NACHO_ERR_INDEX_OVERFLOW;
-    const long long cap = (OP == Op::Union) ? nnz_a + nnz_b : (nnz_a < nnz_b ? nnz_a : nnz_b);
-    const int num_tiles = total > 0 ? static_cast<int>((total + kTile - 1) / kTile) : 1;
+    if (nnz_a + nnz_b + rows > static_cast<long long>(INT_MAX) - 2 * kTile) {
+        return NACHO_ERR_INDEX_OVERFLOW;
+    }
+    const long long cap = intersect ? (nnz_a < nnz_b ? nnz_a : nnz_b) : nnz_a + nnz_b;
 
     Call call(stream, alloc);
-    unsigned long long *status = nullptr;
-    int *splits = nullptr;
-    NACHO_TRY(call.scratch_n(static_cast<size_t>(num_tiles) + kInfoWords / 2, &status));
-    NACHO_TRY(call.scratch_n(3 * (static_cast<size_t>(num_tiles) + 1), &splits));
-    unsigned *info = reinterpret_cast<unsigned *>(status + num_tiles);
-    int *split_r = splits, *split_a = splits + num_tiles + 1, *split_b = splits + 2 * (num_tiles + 1);
-
     int *pc = nullptr, *cc = nullptr;
     float *vc = nullptr;
     NACHO_TRY(call.result_n(static_cast<size_t>(rows) + 1, &pc));
     NACHO_TRY(call.result_n(static_cast<size_t>(cap), &cc));
     NACHO_TRY(call.result_n(static_cast<size_t>(cap), &vc));
 
-    const hipStream_t s = call.stream();
-    csr_partition_kernel<<<ceil_div(static_cast<size_t>(num_tiles) + 1, 256), 256, 0, s>>>(
-        a->dim_j_offsets, a->dim_j_indices, b->dim_j_offsets, b->dim_j_indices, rows,
-        static_cast<int>(total), num_tiles, split_r, split_a, split_b, status, info);
-    NACHO_TRY_HIP(hipGetLastError());
-    auto kernel = csr_merge_tile_kernel<OP, kItemsPerLane>;
-    int resident = 0;
-    NACHO_TRY(resident_grid(reinterpret_cast<const void *>(kernel), kBlock, &resident));
-    const int grid = num_tiles < resident ? num_tiles : resident;
-    NACHO_TRY(call.timer_start(kernel_name));
-    kernel<<<grid, kBlock, 0, s>>>(a->dim_j_offsets, a->dim_j_indices, a->values,
-                                   b->dim_j_offsets, b->dim_j_indices, b->values, num_tiles,
-                                   split_r, split_a, split_b, status, info, rows, pc, cc, vc);
-    NACHO_TRY_HIP(hipGetLastError());
-    NACHO_TRY(call.timer_stop());
-
-    unsigned words[kInfoWords] = {};
-    NACHO_TRY(call.read_back(words, info, sizeof(words)));
-    if (words[kInfoError] != 0) return NACHO_ERR_INTERNAL;
-    const long long nnz = words[kInfoLength];
+    const LevelOperand A{a->dim_j_offsets, a->dim_j_indices, a->values, a->dim_j_length, nullptr};
+    const LevelOperand B{b->dim_j_offsets, b->dim_j_indices, b->values, b->dim_j_length, nullptr};
+    const LevelResult Z{pc, cc, vc, nullptr, nullptr};
+    long long nnz = 0;
+    NACHO_TRY(merge_level(call, intersect, true, false, rows, A, B, Z, &nnz, kernel_name));
     if (nnz > cap) return NACHO_ERR_MALFORMED_INPUT;
     if (nnz == 0) {
         // Empty result: zeroed offsets, no coordinate/value buffers
@@ -458,15 +628,15 @@ extern "C" {
 int nacho_gpu_csr_add_f32(const nacho_csr *a, const nacho_csr *b, nacho_csr *z,
                           int32_t num_blocks, int32_t threads_per_block, void *stream,
                           const nacho_allocator *alloc) {
-    return nacho::csr::csr_binary<nacho::csr::Op::Union>(a, b, z, num_blocks, threads_per_block,
-                                                         stream, alloc, "csr_merge_tile_kernel<Union>");
+    return nacho::csr::csr_binary(false, a, b, z, num_blocks, threads_per_block, stream, alloc,
+                                  "csr_add: partition+count+write");
 }
 
 int nacho_gpu_csr_mul_f32(const nacho_csr *a, const nacho_csr *b, nacho_csr *z,
                           int32_t num_blocks, int32_t threads_per_block, void *stream,
                           const nacho_allocator *alloc) {
-    return nacho::csr::csr_binary<nacho::csr::Op::Intersect>(
-        a, b, z, num_blocks, threads_per_block, stream, alloc, "csr_merge_tile_kernel<Intersect>");
+    return nacho::csr::csr_binary(true, a, b, z, num_blocks, threads_per_block, stream, alloc,
+                                  "csr_mul: partition+count+write");
 }
 
 }  // extern "C"

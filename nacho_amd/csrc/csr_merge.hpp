@@ -1,0 +1,41 @@
+// Level merge shared by CSR add/mul and CSF3 add (see csr_merge.hip).
+#pragma once
+
+#include <cstdint>
+
+#include "runtime.hpp"
+
+namespace nacho {
+namespace csr {
+
+// One operand level: `pos` has rows + 1 entries (pos[0] == 0) indexing `crd`/`val`
+// (`len` entries).  `next` (optional) is the offsets array of the level below, indexed by
+// this level's positions (len + 1 entries).
+struct LevelOperand {
+    const int *pos;
+    const int *crd;
+    const float *val;
+    int len;
+    const int *next;
+};
+
+// Result buffers, sized by the caller for the worst case: pos rows + 1, crd/val the union
+// (or intersection) bound, child_a/child_b that bound + 1.
+struct LevelResult {
+    int *pos;
+    int *crd;
+    float *val;
+    int *child_a;
+    int *child_b;
+};
+
+// Merge A and B row by row: union (or intersection) of each row's coordinates, with values
+// (a+b / a*b / copies) when `values`, or with child pointers when `child`.  Writes Z.pos for
+// every row and returns the result length in *out_len.  The call's kernel timer (if enabled)
+// brackets all of the level's kernels under `kernel_name`.
+int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
+                const LevelOperand &A, const LevelOperand &B, const LevelResult &Z,
+                long long *out_len, const char *kernel_name);
+
+}  // namespace csr
+}  // namespace nacho

@@ -87,9 +87,15 @@ __device__ __forceinline__ unsigned long long peek(const unsigned long long *slo
 constexpr uint32_t kMaxPolls = 1u << 24;
 
 // Executed by every lane of ONE wavefront of the tile's workgroup.  Publishes `aggregate`
-// for `tile`, walks back over predecessors 64 at a time until an inclusive prefix is found,
-// publishes this tile's inclusive prefix, and returns the exclusive prefix (uniform across
-// the wave).
+// for `tile`, walks back over predecessors until an inclusive prefix is found, publishes
+// this tile's inclusive prefix, and returns the exclusive prefix (uniform across the wave).
+// One poll covers kLookbackWindow predecessors (kPerLane status words per lane, nearest
+// first), because with hundreds of tiles in flight the nearest inclusive prefix is usually
+// further back than one word per lane reaches, and every extra round is a device-coherent
+// memory round trip.
+constexpr int kPerLane = 4;
+constexpr int kLookbackWindow = kWave * kPerLane;
+
 __device__ __forceinline__ uint32_t lookback_exclusive(unsigned long long *status, int tile,
                                                        uint32_t aggregate, uint32_t *error) {
     const int l = lane();
@@ -99,20 +105,35 @@ __device__ __forceinline__ uint32_t lookback_exclusive(unsigned long long *statu
     }
     if (l == 0) publish(&status[tile], pack_status(kStateAggregate, aggregate));
     uint32_t exclusive = 0;
-    int nearest = tile - 1;  // predecessor inspected by lane 0; lane l inspects nearest - l
+    int nearest = tile - 1;  // lane l inspects nearest - (kPerLane*l + q), q = 0..kPerLane-1
     uint32_t polls = 0;
     while (true) {
-        const int idx = nearest - l;
-        const unsigned long long word =
-            idx >= 0 ? peek(&status[idx]) : pack_status(kStateInclusive, 0);
-        const uint32_t state = static_cast<uint32_t>(word >> 32);
-        const uint32_t value = static_cast<uint32_t>(word);
-        const unsigned long long inclusive_lanes = __ballot(state == kStateInclusive);
-        const unsigned long long empty_lanes = __ballot(state == kStateEmpty);
+        uint32_t state[kPerLane], value[kPerLane];
+#pragma unroll
+        for (int q = 0; q < kPerLane; ++q) {
+            const int idx = nearest - (kPerLane * l + q);
+            const unsigned long long word =
+                idx >= 0 ? peek(&status[idx]) : pack_status(kStateInclusive, 0);
+            state[q] = static_cast<uint32_t>(word >> 32);
+            value[q] = static_cast<uint32_t>(word);
+        }
+        // First inclusive word in this lane (kPerLane = none), and whether an unpublished
+        // word precedes it.
+        int first = kPerLane;
+#pragma unroll
+        for (int q = kPerLane - 1; q >= 0; --q) {
+            if (state[q] == kStateInclusive) first = q;
+        }
+        bool empty_before = false;
+#pragma unroll
+        for (int q = 0; q < kPerLane; ++q) {
+            if (q <= first && q < kPerLane && state[q] == kStateEmpty) empty_before = true;
+        }
+        const unsigned long long inclusive_lanes = __ballot(first < kPerLane);
         const int stop = inclusive_lanes ? (__ffsll(static_cast<long long>(inclusive_lanes)) - 1)
-                                         : kWave;  // lanes [0, stop] are needed
-        const unsigned long long needed = stop >= kWave - 1 ? ~0ull : ((2ull << stop) - 1);
-        if (empty_lanes & needed) {
+                                         : kWave;  // lanes before `stop` contribute fully
+        const bool lane_needed = l <= stop;
+        if (__ballot(lane_needed && empty_before) != 0ull) {
             if (++polls < kMaxPolls) {
                 __builtin_amdgcn_s_sleep(1);
                 continue;
@@ -120,9 +141,14 @@ __device__ __forceinline__ uint32_t lookback_exclusive(unsigned long long *statu
             if (l == 0) atomicOr(error, 1u);
             break;
         }
-        exclusive += wave_sum(l <= stop ? value : 0u);
+        uint32_t mine = 0;
+#pragma unroll
+        for (int q = 0; q < kPerLane; ++q) {
+            if (l < stop || (l == stop && q <= first)) mine += value[q];
+        }
+        exclusive += wave_sum(mine);
         if (stop < kWave) break;
-        nearest -= kWave;
+        nearest -= kLookbackWindow;
     }
     if (l == 0) publish(&status[tile], pack_status(kStateInclusive, exclusive + aggregate));
     return exclusive;

@@ -119,6 +119,7 @@ Call::Call(void *stream, const nacho_allocator *alloc)
       timing_(g_timing_enabled.load(std::memory_order_relaxed) != 0) {}
 
 Call::~Call() {
+    if (timed_) t_last_ms = timed_ms_;
     for (void *p : scratch_) release(p);
     if (!committed_) {
         for (void *p : results_) release(p);
@@ -180,7 +181,8 @@ int Call::read_back(void *host, const void *device, size_t bytes) {
         t_timer_armed = false;
         float ms = 0.0f;
         NACHO_TRY_HIP(hipEventElapsedTime(&ms, t_ev_start, t_ev_stop));
-        t_last_ms = ms;
+        timed_ms_ += ms;
+        timed_ = true;
     }
     return NACHO_OK;
 }

@@ -68,7 +68,9 @@ class Call {
     // Copy `bytes` from device to a host variable and wait for the stream.
     int read_back(void *host, const void *device, size_t bytes);
 
-    // Kernel timing hook (see nacho_set_kernel_timing).
+    // Kernel timing hook (see nacho_set_kernel_timing): intervals between timer_start and
+    // timer_stop are summed over the call and reported when the call ends.  An interval is
+    // collected at the next read_back (which synchronises the stream).
     int timer_start(const char *name);
     int timer_stop();
 
@@ -82,6 +84,8 @@ class Call {
     std::vector<void *> results_;
     bool committed_ = false;
     bool timing_ = false;
+    bool timed_ = false;
+    float timed_ms_ = 0.0f;  // sum of this call's bracketed intervals
 };
 
 // Validate launch-geometry hints the reference passes (generate_bindings.cpp:292-325).
