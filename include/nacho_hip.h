@@ -24,7 +24,8 @@
  * Input contract (the reference's, made explicit): pos[0] == 0, pos non-decreasing,
  * pos[rows] == length of the coordinate array, coordinates strictly increasing within
  * each fibre (sorted, no duplicates), COO/COO3 coordinates sorted lexicographically and
- * distinct.  nacho_validate_*() check this on the device when asked.
+ * distinct.  As in the reference, the device does not check it: host-side shape and pointer
+ * checks return NACHO_ERR_INVALID_ARGUMENT, but operand contents are trusted.
  */
 #ifndef NACHO_HIP_H
 #define NACHO_HIP_H
@@ -185,6 +186,20 @@ int nacho_gpu_coo3d_add_f32(const nacho_coo3 *a, const nacho_coo3 *b, nacho_coo3
 int nacho_gpu_csf_add_f32(const nacho_csf3 *a, const nacho_csf3 *b, nacho_csf3 *z,
                           int32_t num_blocks, int32_t threads_per_block, void *stream,
                           const nacho_allocator *alloc);
+
+/* Z_ik = sum_j a_ij * b_jk over CSR operands (ESC SpGEMM), int32 result.  Replaces
+ * spgemm::spgemm_gpu_i32_f32 (compiler.cpp:145-148).  Fails with NACHO_ERR_INDEX_OVERFLOW
+ * when nnz(Z) does not fit int32; use nacho_gpu_spgemm64_f32 then. */
+int nacho_gpu_spgemm_f32(const nacho_csr *a, const nacho_csr *b, nacho_csr *z,
+                         int32_t num_blocks, int32_t threads_per_block, void *stream,
+                         const nacho_allocator *alloc);
+
+/* The same product with 64-bit result offsets and 64-bit product counts, for results and
+ * intermediate product counts beyond 2^31 (the R-MAT scale-20 square has 6.0e9 products and
+ * 3.6e9 result entries).  No counterpart in the reference (int32-only). */
+int nacho_gpu_spgemm64_f32(const nacho_csr *a, const nacho_csr *b, nacho_csr64 *z,
+                           int32_t num_blocks, int32_t threads_per_block, void *stream,
+                           const nacho_allocator *alloc);
 
 /* ---- diagnostics ------------------------------------------------------------------ */
 

@@ -17,6 +17,7 @@ from .ops import (  # noqa: F401
     gpu_spgemm64_f32,
     gpu_spgemm_f32,
     last_kernel_ms,
+    release_cached_memory,
     set_kernel_timing,
 )
 from .tensors import COO3_gpu, COO_gpu, CSF3_gpu, CSR64_gpu, CSR_gpu  # noqa: F401

@@ -177,13 +177,17 @@ int Call::read_back(void *host, const void *device, size_t bytes) {
     NACHO_TRY_HIP(hipMemcpyAsync(t_pinned, device, bytes, hipMemcpyDeviceToHost, stream_));
     NACHO_TRY_HIP(hipStreamSynchronize(stream_));
     std::memcpy(host, t_pinned, bytes);
-    if (t_timer_armed) {
-        t_timer_armed = false;
-        float ms = 0.0f;
-        NACHO_TRY_HIP(hipEventElapsedTime(&ms, t_ev_start, t_ev_stop));
-        timed_ms_ += ms;
-        timed_ = true;
-    }
+    return collect_timer();
+}
+
+int Call::collect_timer() {
+    if (!t_timer_armed) return NACHO_OK;
+    t_timer_armed = false;
+    NACHO_TRY_HIP(hipEventSynchronize(t_ev_stop));
+    float ms = 0.0f;
+    NACHO_TRY_HIP(hipEventElapsedTime(&ms, t_ev_start, t_ev_stop));
+    timed_ms_ += ms;
+    timed_ = true;
     return NACHO_OK;
 }
 

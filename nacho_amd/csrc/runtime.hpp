@@ -73,6 +73,9 @@ class Call {
     // collected at the next read_back (which synchronises the stream).
     int timer_start(const char *name);
     int timer_stop();
+    // Wait for the stopped interval (if any) and add it to the call's total, for calls whose
+    // last step is not a read_back.
+    int collect_timer();
 
   private:
     void *allocate(size_t bytes);

@@ -199,6 +199,11 @@ def gpu_spgemm64_f32(a: CSR_gpu, b: CSR_gpu, num_blocks: int = 256,
                  _adopt_csr64, num_blocks, threads_per_block)
 
 
+def release_cached_memory() -> None:
+    """Return the default allocator's cached, unused device buffers to the driver."""
+    _lib.check(_lib.load().nacho_release_cached_memory(), "nacho_release_cached_memory")
+
+
 def set_kernel_timing(enable: bool) -> None:
     _lib.load().nacho_set_kernel_timing(1 if enable else 0)
 

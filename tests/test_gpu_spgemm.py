@@ -1,0 +1,264 @@
+"""GPU parity of the ESC SpGEMM (gfx950 kernels through the C ABI) against the CPU oracle.
+
+Bar: structure (pos, crd) exact; values within rel 1e-5 / abs 1e-6 of the float64-accumulated
+oracle (the GPU sums float32 products in float64 and rounds once, so it sits far inside).
+Cases cover the reference smoke shapes (tests/smoke.py:213-218), the tile geometry (rows
+sharing tiles, rows of exactly one tile, rows needing several merge levels, runs of equal
+columns crossing tiles), wide column ranges (64-bit sort keys), empty operands and the full
+R-MAT scale-20 square, checked by a row sample and a size-independent checksum.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle
+from tests.helpers import check_csr_invariants, csr_from_rows, random_csr
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-5, 1e-6
+
+
+def to_gpu(t, rows, cols, device):
+    import nacho_amd
+
+    pos, crd, val = t
+    return nacho_amd.CSR_gpu(torch.from_numpy(np.asarray(pos, np.int32)).to(device),
+                             torch.from_numpy(np.asarray(crd, np.int32)).to(device),
+                             torch.from_numpy(np.asarray(val, np.float32)).to(device),
+                             torch.tensor([rows, cols], dtype=torch.int32))
+
+
+def spgemm(a, b, rows, inner, cols, device, wide=True):
+    import nacho_amd
+
+    fn = nacho_amd.gpu_spgemm64_f32 if wide else nacho_amd.gpu_spgemm_f32
+    print(f"[gpu] spgemm{'64' if wide else ''} {rows}x{inner} @ {inner}x{cols} "
+          f"nnz=({len(a[1])},{len(b[1])})", flush=True)
+    z = fn(to_gpu(a, rows, inner, device), to_gpu(b, inner, cols, device))
+    torch.cuda.synchronize()
+    assert tuple(z.shape.tolist()) == (rows, cols)
+    return (z.dim_j_offsets.cpu().numpy(), z.dim_j_indices.cpu().numpy(),
+            z.values.cpu().numpy())
+
+
+def check(rows, inner, cols, a, b, z, what):
+    pos, crd, val = z
+    check_csr_invariants(pos, crd, rows, cols)
+    wp, wc, wv = oracle.port_spgemm(rows, inner, cols, *a, *b)
+    np.testing.assert_array_equal(np.asarray(pos, np.int64), wp, err_msg=f"{what}: pos")
+    np.testing.assert_array_equal(crd, wc, err_msg=f"{what}: crd")
+    np.testing.assert_allclose(val, wv, rtol=RTOL, atol=ATOL, err_msg=f"{what}: values")
+
+
+def run_and_check(gpu, rows, inner, cols, a, b, what, wide=True):
+    z = spgemm(a, b, rows, inner, cols, gpu, wide)
+    check(rows, inner, cols, a, b, z, what)
+    return z
+
+
+@pytest.mark.parametrize("wide", [True, False])
+def test_reference_smoke_case(gpu, wide):
+    rng = np.random.default_rng(0)
+    a = random_csr(rng, 200, 180, 0.05)
+    b = random_csr(rng, 180, 200, 0.05)
+    z = run_and_check(gpu, 200, 180, 200, a, b, "smoke", wide)
+    assert z[0].dtype == (np.int64 if wide else np.int32)
+
+
+@pytest.mark.parametrize("shape,density,seed", [((1000, 800, 1200), 0.01, 1),
+                                                ((3000, 3000, 3000), 0.003, 2),
+                                                ((64, 5000, 64), 0.3, 3),
+                                                ((1, 300, 20000), 0.5, 4),
+                                                ((20000, 50, 1), 0.2, 5)])
+def test_random_shapes(gpu, shape, density, seed):
+    rows, inner, cols = shape
+    rng = np.random.default_rng(seed)
+    a = random_csr(rng, rows, inner, density)
+    b = random_csr(rng, inner, cols, density)
+    run_and_check(gpu, rows, inner, cols, a, b, f"random{shape}")
+
+
+def product_rows(lengths, cols, rng):
+    """A (len(lengths) x len(lengths)) diagonal-pattern A times B whose row r has lengths[r]
+    distinct columns: row r of the product has exactly lengths[r] products."""
+    n = len(lengths)
+    a = csr_from_rows(n, n, [[r] for r in range(n)],
+                      rng.uniform(0.5, 1.5, n).astype(np.float32))
+    rows_b = [np.sort(rng.choice(cols, size=L, replace=False)).tolist() for L in lengths]
+    nb = sum(lengths)
+    b = csr_from_rows(n, cols, rows_b, rng.uniform(-1, 1, nb).astype(np.float32))
+    return a, b
+
+
+def test_tile_boundaries(gpu):
+    """Rows of exactly 1, kShort, kShort+1, one tile, one tile + 1 and several tiles of
+    products, with empty rows between (tiles: 4096 products; short rows: <= 2048)."""
+    rng = np.random.default_rng(7)
+    lengths = [0, 1, 2047, 2048, 0, 2049, 4095, 4096, 4097, 0, 0, 8192, 8193, 3, 12289,
+               20481, 1, 1, 1, 2, 40000, 0, 5, 0]
+    a, b = product_rows(lengths, 50000, rng)
+    n = len(lengths)
+    run_and_check(gpu, n, n, 50000, a, b, "tile boundaries")
+
+
+def test_many_short_rows_share_tiles(gpu):
+    rng = np.random.default_rng(8)
+    lengths = rng.integers(0, 40, 30000)
+    lengths[rng.random(30000) < 0.3] = 0
+    lengths[:5] = 0
+    lengths[-7:] = 0
+    a, b = product_rows(lengths.tolist(), 500, rng)
+    n = len(lengths)
+    run_and_check(gpu, n, n, 500, a, b, "short rows")
+
+
+def test_long_runs_cross_tiles(gpu):
+    """One row with 9000 A entries whose B rows all hold columns {5, 7}: two runs of 9000
+    equal columns crossing tile boundaries (and merge levels)."""
+    rng = np.random.default_rng(9)
+    inner = 9000
+    a = csr_from_rows(2, inner, [list(range(inner)), [3, 17]],
+                      rng.uniform(-1, 1, inner + 2).astype(np.float32))
+    b = csr_from_rows(inner, 10, [[5, 7]] * inner,
+                      rng.uniform(-1, 1, 2 * inner).astype(np.float32))
+    pos, crd, val = run_and_check(gpu, 2, inner, 10, a, b, "long runs")
+    assert pos.tolist() == [0, 2, 4] and crd.tolist() == [5, 7, 5, 7]
+
+
+def test_wide_columns_use_64bit_keys(gpu):
+    """cols > 2^20 leaves fewer than 12 free key bits, so the 64-bit sort key path runs."""
+    rng = np.random.default_rng(10)
+    rows, inner, cols = 4000, 3000, 3_000_000
+    a = random_csr(rng, rows, inner, 0.002)
+    pb = np.zeros(inner + 1, np.int32)
+    lens = rng.integers(0, 30, inner)
+    pb[1:] = np.cumsum(lens)
+    cb = np.concatenate([np.sort(rng.choice(cols, size=L, replace=False)) for L in lens])
+    vb = rng.uniform(-1, 1, len(cb)).astype(np.float32)
+    run_and_check(gpu, rows, inner, cols, a, (pb, cb.astype(np.int32), vb), "wide cols")
+
+
+def test_cancellation_keeps_entry(gpu):
+    a = csr_from_rows(1, 2, [[0, 1]], np.array([1.0, -1.0], np.float32))
+    b = csr_from_rows(2, 5, [[3], [3]], np.array([2.5, 2.5], np.float32))
+    pos, crd, val = spgemm(a, b, 1, 2, 5, gpu)
+    assert pos.tolist() == [0, 1] and crd.tolist() == [3] and val.tolist() == [0.0]
+
+
+@pytest.mark.parametrize("wide", [True, False])
+def test_empty_operands(gpu, wide):
+    a = csr_from_rows(3, 4, [[], [], []])
+    b = csr_from_rows(4, 5, [[1], [], [2], []])
+    pos, crd, val = spgemm(a, b, 3, 4, 5, gpu, wide)
+    assert pos.tolist() == [0, 0, 0, 0] and len(crd) == 0 and len(val) == 0
+    # A's columns hit only empty rows of B
+    a = csr_from_rows(3, 4, [[1, 3], [], [1]])
+    pos, crd, val = spgemm(a, b, 3, 4, 5, gpu, wide)
+    assert pos.tolist() == [0, 0, 0, 0] and len(crd) == 0
+    # no rows at all
+    a = csr_from_rows(0, 4, [])
+    pos, crd, val = spgemm(a, b, 0, 4, 5, gpu, wide)
+    assert pos.tolist() == [0]
+
+
+def test_identity_exact(gpu):
+    rng = np.random.default_rng(11)
+    n = 5000
+    a = random_csr(rng, n, n, 0.002)
+    eye = csr_from_rows(n, n, [[i] for i in range(n)], np.ones(n, np.float32))
+    pos, crd, val = spgemm(a, eye, n, n, n, gpu)
+    np.testing.assert_array_equal(pos, a[0])
+    np.testing.assert_array_equal(crd, a[1])
+    np.testing.assert_array_equal(val, a[2])
+
+
+def test_dimension_mismatch_raises(gpu):
+    import nacho_amd
+
+    a = csr_from_rows(2, 3, [[0], [1]])
+    b = csr_from_rows(4, 3, [[0], [], [], []])
+    with pytest.raises(Exception):
+        nacho_amd.gpu_spgemm64_f32(to_gpu(a, 2, 3, gpu), to_gpu(b, 4, 3, gpu))
+
+
+def test_rmat_medium(gpu):
+    from nacho_amd import synth
+
+    n = 1 << 15
+    pos, crd, val = synth.rmat_csr(15, seed=4)
+    t = (pos, crd, val)
+    run_and_check(gpu, n, n, n, t, t, "rmat15")
+
+
+def test_deterministic(gpu):
+    from nacho_amd import synth
+
+    n = 1 << 13
+    t = synth.rmat_csr(13, seed=5)
+    z1 = spgemm(t, t, n, n, n, gpu)
+    z2 = spgemm(t, t, n, n, n, gpu)
+    for x, y in zip(z1, z2):
+        np.testing.assert_array_equal(x, y)
+
+
+def _row_sample(pos, crd, val, rows):
+    """Rows `rows` of a CSR as a new CSR (same column space)."""
+    lens = (pos[rows + 1] - pos[rows]).astype(np.int64)
+    sp = np.zeros(len(rows) + 1, np.int64)
+    sp[1:] = np.cumsum(lens)
+    idx = np.concatenate([np.arange(pos[r], pos[r + 1]) for r in rows]) if sp[-1] else \
+        np.zeros(0, np.int64)
+    return sp.astype(np.int32), crd[idx], val[idx]
+
+
+def test_c4_full_size(gpu):
+    """R-MAT scale 20 squared: 6.0e9 products, 3.6e9 results (int64 offsets).  Checked by the
+    row-sum identity sum_ik C_ik = sum_j colsum(A)_j rowsum(A)_j, exact rows against the
+    oracle on a row sample (including the row with the most products), and the int32 entry
+    point refusing the result."""
+    import nacho_amd
+    from nacho_amd import synth
+
+    n = 1 << 20
+    pos, crd, val = synth.c4_operand()
+    a_gpu = to_gpu((pos, crd, val), n, n, gpu)
+    print("[gpu] spgemm64 C4", flush=True)
+    z = nacho_amd.gpu_spgemm64_f32(a_gpu, a_gpu)
+    torch.cuda.synchronize()
+    zpos = z.dim_j_offsets
+    nnz = int(zpos[-1].item())
+    assert nnz == z.values.numel() == z.dim_j_indices.numel()
+    assert nnz > 2**31  # the reason for 64-bit offsets
+    assert bool((zpos[1:] >= zpos[:-1]).all().item()) and int(zpos[0].item()) == 0
+    # checksum over every value
+    total = float(z.values.to(torch.float64).sum().item())
+    v64 = val.astype(np.float64)
+    lens = np.diff(pos).astype(np.int64)
+    row_of = np.repeat(np.arange(n), lens)
+    colsum = np.bincount(crd, weights=v64, minlength=n)
+    rowsum = np.bincount(row_of, weights=v64, minlength=n)
+    want = float(np.dot(colsum, rowsum))
+    # every entry is rounded once to float32 (relative error <= 2^-24)
+    assert total == pytest.approx(want, rel=1e-7)
+    # exact rows on a sample
+    prods = np.bincount(row_of, weights=lens[crd].astype(np.float64), minlength=n)
+    rng = np.random.default_rng(12)
+    sample = np.unique(np.concatenate([[int(np.argmax(prods))], rng.integers(0, n, 300)]))
+    sa = _row_sample(pos, crd, val, sample)
+    wp, wc, wv = oracle.port_spgemm(len(sample), n, n, *sa, pos, crd, val)
+    zpos_h = zpos.cpu().numpy()
+    for i, r in enumerate(sample):
+        s, e = int(zpos_h[r]), int(zpos_h[r + 1])
+        np.testing.assert_array_equal(z.dim_j_indices[s:e].cpu().numpy(), wc[wp[i]:wp[i + 1]],
+                                      err_msg=f"row {r}")
+        np.testing.assert_allclose(z.values[s:e].cpu().numpy(), wv[wp[i]:wp[i + 1]],
+                                   rtol=RTOL, atol=ATOL, err_msg=f"row {r}")
+    del z
+    try:
+        with pytest.raises(RuntimeError, match="exceeds int32"):
+            nacho_amd.gpu_spgemm_f32(a_gpu, a_gpu)
+    finally:
+        torch.cuda.synchronize()
+        nacho_amd.release_cached_memory()
