@@ -1,6 +1,6 @@
 """Benchmark of the nacho GPU path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|c4]
 
 A step is one call of the hot path over one batch of synthetic input, with the operands
 already resident in HBM: `nacho_amd.gpu_csr_add_f32(A, B)` for the default workload (C2:
@@ -20,6 +20,11 @@ Prints ONE JSON line:
   cpu_baseline     the C restatement of the reference's CPU kernel (oracle/) on this host's
                    cores over a bounded sample of the same workload
 Algorithmic bytes (CSR add/mul) = 3*4*(rows+1) + 8*(nnzA + nnzB + nnzC).
+
+Workload c4 (ESC SpGEMM, C = A*A on the R-MAT 2^20 operand) reports GFLOP/s = 2*P / call
+time, P = number of intermediate products; its roofline bytes are
+4*(n+1) + 8*nnzA + 8*P (B's gathered entries) + 8*(n+1) + 8*nnzC, and its CPU baseline is
+the row-parallel C SpGEMM of oracle/ on a random row sample.
 """
 
 from __future__ import annotations
@@ -48,6 +53,12 @@ WORKLOADS = {
                               "csr_write_kernel<Intersect> (one call's device pipeline)",
                desc="C3 csr_mul f32 2^20x2^20, A as C2, B = 50% of A + fresh columns "
                     "(seed 3)"),
+    "c4": dict(op="spgemm", kernel="expand_kernel + sort_tiles_kernel + level_merge_kernel + "
+                                 "compress_{count,write}_kernel (one call's device "
+                                 "pipeline, host planning gaps excluded)",
+               desc="C4 ESC SpGEMM C=A*A f32, R-MAT 2^20 (a,b,c,d)=(.57,.19,.19,.05), "
+                    "8*2^20 draws deduplicated, no vertex permutation, values U[0.5,1.5], "
+                    "seed 1; int64 result offsets"),
 }
 
 
@@ -63,9 +74,9 @@ def make_operands(workload):
     return synth.c3_operands()
 
 
-def traffic_from_profiles(workload):
+def traffic_from_profiles(workload, family="csr_merge"):
     """Measured HBM bytes per launch of the dominant kernel, if profiled (else None)."""
-    path = REPO / "profiles" / f"csr_merge_{workload}_traffic.json"
+    path = REPO / "profiles" / f"{family}_{workload}_traffic.json"
     if not path.exists():
         return None
     try:
@@ -97,6 +108,153 @@ def cpu_baseline(workload, op, a, b, rows, bytes_per_call, budget_s):
         "sample": f"{len(times)} full {workload} calls of the C restatement "
                   f"(oracle/nacho_oracle.c), mean of the middle {len(trimmed)}: "
                   f"{sec * 1e3:.1f} ms/call",
+    }
+
+
+def spgemm_products(pos, crd):
+    """P = sum over A entries (i, j) of |row j| (A times A)."""
+    import numpy as np
+
+    lens = np.diff(pos.astype(np.int64))
+    return int(lens[crd].sum())
+
+
+def spgemm_cpu_baseline(pos, crd, val, budget_s):
+    """Row-parallel CPU SpGEMM with the reference's ESC result semantics (oracle/), on a
+    uniform random sample of A's rows sized to take about `budget_s` in total."""
+    import numpy as np
+
+    from oracle import oracle
+
+    n = len(pos) - 1
+    cores = max(1, min(len(os.sched_getaffinity(0)), 64))
+    lens = np.diff(pos.astype(np.int64))
+    rng = np.random.default_rng(99)
+
+    def run(frac):
+        rows = np.sort(rng.choice(n, size=max(1, int(n * frac)), replace=False))
+        sl = lens[rows]
+        sp = np.zeros(len(rows) + 1, np.int64)
+        sp[1:] = np.cumsum(sl)
+        idx = np.repeat(pos[rows].astype(np.int64) - sp[:-1], sl) + np.arange(sp[-1])
+        sub = (sp.astype(np.int32), crd[idx], val[idx])
+        prods = int(lens[sub[1]].sum())
+        t0 = time.perf_counter()
+        oracle.port_spgemm(len(rows), n, n, *sub, pos, crd, val, nthreads=cores)
+        return prods, time.perf_counter() - t0, len(rows)
+
+    p0, t0, _ = run(1 / 512)
+    rate = p0 / max(t0, 1e-6)
+    total_p = lens[crd].sum()
+    frac = min(1.0, max(1 / 512, rate * budget_s / 2 / total_p))
+    samples = [run(frac) for _ in range(2)]
+    prods = sum(x[0] for x in samples)
+    sec = sum(x[1] for x in samples)
+    return {
+        "value": round(2 * prods / sec / 1e9, 3),
+        "unit": "GFLOP/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"2 runs of A[rows] @ A on uniform random samples of {samples[0][2]} rows "
+                  f"({frac:.4f} of rows; {prods} products in {sec:.1f} s) with the "
+                  f"row-parallel C SpGEMM (oracle/nacho_oracle.c, float64 sums)",
+    }
+
+
+def bench_spgemm(args, device):
+    import torch
+
+    import nacho_amd
+    from nacho_amd import synth
+
+    spec = WORKLOADS["c4"]
+    t0 = time.perf_counter()
+    pos, crd, val = synth.c4_operand()
+    n = len(pos) - 1
+    P = spgemm_products(pos, crd)
+    log(f"generated c4: n={n} nnzA={len(crd)} products={P} in {time.perf_counter() - t0:.1f}s")
+
+    def upload():
+        t = (torch.from_numpy(x).to(device) for x in (pos, crd, val))
+        return nacho_amd.CSR_gpu(*t, torch.tensor([n, n], dtype=torch.int32))
+
+    copies = [upload() for _ in range(2)]
+    fn = nacho_amd.gpu_spgemm64_f32
+    z = fn(copies[0], copies[0])
+    torch.cuda.synchronize()
+    nnz_c = int(z.dim_j_indices.numel())
+    del z
+    flops = 2 * P
+    # algorithmic bytes: A as left operand, B's gathered entries, the int64-offset result
+    compulsory = 4 * (n + 1) + 8 * len(crd) + 8 * (n + 1) + 8 * nnz_c
+    alg_bytes = compulsory + 8 * P
+    log(f"nnzC={nnz_c} flops/call={flops} algorithmic bytes/call={alg_bytes}")
+
+    nacho_amd.set_kernel_timing(True)
+    for i in range(args.warmup):
+        fn(copies[i % 2], copies[i % 2])
+    torch.cuda.synchronize()
+    kernel_ms = []
+    for i in range(args.steps):
+        fn(copies[i % 2], copies[i % 2])
+        kernel_ms.append(nacho_amd.last_kernel_ms())
+    nacho_amd.set_kernel_timing(False)
+    torch.cuda.synchronize()
+
+    start = time.perf_counter()
+    for i in range(args.steps):
+        fn(copies[i % 2], copies[i % 2])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - start
+    ms_per_step = elapsed * 1e3 / args.steps
+    value = flops / (ms_per_step * 1e-3) / 1e9
+    kernel_avg_ms = sum(kernel_ms) / len(kernel_ms)
+    achieved = alg_bytes / (kernel_avg_ms * 1e-3) / 1e9
+    log(f"pipeline avg {kernel_avg_ms:.2f} ms -> {achieved:.0f} GB/s; call {ms_per_step:.2f} ms "
+        f"-> {value:.1f} GFLOP/s")
+
+    cpu = None
+    if args.cpu_budget > 0:
+        cpu = spgemm_cpu_baseline(pos, crd, val, args.cpu_budget)
+        log(f"cpu baseline {cpu['value']} GFLOP/s on {cpu['cores']} threads")
+    nacho_amd.release_cached_memory()
+
+    return {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded generators in nacho_amd/synth.py)",
+        "config": {
+            "workload": spec["desc"],
+            "rows": n,
+            "nnz_a": len(crd),
+            "products": P,
+            "nnz_c": nnz_c,
+            "flops_per_step": flops,
+            "algorithmic_bytes_per_step": alg_bytes,
+            "compulsory_bytes_per_step": compulsory,
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": spec["kernel"],
+            "achieved": round(achieved, 2),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4),
+            "traffic": traffic_from_profiles("c4", "spgemm"),
+            "kernel_avg_us": round(kernel_avg_ms * 1e3, 2),
+        },
+        "cpu_baseline": cpu,
+        "gpu_over_cpu": round(value / cpu["value"], 1) if cpu else None,
     }
 
 
@@ -133,6 +291,10 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"calibration": "copy", "bytes_read": 4 * n, "bytes_written": 4 * n,
                           "launches": 5}))
+        return
+
+    if args.workload == "c4":
+        print(json.dumps(bench_spgemm(args, device)), flush=True)
         return
 
     import nacho_amd

@@ -646,9 +646,12 @@ typedef struct {
     int64_t *pz;
     int32_t *cz;
     float *vz;
-    int64_t rows_per_chunk;
     int phase;
+    int next_row; /* dynamic schedule: rows are claimed in chunks of SP_CHUNK */
+    int failed;
 } sp_job;
+
+#define SP_CHUNK 16
 
 /* Per-thread dense accumulator over k (an SPA): the row's distinct columns are the keys of
  * the expanded products; emitting them in ascending k order is the sort + compress. */
@@ -658,66 +661,92 @@ typedef struct {
     int32_t *keys;
 } spa;
 
-static int cmp_i32(const void *x, const void *y) {
-    const int32_t p = *(const int32_t *)x, q = *(const int32_t *)y;
-    return (p > q) - (p < q);
-}
-
-static void sp_row_range(sp_job *J, int t, int *r0, int *r1) {
-    const long per = (J->rows + J->nthreads - 1) / J->nthreads;
-    long s = (long)t * per, e = s + per;
-    if (s > J->rows) s = J->rows;
-    if (e > J->rows) e = J->rows;
-    *r0 = (int)s;
-    *r1 = (int)e;
-}
-
-static void sp_task(int t, void *arg) {
-    sp_job *J = (sp_job *)arg;
-    int r0, r1;
-    sp_row_range(J, t, &r0, &r1);
-    if (r0 >= r1) return;
-    spa s;
-    s.acc = (double *)calloc((size_t)J->cols + 1, sizeof(double));
-    s.mark = (int32_t *)calloc((size_t)J->cols + 1, sizeof(int32_t));
-    s.keys = (int32_t *)malloc(sizeof(int32_t) * ((size_t)J->cols + 1));
-    if (!s.acc || !s.mark || !s.keys) {
-        free(s.acc);
-        free(s.mark);
-        free(s.keys);
-        for (int r = r0; r < r1; ++r) J->row_nnz[r] = -1;
+/* Ascending sort of n column ids in [0, cols): insertion sort for short rows, else an LSD
+ * radix sort with 11-bit digits over the bits `cols` needs (tmp holds n entries). */
+static void sort_keys(int32_t *keys, int32_t *tmp, int n, int cols) {
+    if (n < 64) {
+        for (int i = 1; i < n; ++i) {
+            const int32_t v = keys[i];
+            int j = i - 1;
+            while (j >= 0 && keys[j] > v) {
+                keys[j + 1] = keys[j];
+                --j;
+            }
+            keys[j + 1] = v;
+        }
         return;
     }
-    for (int r = r0; r < r1; ++r) {
-        int nkeys = 0;
-        for (int p = J->pa[r]; p < J->pa[r + 1]; ++p) {
-            const int j = J->ca[p];
-            const float a = J->va[p];
-            for (int q = J->pb[j]; q < J->pb[j + 1]; ++q) {
-                const int k = J->cb[q];
-                if (s.mark[k] != r + 1) {
-                    s.mark[k] = r + 1;
-                    s.acc[k] = 0.0;
-                    s.keys[nkeys++] = k;
-                }
-                if (J->phase == 1) s.acc[k] += (double)(a * J->vb[q]); /* f32 product */
+    int bits = 1;
+    while (bits < 31 && (1L << bits) < cols) ++bits;
+    int32_t *src = keys, *dst = tmp;
+    for (int shift = 0; shift < bits; shift += 11) {
+        int count[2049];
+        memset(count, 0, sizeof(count));
+        for (int i = 0; i < n; ++i) ++count[((src[i] >> shift) & 2047) + 1];
+        for (int d = 0; d < 2048; ++d) count[d + 1] += count[d];
+        for (int i = 0; i < n; ++i) dst[count[(src[i] >> shift) & 2047]++] = src[i];
+        int32_t *t = src;
+        src = dst;
+        dst = t;
+    }
+    if (src != keys) memcpy(keys, src, sizeof(int32_t) * (size_t)n);
+}
+
+/* One row of Z: scatter the row's products into the accumulator (float32 products summed in
+ * float64), then emit the distinct columns in ascending order (phase 1) or count them
+ * (phase 0). */
+static void sp_row(sp_job *J, spa *s, int32_t *tmp, int r) {
+    int nkeys = 0;
+    for (int p = J->pa[r]; p < J->pa[r + 1]; ++p) {
+        const int j = J->ca[p];
+        const float a = J->va[p];
+        for (int q = J->pb[j]; q < J->pb[j + 1]; ++q) {
+            const int k = J->cb[q];
+            if (s->mark[k] != r + 1) {
+                s->mark[k] = r + 1;
+                s->acc[k] = 0.0;
+                s->keys[nkeys++] = k;
             }
+            if (J->phase == 1) s->acc[k] += (double)(a * J->vb[q]); /* f32 product */
         }
-        if (J->phase == 0) {
-            J->row_nnz[r] = nkeys;
-            continue;
-        }
-        qsort(s.keys, (size_t)nkeys, sizeof(int32_t), cmp_i32);
-        int64_t off = J->pz[r];
-        for (int x = 0; x < nkeys; ++x) {
-            J->cz[off] = s.keys[x];
-            J->vz[off] = (float)s.acc[s.keys[x]];
-            ++off;
+    }
+    if (J->phase == 0) {
+        J->row_nnz[r] = nkeys;
+        return;
+    }
+    sort_keys(s->keys, tmp, nkeys, J->cols);
+    int64_t off = J->pz[r];
+    for (int x = 0; x < nkeys; ++x) {
+        J->cz[off] = s->keys[x];
+        J->vz[off] = (float)s->acc[s->keys[x]];
+        ++off;
+    }
+}
+
+/* Rows are claimed dynamically in chunks (row costs are very uneven on power-law inputs). */
+static void sp_task(int t, void *arg) {
+    sp_job *J = (sp_job *)arg;
+    (void)t;
+    spa s;
+    const size_t n = (size_t)J->cols + 1;
+    s.acc = (double *)calloc(n, sizeof(double));
+    s.mark = (int32_t *)calloc(n, sizeof(int32_t));
+    s.keys = (int32_t *)malloc(sizeof(int32_t) * n);
+    int32_t *tmp = (int32_t *)malloc(sizeof(int32_t) * n);
+    if (!s.acc || !s.mark || !s.keys || !tmp) {
+        __atomic_store_n(&J->failed, 1, __ATOMIC_RELAXED);
+    } else {
+        for (;;) {
+            const int r0 = __atomic_fetch_add(&J->next_row, SP_CHUNK, __ATOMIC_RELAXED);
+            if (r0 >= J->rows) break;
+            const int r1 = r0 + SP_CHUNK < J->rows ? r0 + SP_CHUNK : J->rows;
+            for (int r = r0; r < r1; ++r) sp_row(J, &s, tmp, r);
         }
     }
     free(s.acc);
     free(s.mark);
     free(s.keys);
+    free(tmp);
 }
 
 /* Z = A B (rows x cols result).  Offsets are int64.  Returns 0 or error. */
@@ -745,14 +774,15 @@ int oracle_spgemm(int rows, int inner, int cols, const int32_t *pa, const int32_
         return ORC_ENOMEM;
     }
     J.phase = 0; /* symbolic */
+    J.next_row = 0;
     parallel_for(J.nthreads, sp_task, &J);
+    if (J.failed) {
+        free(J.row_nnz);
+        free(J.pz);
+        return ORC_ENOMEM;
+    }
     int64_t total = 0;
     for (int r = 0; r < rows; ++r) {
-        if (J.row_nnz[r] < 0) {
-            free(J.row_nnz);
-            free(J.pz);
-            return ORC_ENOMEM;
-        }
         J.pz[r] = total;
         total += J.row_nnz[r];
     }
@@ -767,8 +797,15 @@ int oracle_spgemm(int rows, int inner, int cols, const int32_t *pa, const int32_
         return ORC_ENOMEM;
     }
     J.phase = 1; /* numeric */
+    J.next_row = 0;
     parallel_for(J.nthreads, sp_task, &J);
     free(J.row_nnz);
+    if (J.failed) {
+        free(J.pz);
+        free(J.cz);
+        free(J.vz);
+        return ORC_ENOMEM;
+    }
     *out_pos = J.pz;
     *out_crd = J.cz;
     *out_val = J.vz;
