@@ -10,26 +10,35 @@
 //
 // Pipeline (every count and offset is int64):
 //   1. sizes: len[p] = |row crdA[p] of B| per A entry; exclusive scan -> off[p], P = off[nnzA];
-//      row i's products are [off[posA[i]], off[posA[i+1]]) in (j, k) order.
-//   2. tiles: a row with more than kShort products is cut into tiles of kTile products; the
-//      shorter rows whose first product falls in the same kShort-aligned window share one
-//      tile (fewer than kTile products, since each has at most kShort).  Tiles cover [0, P)
-//      in order: tile t is [tile_start[t], tile_start[t+1]).
-//   3. expand: each workgroup writes kTile consecutive products (k, a_ij * b_jk).
-//   4. sort: one workgroup per tile sorts by (row ordinal inside the tile, k) in LDS.
-//   5. merge: a row longer than one tile merges its sorted tile runs pairwise, level by
-//      level (runs of kTile << l), device-wide; the buffers ping-pong and each row starts in
-//      the one that makes its last level end in the primary buffer.
-//   6. compress: per tile, count the distinct (row, k) runs; scan -> output offsets; then a
-//      segmented float64 reduction writes (k, sum rounded once to float32) and the row
-//      offsets.  Every distinct column is kept (structural result, as the reference).
+//      row i's products are [row_off[i], row_off[i+1]) in natural (j, k) order.
+//   2. segments: a row with at most kShort products is one segment.  A longer row is split by
+//      column into nb buckets of 2^shift columns (one device-wide radix digit, k >> shift);
+//      each bucket is a segment.  Segments are numbered row-major, bucket-minor, so their
+//      concatenation in order is every row's products grouped by column range.
+//   3. histogram + scatter: chunks of kChunk consecutive products decode their (A entry, row)
+//      with a load-balanced search in LDS, gather (k, a_ij * b_jk) from B with coalesced
+//      loads, count long-row products per segment, and after the scan of segment lengths
+//      scatter them into their segment (ranges reserved per chunk with one atomic per
+//      segment; short rows keep natural order).
+//   4. units: a segment with more than kShort products is a dense unit; smaller segments
+//      whose first product falls in the same kShort-aligned window share one sort unit
+//      (fewer than 2*kShort products).
+//   5. reduce: a sort unit sorts (segment ordinal, k) in LDS and sums each run in float64;
+//      a dense unit accumulates its 2^shift-column range in an LDS float64 array (windows of
+//      kDenseCols columns) and compacts the touched columns in order.  Both write the
+//      distinct (k, sum rounded once to float32) at the unit's product offset in a second
+//      buffer and record the unit's count and the local offset of every row starting in it.
+//   6. output: scan of unit counts -> result offsets; copy each unit's entries; row offsets
+//      from the unit offsets.  Every distinct column is kept (structural result, as the
+//      reference).
+// Summation order inside a segment follows the scatter's arrival order and LDS atomics, so
+// values are reproducible to within one float32 rounding of the float64 sum (the reference's
+// own order is not deterministic either).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
 #include <climits>
 #include <cstdint>
-#include <utility>
-#include <vector>
 
 #include "device_utils.hpp"
 #include "runtime.hpp"
@@ -39,15 +48,63 @@ namespace nacho {
 namespace spgemm {
 
 constexpr int kBlock = 256;
-constexpr int kTile = 4096;            // products per sort / merge / compress tile
-constexpr int kPer = kTile / kBlock;   // 16 positions per lane
-constexpr int kShort = kTile / 2;      // rows with at most this many products share tiles
-constexpr int kOrdBits = 12;           // a shared tile holds fewer than 2^12 rows
-constexpr int kMaxRowTiles = 1 << 18;  // keeps every in-row merge position below 2^31
+constexpr int kChunk = 4096;            // products per histogram / scatter workgroup
+constexpr int kTile = 4096;             // LDS capacity of a sort unit
+constexpr int kPer = kTile / kBlock;    // 16 positions per lane
+constexpr int kShort = kTile / 2;       // segments with at most this many products are sorted
+constexpr int kOrdBits = 12;            // a sort unit holds fewer than 2^12 segments
+constexpr int kDenseBits = 13;          // dense accumulation window: 8192 columns
+constexpr int kDenseCols = 1 << kDenseBits;
+constexpr int kMaxBucketBits = 10;      // at most 1024 column buckets per long row
+constexpr int kMaxBuckets = 1 << kMaxBucketBits;
+constexpr int kMaxLongPerChunk = 3;     // rows longer than kShort meeting one chunk
 
-static_assert(kTile == 1 << kOrdBits, "row ordinals must fit kOrdBits");
+static_assert(kTile == 1 << kOrdBits, "segment ordinals must fit kOrdBits");
+static_assert(kChunk == kBlock * kPer, "chunk decode assumes kPer products per lane");
 
-// ---- 1-2: sizes and tiles --------------------------------------------------------------
+// ---- small device helpers --------------------------------------------------------------
+
+// LDS index with one pad word per kPer words: a lane's kPer consecutive (blocked) positions
+// then start kPer + 1 words after its neighbour's, so blocked accesses are free of bank
+// conflicts.
+constexpr int kPadded = kTile + kTile / 16;
+__device__ __forceinline__ int pad(int i) { return i + (i >> 4); }
+
+// Last index x in [lo, hi] with a[x] <= q (a non-decreasing, a[lo] <= q).
+template <typename T>
+__device__ __forceinline__ int64_t last_le(const T *__restrict__ a, int64_t lo, int64_t hi,
+                                           int64_t q) {
+    while (lo < hi) {
+        const int64_t mid = (lo + hi + 1) >> 1;
+        if (static_cast<int64_t>(a[mid]) <= q) {
+            lo = mid;
+        } else {
+            hi = mid - 1;
+        }
+    }
+    return lo;
+}
+
+// Exclusive max over the workgroup (values >= 0, identity 0).  Ends synchronised.
+__device__ __forceinline__ int block_exclusive_max(int v, int *s_wave) {
+    const int l = dev::lane();
+    const int w = threadIdx.x / dev::kWave;
+    int incl = v;
+#pragma unroll
+    for (int o = 1; o < dev::kWave; o <<= 1) {
+        const int n = __shfl_up(incl, o, dev::kWave);
+        if (l >= o) incl = max(incl, n);
+    }
+    if (l == dev::kWave - 1) s_wave[w] = incl;
+    int excl = __shfl_up(incl, 1, dev::kWave);
+    if (l == 0) excl = 0;
+    __syncthreads();
+    for (int i = 0; i < w; ++i) excl = max(excl, s_wave[i]);
+    __syncthreads();
+    return excl;
+}
+
+// ---- 1-2: sizes and segments -----------------------------------------------------------
 
 __global__ void lengths_kernel(const int *__restrict__ crd_a, int64_t nnz_a,
                                const int *__restrict__ pos_b, int64_t *__restrict__ len) {
@@ -58,303 +115,304 @@ __global__ void lengths_kernel(const int *__restrict__ crd_a, int64_t nnz_a,
     }
 }
 
-__global__ void row_off_kernel(const int *__restrict__ pos_a, int rows,
-                               const int64_t *__restrict__ off, int64_t *__restrict__ row_off) {
+// row_off[i] = off[posA[i]]; seg_count[i] = segments of row i (1, or nb for a long row).
+__global__ void rows_kernel(const int *__restrict__ pos_a, int rows,
+                            const int64_t *__restrict__ off, int nb,
+                            int64_t *__restrict__ row_off, int64_t *__restrict__ seg_count) {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i <= rows; i += gridDim.x * blockDim.x) {
         row_off[i] = off[pos_a[i]];
-    }
-}
-
-// Tiles owned by row r: ceil(prod / kTile) for a long row; 1 for the first short row whose
-// products start in a kShort window (the previous nonempty row is long or starts in an
-// earlier window); 0 otherwise.
-__device__ inline int64_t row_tile_count(const int64_t *__restrict__ row_off, int r) {
-    const int64_t s = row_off[r], prod = row_off[r + 1] - s;
-    if (prod == 0) return 0;
-    if (prod > kShort) return (prod + kTile - 1) / kTile;
-    if (s == 0) return 1;
-    int lo = 0, hi = r - 1;  // the previous nonempty row: last x < r with row_off[x] < s
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (row_off[mid] < s) {
-            lo = mid;
-        } else {
-            hi = mid - 1;
-        }
-    }
-    const int64_t ps = row_off[lo];
-    if (s - ps > kShort) return 1;
-    return (ps / kShort != s / kShort) ? 1 : 0;
-}
-
-__global__ void row_tiles_kernel(const int64_t *__restrict__ row_off, int rows,
-                                 int64_t *__restrict__ row_tiles) {
-    for (int r = blockIdx.x * blockDim.x + threadIdx.x; r < rows; r += gridDim.x * blockDim.x) {
-        row_tiles[r] = row_tile_count(row_off, r);
-    }
-}
-
-__global__ void tile_map_kernel(const int64_t *__restrict__ row_off,
-                                const int64_t *__restrict__ tile_prefix, int rows,
-                                int *__restrict__ tile_row, int64_t *__restrict__ tile_start) {
-    for (int r = blockIdx.x * blockDim.x + threadIdx.x; r <= rows; r += gridDim.x * blockDim.x) {
-        if (r == rows) {
-            tile_start[tile_prefix[rows]] = row_off[rows];
-            continue;
-        }
-        const int64_t t0 = tile_prefix[r], t1 = tile_prefix[r + 1];
-        for (int64_t t = t0; t < t1; ++t) {
-            tile_row[t] = r;
-            tile_start[t] = row_off[r] + (t - t0) * kTile;
+        if (i < rows) {
+            const int64_t prod = off[pos_a[i + 1]] - off[pos_a[i]];
+            seg_count[i] = prod > kShort ? nb : 1;
         }
     }
 }
 
-// Merge levels of a row with `tiles` tiles: ceil(log2(tiles)).
-__host__ __device__ inline int merge_levels(int64_t tiles) {
-    int l = 0;
-    while ((static_cast<int64_t>(1) << l) < tiles) ++l;
-    return l;
-}
-
-// ---- 3: expand -------------------------------------------------------------------------
-
-// Last A entry p in [lo, hi] with off[p] <= q.
-__device__ __forceinline__ int64_t entry_of(const int64_t *__restrict__ off, int64_t lo,
-                                            int64_t hi, int64_t q) {
-    while (lo < hi) {
-        const int64_t mid = (lo + hi + 1) >> 1;
-        if (off[mid] <= q) {
-            lo = mid;
-        } else {
-            hi = mid - 1;
+// Segment table: row of each segment, lengths (short rows known now, long rows counted by the
+// histogram pass) and the scatter's fill counters.
+__global__ void segments_kernel(const int64_t *__restrict__ row_off,
+                                const int64_t *__restrict__ seg_prefix, int rows,
+                                int *__restrict__ seg_row, int64_t *__restrict__ seg_len,
+                                int64_t *__restrict__ seg_fill) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < rows; i += gridDim.x * blockDim.x) {
+        const int64_t s0 = seg_prefix[i], s1 = seg_prefix[i + 1];
+        const int64_t prod = row_off[i + 1] - row_off[i];
+        for (int64_t s = s0; s < s1; ++s) {
+            seg_row[s] = i;
+            seg_len[s] = prod > kShort ? 0 : prod;
+            seg_fill[s] = 0;
         }
     }
-    return lo;
 }
 
-// Workgroup w writes products [w*kTile, (w+1)*kTile); lane t the kPer consecutive products
-// from w*kTile + t*kPer, as 16-byte stores.
-__global__ __launch_bounds__(kBlock) void expand_kernel(
-    const int *__restrict__ crd_a, const float *__restrict__ val_a, int64_t nnz_a,
-    const int64_t *__restrict__ off, int64_t P, const int *__restrict__ pos_b,
-    const int *__restrict__ crd_b, const float *__restrict__ val_b, int *__restrict__ key,
-    float *__restrict__ val) {
-    __shared__ int64_t s_range[2];
-    const int64_t c0 = blockIdx.x * static_cast<int64_t>(kTile);
-    if (threadIdx.x < 2) {
-        const int64_t q = min(c0 + (threadIdx.x ? kTile - 1 : 0), P - 1);
-        s_range[threadIdx.x] = entry_of(off, 0, nnz_a - 1, q);
+// ---- 3: histogram and scatter over product chunks --------------------------------------
+
+struct ChunkHeader {
+    int64_t p_lo;  // A entry of the chunk's first product
+    int r_lo;      // row of the chunk's first product
+    int n_long;    // long rows meeting the chunk
+    int long_row[kMaxLongPerChunk];
+};
+
+// Load-balanced search for the chunk [c0, c0 + n): s_e[x] = entry of product c0+x minus
+// p_lo, s_r[x] = its row minus r_lo (an inclusive max-scan of the entries' and rows' start
+// marks), and the long rows meeting the chunk.
+__device__ __forceinline__ void decode_chunk(const int64_t *__restrict__ off, int64_t nnz_a,
+                                             const int64_t *__restrict__ row_off, int rows,
+                                             int64_t c0, int n, int *s_e, int *s_r,
+                                             ChunkHeader *hdr, int64_t *s_bounds, int *s_wave) {
+    if (threadIdx.x == 0) {
+        s_bounds[0] = last_le(off, 0, nnz_a - 1, c0);
+        s_bounds[1] = last_le(off, 0, nnz_a - 1, c0 + n - 1);
+        s_bounds[2] = last_le(row_off, 0, rows - 1, c0);
+        s_bounds[3] = last_le(row_off, 0, rows - 1, c0 + n - 1);
+    }
+    for (int x = threadIdx.x; x < kChunk; x += kBlock) {
+        s_e[pad(x)] = 0;
+        s_r[pad(x)] = 0;
     }
     __syncthreads();
-    const int64_t q0 = c0 + static_cast<int64_t>(threadIdx.x) * kPer;
-    if (q0 >= P) return;
-    int64_t p = entry_of(off, s_range[0], s_range[1], q0);
-    int64_t next = off[p + 1];
-    float a = val_a[p];
-    int64_t bbase = pos_b[crd_a[p]] - off[p];
+    const int64_t p_lo = s_bounds[0], p_hi = s_bounds[1];
+    const int r_lo = static_cast<int>(s_bounds[2]), r_hi = static_cast<int>(s_bounds[3]);
+    if (threadIdx.x == 0) {
+        hdr->p_lo = p_lo;
+        hdr->r_lo = r_lo;
+        const bool first_long = row_off[r_lo + 1] - row_off[r_lo] > kShort;
+        hdr->n_long = first_long ? 1 : 0;
+        hdr->long_row[0] = r_lo;
+    }
+    __syncthreads();
+    for (int64_t p = p_lo + 1 + threadIdx.x; p <= p_hi; p += kBlock) {
+        const int64_t x = off[p] - c0;
+        if (x >= 0 && x < n) atomicMax(&s_e[pad(static_cast<int>(x))], static_cast<int>(p - p_lo));
+    }
+    for (int r = r_lo + 1 + threadIdx.x; r <= r_hi; r += kBlock) {
+        const int64_t x = row_off[r] - c0;
+        if (x >= 0 && x < n) {
+            atomicMax(&s_r[pad(static_cast<int>(x))], r - r_lo);
+            if (row_off[r + 1] - row_off[r] > kShort) {
+                const int slot = atomicAdd(&hdr->n_long, 1);
+                hdr->long_row[slot] = r;
+            }
+        }
+    }
+    __syncthreads();
+    // inclusive max-scan of both arrays, blocked kPer per lane
+    const int base = threadIdx.x * kPer;
+    int me = 0, mr = 0;
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        me = max(me, s_e[pad(base + u)]);
+        mr = max(mr, s_r[pad(base + u)]);
+    }
+    int ce = block_exclusive_max(me, s_wave);
+    int cr = block_exclusive_max(mr, s_wave);
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        ce = max(ce, s_e[pad(base + u)]);
+        cr = max(cr, s_r[pad(base + u)]);
+        s_e[pad(base + u)] = ce;
+        s_r[pad(base + u)] = cr;
+    }
+    __syncthreads();
+}
+
+__device__ __forceinline__ int long_slot(const ChunkHeader &h, int row) {
+    int slot = -1;
+#pragma unroll
+    for (int i = 0; i < kMaxLongPerChunk; ++i) {
+        if (i < h.n_long && h.long_row[i] == row) slot = i;
+    }
+    return slot;
+}
+
+// SCATTER = false: add each long row's per-bucket product counts of this chunk to seg_len.
+// SCATTER = true: write every product to its segment (key/val at seg_off + reserved rank;
+// short rows at their natural position, which is their segment's offset).
+template <bool SCATTER>
+__global__ __launch_bounds__(kBlock) void chunk_kernel(
+    const int *__restrict__ crd_a, const float *__restrict__ val_a, int64_t nnz_a,
+    const int64_t *__restrict__ off, const int64_t *__restrict__ row_off, int rows, int64_t P,
+    const int *__restrict__ pos_b, const int *__restrict__ crd_b, const float *__restrict__ val_b,
+    int shift, int nb, const int64_t *__restrict__ seg_prefix, int64_t *__restrict__ seg_len,
+    const int64_t *__restrict__ seg_off, int64_t *__restrict__ seg_fill, int *__restrict__ key,
+    float *__restrict__ val) {
+    // entry and row maps of the decode; reused for the reserved bases of the scatter
+    __shared__ int64_t s_dec[kPadded];
+    int *s_e = reinterpret_cast<int *>(s_dec);
+    int *s_r = s_e + kPadded;
+    __shared__ int s_hist[kMaxLongPerChunk * kMaxBuckets];
+    __shared__ int64_t s_bounds[4];
+    __shared__ int s_wave[kBlock / dev::kWave];
+    __shared__ ChunkHeader hdr;
+    const int64_t c0 = blockIdx.x * static_cast<int64_t>(kChunk);
+    const int n = static_cast<int>(min(static_cast<int64_t>(kChunk), P - c0));
+    decode_chunk(off, nnz_a, row_off, rows, c0, n, s_e, s_r, &hdr, s_bounds, s_wave);
+    const ChunkHeader h = hdr;
+    if (!SCATTER && h.n_long == 0) return;  // uniform across the workgroup
+    for (int i = threadIdx.x; i < h.n_long * nb; i += kBlock) s_hist[i] = 0;
+    __syncthreads();
+
+    // Striped positions (neighbouring lanes read neighbouring B entries).  The gathers are
+    // issued in dependent batches over all kPer products so that their latencies overlap.
     int kk[kPer];
     float vv[kPer];
+    int where[kPer];  // slot*nb + bucket, or -1 for a short row's product
+    int rank[kPer];
+    int64_t bpos[kPer];
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
-        const int64_t q = q0 + u;
-        kk[u] = 0;
-        vv[u] = 0.0f;
-        if (q < P) {
-            if (next <= q) {
-                do {
-                    ++p;
-                    next = off[p + 1];
-                } while (next <= q);
-                a = val_a[p];
-                bbase = pos_b[crd_a[p]] - off[p];
-            }
-            kk[u] = crd_b[bbase + q];
-            vv[u] = a * val_b[bbase + q];
-        }
+        const int x = min(static_cast<int>(threadIdx.x) + u * kBlock, n - 1);
+        const int64_t p = h.p_lo + s_e[pad(x)];
+        where[u] = long_slot(h, h.r_lo + s_r[pad(x)]);
+        bpos[u] = p;
+        kk[u] = crd_a[p];
+        if (SCATTER) vv[u] = val_a[p];
     }
-    if (q0 + kPer <= P) {
-        int4 *kd = reinterpret_cast<int4 *>(key + q0);
-        float4 *vd = reinterpret_cast<float4 *>(val + q0);
-#pragma unroll
-        for (int u = 0; u < kPer / 4; ++u) {
-            kd[u] = make_int4(kk[4 * u], kk[4 * u + 1], kk[4 * u + 2], kk[4 * u + 3]);
-            vd[u] = make_float4(vv[4 * u], vv[4 * u + 1], vv[4 * u + 2], vv[4 * u + 3]);
-        }
-    } else {
-#pragma unroll
-        for (int u = 0; u < kPer; ++u) {
-            if (q0 + u < P) {
-                key[q0 + u] = kk[u];
-                val[q0 + u] = vv[u];
-            }
-        }
-    }
-}
-
-// ---- tile geometry shared by the sort and compress kernels ------------------------------
-
-struct Tile {
-    int row;           // owner row (the long row, or the first row of a shared tile)
-    int64_t s, e;      // product range
-    int n;             // e - s
-    bool shared_tile;  // short rows
-};
-
-__device__ __forceinline__ Tile load_tile(const int *__restrict__ tile_row,
-                                          const int64_t *__restrict__ tile_start,
-                                          const int64_t *__restrict__ row_off, int64_t t) {
-    Tile g;
-    g.row = tile_row[t];
-    g.s = tile_start[t];
-    g.e = tile_start[t + 1];
-    g.n = static_cast<int>(g.e - g.s);
-    g.shared_tile = row_off[g.row + 1] - row_off[g.row] <= kShort;
-    return g;
-}
-
-// s_mark[q] = r + 1 where row r starts at tile position q (other entries are left as the
-// caller cleared them).  A shared tile's rows run from its owner to the next tile's owner.
-__device__ __forceinline__ void mark_rows(int *s_mark, const Tile &g,
-                                          const int *__restrict__ tile_row,
-                                          const int64_t *__restrict__ row_off, int64_t t,
-                                          int64_t n_tiles, int rows) {
-    if (g.shared_tile) {
-        const int r_end = t + 1 < n_tiles ? tile_row[t + 1] : rows;
-        for (int r = g.row + threadIdx.x; r < r_end; r += kBlock) {
-            const int64_t rs = row_off[r];
-            if (rs < g.e && row_off[r + 1] > rs) s_mark[rs - g.s] = r + 1;
-        }
-    } else if (threadIdx.x == 0 && g.s == row_off[g.row]) {
-        s_mark[0] = g.row + 1;
-    }
-}
-
-// ---- 4: per-tile sort in LDS -----------------------------------------------------------
-
-// Bitonic sort of n2 (a power of two, <= kTile) key/value pairs in LDS, ascending.
-template <typename K>
-__device__ __forceinline__ void bitonic_sort(K *s_key, float *s_val, int n2) {
-    for (int size = 2; size <= n2; size <<= 1) {
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            for (int m = threadIdx.x; m < n2 / 2; m += kBlock) {
-                const int i = 2 * m - (m & (stride - 1));
-                const int j = i + stride;
-                const bool ascending = (i & size) == 0;
-                const K ki = s_key[i], kj = s_key[j];
-                if ((ki > kj) == ascending) {
-                    s_key[i] = kj;
-                    s_key[j] = ki;
-                    const float vi = s_val[i];
-                    s_val[i] = s_val[j];
-                    s_val[j] = vi;
-                }
-            }
-            __syncthreads();
-        }
-    }
-}
-
-// K is uint32_t when kOrdBits + col_shift <= 32, else uint64_t (col_shift = 32).  The tile
-// is read from buffer 1 and written, sorted, to buffer 1 or 2 (where the row's merge levels
-// start); one workgroup reads and writes only its own tile.
-template <typename K>
-__global__ __launch_bounds__(kBlock) void sort_tiles_kernel(
-    const int *__restrict__ tile_row, const int64_t *__restrict__ tile_start, int64_t n_tiles,
-    int rows, const int64_t *__restrict__ row_off, const int64_t *__restrict__ tile_prefix,
-    int col_shift, int *key1, float *val1, int *__restrict__ key2, float *__restrict__ val2) {
-    __shared__ K s_key[kTile];
-    __shared__ float s_val[kTile];
-    __shared__ int s_wave[kBlock / dev::kWave];
-    const int64_t t = blockIdx.x;
-    const Tile g = load_tile(tile_row, tile_start, row_off, t);
-    const int base = threadIdx.x * kPer;  // blocked positions of this lane
-    int ord[kPer];
-#pragma unroll
-    for (int u = 0; u < kPer; ++u) ord[u] = 0;
-    if (g.shared_tile) {
-        int *s_mark = reinterpret_cast<int *>(s_val);
-        for (int q = threadIdx.x; q < kTile; q += kBlock) s_mark[q] = 0;
-        __syncthreads();
-        mark_rows(s_mark, g, tile_row, row_off, t, n_tiles, rows);
-        __syncthreads();
-        int c = 0;
-#pragma unroll
-        for (int u = 0; u < kPer; ++u) c += s_mark[base + u] != 0;
-        int total = 0;
-        int run = dev::block_exclusive_sum<kBlock>(c, s_wave, total);
-#pragma unroll
-        for (int u = 0; u < kPer; ++u) {
-            run += s_mark[base + u] != 0;
-            ord[u] = run - 1;
-        }
-        __syncthreads();
-    }
-    int n2 = 1;
-    while (n2 < g.n) n2 <<= 1;
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
-        const int q = base + u;
-        if (q < g.n) {
-            s_key[q] = (static_cast<K>(ord[u]) << col_shift) |
-                       static_cast<K>(static_cast<uint32_t>(key1[g.s + q]));
-            s_val[q] = val1[g.s + q];
-        } else if (q < n2) {
-            s_key[q] = ~static_cast<K>(0);
-            s_val[q] = 0.0f;
+        const int x = min(static_cast<int>(threadIdx.x) + u * kBlock, n - 1);
+        bpos[u] = pos_b[kk[u]] + (c0 + x - off[bpos[u]]);
+    }
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        kk[u] = crd_b[bpos[u]];
+        if (SCATTER) vv[u] *= val_b[bpos[u]];
+    }
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        const int x = static_cast<int>(threadIdx.x) + u * kBlock;
+        rank[u] = 0;
+        if (x >= n) where[u] = -2;  // past the chunk: nothing to count or write
+        if (where[u] >= 0) {
+            where[u] = where[u] * nb + (kk[u] >> shift);
+            rank[u] = atomicAdd(&s_hist[where[u]], 1);
         }
     }
     __syncthreads();
-    bitonic_sort(s_key, s_val, n2);
-    const int levels =
-        g.shared_tile ? 0 : merge_levels(tile_prefix[g.row + 1] - tile_prefix[g.row]);
-    int *kd = (levels & 1) ? key2 : key1;
-    float *vd = (levels & 1) ? val2 : val1;
-    const K mask = (static_cast<K>(1) << col_shift) - 1;
-    for (int q = threadIdx.x; q < g.n; q += kBlock) {
-        kd[g.s + q] = static_cast<int>(s_key[q] & mask);
-        vd[g.s + q] = s_val[q];
+    if (!SCATTER) {
+        for (int i = threadIdx.x; i < h.n_long * nb; i += kBlock) {
+            const int c = s_hist[i];
+            if (c > 0) {
+                const int64_t s = seg_prefix[h.long_row[i / nb]] + (i % nb);
+                atomicAdd(reinterpret_cast<unsigned long long *>(&seg_len[s]),
+                          static_cast<unsigned long long>(c));
+            }
+        }
+        return;
+    }
+    // reserve each bin's range in its segment; the bases reuse the decode arrays
+    int64_t *s_base = s_dec;
+    static_assert(kMaxLongPerChunk * kMaxBuckets <= kChunk, "bases must fit the decode arrays");
+    for (int i = threadIdx.x; i < h.n_long * nb; i += kBlock) {
+        const int c = s_hist[i];
+        if (c > 0) {
+            const int64_t s = seg_prefix[h.long_row[i / nb]] + (i % nb);
+            const unsigned long long got = atomicAdd(
+                reinterpret_cast<unsigned long long *>(&seg_fill[s]),
+                static_cast<unsigned long long>(c));
+            s_base[i] = seg_off[s] + static_cast<int64_t>(got);
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        const int x = threadIdx.x + u * kBlock;
+        if (where[u] != -2) {
+            const int64_t dst = where[u] < 0 ? c0 + x : s_base[where[u]] + rank[u];
+            key[dst] = kk[u];
+            val[dst] = vv[u];
+        }
     }
 }
 
-// ---- 5: merge levels of long rows -------------------------------------------------------
+// ---- 4: units --------------------------------------------------------------------------
 
-struct PairGeom {
-    int64_t a_begin;  // absolute position of run A; run B follows it
-    int a_len, b_len;
-    int d0, d1;  // this tile's output range inside the pair
-    int u, tiles_in_pair;
-};
+// Units owned by segment s: 1 for a dense segment (more than kShort products) and for the
+// first nonempty small segment whose products start in a kShort window (the previous
+// nonempty segment is dense or starts in an earlier window); 0 otherwise.
+__global__ void unit_count_kernel(const int64_t *__restrict__ seg_len,
+                                  const int64_t *__restrict__ seg_off, int64_t n_seg,
+                                  int64_t *__restrict__ seg_units) {
+    for (int64_t s = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; s < n_seg;
+         s += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t len = seg_len[s], start = seg_off[s];
+        int64_t u;
+        if (len == 0) {
+            u = 0;
+        } else if (len > kShort || start == 0) {
+            u = 1;
+        } else {
+            // previous nonempty segment: last x < s with seg_off[x] < start
+            int64_t lo = 0, hi = s - 1;
+            while (lo < hi) {
+                const int64_t mid = (lo + hi + 1) >> 1;
+                if (seg_off[mid] < start) {
+                    lo = mid;
+                } else {
+                    hi = mid - 1;
+                }
+            }
+            const int64_t ps = seg_off[lo];
+            u = (start - ps > kShort || ps / kShort != start / kShort) ? 1 : 0;
+        }
+        seg_units[s] = u;
+    }
+}
 
-__device__ __forceinline__ PairGeom pair_geometry(const int64_t *__restrict__ row_off,
-                                                  const int64_t *__restrict__ tile_prefix,
-                                                  int row, int64_t tile, int level) {
-    PairGeom g;
-    const int64_t lt = tile - tile_prefix[row];
-    const int64_t row_s = row_off[row], row_len = row_off[row + 1] - row_s;
-    const int64_t run = static_cast<int64_t>(kTile) << level;
-    const int64_t pair = lt >> (level + 1);
-    const int64_t pair_s = pair * 2 * run;
-    g.a_begin = row_s + pair_s;
-    const int64_t a_len = min(run, row_len - pair_s);
-    const int64_t b_len = max(static_cast<int64_t>(0), min(run, row_len - pair_s - run));
-    g.a_len = static_cast<int>(a_len);
-    g.b_len = static_cast<int>(b_len);
-    g.u = static_cast<int>(lt - (pair << (level + 1)));
-    g.tiles_in_pair = static_cast<int>((a_len + b_len + kTile - 1) / kTile);
-    g.d0 = g.u * kTile;
-    g.d1 = static_cast<int>(min(static_cast<int64_t>(g.d0) + kTile, a_len + b_len));
-    return g;
+__global__ void unit_map_kernel(const int64_t *__restrict__ seg_units,
+                                const int64_t *__restrict__ unit_prefix,
+                                const int64_t *__restrict__ seg_off, int64_t n_seg, int64_t P,
+                                int *__restrict__ unit_seg, int64_t *__restrict__ unit_start) {
+    for (int64_t s = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; s <= n_seg;
+         s += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        if (s == n_seg) {
+            unit_start[unit_prefix[n_seg]] = P;
+        } else if (seg_units[s]) {
+            const int64_t u = unit_prefix[s];
+            unit_seg[u] = static_cast<int>(s);
+            unit_start[u] = seg_off[s];
+        }
+    }
+}
+
+// ---- 5a: sort units --------------------------------------------------------------------
+
+// Ascending sort of one lane's kPer (key, value) pairs in registers (bitonic network with
+// compile-time indices).
+template <typename K>
+__device__ __forceinline__ void sort_registers(K (&k)[kPer], float (&v)[kPer]) {
+#pragma unroll
+    for (int size = 2; size <= kPer; size <<= 1) {
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+#pragma unroll
+            for (int i = 0; i < kPer; ++i) {
+                const int j = i ^ stride;
+                if (j > i) {
+                    const bool ascending = (i & size) == 0;
+                    const bool swap = (k[i] > k[j]) == ascending;
+                    const K ki = k[i], kj = k[j];
+                    const float vi = v[i], vj = v[j];
+                    k[i] = swap ? kj : ki;
+                    k[j] = swap ? ki : kj;
+                    v[i] = swap ? vj : vi;
+                    v[j] = swap ? vi : vj;
+                }
+            }
+        }
+    }
 }
 
 // Merge-path split of output diagonal d over A[0, na) and B[0, nb), equal keys from A first:
 // the number of A items among the first d outputs.
-template <typename KA, typename KB>
-__device__ __forceinline__ int merge_path(KA A, KB B, int na, int nb, int d) {
+// A and B are offsets of the two runs in the padded LDS array.
+template <typename K>
+__device__ __forceinline__ int merge_split(const K *s_key, int A, int B, int na, int nb, int d) {
     int lo = max(0, d - nb), hi = min(d, na);
     while (lo < hi) {
         const int mid = (lo + hi) >> 1;
-        if (A(mid) <= B(d - 1 - mid)) {
+        if (s_key[pad(A + mid)] <= s_key[pad(B + d - 1 - mid)]) {
             lo = mid + 1;
         } else {
             hi = mid;
@@ -363,156 +421,76 @@ __device__ __forceinline__ int merge_path(KA A, KB B, int na, int nb, int d) {
     return lo;
 }
 
-// Level `level` of a row with `levels` levels reads buffer 2 when (levels - level) is odd.
-__device__ __forceinline__ bool reads_buffer2(int levels, int level) {
-    return ((levels - level) & 1) != 0;
-}
-
-__global__ void level_partition_kernel(const int64_t *__restrict__ tiles, int64_t n_tiles,
-                                       const int *__restrict__ tile_row,
-                                       const int64_t *__restrict__ row_off,
-                                       const int64_t *__restrict__ tile_prefix, int level,
-                                       const int *__restrict__ key1,
-                                       const int *__restrict__ key2, int *__restrict__ split) {
-    for (int64_t x = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; x < n_tiles;
-         x += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        const int64_t tile = tiles[x];
-        const int row = tile_row[tile];
-        const PairGeom g = pair_geometry(row_off, tile_prefix, row, tile, level);
-        const int levels = merge_levels(tile_prefix[row + 1] - tile_prefix[row]);
-        const int *A = (reads_buffer2(levels, level) ? key2 : key1) + g.a_begin;
-        const int *B = A + g.a_len;
-        split[x] = merge_path([&](int i) { return A[i]; }, [&](int i) { return B[i]; }, g.a_len,
-                              g.b_len, g.d0);
-    }
-}
-
-__global__ __launch_bounds__(kBlock) void level_merge_kernel(
-    const int64_t *__restrict__ tiles, const int *__restrict__ tile_row,
-    const int64_t *__restrict__ row_off, const int64_t *__restrict__ tile_prefix, int level,
-    const int *__restrict__ split, int *__restrict__ key1, float *__restrict__ val1,
-    int *__restrict__ key2, float *__restrict__ val2) {
-    __shared__ int s_key[kTile];
-    __shared__ float s_val[kTile];
-    const int64_t x = blockIdx.x;
-    const int64_t tile = tiles[x];
-    const int row = tile_row[tile];
-    const PairGeom g = pair_geometry(row_off, tile_prefix, row, tile, level);
-    const int levels = merge_levels(tile_prefix[row + 1] - tile_prefix[row]);
-    const bool from2 = reads_buffer2(levels, level);
-    const int *ks = from2 ? key2 : key1;
-    const float *vs = from2 ? val2 : val1;
-    int *kd = from2 ? key1 : key2;
-    float *vd = from2 ? val1 : val2;
-    const int a0 = split[x];
-    const int a1 = (g.u + 1 < g.tiles_in_pair) ? split[x + 1] : g.a_len;
-    const int b0 = g.d0 - a0, b1 = g.d1 - a1;
-    const int na = a1 - a0, nab = na + (b1 - b0), nb = nab - na;
-    const int64_t A = g.a_begin + a0, B = g.a_begin + g.a_len + b0;
-    for (int q = threadIdx.x; q < nab; q += kBlock) {
-        const int64_t src = q < na ? A + q : B + (q - na);
-        s_key[q] = ks[src];
-        s_val[q] = vs[src];
-    }
-    __syncthreads();
-    // lane t merges output items [t*kPer, (t+1)*kPer) of this tile into registers
-    const int d = min(static_cast<int>(threadIdx.x) * kPer, nab);
-    int a = merge_path([&](int i) { return s_key[i]; }, [&](int i) { return s_key[na + i]; },
-                       na, nb, d);
-    int b = d - a;
-    int ok[kPer];
-    float ov[kPer];
-#pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-        const bool take_a = a < na && (b >= nb || s_key[a] <= s_key[na + b]);
-        // past the tile's end both sources are spent: read a valid slot, never stored
-        const int src = take_a ? a : (b < nb ? na + b : 0);
-        ok[u] = s_key[src];
-        ov[u] = s_val[src];
-        a += take_a;
-        b += !take_a;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-        if (d + u < nab) {
-            s_key[d + u] = ok[u];
-            s_val[d + u] = ov[u];
-        }
-    }
-    __syncthreads();
-    const int64_t out = g.a_begin + g.d0;
-    for (int q = threadIdx.x; q < nab; q += kBlock) {
-        kd[out + q] = s_key[q];
-        vd[out + q] = s_val[q];
-    }
-}
-
-// ---- 6: compress -----------------------------------------------------------------------
-
-// Bit u set: blocked position threadIdx.x*kPer + u starts a run, i.e. a row starts there or
-// its key differs from the previous position's (for position 0 of a long row's later tile,
-// from the previous tile's last key).
-__device__ __forceinline__ unsigned run_starts(const int *s_key, const int *s_mark,
-                                               const Tile &g, const int *__restrict__ key) {
-    unsigned bits = 0u;
+// Ascending sort of n2 (a power of two, kPer <= n2 <= kTile) pairs: lane t holds positions
+// [t*kPer, (t+1)*kPer) in k/v (registers), sorts them, then sorted runs of kPer << l are
+// merged pairwise through LDS, each lane producing its kPer outputs from a merge-path split.
+// On return s_key/s_val hold the sorted sequence and k/v the lane's part of it.
+template <typename K>
+__device__ __forceinline__ void merge_sort(K (&k)[kPer], float (&v)[kPer], K *s_key,
+                                           float *s_val, int n2) {
     const int base = threadIdx.x * kPer;
+    const bool active = base < n2;
+    sort_registers(k, v);
+    if (active) {
 #pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-        const int q = base + u;
-        if (q < g.n) {
-            bool st;
-            if (s_mark[q]) {
-                st = true;
-            } else if (q > 0) {
-                st = s_key[q] != s_key[q - 1];
-            } else {
-                st = s_key[0] != key[g.s - 1];
-            }
-            if (st) bits |= 1u << u;
+        for (int u = 0; u < kPer; ++u) {
+            s_key[pad(base + u)] = k[u];
+            s_val[pad(base + u)] = v[u];
         }
     }
-    return bits;
-}
-
-__global__ __launch_bounds__(kBlock) void compress_count_kernel(
-    const int *__restrict__ tile_row, const int64_t *__restrict__ tile_start, int64_t n_tiles,
-    int rows, const int64_t *__restrict__ row_off, const int *__restrict__ key,
-    int64_t *__restrict__ tile_count) {
-    __shared__ int s_key[kTile];
-    __shared__ int s_mark[kTile];
-    __shared__ int s_wave[kBlock / dev::kWave];
-    const int64_t t = blockIdx.x;
-    const Tile g = load_tile(tile_row, tile_start, row_off, t);
-    for (int q = threadIdx.x; q < kTile; q += kBlock) {
-        s_mark[q] = 0;
-        if (q < g.n) s_key[q] = key[g.s + q];
+    for (int len = kPer; len < n2; len <<= 1) {
+        __syncthreads();
+        const int A = base & ~(2 * len - 1);
+        const int B = A + len;
+        // runs already in order (typically two different segments) merge to themselves: the
+        // lane's registers and LDS positions already hold its outputs
+        const bool merge = active && s_key[pad(B - 1)] > s_key[pad(B)];
+        if (merge) {
+            int a = merge_split(s_key, A, B, len, len, base - A);
+            int b = (base - A) - a;
+            K ka = s_key[pad(A + min(a, len - 1))];
+            K kb = s_key[pad(B + min(b, len - 1))];
+#pragma unroll
+            for (int u = 0; u < kPer; ++u) {
+                const bool take_a = a < len && (b >= len || ka <= kb);
+                const int src = take_a ? A + a : B + min(b, len - 1);
+                k[u] = take_a ? ka : kb;
+                v[u] = s_val[pad(src)];
+                a += take_a;
+                b += !take_a;
+                if (take_a) {
+                    ka = s_key[pad(A + min(a, len - 1))];
+                } else {
+                    kb = s_key[pad(B + min(b, len - 1))];
+                }
+            }
+        }
+        __syncthreads();
+        if (merge) {
+#pragma unroll
+            for (int u = 0; u < kPer; ++u) {
+                s_key[pad(base + u)] = k[u];
+                s_val[pad(base + u)] = v[u];
+            }
+        }
     }
     __syncthreads();
-    mark_rows(s_mark, g, tile_row, row_off, t, n_tiles, rows);
-    __syncthreads();
-    const unsigned st = run_starts(s_key, s_mark, g, key);
-    int total = 0;
-    (void)dev::block_exclusive_sum<kBlock>(static_cast<int>(__popc(st)), s_wave, total);
-    if (threadIdx.x == 0) tile_count[t] = total;
 }
 
 // Exclusive segmented sum across the workgroup's lanes.  Lane input: f = the lane holds a run
 // start, s = the sum of its positions after its last start (all of them if none).  Output:
-// carry_f = an earlier lane holds a start, carry_s = the sum of the run open where the lane
-// begins (from the earlier lanes).
-__device__ __forceinline__ void block_segmented_carry(bool f, double s, double *s_sum,
-                                                      int *s_flag, bool &carry_f,
-                                                      double &carry_s) {
+// the sum of the run open where the lane begins (from earlier lanes; 0 if none).
+__device__ __forceinline__ double block_segmented_carry(bool f, double s, double *s_sum,
+                                                        int *s_flag) {
     const int l = dev::lane();
     const int w = threadIdx.x / dev::kWave;
     int fi = f ? 1 : 0;
     double si = s;
 #pragma unroll
-    for (int off = 1; off < dev::kWave; off <<= 1) {
-        const int fu = __shfl_up(fi, off, dev::kWave);
-        const double su = __shfl_up(si, off, dev::kWave);
-        if (l >= off) {
+    for (int o = 1; o < dev::kWave; o <<= 1) {
+        const int fu = __shfl_up(fi, o, dev::kWave);
+        const double su = __shfl_up(si, o, dev::kWave);
+        if (l >= o) {
             if (!fi) si += su;
             fi |= fu;
         }
@@ -528,127 +506,231 @@ __device__ __forceinline__ void block_segmented_carry(bool f, double s, double *
         s_sum[w] = si;
     }
     __syncthreads();
-    int cf = 0;
     double cs = 0.0;
-    for (int i = 0; i < w; ++i) {
-        cs = s_flag[i] ? s_sum[i] : cs + s_sum[i];
-        cf |= s_flag[i];
-    }
+    for (int i = 0; i < w; ++i) cs = s_flag[i] ? s_sum[i] : cs + s_sum[i];
     __syncthreads();
-    carry_f = (cf | fe) != 0;
-    carry_s = fe ? se : cs + se;
+    return fe ? se : cs + se;
 }
 
-template <typename PosT>
-__global__ __launch_bounds__(kBlock) void compress_write_kernel(
-    const int *__restrict__ tile_row, const int64_t *__restrict__ tile_start, int64_t n_tiles,
-    int rows, const int64_t *__restrict__ row_off, const int *__restrict__ key,
-    const float *__restrict__ val, const int64_t *__restrict__ out_off,
-    PosT *__restrict__ out_pos, int *__restrict__ out_crd, float *__restrict__ out_val) {
-    __shared__ int s_key[kTile];
-    __shared__ float s_val[kTile];
-    __shared__ int s_mark[kTile];
+// One workgroup per unit; dense units return at once.  Sorts the unit's products by
+// (segment ordinal, k), sums each run in float64, writes the distinct entries at the unit's
+// start in ukey/uval, the unit's count, and (row_unit, row_local) for rows starting here.
+// K is uint32_t when kOrdBits + col_shift <= 32, else uint64_t (col_shift = 32).
+template <typename K>
+__global__ __launch_bounds__(kBlock) void sort_unit_kernel(
+    const int *__restrict__ unit_seg, const int64_t *__restrict__ unit_start, int64_t n_units,
+    int64_t n_seg, const int64_t *__restrict__ seg_len, const int64_t *__restrict__ seg_off,
+    const int *__restrict__ seg_row, const int64_t *__restrict__ row_off, int col_shift,
+    const int *__restrict__ key, const float *__restrict__ val, int *__restrict__ ukey,
+    float *__restrict__ uval, int64_t *__restrict__ unit_nnz, int *__restrict__ row_unit,
+    int *__restrict__ row_local) {
+    __shared__ K s_key[kPadded];
+    __shared__ float s_val[kPadded];
+    __shared__ int s_mark[kPadded];
     __shared__ int s_wave[kBlock / dev::kWave];
     __shared__ double s_sum[kBlock / dev::kWave];
     __shared__ int s_flag[kBlock / dev::kWave];
-    const int64_t t = blockIdx.x;
-    const Tile g = load_tile(tile_row, tile_start, row_off, t);
+    const int64_t u = blockIdx.x;
+    const int s0 = unit_seg[u];
+    if (seg_len[s0] > kShort) return;
+    const int64_t start = unit_start[u];
+    const int n = static_cast<int>(unit_start[u + 1] - start);
+    const int64_t s_end = u + 1 < n_units ? unit_seg[u + 1] : n_seg;
     for (int q = threadIdx.x; q < kTile; q += kBlock) {
-        s_mark[q] = 0;
-        if (q < g.n) {
-            s_key[q] = key[g.s + q];
-            s_val[q] = val[g.s + q];
+        s_mark[pad(q)] = 0;
+        if (q < n) {  // coalesced staging of the raw columns and values
+            s_key[pad(q)] = static_cast<K>(static_cast<uint32_t>(key[start + q]));
+            s_val[pad(q)] = val[start + q];
         }
     }
     __syncthreads();
-    mark_rows(s_mark, g, tile_row, row_off, t, n_tiles, rows);
+    for (int64_t s = s0 + threadIdx.x; s < s_end; s += kBlock) {
+        if (seg_len[s] > 0) s_mark[pad(static_cast<int>(seg_off[s] - start))] = static_cast<int>(s) + 1;
+    }
     __syncthreads();
-    const unsigned st = run_starts(s_key, s_mark, g, key);
+    const int base = threadIdx.x * kPer;  // blocked positions of this lane
+    int c = 0;
+#pragma unroll
+    for (int v = 0; v < kPer; ++v) c += s_mark[pad(base + v)] != 0;
     int total = 0;
-    const int rank0 = dev::block_exclusive_sum<kBlock>(static_cast<int>(__popc(st)), s_wave, total);
-    const int base = threadIdx.x * kPer;
-    // lane-local segmented sums
-    double part[kPer];
+    int ord = dev::block_exclusive_sum<kBlock>(c, s_wave, total) - 1;
+    int n2 = kPer;
+    while (n2 < n) n2 <<= 1;
+    K rk0[kPer];
+    float rv0[kPer];
+#pragma unroll
+    for (int v = 0; v < kPer; ++v) {
+        const int q = base + v;
+        ord += s_mark[pad(q)] != 0;
+        rk0[v] = q < n ? (static_cast<K>(ord) << col_shift) | s_key[pad(q)] : ~static_cast<K>(0);
+        rv0[v] = q < n ? s_val[pad(q)] : 0.0f;
+    }
+    __syncthreads();
+    merge_sort(rk0, rv0, s_key, s_val, n2);
+    // Segments keep their positions (sorted by ordinal first), so s_mark still marks them.
+    // rk0/rv0 hold this lane's sorted positions; neighbours come from LDS.
+    const K prev = base > 0 && base < n ? s_key[pad(base - 1)] : ~static_cast<K>(0);
+    unsigned st = 0;
     double acc = 0.0;
 #pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-        const int q = base + u;
-        const double v = q < g.n ? static_cast<double>(s_val[q]) : 0.0;
-        acc = (st & (1u << u)) ? v : acc + v;
-        part[u] = acc;
+    for (int v = 0; v < kPer; ++v) {
+        const int q = base + v;
+        const bool start_run = q < n && (q == 0 || rk0[v] != (v > 0 ? rk0[v - 1] : prev));
+        if (start_run) st |= 1u << v;
+        const double x = q < n ? static_cast<double>(rv0[v]) : 0.0;
+        acc = start_run ? x : acc + x;
     }
-    bool carry_f = false;
-    double carry_s = 0.0;
-    block_segmented_carry(st != 0, acc, s_sum, s_flag, carry_f, carry_s);
-    // A run ends at q when q + 1 starts a run or q is the tile's last position; its result
-    // goes to the index of its start.  Positions before the tile's first start continue the
-    // previous tile's last run, which that tile completes.
-    const int64_t out_base = out_off[t];
-    const int64_t row_end = g.shared_tile ? g.e : row_off[g.row + 1];
-    int rk[kPer];
-    float rv[kPer];
+    int runs = 0;
+    const int rank0 =
+        dev::block_exclusive_sum<kBlock>(static_cast<int>(__popc(st)), s_wave, runs);
+    const double carry = block_segmented_carry(st != 0, acc, s_sum, s_flag);
+    const K next = base + kPer < n ? s_key[pad(base + kPer)] : ~static_cast<K>(0);
+    const K mask = (static_cast<K>(1) << col_shift) - 1;
+    // second pass: each run's sum is complete at its last position; it goes to the index of
+    // the run's start (one entry per run, in order)
+    acc = carry;
+    int idx = rank0 - 1;
+    int ok[kPer];
+    float ov[kPer];
     unsigned ends = 0;
+    int first_end = 0;  // run index of the lane's first run end (its later ends follow)
 #pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-        const int q = base + u;
-        rk[u] = 0;
-        rv[u] = 0.0f;
-        if (q >= g.n) continue;
-        const unsigned upto = st & ((2u << u) - 1);
-        if (!carry_f && upto == 0) continue;
-        bool end = true;
-        if (q + 1 < g.n) {
-            end = (u + 1 < kPer) ? (st & (1u << (u + 1))) != 0
-                                 : (s_mark[q + 1] != 0 || s_key[q + 1] != s_key[q]);
-        }
-        if (!end) continue;
-        double sum = upto ? part[u] : carry_s + part[u];
-        const int k = s_key[q];
-        if (q + 1 == g.n) {
-            // a long row's run may continue into the following tiles
-            for (int64_t x = g.e; x < row_end && key[x] == k; ++x) {
-                sum += static_cast<double>(val[x]);
+    for (int v = 0; v < kPer; ++v) {
+        const int q = base + v;
+        ok[v] = 0;
+        ov[v] = 0.0f;
+        if (q < n) {
+            const bool start_run = (st >> v) & 1u;
+            if (start_run) ++idx;
+            acc = start_run ? static_cast<double>(rv0[v]) : acc + static_cast<double>(rv0[v]);
+            const K after = v + 1 < kPer ? rk0[v + 1] : next;
+            if (q + 1 == n || after != rk0[v]) {
+                if (ends == 0) first_end = idx;
+                ends |= 1u << v;
+                ok[v] = static_cast<int>(rk0[v] & mask);
+                ov[v] = static_cast<float>(acc);
+            }
+            // rows starting here: the first position of their first nonempty segment
+            if (s_mark[pad(q)]) {
+                const int sg = s_mark[pad(q)] - 1;
+                const int r = seg_row[sg];
+                if (row_off[r] == seg_off[sg]) {
+                    row_unit[r] = static_cast<int>(u);
+                    row_local[r] = idx;
+                }
             }
         }
-        ends |= 1u << u;
-        rk[u] = k;
-        rv[u] = static_cast<float>(sum);
     }
-    // row offsets: a row's first run; the empty rows just before it share its offset
+    // stage the unit's distinct entries in LDS (run j at slot j), then store them coalesced
+    __syncthreads();
+    int *s_ok = s_mark;
+    idx = first_end;
 #pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-        const int q = base + u;
-        if (q < g.n && s_mark[q]) {
-            const int r = s_mark[q] - 1;
-            const PosT v = static_cast<PosT>(out_base + rank0 + __popc(st & ((1u << u) - 1)));
-            out_pos[r] = v;
-            const int64_t rs = row_off[r];
-            for (int x = r - 1; x >= 0 && row_off[x] == rs; --x) out_pos[x] = v;
+    for (int v = 0; v < kPer; ++v) {
+        if ((ends >> v) & 1u) {
+            s_ok[pad(idx)] = ok[v];
+            s_val[pad(idx)] = ov[v];
+            ++idx;
         }
     }
     __syncthreads();
-    // the run ending at u started at the last start at or before u
-#pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-        if (ends & (1u << u)) {
-            const int idx = rank0 + __popc(st & ((2u << u) - 1)) - 1;
-            s_key[idx] = rk[u];
-            s_val[idx] = rv[u];
-        }
+    for (int j = threadIdx.x; j < runs; j += kBlock) {
+        ukey[start + j] = s_ok[pad(j)];
+        uval[start + j] = s_val[pad(j)];
     }
-    __syncthreads();
-    for (int q = threadIdx.x; q < total; q += kBlock) {
-        out_crd[out_base + q] = s_key[q];
-        out_val[out_base + q] = s_val[q];
+    if (threadIdx.x == 0) unit_nnz[u] = runs;
+}
+
+// ---- 5b: dense units -------------------------------------------------------------------
+
+// One workgroup per unit; sort units return at once.  The segment's column range
+// [bucket << shift, (bucket + 1) << shift) is accumulated kDenseCols columns at a time in an
+// LDS float64 array (plus a bitmap of touched columns), then compacted in column order.
+__global__ __launch_bounds__(kBlock) void dense_unit_kernel(
+    const int *__restrict__ unit_seg, const int64_t *__restrict__ unit_start,
+    const int64_t *__restrict__ seg_len, const int64_t *__restrict__ seg_prefix,
+    const int *__restrict__ seg_row, const int64_t *__restrict__ row_off, int shift, int cols,
+    const int *__restrict__ key, const float *__restrict__ val, int *__restrict__ ukey,
+    float *__restrict__ uval, int64_t *__restrict__ unit_nnz, int *__restrict__ row_unit,
+    int *__restrict__ row_local) {
+    __shared__ double s_acc[kDenseCols];
+    __shared__ unsigned s_bits[kDenseCols / 32];
+    __shared__ int s_wave[kBlock / dev::kWave];
+    static_assert(kDenseCols / 32 == kBlock, "one bitmap word per lane");
+    const int64_t u = blockIdx.x;
+    const int s = unit_seg[u];
+    const int64_t len = seg_len[s];
+    if (len <= kShort) return;
+    const int64_t start = unit_start[u];
+    const int row = seg_row[s];
+    const int64_t bucket = s - seg_prefix[row];
+    const int64_t c_lo = bucket << shift;
+    const int64_t c_hi = min(static_cast<int64_t>(cols), (bucket + 1) << shift);
+    if (threadIdx.x == 0 && row_off[row] == start) {
+        row_unit[row] = static_cast<int>(u);
+        row_local[row] = 0;
+    }
+    int64_t written = 0;
+    for (int64_t w0 = c_lo; w0 < c_hi; w0 += kDenseCols) {
+        for (int i = threadIdx.x; i < kDenseCols; i += kBlock) s_acc[i] = 0.0;
+        s_bits[threadIdx.x] = 0u;
+        __syncthreads();
+        for (int64_t x = threadIdx.x; x < len; x += kBlock) {
+            const int64_t c = key[start + x] - w0;
+            if (c >= 0 && c < kDenseCols) {
+                atomicAdd(&s_acc[c], static_cast<double>(val[start + x]));
+                atomicOr(&s_bits[c >> 5], 1u << (c & 31));
+            }
+        }
+        __syncthreads();
+        const unsigned word = s_bits[threadIdx.x];
+        int total = 0;
+        int rank = dev::block_exclusive_sum<kBlock>(static_cast<int>(__popc(word)), s_wave, total);
+        unsigned m = word;
+        while (m) {
+            const int bit = __ffs(m) - 1;
+            m &= m - 1;
+            const int c = threadIdx.x * 32 + bit;
+            ukey[start + written + rank] = static_cast<int>(w0 + c);
+            uval[start + written + rank] = static_cast<float>(s_acc[c]);
+            ++rank;
+        }
+        written += total;
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) unit_nnz[u] = written;
+}
+
+// ---- 6: output -------------------------------------------------------------------------
+
+__global__ __launch_bounds__(kBlock) void copy_units_kernel(
+    const int64_t *__restrict__ unit_start, const int64_t *__restrict__ unit_nnz,
+    const int64_t *__restrict__ unit_out, const int *__restrict__ ukey,
+    const float *__restrict__ uval, int *__restrict__ out_crd, float *__restrict__ out_val) {
+    const int64_t u = blockIdx.x;
+    const int64_t src = unit_start[u], dst = unit_out[u], n = unit_nnz[u];
+    for (int64_t x = threadIdx.x; x < n; x += kBlock) {
+        out_crd[dst + x] = ukey[src + x];
+        out_val[dst + x] = uval[src + x];
     }
 }
 
-// Rows that start at P (trailing empty rows, and the final offset) get nnz.
+// Row offsets: a row with products starts at its unit's offset plus its local offset; the
+// empty rows just before it share that offset; rows starting at P (and pos[rows]) get nnz.
 template <typename PosT>
-__global__ void tail_pos_kernel(const int64_t *__restrict__ row_off, int rows, int64_t P,
-                                int64_t nnz, PosT *__restrict__ out_pos) {
-    for (int r = blockIdx.x * blockDim.x + threadIdx.x; r <= rows; r += gridDim.x * blockDim.x) {
-        if (row_off[r] == P) out_pos[r] = static_cast<PosT>(nnz);
+__global__ void row_pos_kernel(const int64_t *__restrict__ row_off, int rows, int64_t P,
+                               int64_t nnz, const int *__restrict__ row_unit,
+                               const int *__restrict__ row_local,
+                               const int64_t *__restrict__ unit_out, PosT *__restrict__ pos) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i <= rows; i += gridDim.x * blockDim.x) {
+        const int64_t rs = row_off[i];
+        if (rs == P) {
+            pos[i] = static_cast<PosT>(nnz);
+        } else if (row_off[i + 1] > rs) {
+            const PosT v = static_cast<PosT>(unit_out[row_unit[i]] + row_local[i]);
+            pos[i] = v;
+            for (int x = i - 1; x >= 0 && row_off[x] == rs; --x) pos[x] = v;
+        }
     }
 }
 
@@ -685,158 +767,145 @@ struct Product {
 // NACHO_ERR_INDEX_OVERFLOW (before allocating the result) when nnz(Z) exceeds INT_MAX.
 template <typename PosT>
 int multiply(Call &call, const nacho_csr *a, const nacho_csr *b, Product *z) {
-    const hipStream_t s = call.stream();
+    const hipStream_t st = call.stream();
     const int rows = a->dim_i_size;
+    const int cols = b->dim_j_size;
     const int64_t nnz_a = a->dim_j_length;
-    const char *name = "spgemm: expand+sort+merge+compress";
+    const int cb = col_bits(cols);
+    // one radix digit over the columns: buckets of 2^shift columns, at most kMaxBuckets
+    const int shift = std::max(std::min(kDenseBits, cb), cb - kMaxBucketBits);
+    const int nb = cols > 0 ? ((cols - 1) >> shift) + 1 : 1;
+    const char *name = "spgemm: expand+scatter+reduce+copy";
     NACHO_TRY(call.timer_start(name));
 
-    // 1. products per A entry and per row
-    int64_t *len = nullptr, *off = nullptr, *row_off = nullptr;
+    // 1-2. products per A entry, per row; segments per row
+    int64_t *len = nullptr, *off = nullptr, *row_off = nullptr, *seg_count = nullptr;
+    int64_t *seg_prefix = nullptr;
     NACHO_TRY(call.scratch_n(static_cast<size_t>(nnz_a) + 1, &len));
     NACHO_TRY(call.scratch_n(static_cast<size_t>(nnz_a) + 1, &off));
     NACHO_TRY(call.scratch_n(static_cast<size_t>(rows) + 1, &row_off));
+    NACHO_TRY(call.scratch_n(static_cast<size_t>(rows) + 1, &seg_count));
+    NACHO_TRY(call.scratch_n(static_cast<size_t>(rows) + 1, &seg_prefix));
     if (nnz_a > 0) {
-        lengths_kernel<<<grid_for(nnz_a, 256), 256, 0, s>>>(a->dim_j_indices, nnz_a,
-                                                            b->dim_j_offsets, len);
+        lengths_kernel<<<grid_for(nnz_a, 256), 256, 0, st>>>(a->dim_j_indices, nnz_a,
+                                                             b->dim_j_offsets, len);
         NACHO_TRY_HIP(hipGetLastError());
     }
     NACHO_TRY(scan::exclusive_scan_i64(call, len, nnz_a, off));
-    row_off_kernel<<<grid_for(static_cast<int64_t>(rows) + 1, 256), 256, 0, s>>>(
-        a->dim_j_offsets, rows, off, row_off);
+    rows_kernel<<<grid_for(static_cast<int64_t>(rows) + 1, 256), 256, 0, st>>>(
+        a->dim_j_offsets, rows, off, nb, row_off, seg_count);
     NACHO_TRY_HIP(hipGetLastError());
-
-    // 2. tiles
-    int64_t *row_tiles = nullptr, *tile_prefix = nullptr;
-    NACHO_TRY(call.scratch_n(static_cast<size_t>(rows) + 1, &row_tiles));
-    NACHO_TRY(call.scratch_n(static_cast<size_t>(rows) + 1, &tile_prefix));
-    if (rows > 0) {
-        row_tiles_kernel<<<grid_for(rows, 256), 256, 0, s>>>(row_off, rows, row_tiles);
-        NACHO_TRY_HIP(hipGetLastError());
-    }
-    NACHO_TRY(scan::exclusive_scan_i64(call, row_tiles, rows, tile_prefix));
-    std::vector<int64_t> h_prefix(static_cast<size_t>(rows) + 1);
-    NACHO_TRY_HIP(hipMemcpyAsync(h_prefix.data(), tile_prefix, sizeof(int64_t) * (rows + 1),
-                                 hipMemcpyDeviceToHost, s));
-    int64_t P = 0;
+    NACHO_TRY(scan::exclusive_scan_i64(call, seg_count, rows, seg_prefix));
+    int64_t P = 0, n_seg = 0;
     NACHO_TRY(call.timer_stop());
-    NACHO_TRY(call.read_back(&P, row_off + rows, sizeof(P)));  // synchronises the copy too
-    const int64_t T = h_prefix[static_cast<size_t>(rows)];
+    NACHO_TRY(call.read_back(&P, row_off + rows, sizeof(P)));
+    NACHO_TRY(call.read_back(&n_seg, seg_prefix + rows, sizeof(n_seg)));
     NACHO_TRY(call.timer_start(name));
+    if (n_seg >= INT_MAX) return NACHO_ERR_INDEX_OVERFLOW;  // segment ids are int32
 
-    // merge plan: long rows ordered by level count, so each level's active tiles are a prefix
-    std::vector<std::pair<int, int>> long_rows;  // (levels, row)
-    int max_levels = 0;
-    for (int i = 0; i < rows; ++i) {
-        const int64_t nt = h_prefix[static_cast<size_t>(i) + 1] - h_prefix[static_cast<size_t>(i)];
-        if (nt > kMaxRowTiles) return NACHO_ERR_INDEX_OVERFLOW;
-        const int lv = merge_levels(nt);
-        if (lv > 0) long_rows.emplace_back(lv, i);
-        max_levels = std::max(max_levels, lv);
-    }
-    std::stable_sort(long_rows.begin(), long_rows.end(),
-                     [](const std::pair<int, int> &x, const std::pair<int, int> &y) {
-                         return x.first > y.first;
-                     });
-    std::vector<int64_t> h_tiles;
-    std::vector<int64_t> level_tiles(static_cast<size_t>(max_levels), 0);
-    for (const auto &lr : long_rows) {
-        const int64_t t0 = h_prefix[static_cast<size_t>(lr.second)];
-        const int64_t t1 = h_prefix[static_cast<size_t>(lr.second) + 1];
-        for (int64_t t = t0; t < t1; ++t) h_tiles.push_back(t);
-        for (int l = 0; l < lr.first; ++l) level_tiles[static_cast<size_t>(l)] += t1 - t0;
-    }
-
-    int *key1 = nullptr, *key2 = nullptr, *tile_row = nullptr, *split = nullptr;
-    float *val1 = nullptr, *val2 = nullptr;
-    int64_t *tile_start = nullptr, *d_tiles = nullptr;
-    NACHO_TRY(call.scratch_n(static_cast<size_t>(T) + 1, &tile_start));
+    int64_t n_units = 0;
+    int64_t *unit_start = nullptr, *unit_nnz = nullptr, *unit_out = nullptr;
+    int *row_unit = nullptr, *row_local = nullptr;
+    NACHO_TRY(call.scratch_n(static_cast<size_t>(rows) + 1, &row_unit));
+    NACHO_TRY(call.scratch_n(static_cast<size_t>(rows) + 1, &row_local));
     if (P > 0) {
-        NACHO_TRY(call.scratch_n(static_cast<size_t>(P), &key1));
-        NACHO_TRY(call.scratch_n(static_cast<size_t>(P), &val1));
-        NACHO_TRY(call.scratch_n(static_cast<size_t>(T), &tile_row));
-        if (max_levels > 0) {
-            NACHO_TRY(call.scratch_n(static_cast<size_t>(P), &key2));
-            NACHO_TRY(call.scratch_n(static_cast<size_t>(P), &val2));
-            NACHO_TRY(call.scratch_n(h_tiles.size(), &d_tiles));
-            NACHO_TRY(call.scratch_n(h_tiles.size(), &split));
-            NACHO_TRY_HIP(hipMemcpyAsync(d_tiles, h_tiles.data(),
-                                         sizeof(int64_t) * h_tiles.size(),
-                                         hipMemcpyHostToDevice, s));
-            NACHO_TRY_HIP(hipStreamSynchronize(s));  // h_tiles is pageable host memory
-        }
-    }
-    tile_map_kernel<<<grid_for(static_cast<int64_t>(rows) + 1, 256), 256, 0, s>>>(
-        row_off, tile_prefix, rows, tile_row, tile_start);
-    NACHO_TRY_HIP(hipGetLastError());
-
-    if (P > 0) {
-        // 3. expand
-        expand_kernel<<<static_cast<unsigned>((P + kTile - 1) / kTile), kBlock, 0, s>>>(
-            a->dim_j_indices, a->values, nnz_a, off, P, b->dim_j_offsets, b->dim_j_indices,
-            b->values, key1, val1);
+        // segment table
+        int *seg_row = nullptr;
+        int64_t *seg_len = nullptr, *seg_off = nullptr, *seg_fill = nullptr;
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(n_seg), &seg_row));
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(n_seg) + 1, &seg_len));
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(n_seg) + 1, &seg_off));
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(n_seg), &seg_fill));
+        segments_kernel<<<grid_for(rows, 256), 256, 0, st>>>(row_off, seg_prefix, rows, seg_row,
+                                                            seg_len, seg_fill);
         NACHO_TRY_HIP(hipGetLastError());
-        // 4. sort
-        const int cb = col_bits(b->dim_j_size);
+
+        // 3. histogram, segment offsets, scatter
+        int *key = nullptr, *ukey = nullptr;
+        float *val = nullptr, *uval = nullptr;
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(P), &key));
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(P), &val));
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(P), &ukey));
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(P), &uval));
+        const unsigned chunks = static_cast<unsigned>((P + kChunk - 1) / kChunk);
+        chunk_kernel<false><<<chunks, kBlock, 0, st>>>(
+            a->dim_j_indices, a->values, nnz_a, off, row_off, rows, P, b->dim_j_offsets,
+            b->dim_j_indices, b->values, shift, nb, seg_prefix, seg_len, seg_off, seg_fill, key,
+            val);
+        NACHO_TRY_HIP(hipGetLastError());
+        NACHO_TRY(scan::exclusive_scan_i64(call, seg_len, n_seg, seg_off));
+        chunk_kernel<true><<<chunks, kBlock, 0, st>>>(
+            a->dim_j_indices, a->values, nnz_a, off, row_off, rows, P, b->dim_j_offsets,
+            b->dim_j_indices, b->values, shift, nb, seg_prefix, seg_len, seg_off, seg_fill, key,
+            val);
+        NACHO_TRY_HIP(hipGetLastError());
+
+        // 4. units
+        int64_t *seg_units = seg_fill;  // the fill counters are spent
+        int64_t *unit_prefix = nullptr;
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(n_seg) + 1, &unit_prefix));
+        unit_count_kernel<<<grid_for(n_seg, 256), 256, 0, st>>>(seg_len, seg_off, n_seg,
+                                                               seg_units);
+        NACHO_TRY_HIP(hipGetLastError());
+        NACHO_TRY(scan::exclusive_scan_i64(call, seg_units, n_seg, unit_prefix));
+        NACHO_TRY(call.timer_stop());
+        NACHO_TRY(call.read_back(&n_units, unit_prefix + n_seg, sizeof(n_units)));
+        NACHO_TRY(call.timer_start(name));
+        if (n_units > INT_MAX) return NACHO_ERR_INDEX_OVERFLOW;
+        int *unit_seg = nullptr;
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(n_units), &unit_seg));
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(n_units) + 1, &unit_start));
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(n_units) + 1, &unit_nnz));
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(n_units) + 1, &unit_out));
+        unit_map_kernel<<<grid_for(n_seg + 1, 256), 256, 0, st>>>(
+            seg_units, unit_prefix, seg_off, n_seg, P, unit_seg, unit_start);
+        NACHO_TRY_HIP(hipGetLastError());
+
+        // 5. reduce
+        const unsigned ug = static_cast<unsigned>(n_units);
         if (cb + kOrdBits <= 32) {
-            sort_tiles_kernel<uint32_t><<<static_cast<unsigned>(T), kBlock, 0, s>>>(
-                tile_row, tile_start, T, rows, row_off, tile_prefix, cb, key1, val1, key2, val2);
+            sort_unit_kernel<uint32_t><<<ug, kBlock, 0, st>>>(
+                unit_seg, unit_start, n_units, n_seg, seg_len, seg_off, seg_row, row_off, cb,
+                key, val, ukey, uval, unit_nnz, row_unit, row_local);
         } else {
-            sort_tiles_kernel<uint64_t><<<static_cast<unsigned>(T), kBlock, 0, s>>>(
-                tile_row, tile_start, T, rows, row_off, tile_prefix, 32, key1, val1, key2, val2);
+            sort_unit_kernel<uint64_t><<<ug, kBlock, 0, st>>>(
+                unit_seg, unit_start, n_units, n_seg, seg_len, seg_off, seg_row, row_off, 32,
+                key, val, ukey, uval, unit_nnz, row_unit, row_local);
         }
         NACHO_TRY_HIP(hipGetLastError());
-        // 5. merge levels
-        for (int level = 0; level < max_levels; ++level) {
-            const int64_t n = level_tiles[static_cast<size_t>(level)];
-            level_partition_kernel<<<grid_for(n, 256), 256, 0, s>>>(
-                d_tiles, n, tile_row, row_off, tile_prefix, level, key1, key2, split);
-            NACHO_TRY_HIP(hipGetLastError());
-            level_merge_kernel<<<static_cast<unsigned>(n), kBlock, 0, s>>>(
-                d_tiles, tile_row, row_off, tile_prefix, level, split, key1, val1, key2, val2);
+        dense_unit_kernel<<<ug, kBlock, 0, st>>>(unit_seg, unit_start, seg_len, seg_prefix,
+                                                 seg_row, row_off, shift, cols, key, val, ukey,
+                                                 uval, unit_nnz, row_unit, row_local);
+        NACHO_TRY_HIP(hipGetLastError());
+        NACHO_TRY(scan::exclusive_scan_i64(call, unit_nnz, n_units, unit_out));
+
+        int64_t nnz = 0;
+        NACHO_TRY(call.timer_stop());
+        NACHO_TRY(call.read_back(&nnz, unit_out + n_units, sizeof(nnz)));
+        if (sizeof(PosT) == sizeof(int32_t) && nnz > INT_MAX) return NACHO_ERR_INDEX_OVERFLOW;
+        NACHO_TRY(call.timer_start(name));
+
+        // 6. output
+        NACHO_TRY(call.result_n(static_cast<size_t>(nnz), &z->crd));
+        NACHO_TRY(call.result_n(static_cast<size_t>(nnz), &z->val));
+        if (nnz > 0) {
+            copy_units_kernel<<<ug, kBlock, 0, st>>>(unit_start, unit_nnz, unit_out, ukey,
+                                                     uval, z->crd, z->val);
             NACHO_TRY_HIP(hipGetLastError());
         }
+        z->nnz = nnz;
     }
-
-    // 6. compress
-    int64_t *tile_count = nullptr, *out_off = nullptr;
-    NACHO_TRY(call.scratch_n(static_cast<size_t>(T) + 1, &tile_count));
-    NACHO_TRY(call.scratch_n(static_cast<size_t>(T) + 1, &out_off));
-    if (T > 0) {
-        compress_count_kernel<<<static_cast<unsigned>(T), kBlock, 0, s>>>(
-            tile_row, tile_start, T, rows, row_off, key1, tile_count);
-        NACHO_TRY_HIP(hipGetLastError());
-    }
-    NACHO_TRY(scan::exclusive_scan_i64(call, tile_count, T, out_off));
-    int64_t nnz = 0;
-    NACHO_TRY(call.timer_stop());
-    NACHO_TRY(call.read_back(&nnz, out_off + T, sizeof(nnz)));
-    if (sizeof(PosT) == sizeof(int32_t) && nnz > INT_MAX) return NACHO_ERR_INDEX_OVERFLOW;
-    NACHO_TRY(call.timer_start(name));
-
     PosT *pos = nullptr;
-    int *crd = nullptr;
-    float *val = nullptr;
     NACHO_TRY(call.result_n(static_cast<size_t>(rows) + 1, &pos));
-    NACHO_TRY(call.result_n(static_cast<size_t>(nnz), &crd));
-    NACHO_TRY(call.result_n(static_cast<size_t>(nnz), &val));
-    tail_pos_kernel<PosT><<<grid_for(static_cast<int64_t>(rows) + 1, 256), 256, 0, s>>>(
-        row_off, rows, P, nnz, pos);
+    row_pos_kernel<PosT><<<grid_for(static_cast<int64_t>(rows) + 1, 256), 256, 0, st>>>(
+        row_off, rows, P, z->nnz, row_unit, row_local, unit_out, pos);
     NACHO_TRY_HIP(hipGetLastError());
-    if (T > 0) {
-        compress_write_kernel<PosT><<<static_cast<unsigned>(T), kBlock, 0, s>>>(
-            tile_row, tile_start, T, rows, row_off, key1, val1, out_off, pos, crd, val);
-        NACHO_TRY_HIP(hipGetLastError());
-    }
     NACHO_TRY(call.timer_stop());
     NACHO_TRY(call.collect_timer());
 
     z->rows = rows;
-    z->cols = b->dim_j_size;
-    z->nnz = nnz;
+    z->cols = cols;
     z->pos = pos;
-    z->crd = crd;
-    z->val = val;
     return NACHO_OK;
 }
 
