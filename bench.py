@@ -1,6 +1,6 @@
 """Benchmark of the nacho GPU path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|c4]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|c4|c5|c5coo|c2coo]
 
 A step is one call of the hot path over one batch of synthetic input, with the operands
 already resident in HBM: `nacho_amd.gpu_csr_add_f32(A, B)` for the default workload (C2:
@@ -25,6 +25,10 @@ Workload c4 (ESC SpGEMM, C = A*A on the R-MAT 2^20 operand) reports GFLOP/s = 2*
 time, P = number of intermediate products; its roofline bytes are
 4*(n+1) + 8*nnzA + 8*P (B's gathered entries) + 8*(n+1) + 8*nnzC, and its CPU baseline is
 the row-parallel C SpGEMM of oracle/ on a random row sample.
+
+Workloads c5 (csf_add), c5coo (coo3d_add) and c2coo (coo_add) report GB/s of algorithmic
+bytes: CSF3 counts every level array of A, B and C once; COO3 16 bytes and COO 12 bytes per
+entry of A, B and C.
 """
 
 from __future__ import annotations
@@ -53,6 +57,16 @@ WORKLOADS = {
                               "csr_write_kernel<Intersect> (one call's device pipeline)",
                desc="C3 csr_mul f32 2^20x2^20, A as C2, B = 50% of A + fresh columns "
                     "(seed 3)"),
+    "c5": dict(op="csf_add", kernel="three chained level merges (csr_partition_kernel + "
+                                   "csr_count_kernel + csr_write_kernel per level)",
+               desc="C5 csf_add f32, two CSF3 tensors of shape (200000, 100000, 1000), 20M "
+                    "draws each (mode 0 Zipf(1.3), modes 1-2 uniform), deduplicated, seeds 1/2"),
+    "c5coo": dict(op="coo3d_add", kernel="coo_partition_kernel + coo_count_kernel + "
+                                         "coo_write_kernel (packed 64-bit keys)",
+                  desc="C5 as COO3: coo3d_add f32 of the same (i, j, k) tuples"),
+    "c2coo": dict(op="coo_add", kernel="coo_partition_kernel + coo_count_kernel + "
+                                      "coo_write_kernel (packed 64-bit keys)",
+                  desc="C2 as COO: coo_add f32 of the C2 operands' (i, j) tuples"),
     "c4": dict(op="spgemm", kernel="expand_kernel + sort_tiles_kernel + level_merge_kernel + "
                                  "compress_{count,write}_kernel (one call's device "
                                  "pipeline, host planning gaps excluded)",
@@ -258,6 +272,156 @@ def bench_spgemm(args, device):
     }
 
 
+def csf_bytes(levels_list):
+    """Every array of every CSF3 tensor once: crd_i, pos_j, crd_j, pos_k, crd_k, val."""
+    total = 0
+    for levels in levels_list:
+        ci, pj, cj, pk, ck = levels
+        total += 4 * (len(ci) + len(pj) + len(cj) + len(pk) + 2 * len(ck))
+    return total
+
+
+def bench_tuple_workload(args, device, workload):
+    """c5 (csf_add), c5coo (coo3d_add), c2coo (coo_add): element-wise union of coordinate
+    tuples; one step = one call with operands resident in HBM."""
+    import numpy as np
+    import torch
+
+    import nacho_amd
+    from nacho_amd import synth
+    from nacho_amd.convert import csf3_levels
+
+    spec = WORKLOADS[workload]
+    t0 = time.perf_counter()
+    if workload == "c2coo":
+        (pa, ca, va), (pb, cb, vb) = synth.c2_operands()
+        rows = len(pa) - 1
+        ia = np.repeat(np.arange(rows, dtype=np.int32), np.diff(pa))
+        ib = np.repeat(np.arange(rows, dtype=np.int32), np.diff(pb))
+        ops_np = [((ia, ca), va), ((ib, cb), vb)]
+        shape = (rows, rows)
+    else:
+        (ac, av), (bc, bv) = synth.c5_operands()
+        ops_np = [(tuple(ac[:, d] for d in range(3)), av), (tuple(bc[:, d] for d in range(3)), bv)]
+        shape = synth.C5_SHAPE
+    log(f"generated {workload}: nnzA={len(ops_np[0][1])} nnzB={len(ops_np[1][1])} "
+        f"in {time.perf_counter() - t0:.1f}s")
+
+    def upload(crd, val):
+        t = [torch.from_numpy(np.ascontiguousarray(c, dtype=np.int32)).to(device) for c in crd]
+        v = torch.from_numpy(np.ascontiguousarray(val, dtype=np.float32)).to(device)
+        dims = torch.tensor(list(shape), dtype=torch.int32)
+        if workload == "c2coo":
+            return nacho_amd.COO_gpu(t[0], t[1], v, dims)
+        if workload == "c5coo":
+            return nacho_amd.COO3_gpu(t[0], t[1], t[2], v, dims)
+        levels = csf3_levels(np.stack(crd, axis=1))
+        lv = [torch.from_numpy(np.ascontiguousarray(x, dtype=np.int32)).to(device) for x in levels]
+        return nacho_amd.CSF3_gpu(*lv, v, dims)
+
+    copies = [tuple(upload(*o) for o in ops_np) for _ in range(ROTATE)]
+    fn = {"c2coo": nacho_amd.gpu_coo_add_f32, "c5coo": nacho_amd.gpu_coo3d_add_f32,
+          "c5": nacho_amd.gpu_csf_add_f32}[workload]
+    z = fn(*copies[0])
+    torch.cuda.synchronize()
+    nnz = [len(ops_np[0][1]), len(ops_np[1][1]), int(z.values.numel())]
+    if workload == "c5":
+        lz = [z.dim_i_indices.numel(), z.dim_j_offsets.numel(), z.dim_j_indices.numel(),
+              z.dim_k_offsets.numel(), z.dim_k_indices.numel()]
+        alg_bytes = csf_bytes([csf3_levels(np.stack(o[0], axis=1)) for o in ops_np])
+        alg_bytes += 4 * (sum(lz) + lz[4])
+    else:
+        alg_bytes = (12 if workload == "c2coo" else 16) * sum(nnz)
+    del z
+    log(f"nnzC={nnz[2]} algorithmic bytes/call={alg_bytes}")
+
+    nacho_amd.set_kernel_timing(True)
+    for i in range(args.warmup):
+        fn(*copies[i % ROTATE])
+    torch.cuda.synchronize()
+    kernel_ms = []
+    for i in range(args.steps):
+        fn(*copies[i % ROTATE])
+        kernel_ms.append(nacho_amd.last_kernel_ms())
+    nacho_amd.set_kernel_timing(False)
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    for i in range(args.steps):
+        fn(*copies[i % ROTATE])
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - start) * 1e3 / args.steps
+    value = alg_bytes / (ms_per_step * 1e-3) / 1e9
+    kernel_avg_ms = sum(kernel_ms) / len(kernel_ms)
+    achieved = alg_bytes / (kernel_avg_ms * 1e-3) / 1e9
+    log(f"kernel avg {kernel_avg_ms * 1e3:.1f} us -> {achieved:.0f} GB/s; "
+        f"call {ms_per_step * 1e3:.1f} us -> {value:.0f} GB/s")
+
+    cpu = None
+    if args.cpu_budget > 0:
+        from oracle import oracle
+
+        cores = max(1, min(len(os.sched_getaffinity(0)), 64))
+        times = []
+        begin = time.perf_counter()
+        while time.perf_counter() - begin < args.cpu_budget and len(times) < 20:
+            t = {}
+            if workload == "c5":
+                oracle.port_csf3_union(csf3_levels(np.stack(ops_np[0][0], axis=1)), ops_np[0][1],
+                                       csf3_levels(np.stack(ops_np[1][0], axis=1)), ops_np[1][1],
+                                       timing=t)
+            else:
+                oracle.port_coo_binary("add", ops_np[0][0], ops_np[0][1], ops_np[1][0],
+                                       ops_np[1][1], nthreads=cores, timing=t)
+            times.append(t["seconds"])
+        sec = sorted(times)[len(times) // 2]
+        serial = workload == "c5"
+        cpu = {
+            "value": round(alg_bytes / sec / 1e9, 3),
+            "unit": "GB/s",
+            "cores": 1 if serial else cores,
+            "kind": "port",
+            "sample": f"{len(times)} full {workload} calls of the C restatement "
+                      f"(oracle/nacho_oracle.c{', serial lattice' if serial else ''}), "
+                      f"median {sec * 1e3:.1f} ms/call",
+        }
+        log(f"cpu baseline {cpu['value']} GB/s on {cpu['cores']} threads")
+
+    return {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded generators in nacho_amd/synth.py)",
+        "config": {
+            "workload": spec["desc"],
+            "nnz_a": nnz[0],
+            "nnz_b": nnz[1],
+            "nnz_c": nnz[2],
+            "algorithmic_bytes_per_step": alg_bytes,
+            "percent_of_peak_hbm": round(100.0 * value / PEAK_HBM_GBS, 2),
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": spec["kernel"],
+            "achieved": round(achieved, 2),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4),
+            "traffic": traffic_from_profiles(workload, "tuple_merge"),
+            "kernel_avg_us": round(kernel_avg_ms * 1e3, 2),
+        },
+        "cpu_baseline": cpu,
+    }
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -295,6 +459,9 @@ def main():
 
     if args.workload == "c4":
         print(json.dumps(bench_spgemm(args, device)), flush=True)
+        return
+    if args.workload in ("c5", "c5coo", "c2coo"):
+        print(json.dumps(bench_tuple_workload(args, device, args.workload)), flush=True)
         return
 
     import nacho_amd

@@ -124,8 +124,11 @@ def port_csr_binary(op, rows, pa, ca, va, pb, cb, vb, nthreads=0, timing=None):
             _take(oval, n, np.float32))
 
 
-def port_coo_binary(op, a_crd, va, b_crd, vb, nthreads=0):
-    """a_crd / b_crd: tuple of 2 or 3 int arrays (lexicographically sorted, distinct)."""
+def port_coo_binary(op, a_crd, va, b_crd, vb, nthreads=0, timing=None):
+    """a_crd / b_crd: tuple of 2 or 3 int arrays (lexicographically sorted, distinct).  If
+    `timing` is a dict, timing["seconds"] receives the duration of the C call alone."""
+    import time
+
     lib = load()
     arity = len(a_crd)
     a = [_as(x, np.int32) for x in a_crd]
@@ -136,9 +139,12 @@ def port_coo_binary(op, a_crd, va, b_crd, vb, nthreads=0):
     bp = arr_t(*[_ptr(x, ctypes.c_int32) for x in b] + [None] * (3 - arity))
     out = arr_t()
     oval, onnz = _f32p(), ctypes.c_int()
+    t0 = time.perf_counter()
     rc = lib.oracle_coo_binary(1 if op == "mul" else 0, arity, ap, _ptr(fa, ctypes.c_float),
                                int(len(va)), bp, _ptr(fb, ctypes.c_float), int(len(vb)),
                                int(nthreads), out, ctypes.byref(oval), ctypes.byref(onnz))
+    if timing is not None:
+        timing["seconds"] = time.perf_counter() - t0
     if rc != 0:
         raise RuntimeError(f"oracle_coo_binary failed ({rc})")
     n = onnz.value
@@ -146,8 +152,11 @@ def port_coo_binary(op, a_crd, va, b_crd, vb, nthreads=0):
     return crd, _take(oval, n, np.float32)
 
 
-def port_csf3_union(a_levels, a_val, b_levels, b_val):
-    """levels = (crd_i, pos_j, crd_j, pos_k, crd_k).  Returns (levels, val)."""
+def port_csf3_union(a_levels, a_val, b_levels, b_val, timing=None):
+    """levels = (crd_i, pos_j, crd_j, pos_k, crd_k).  Returns (levels, val).  If `timing` is
+    a dict, timing["seconds"] receives the duration of the C call alone."""
+    import time
+
     lib = load()
 
     def prep(levels, val):
@@ -166,8 +175,11 @@ def port_csf3_union(a_levels, a_val, b_levels, b_val):
     outs = [_i32p() for _ in range(5)]
     oval = _f32p()
     ns = [ctypes.c_int() for _ in range(3)]
+    t0 = time.perf_counter()
     rc = lib.oracle_csf3_union(*args(pa), *args(pb), *[ctypes.byref(o) for o in outs],
                                ctypes.byref(oval), *[ctypes.byref(n) for n in ns])
+    if timing is not None:
+        timing["seconds"] = time.perf_counter() - t0
     if rc != 0:
         raise RuntimeError(f"oracle_csf3_union failed ({rc})")
     ni, nj, nk = (n.value for n in ns)
