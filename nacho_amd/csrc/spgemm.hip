@@ -22,7 +22,7 @@
 //      segment; short rows keep natural order).
 //   4. units: a segment with more than kShort products is a dense unit; smaller segments
 //      whose first product falls in the same kShort-aligned window share one sort unit
-//      (fewer than 2*kShort products).
+//      (fewer than 2*kShort products).  Each kind gets a compacted work list.
 //   5. reduce: a sort unit sorts (segment ordinal, k) in LDS and sums each run in float64;
 //      a dense unit accumulates its 2^shift-column range in an LDS float64 array (windows of
 //      kDenseCols columns) and compacts the touched columns in order.  Both write the
@@ -58,6 +58,7 @@ constexpr int kDenseCols = 1 << kDenseBits;
 constexpr int kMaxBucketBits = 10;      // at most 1024 column buckets per long row
 constexpr int kMaxBuckets = 1 << kMaxBucketBits;
 constexpr int kMaxLongPerChunk = 3;     // rows longer than kShort meeting one chunk
+constexpr int kDenseMin = kShort;       // a long row's bucket above this is accumulated densely
 
 static_assert(kTile == 1 << kOrdBits, "segment ordinals must fit kOrdBits");
 static_assert(kChunk == kBlock * kPer, "chunk decode assumes kPer products per lane");
@@ -328,11 +329,27 @@ __global__ __launch_bounds__(kBlock) void chunk_kernel(
 
 // ---- 4: units --------------------------------------------------------------------------
 
-// Units owned by segment s: 1 for a dense segment (more than kShort products) and for the
-// first nonempty small segment whose products start in a kShort window (the previous
-// nonempty segment is dense or starts in an earlier window); 0 otherwise.
+// A segment is accumulated densely when it has more than kShort products, or more than
+// dense_min products and is a column bucket of a long row (dense_min is kShort when buckets
+// are wider than one kDenseCols window).  Dense accumulation costs a fixed LDS clear and
+// scan of the window plus one atomic per product; sorting costs several passes per product.
+__device__ __forceinline__ bool dense_segment(int64_t len, int64_t s,
+                                              const int *__restrict__ seg_row,
+                                              const int64_t *__restrict__ row_off,
+                                              int dense_min) {
+    if (len > kShort) return true;
+    if (len <= dense_min) return false;
+    const int r = seg_row[s];
+    return row_off[r + 1] - row_off[r] > kShort;
+}
+
+// Units owned by segment s: 1 for a dense segment and for the first nonempty sorted segment
+// whose products start in a kShort window (the previous nonempty segment is dense or starts
+// in an earlier window); 0 otherwise.
 __global__ void unit_count_kernel(const int64_t *__restrict__ seg_len,
                                   const int64_t *__restrict__ seg_off, int64_t n_seg,
+                                  const int *__restrict__ seg_row,
+                                  const int64_t *__restrict__ row_off, int dense_min,
                                   int64_t *__restrict__ seg_units) {
     for (int64_t s = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; s < n_seg;
          s += static_cast<int64_t>(gridDim.x) * blockDim.x) {
@@ -340,7 +357,7 @@ __global__ void unit_count_kernel(const int64_t *__restrict__ seg_len,
         int64_t u;
         if (len == 0) {
             u = 0;
-        } else if (len > kShort || start == 0) {
+        } else if (start == 0 || dense_segment(len, s, seg_row, row_off, dense_min)) {
             u = 1;
         } else {
             // previous nonempty segment: last x < s with seg_off[x] < start
@@ -354,16 +371,25 @@ __global__ void unit_count_kernel(const int64_t *__restrict__ seg_len,
                 }
             }
             const int64_t ps = seg_off[lo];
-            u = (start - ps > kShort || ps / kShort != start / kShort) ? 1 : 0;
+            u = (dense_segment(start - ps, lo, seg_row, row_off, dense_min) ||
+                 ps / kShort != start / kShort)
+                    ? 1
+                    : 0;
         }
         seg_units[s] = u;
     }
 }
 
+// Unit table: first segment and product offset of each unit, and whether it is dense.
 __global__ void unit_map_kernel(const int64_t *__restrict__ seg_units,
                                 const int64_t *__restrict__ unit_prefix,
-                                const int64_t *__restrict__ seg_off, int64_t n_seg, int64_t P,
-                                int *__restrict__ unit_seg, int64_t *__restrict__ unit_start) {
+                                const int64_t *__restrict__ seg_off,
+                                const int64_t *__restrict__ seg_len,
+                                const int *__restrict__ seg_row,
+                                const int64_t *__restrict__ row_off, int dense_min,
+                                int64_t n_seg, int64_t P, int *__restrict__ unit_seg,
+                                int64_t *__restrict__ unit_start,
+                                int64_t *__restrict__ unit_dense) {
     for (int64_t s = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; s <= n_seg;
          s += static_cast<int64_t>(gridDim.x) * blockDim.x) {
         if (s == n_seg) {
@@ -372,6 +398,23 @@ __global__ void unit_map_kernel(const int64_t *__restrict__ seg_units,
             const int64_t u = unit_prefix[s];
             unit_seg[u] = static_cast<int>(s);
             unit_start[u] = seg_off[s];
+            unit_dense[u] = dense_segment(seg_len[s], s, seg_row, row_off, dense_min) ? 1 : 0;
+        }
+    }
+}
+
+// The two work lists, in unit order: dense units at their rank among dense units, sort
+// units at theirs (dense_rank = exclusive scan of the dense flags).
+__global__ void unit_lists_kernel(const int64_t *__restrict__ unit_dense,
+                                  const int64_t *__restrict__ dense_rank, int64_t n_units,
+                                  int *__restrict__ dense_list, int *__restrict__ sort_list) {
+    for (int64_t u = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; u < n_units;
+         u += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t r = dense_rank[u];
+        if (unit_dense[u]) {
+            dense_list[r] = static_cast<int>(u);
+        } else {
+            sort_list[u - r] = static_cast<int>(u);
         }
     }
 }
@@ -512,13 +555,14 @@ __device__ __forceinline__ double block_segmented_carry(bool f, double s, double
     return fe ? se : cs + se;
 }
 
-// One workgroup per unit; dense units return at once.  Sorts the unit's products by
+// One workgroup per sort unit (from the sort list).  Sorts the unit's products by
 // (segment ordinal, k), sums each run in float64, writes the distinct entries at the unit's
 // start in ukey/uval, the unit's count, and (row_unit, row_local) for rows starting here.
 // K is uint32_t when kOrdBits + col_shift <= 32, else uint64_t (col_shift = 32).
 template <typename K>
 __global__ __launch_bounds__(kBlock) void sort_unit_kernel(
-    const int *__restrict__ unit_seg, const int64_t *__restrict__ unit_start, int64_t n_units,
+    const int *__restrict__ sort_list, const int *__restrict__ unit_seg,
+    const int64_t *__restrict__ unit_start, int64_t n_units,
     int64_t n_seg, const int64_t *__restrict__ seg_len, const int64_t *__restrict__ seg_off,
     const int *__restrict__ seg_row, const int64_t *__restrict__ row_off, int col_shift,
     const int *__restrict__ key, const float *__restrict__ val, int *__restrict__ ukey,
@@ -530,9 +574,8 @@ __global__ __launch_bounds__(kBlock) void sort_unit_kernel(
     __shared__ int s_wave[kBlock / dev::kWave];
     __shared__ double s_sum[kBlock / dev::kWave];
     __shared__ int s_flag[kBlock / dev::kWave];
-    const int64_t u = blockIdx.x;
+    const int64_t u = sort_list[blockIdx.x];
     const int s0 = unit_seg[u];
-    if (seg_len[s0] > kShort) return;
     const int64_t start = unit_start[u];
     const int n = static_cast<int>(unit_start[u + 1] - start);
     const int64_t s_end = u + 1 < n_units ? unit_seg[u + 1] : n_seg;
@@ -643,11 +686,12 @@ __global__ __launch_bounds__(kBlock) void sort_unit_kernel(
 
 // ---- 5b: dense units -------------------------------------------------------------------
 
-// One workgroup per unit; sort units return at once.  The segment's column range
+// One workgroup per dense unit (from the dense list).  The segment's column range
 // [bucket << shift, (bucket + 1) << shift) is accumulated kDenseCols columns at a time in an
 // LDS float64 array (plus a bitmap of touched columns), then compacted in column order.
 __global__ __launch_bounds__(kBlock) void dense_unit_kernel(
-    const int *__restrict__ unit_seg, const int64_t *__restrict__ unit_start,
+    const int *__restrict__ dense_list, const int *__restrict__ unit_seg,
+    const int64_t *__restrict__ unit_start,
     const int64_t *__restrict__ seg_len, const int64_t *__restrict__ seg_prefix,
     const int *__restrict__ seg_row, const int64_t *__restrict__ row_off, int shift, int cols,
     const int *__restrict__ key, const float *__restrict__ val, int *__restrict__ ukey,
@@ -657,10 +701,9 @@ __global__ __launch_bounds__(kBlock) void dense_unit_kernel(
     __shared__ unsigned s_bits[kDenseCols / 32];
     __shared__ int s_wave[kBlock / dev::kWave];
     static_assert(kDenseCols / 32 == kBlock, "one bitmap word per lane");
-    const int64_t u = blockIdx.x;
+    const int64_t u = dense_list[blockIdx.x];
     const int s = unit_seg[u];
     const int64_t len = seg_len[s];
-    if (len <= kShort) return;
     const int64_t start = unit_start[u];
     const int row = seg_row[s];
     const int64_t bucket = s - seg_prefix[row];
@@ -775,6 +818,7 @@ int multiply(Call &call, const nacho_csr *a, const nacho_csr *b, Product *z) {
     // one radix digit over the columns: buckets of 2^shift columns, at most kMaxBuckets
     const int shift = std::max(std::min(kDenseBits, cb), cb - kMaxBucketBits);
     const int nb = cols > 0 ? ((cols - 1) >> shift) + 1 : 1;
+    const int dense_min = shift <= kDenseBits ? kDenseMin : kShort;
     const char *name = "spgemm: expand+scatter+reduce+copy";
     NACHO_TRY(call.timer_start(name));
 
@@ -844,8 +888,8 @@ int multiply(Call &call, const nacho_csr *a, const nacho_csr *b, Product *z) {
         int64_t *seg_units = seg_fill;  // the fill counters are spent
         int64_t *unit_prefix = nullptr;
         NACHO_TRY(call.scratch_n(static_cast<size_t>(n_seg) + 1, &unit_prefix));
-        unit_count_kernel<<<grid_for(n_seg, 256), 256, 0, st>>>(seg_len, seg_off, n_seg,
-                                                               seg_units);
+        unit_count_kernel<<<grid_for(n_seg, 256), 256, 0, st>>>(
+            seg_len, seg_off, n_seg, seg_row, row_off, dense_min, seg_units);
         NACHO_TRY_HIP(hipGetLastError());
         NACHO_TRY(scan::exclusive_scan_i64(call, seg_units, n_seg, unit_prefix));
         NACHO_TRY(call.timer_stop());
@@ -857,26 +901,44 @@ int multiply(Call &call, const nacho_csr *a, const nacho_csr *b, Product *z) {
         NACHO_TRY(call.scratch_n(static_cast<size_t>(n_units) + 1, &unit_start));
         NACHO_TRY(call.scratch_n(static_cast<size_t>(n_units) + 1, &unit_nnz));
         NACHO_TRY(call.scratch_n(static_cast<size_t>(n_units) + 1, &unit_out));
+        int *lists = nullptr;  // dense list, then sort list
+        int64_t *unit_dense = nullptr, *dense_rank = nullptr;
+        NACHO_TRY(call.scratch_n(2 * static_cast<size_t>(n_units), &lists));
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(n_units) + 1, &unit_dense));
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(n_units) + 1, &dense_rank));
+        int *dense_list = lists, *sort_list = lists + n_units;
         unit_map_kernel<<<grid_for(n_seg + 1, 256), 256, 0, st>>>(
-            seg_units, unit_prefix, seg_off, n_seg, P, unit_seg, unit_start);
+            seg_units, unit_prefix, seg_off, seg_len, seg_row, row_off, dense_min, n_seg, P,
+            unit_seg, unit_start, unit_dense);
         NACHO_TRY_HIP(hipGetLastError());
+        NACHO_TRY(scan::exclusive_scan_i64(call, unit_dense, n_units, dense_rank));
+        unit_lists_kernel<<<grid_for(n_units, 256), 256, 0, st>>>(unit_dense, dense_rank, n_units,
+                                                                  dense_list, sort_list);
+        NACHO_TRY_HIP(hipGetLastError());
+        int64_t n_dense = 0;
+        NACHO_TRY(call.timer_stop());
+        NACHO_TRY(call.read_back(&n_dense, dense_rank + n_units, sizeof(n_dense)));
+        NACHO_TRY(call.timer_start(name));
+        const int n_kind[2] = {static_cast<int>(n_dense), static_cast<int>(n_units - n_dense)};
 
         // 5. reduce
         const unsigned ug = static_cast<unsigned>(n_units);
-        if (cb + kOrdBits <= 32) {
-            sort_unit_kernel<uint32_t><<<ug, kBlock, 0, st>>>(
-                unit_seg, unit_start, n_units, n_seg, seg_len, seg_off, seg_row, row_off, cb,
-                key, val, ukey, uval, unit_nnz, row_unit, row_local);
-        } else {
-            sort_unit_kernel<uint64_t><<<ug, kBlock, 0, st>>>(
-                unit_seg, unit_start, n_units, n_seg, seg_len, seg_off, seg_row, row_off, 32,
-                key, val, ukey, uval, unit_nnz, row_unit, row_local);
+        if (n_kind[1] > 0 && cb + kOrdBits <= 32) {
+            sort_unit_kernel<uint32_t><<<static_cast<unsigned>(n_kind[1]), kBlock, 0, st>>>(
+                sort_list, unit_seg, unit_start, n_units, n_seg, seg_len, seg_off, seg_row,
+                row_off, cb, key, val, ukey, uval, unit_nnz, row_unit, row_local);
+        } else if (n_kind[1] > 0) {
+            sort_unit_kernel<uint64_t><<<static_cast<unsigned>(n_kind[1]), kBlock, 0, st>>>(
+                sort_list, unit_seg, unit_start, n_units, n_seg, seg_len, seg_off, seg_row,
+                row_off, 32, key, val, ukey, uval, unit_nnz, row_unit, row_local);
         }
         NACHO_TRY_HIP(hipGetLastError());
-        dense_unit_kernel<<<ug, kBlock, 0, st>>>(unit_seg, unit_start, seg_len, seg_prefix,
-                                                 seg_row, row_off, shift, cols, key, val, ukey,
-                                                 uval, unit_nnz, row_unit, row_local);
-        NACHO_TRY_HIP(hipGetLastError());
+        if (n_kind[0] > 0) {
+            dense_unit_kernel<<<static_cast<unsigned>(n_kind[0]), kBlock, 0, st>>>(
+                dense_list, unit_seg, unit_start, seg_len, seg_prefix, seg_row, row_off, shift,
+                cols, key, val, ukey, uval, unit_nnz, row_unit, row_local);
+            NACHO_TRY_HIP(hipGetLastError());
+        }
         NACHO_TRY(scan::exclusive_scan_i64(call, unit_nnz, n_units, unit_out));
 
         int64_t nnz = 0;
