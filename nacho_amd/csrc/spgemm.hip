@@ -280,15 +280,24 @@ __global__ __launch_bounds__(kBlock) void chunk_kernel(
         kk[u] = crd_b[bpos[u]];
         if (SCATTER) vv[u] *= val_b[bpos[u]];
     }
+    // Neighbouring lanes hold neighbouring products, mostly of one B row with ascending
+    // columns, so equal bins come in runs: one LDS atomic per run reserves its ranks.
+    const int l = dev::lane();
+    const unsigned long long upto = l == dev::kWave - 1 ? ~0ull : (2ull << l) - 1ull;
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
         const int x = static_cast<int>(threadIdx.x) + u * kBlock;
-        rank[u] = 0;
         if (x >= n) where[u] = -2;  // past the chunk: nothing to count or write
-        if (where[u] >= 0) {
-            where[u] = where[u] * nb + (kk[u] >> shift);
-            rank[u] = atomicAdd(&s_hist[where[u]], 1);
-        }
+        if (where[u] >= 0) where[u] = where[u] * nb + (kk[u] >> shift);
+        const int bin = where[u];
+        const int prev = __shfl_up(bin, 1, dev::kWave);
+        const unsigned long long bounds = __ballot(l == 0 || prev != bin);
+        const int leader = 63 - __clzll(bounds & upto);
+        const unsigned long long above = bounds & ~upto;
+        const int next = above ? __ffsll(above) - 1 : dev::kWave;
+        int got = 0;
+        if (bin >= 0 && l == leader) got = atomicAdd(&s_hist[bin], next - l);
+        rank[u] = __shfl(got, leader, dev::kWave) + (l - leader);
     }
     __syncthreads();
     if (!SCATTER) {
