@@ -59,6 +59,9 @@ constexpr int kMaxBucketBits = 10;      // at most 1024 column buckets per long 
 constexpr int kMaxBuckets = 1 << kMaxBucketBits;
 constexpr int kMaxLongPerChunk = 3;     // rows longer than kShort meeting one chunk
 constexpr int kDenseMin = kShort;       // a long row's bucket above this is accumulated densely
+constexpr int kMaxBitmapSegs = 256;     // segments (empty ones included) of a bitmap unit
+constexpr int kMaxBitmapBuckets = 16;   // nonempty buckets of a bitmap unit (larger buckets)
+constexpr int kBitmapWords = 8192 / 32; // one bit per column of an 8192-column bucket
 
 static_assert(kTile == 1 << kOrdBits, "segment ordinals must fit kOrdBits");
 static_assert(kChunk == kBlock * kPer, "chunk decode assumes kPer products per lane");
@@ -412,18 +415,49 @@ __global__ void unit_map_kernel(const int64_t *__restrict__ seg_units,
     }
 }
 
-// The two work lists, in unit order: dense units at their rank among dense units, sort
-// units at theirs (dense_rank = exclusive scan of the dense flags).
-__global__ void unit_lists_kernel(const int64_t *__restrict__ unit_dense,
-                                  const int64_t *__restrict__ dense_rank, int64_t n_units,
-                                  int *__restrict__ dense_list, int *__restrict__ sort_list) {
+// A unit that is not dense is a bitmap unit when its buckets span at most 8192 columns and
+// every one of its (at most kMaxBitmapSegs) segments is a column bucket of a long row: each
+// bucket's distinct columns then fit one 8192-bit LDS bitmap.  A bitmap bucket has a fixed
+// cost (clearing and scanning its bitmap), so units of many small buckets are sorted
+// instead: at most kMaxBitmapBuckets nonempty buckets.
+__global__ void unit_bitmap_kernel(const int *__restrict__ unit_seg,
+                                   const int64_t *__restrict__ unit_dense, int64_t n_units,
+                                   int64_t n_seg, const int64_t *__restrict__ seg_len,
+                                   const int *__restrict__ seg_row,
+                                   const int64_t *__restrict__ row_off, bool narrow_buckets,
+                                   int64_t *__restrict__ unit_bitmap) {
     for (int64_t u = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; u < n_units;
          u += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        const int64_t r = dense_rank[u];
+        const int64_t s0 = unit_seg[u];
+        const int64_t s1 = u + 1 < n_units ? unit_seg[u + 1] : n_seg;
+        bool ok = narrow_buckets && !unit_dense[u] && s1 - s0 <= kMaxBitmapSegs;
+        int buckets = 0;
+        for (int64_t s = s0; ok && s < s1; ++s) {
+            if (seg_len[s] == 0) continue;
+            const int r = seg_row[s];
+            ok = row_off[r + 1] - row_off[r] > kShort && ++buckets <= kMaxBitmapBuckets;
+        }
+        unit_bitmap[u] = ok ? 1 : 0;
+    }
+}
+
+// The three work lists, in unit order: each unit at its rank among units of its kind
+// (dense_rank and bitmap_rank are exclusive scans of the kind flags).
+__global__ void unit_lists_kernel(const int64_t *__restrict__ unit_dense,
+                                  const int64_t *__restrict__ dense_rank,
+                                  const int64_t *__restrict__ unit_bitmap,
+                                  const int64_t *__restrict__ bitmap_rank, int64_t n_units,
+                                  int *__restrict__ dense_list, int *__restrict__ bitmap_list,
+                                  int *__restrict__ sort_list) {
+    for (int64_t u = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; u < n_units;
+         u += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t rd = dense_rank[u], rb = bitmap_rank[u];
         if (unit_dense[u]) {
-            dense_list[r] = static_cast<int>(u);
+            dense_list[rd] = static_cast<int>(u);
+        } else if (unit_bitmap[u]) {
+            bitmap_list[rb] = static_cast<int>(u);
         } else {
-            sort_list[u - r] = static_cast<int>(u);
+            sort_list[u - rd - rb] = static_cast<int>(u);
         }
     }
 }
@@ -693,7 +727,156 @@ __global__ __launch_bounds__(kBlock) void sort_unit_kernel(
     if (threadIdx.x == 0) unit_nnz[u] = runs;
 }
 
-// ---- 5b: dense units -------------------------------------------------------------------
+// ---- 5b: bitmap units ------------------------------------------------------------------
+
+// Orders one wavefront's LDS accesses across its lanes.  The LDS processes a wavefront's
+// instructions in order, so only the compiler must not move accesses across this point; a
+// workgroup-scope fence would also wait for the wavefront's outstanding global stores.
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+
+// Marks the columns of a bucket (window offsets s_col[x0, x1)) in bm.
+__device__ __forceinline__ void mark_bucket(unsigned *bm, const unsigned short *s_col, int x0,
+                                            int x1) {
+    const int l = dev::lane();
+#pragma unroll
+    for (int i = 0; i < kBitmapWords / dev::kWave; ++i) bm[l + i * dev::kWave] = 0u;
+    wave_sync();
+    for (int x = x0 + l; x < x1; x += dev::kWave) {
+        const int c = s_col[x];
+        atomicOr(&bm[c >> 5], 1u << (c & 31));
+    }
+    wave_sync();
+}
+
+// One workgroup per bitmap unit; one wavefront per bucket at a time.  A bucket's distinct
+// columns are the set bits of its 8192-bit window bitmap; the rank of a column (prefix
+// popcount) indexes its float64 accumulator, and reading the bits in order emits the
+// distinct columns sorted.  Pass A counts each bucket's distinct columns (for the output
+// offsets inside the unit); pass B accumulates and writes.  Accumulators of a bucket live
+// in its own product range of the unit.
+__global__ __launch_bounds__(kBlock) void bitmap_unit_kernel(
+    const int *__restrict__ bitmap_list, const int *__restrict__ unit_seg,
+    const int64_t *__restrict__ unit_start, int64_t n_units, int64_t n_seg,
+    const int64_t *__restrict__ seg_len, const int64_t *__restrict__ seg_off,
+    const int64_t *__restrict__ seg_prefix, const int *__restrict__ seg_row,
+    const int64_t *__restrict__ row_off, int shift, const int *__restrict__ key,
+    const float *__restrict__ val, int *__restrict__ ukey, float *__restrict__ uval,
+    int64_t *__restrict__ unit_nnz, int *__restrict__ row_unit, int *__restrict__ row_local) {
+    constexpr int kWaves = kBlock / dev::kWave;
+    __shared__ double s_acc[kTile];
+    __shared__ float s_val[kTile];
+    __shared__ unsigned short s_col[kTile];  // column offset inside its bucket's window
+    __shared__ unsigned s_bits[kWaves][kBitmapWords];
+    __shared__ int s_pre[kWaves][kBitmapWords];
+    __shared__ int s_x0[kMaxBitmapSegs + 1];
+    __shared__ int s_base[kMaxBitmapSegs];
+    __shared__ int s_sid[kMaxBitmapSegs];
+    __shared__ int s_out[kMaxBitmapSegs];
+    __shared__ int s_wave[kWaves];
+    const int64_t u = bitmap_list[blockIdx.x];
+    const int64_t s0 = unit_seg[u];
+    const int64_t s1 = u + 1 < n_units ? unit_seg[u + 1] : n_seg;
+    const int64_t start = unit_start[u];
+    const int n = static_cast<int>(unit_start[u + 1] - start);
+    // the unit's nonempty buckets in order (at most kMaxBitmapSegs segments: one per lane)
+    const int64_t s = s0 + threadIdx.x;
+    const bool here = s < s1 && seg_len[s] > 0;
+    int n_buckets = 0;
+    const int ord = dev::block_exclusive_sum<kBlock>(here ? 1 : 0, s_wave, n_buckets);
+    if (here) {
+        s_x0[ord] = static_cast<int>(seg_off[s] - start);
+        s_base[ord] = static_cast<int>((s - seg_prefix[seg_row[s]]) << shift);
+        s_sid[ord] = static_cast<int>(s);
+    }
+    if (threadIdx.x == 0) s_x0[n_buckets] = n;
+    // the unit's products, staged once (bucket = column >> shift, so the window offset is
+    // the column's low bits)
+    const int low = (1 << shift) - 1;
+    for (int q = threadIdx.x; q < n; q += kBlock) {
+        s_col[q] = static_cast<unsigned short>(key[start + q] & low);
+        s_val[q] = val[start + q];
+    }
+    __syncthreads();
+    const int w = threadIdx.x / dev::kWave, l = dev::lane();
+    unsigned *bm = s_bits[w];
+    int *pre = s_pre[w];
+    // pass A: distinct columns per bucket
+    for (int o = w; o < n_buckets; o += kWaves) {
+        mark_bucket(bm, s_col, s_x0[o], s_x0[o + 1]);
+        int c = 0;
+#pragma unroll
+        for (int i = 0; i < kBitmapWords / dev::kWave; ++i) c += __popc(bm[l + i * dev::kWave]);
+        c = dev::wave_sum(c);
+        if (l == 0) s_out[o] = c;
+        wave_sync();
+    }
+    __syncthreads();
+    // output offset of each bucket inside the unit
+    int total = 0;
+    const int cnt = static_cast<int>(threadIdx.x) < n_buckets ? s_out[threadIdx.x] : 0;
+    const int off = dev::block_exclusive_sum<kBlock>(cnt, s_wave, total);
+    if (static_cast<int>(threadIdx.x) < n_buckets) s_out[threadIdx.x] = off;
+    __syncthreads();
+    // pass B: accumulate by rank, emit in column order
+    constexpr int kWordsPerLane = kBitmapWords / dev::kWave;
+    for (int o = w; o < n_buckets; o += kWaves) {
+        const int x0 = s_x0[o], x1 = s_x0[o + 1], base = s_base[o];
+        for (int x = x0 + l; x < x1; x += dev::kWave) s_acc[x] = 0.0;
+        mark_bucket(bm, s_col, x0, x1);
+        // exclusive popcount prefix per word; lane l owns words [l*4, l*4 + 4)
+        int pc[kWordsPerLane];
+        int mine = 0;
+#pragma unroll
+        for (int i = 0; i < kWordsPerLane; ++i) {
+            pc[i] = __popc(bm[l * kWordsPerLane + i]);
+            mine += pc[i];
+        }
+        int run = dev::wave_inclusive_sum(mine) - mine;
+#pragma unroll
+        for (int i = 0; i < kWordsPerLane; ++i) {
+            pre[l * kWordsPerLane + i] = run;
+            run += pc[i];
+        }
+        wave_sync();
+        for (int x = x0 + l; x < x1; x += dev::kWave) {
+            const int c = s_col[x];
+            const int wd = c >> 5;
+            const int r = pre[wd] + __popc(bm[wd] & ((1u << (c & 31)) - 1u));
+            atomicAdd(&s_acc[x0 + r], static_cast<double>(s_val[x]));
+        }
+        wave_sync();
+        const int64_t out = start + s_out[o];
+#pragma unroll
+        for (int i = 0; i < kWordsPerLane; ++i) {
+            const int wd = l * kWordsPerLane + i;
+            unsigned m = bm[wd];
+            int r = pre[wd];
+            while (m) {
+                const int bit = __ffs(m) - 1;
+                m &= m - 1u;
+                ukey[out + r] = base + wd * 32 + bit;
+                uval[out + r] = static_cast<float>(s_acc[x0 + r]);
+                ++r;
+            }
+        }
+        wave_sync();
+    }
+    // rows starting in this unit, and the unit's count
+    if (static_cast<int>(threadIdx.x) < n_buckets) {
+        const int sg = s_sid[threadIdx.x];
+        const int r = seg_row[sg];
+        if (row_off[r] == seg_off[sg]) {
+            row_unit[r] = static_cast<int>(u);
+            row_local[r] = s_out[threadIdx.x];
+        }
+    }
+    if (threadIdx.x == 0) unit_nnz[u] = total;
+}
+
+// ---- 5c: dense units -------------------------------------------------------------------
 
 // One workgroup per dense unit (from the dense list).  The segment's column range
 // [bucket << shift, (bucket + 1) << shift) is accumulated kDenseCols columns at a time in an
@@ -910,25 +1093,35 @@ int multiply(Call &call, const nacho_csr *a, const nacho_csr *b, Product *z) {
         NACHO_TRY(call.scratch_n(static_cast<size_t>(n_units) + 1, &unit_start));
         NACHO_TRY(call.scratch_n(static_cast<size_t>(n_units) + 1, &unit_nnz));
         NACHO_TRY(call.scratch_n(static_cast<size_t>(n_units) + 1, &unit_out));
-        int *lists = nullptr;  // dense list, then sort list
-        int64_t *unit_dense = nullptr, *dense_rank = nullptr;
-        NACHO_TRY(call.scratch_n(2 * static_cast<size_t>(n_units), &lists));
-        NACHO_TRY(call.scratch_n(static_cast<size_t>(n_units) + 1, &unit_dense));
-        NACHO_TRY(call.scratch_n(static_cast<size_t>(n_units) + 1, &dense_rank));
-        int *dense_list = lists, *sort_list = lists + n_units;
+        int *lists = nullptr;  // dense list, bitmap list, sort list
+        int64_t *kinds = nullptr;  // dense flags, their ranks, bitmap flags, their ranks
+        NACHO_TRY(call.scratch_n(3 * static_cast<size_t>(n_units), &lists));
+        NACHO_TRY(call.scratch_n(4 * (static_cast<size_t>(n_units) + 1), &kinds));
+        int64_t *unit_dense = kinds, *dense_rank = kinds + (n_units + 1);
+        int64_t *unit_bitmap = kinds + 2 * (n_units + 1), *bitmap_rank = kinds + 3 * (n_units + 1);
+        int *dense_list = lists, *bitmap_list = lists + n_units, *sort_list = lists + 2 * n_units;
         unit_map_kernel<<<grid_for(n_seg + 1, 256), 256, 0, st>>>(
             seg_units, unit_prefix, seg_off, seg_len, seg_row, row_off, dense_min, n_seg, P,
             unit_seg, unit_start, unit_dense);
         NACHO_TRY_HIP(hipGetLastError());
-        NACHO_TRY(scan::exclusive_scan_i64(call, unit_dense, n_units, dense_rank));
-        unit_lists_kernel<<<grid_for(n_units, 256), 256, 0, st>>>(unit_dense, dense_rank, n_units,
-                                                                  dense_list, sort_list);
+        unit_bitmap_kernel<<<grid_for(n_units, 256), 256, 0, st>>>(
+            unit_seg, unit_dense, n_units, n_seg, seg_len, seg_row, row_off, shift <= kDenseBits,
+            unit_bitmap);
         NACHO_TRY_HIP(hipGetLastError());
-        int64_t n_dense = 0;
+        NACHO_TRY(scan::exclusive_scan_i64(call, unit_dense, n_units, dense_rank));
+        NACHO_TRY(scan::exclusive_scan_i64(call, unit_bitmap, n_units, bitmap_rank));
+        unit_lists_kernel<<<grid_for(n_units, 256), 256, 0, st>>>(
+            unit_dense, dense_rank, unit_bitmap, bitmap_rank, n_units, dense_list, bitmap_list,
+            sort_list);
+        NACHO_TRY_HIP(hipGetLastError());
+        int64_t n_dense = 0, n_bitmap = 0;
         NACHO_TRY(call.timer_stop());
         NACHO_TRY(call.read_back(&n_dense, dense_rank + n_units, sizeof(n_dense)));
+        NACHO_TRY(call.read_back(&n_bitmap, bitmap_rank + n_units, sizeof(n_bitmap)));
         NACHO_TRY(call.timer_start(name));
-        const int n_kind[2] = {static_cast<int>(n_dense), static_cast<int>(n_units - n_dense)};
+        const int n_kind[3] = {static_cast<int>(n_dense),
+                               static_cast<int>(n_units - n_dense - n_bitmap),
+                               static_cast<int>(n_bitmap)};
 
         // 5. reduce
         const unsigned ug = static_cast<unsigned>(n_units);
@@ -942,6 +1135,12 @@ int multiply(Call &call, const nacho_csr *a, const nacho_csr *b, Product *z) {
                 row_off, 32, key, val, ukey, uval, unit_nnz, row_unit, row_local);
         }
         NACHO_TRY_HIP(hipGetLastError());
+        if (n_kind[2] > 0) {
+            bitmap_unit_kernel<<<static_cast<unsigned>(n_kind[2]), kBlock, 0, st>>>(
+                bitmap_list, unit_seg, unit_start, n_units, n_seg, seg_len, seg_off, seg_prefix,
+                seg_row, row_off, shift, key, val, ukey, uval, unit_nnz, row_unit, row_local);
+            NACHO_TRY_HIP(hipGetLastError());
+        }
         if (n_kind[0] > 0) {
             dense_unit_kernel<<<static_cast<unsigned>(n_kind[0]), kBlock, 0, st>>>(
                 dense_list, unit_seg, unit_start, seg_len, seg_prefix, seg_row, row_off, shift,
