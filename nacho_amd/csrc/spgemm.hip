@@ -158,26 +158,35 @@ struct ChunkHeader {
     int long_row[kMaxLongPerChunk];
 };
 
+// Per chunk of kChunk products: the A entries and rows of its first and last products
+// (searched here for all chunks at once rather than serially at each chunk's start).
+__global__ void chunk_bounds_kernel(const int64_t *__restrict__ off, int64_t nnz_a,
+                                    const int64_t *__restrict__ row_off, int rows, int64_t P,
+                                    int64_t chunks, int *__restrict__ bounds) {
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+         i < 2 * chunks; i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t c = i >> 1;
+        const int64_t q = (i & 1) ? min((c + 1) * kChunk, P) - 1 : c * kChunk;
+        bounds[4 * c + (i & 1)] = static_cast<int>(last_le(off, 0, nnz_a - 1, q));
+        bounds[4 * c + 2 + (i & 1)] = static_cast<int>(last_le(row_off, 0, rows - 1, q));
+    }
+}
+
 // Load-balanced search for the chunk [c0, c0 + n): s_e[x] = entry of product c0+x minus
 // p_lo, s_r[x] = its row minus r_lo (an inclusive max-scan of the entries' and rows' start
 // marks), and the long rows meeting the chunk.
-__device__ __forceinline__ void decode_chunk(const int64_t *__restrict__ off, int64_t nnz_a,
-                                             const int64_t *__restrict__ row_off, int rows,
-                                             int64_t c0, int n, int *s_e, int *s_r,
-                                             ChunkHeader *hdr, int64_t *s_bounds, int *s_wave) {
-    if (threadIdx.x == 0) {
-        s_bounds[0] = last_le(off, 0, nnz_a - 1, c0);
-        s_bounds[1] = last_le(off, 0, nnz_a - 1, c0 + n - 1);
-        s_bounds[2] = last_le(row_off, 0, rows - 1, c0);
-        s_bounds[3] = last_le(row_off, 0, rows - 1, c0 + n - 1);
-    }
+__device__ __forceinline__ void decode_chunk(const int64_t *__restrict__ off,
+                                             const int64_t *__restrict__ row_off,
+                                             const int *__restrict__ bounds, int64_t c0, int n,
+                                             int *s_e, int *s_r, ChunkHeader *hdr,
+                                             int *s_wave) {
+    // bounds (chunk_bounds_kernel): entries and rows of the chunk's first and last products
+    const int64_t p_lo = bounds[4 * blockIdx.x], p_hi = bounds[4 * blockIdx.x + 1];
+    const int r_lo = bounds[4 * blockIdx.x + 2], r_hi = bounds[4 * blockIdx.x + 3];
     for (int x = threadIdx.x; x < kChunk; x += kBlock) {
         s_e[pad(x)] = 0;
         s_r[pad(x)] = 0;
     }
-    __syncthreads();
-    const int64_t p_lo = s_bounds[0], p_hi = s_bounds[1];
-    const int r_lo = static_cast<int>(s_bounds[2]), r_hi = static_cast<int>(s_bounds[3]);
     if (threadIdx.x == 0) {
         hdr->p_lo = p_lo;
         hdr->r_lo = r_lo;
@@ -239,19 +248,18 @@ __global__ __launch_bounds__(kBlock) void chunk_kernel(
     const int64_t *__restrict__ off, const int64_t *__restrict__ row_off, int rows, int64_t P,
     const int *__restrict__ pos_b, const int *__restrict__ crd_b, const float *__restrict__ val_b,
     int shift, int nb, const int64_t *__restrict__ seg_prefix, int64_t *__restrict__ seg_len,
-    const int64_t *__restrict__ seg_off, int64_t *__restrict__ seg_fill, int *__restrict__ key,
-    float *__restrict__ val) {
+    const int64_t *__restrict__ seg_off, int64_t *__restrict__ seg_fill,
+    const int *__restrict__ bounds, int *__restrict__ key, float *__restrict__ val) {
     // entry and row maps of the decode; reused for the reserved bases of the scatter
     __shared__ int64_t s_dec[kPadded];
     int *s_e = reinterpret_cast<int *>(s_dec);
     int *s_r = s_e + kPadded;
     __shared__ int s_hist[kMaxLongPerChunk * kMaxBuckets];
-    __shared__ int64_t s_bounds[4];
     __shared__ int s_wave[kBlock / dev::kWave];
     __shared__ ChunkHeader hdr;
     const int64_t c0 = blockIdx.x * static_cast<int64_t>(kChunk);
     const int n = static_cast<int>(min(static_cast<int64_t>(kChunk), P - c0));
-    decode_chunk(off, nnz_a, row_off, rows, c0, n, s_e, s_r, &hdr, s_bounds, s_wave);
+    decode_chunk(off, row_off, bounds, c0, n, s_e, s_r, &hdr, s_wave);
     const ChunkHeader h = hdr;
     if (!SCATTER && h.n_long == 0) return;  // uniform across the workgroup
     for (int i = threadIdx.x; i < h.n_long * nb; i += kBlock) s_hist[i] = 0;
@@ -1064,16 +1072,21 @@ int multiply(Call &call, const nacho_csr *a, const nacho_csr *b, Product *z) {
         NACHO_TRY(call.scratch_n(static_cast<size_t>(P), &ukey));
         NACHO_TRY(call.scratch_n(static_cast<size_t>(P), &uval));
         const unsigned chunks = static_cast<unsigned>((P + kChunk - 1) / kChunk);
+        int *bounds = nullptr;
+        NACHO_TRY(call.scratch_n(4 * static_cast<size_t>(chunks), &bounds));
+        chunk_bounds_kernel<<<grid_for(2 * static_cast<int64_t>(chunks), 256), 256, 0, st>>>(
+            off, nnz_a, row_off, rows, P, chunks, bounds);
+        NACHO_TRY_HIP(hipGetLastError());
         chunk_kernel<false><<<chunks, kBlock, 0, st>>>(
             a->dim_j_indices, a->values, nnz_a, off, row_off, rows, P, b->dim_j_offsets,
-            b->dim_j_indices, b->values, shift, nb, seg_prefix, seg_len, seg_off, seg_fill, key,
-            val);
+            b->dim_j_indices, b->values, shift, nb, seg_prefix, seg_len, seg_off, seg_fill,
+            bounds, key, val);
         NACHO_TRY_HIP(hipGetLastError());
         NACHO_TRY(scan::exclusive_scan_i64(call, seg_len, n_seg, seg_off));
         chunk_kernel<true><<<chunks, kBlock, 0, st>>>(
             a->dim_j_indices, a->values, nnz_a, off, row_off, rows, P, b->dim_j_offsets,
-            b->dim_j_indices, b->values, shift, nb, seg_prefix, seg_len, seg_off, seg_fill, key,
-            val);
+            b->dim_j_indices, b->values, shift, nb, seg_prefix, seg_len, seg_off, seg_fill,
+            bounds, key, val);
         NACHO_TRY_HIP(hipGetLastError());
 
         // 4. units
