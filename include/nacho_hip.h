@@ -105,6 +105,22 @@ typedef struct nacho_coo3 {
     int32_t nnz;
 } nacho_coo3;
 
+/* DCSR, format {i, j: Compressed_unique} named "DCSR" (compiler.cpp:39-42): rows are
+ * compressed too, so only rows with entries are stored (nacho.to_dcsr drops empty rows,
+ * python/nacho/convert.py:34-53).  The outermost compressed level has no offsets
+ * (tensor.cpp:36-39). */
+typedef struct nacho_dcsr {
+    int32_t dim_i_size;
+    int32_t dim_j_size;
+    int32_t dim_i_length;   /* stored rows                 */
+    int32_t *dim_i_indices; /* dim_i_length row ids        */
+    int32_t *dim_j_offsets; /* dim_i_length + 1 entries    */
+    int32_t dim_j_length;
+    int32_t *dim_j_indices; /* dim_j_length entries        */
+    float *values;          /* dim_j_length entries        */
+    int32_t nnz;
+} nacho_dcsr;
+
 /* CSF3, format {i, j, k: Compressed_unique} named "CSF3" (compiler.cpp:44-48).  The
  * outermost compressed level has no offsets (tensor.cpp:36-39). */
 typedef struct nacho_csf3 {
@@ -186,6 +202,27 @@ int nacho_gpu_coo3d_add_f32(const nacho_coo3 *a, const nacho_coo3 *b, nacho_coo3
 int nacho_gpu_csf_add_f32(const nacho_csf3 *a, const nacho_csf3 *b, nacho_csf3 *z,
                           int32_t num_blocks, int32_t threads_per_block, void *stream,
                           const nacho_allocator *alloc);
+
+/* Z = a + b over DCSR (union of row ids, then of each row's columns).  Replaces
+ * dcsr_add::dcsr_add_gpu_i32_f32 (compiler.cpp:124). */
+int nacho_gpu_dcsr_add_f32(const nacho_dcsr *a, const nacho_dcsr *b, nacho_dcsr *z,
+                           int32_t num_blocks, int32_t threads_per_block, void *stream,
+                           const nacho_allocator *alloc);
+
+/* Z = a * b elementwise over DCSR.  The result's rows are the row ids stored in both
+ * operands, each with the intersection of its columns (possibly empty: the generated code
+ * emits the row at its i lattice point whatever the inner level yields, compute.cpp:945-990).
+ * Replaces dcsr_mul::dcsr_mul_gpu_i32_f32 (compiler.cpp:126). */
+int nacho_gpu_dcsr_mul_f32(const nacho_dcsr *a, const nacho_dcsr *b, nacho_dcsr *z,
+                           int32_t num_blocks, int32_t threads_per_block, void *stream,
+                           const nacho_allocator *alloc);
+
+/* The same product as nacho_gpu_dcsr_mul_f32.  Replaces
+ * dcsr_mul_without_recursive_partitioning (compiler.cpp:128-133), which differs from
+ * dcsr_mul only in how the reference partitions work; the result is identical. */
+int nacho_gpu_dcsr_mul_without_recursive_partitioning_f32(
+    const nacho_dcsr *a, const nacho_dcsr *b, nacho_dcsr *z, int32_t num_blocks,
+    int32_t threads_per_block, void *stream, const nacho_allocator *alloc);
 
 /* Z_ik = sum_j a_ij * b_jk over CSR operands (ESC SpGEMM), int32 result.  Replaces
  * spgemm::spgemm_gpu_i32_f32 (compiler.cpp:145-148).  Fails with NACHO_ERR_INDEX_OVERFLOW

@@ -6,7 +6,7 @@ entry point runs hand-written HIP kernels from libnacho_hip.so through its C ABI
 (include/nacho_hip.h); nothing here computes on the CPU.
 """
 
-from .convert import to_coo, to_coo3, to_csf3, to_csr  # noqa: F401
+from .convert import to_coo, to_coo3, to_csf3, to_csr, to_dcsr  # noqa: F401
 from .ops import (  # noqa: F401
     gpu_coo3d_add_f32,
     gpu_coo_add_f32,
@@ -14,12 +14,15 @@ from .ops import (  # noqa: F401
     gpu_csf_add_f32,
     gpu_csr_add_f32,
     gpu_csr_mul_f32,
+    gpu_dcsr_add_f32,
+    gpu_dcsr_mul_f32,
+    gpu_dcsr_mul_without_recursive_partitioning_f32,
     gpu_spgemm64_f32,
     gpu_spgemm_f32,
     last_kernel_ms,
     release_cached_memory,
     set_kernel_timing,
 )
-from .tensors import COO3_gpu, COO_gpu, CSF3_gpu, CSR64_gpu, CSR_gpu  # noqa: F401
+from .tensors import COO3_gpu, COO_gpu, CSF3_gpu, CSR64_gpu, CSR_gpu, DCSR_gpu  # noqa: F401
 
 __version__ = "0.1.0"

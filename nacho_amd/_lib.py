@@ -69,6 +69,20 @@ class Coo3Desc(ctypes.Structure):
     ]
 
 
+class DcsrDesc(ctypes.Structure):
+    _fields_ = [
+        ("dim_i_size", ctypes.c_int32),
+        ("dim_j_size", ctypes.c_int32),
+        ("dim_i_length", ctypes.c_int32),
+        ("dim_i_indices", ctypes.c_void_p),
+        ("dim_j_offsets", ctypes.c_void_p),
+        ("dim_j_length", ctypes.c_int32),
+        ("dim_j_indices", ctypes.c_void_p),
+        ("values", ctypes.c_void_p),
+        ("nnz", ctypes.c_int32),
+    ]
+
+
 class Csf3Desc(ctypes.Structure):
     _fields_ = [
         ("dim_i_size", ctypes.c_int32),
@@ -103,6 +117,9 @@ ENTRY_POINTS = {
     "nacho_gpu_coo_add_f32": (CooDesc, CooDesc),
     "nacho_gpu_coo_mul_f32": (CooDesc, CooDesc),
     "nacho_gpu_coo3d_add_f32": (Coo3Desc, Coo3Desc),
+    "nacho_gpu_dcsr_add_f32": (DcsrDesc, DcsrDesc),
+    "nacho_gpu_dcsr_mul_f32": (DcsrDesc, DcsrDesc),
+    "nacho_gpu_dcsr_mul_without_recursive_partitioning_f32": (DcsrDesc, DcsrDesc),
     "nacho_gpu_csf_add_f32": (Csf3Desc, Csf3Desc),
     "nacho_gpu_spgemm_f32": (CsrDesc, CsrDesc),
     "nacho_gpu_spgemm64_f32": (CsrDesc, Csr64Desc),

@@ -11,9 +11,9 @@ from __future__ import annotations
 import numpy as np
 import torch
 
-from .tensors import COO3_gpu, COO_gpu, CSF3_gpu, CSR_gpu
+from .tensors import COO3_gpu, COO_gpu, CSF3_gpu, CSR_gpu, DCSR_gpu
 
-__all__ = ["to_csr", "to_coo", "to_coo3", "to_csf3"]
+__all__ = ["to_csr", "to_dcsr", "to_coo", "to_coo3", "to_csf3"]
 
 
 def _gpu(device) -> torch.device:
@@ -32,6 +32,24 @@ def to_csr(csr: torch.Tensor, device="cuda") -> CSR_gpu:
     device = _gpu(device)
     return CSR_gpu(
         csr.crow_indices().to(dtype=torch.int32, device=device).contiguous(),
+        csr.col_indices().to(dtype=torch.int32, device=device).contiguous(),
+        csr.values().to(dtype=torch.float32, device=device).contiguous(),
+        _shape(csr.shape[0], csr.shape[1]),
+    )
+
+
+def to_dcsr(csr: torch.Tensor, device="cuda") -> DCSR_gpu:
+    """torch sparse CSR -> DCSR_gpu: the row dimension is compressed too, so empty rows are
+    dropped and the remaining row ids stored (python/nacho/convert.py:34-53)."""
+    device = _gpu(device)
+    indptr = csr.crow_indices().to(dtype=torch.int64, device="cpu")
+    lengths = indptr[1:] - indptr[:-1]
+    present = (lengths > 0).nonzero(as_tuple=False).squeeze(-1)
+    offsets = torch.zeros(present.numel() + 1, dtype=torch.int64)
+    offsets[1:] = lengths[present].cumsum(0)
+    return DCSR_gpu(
+        present.to(dtype=torch.int32, device=device).contiguous(),
+        offsets.to(dtype=torch.int32, device=device).contiguous(),
         csr.col_indices().to(dtype=torch.int32, device=device).contiguous(),
         csr.values().to(dtype=torch.float32, device=device).contiguous(),
         _shape(csr.shape[0], csr.shape[1]),

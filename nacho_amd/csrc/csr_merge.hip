@@ -386,7 +386,8 @@ __global__ __launch_bounds__(kBlock) void csr_count_kernel(
 
 // Writes the result: crd/val (VALUES) or crd plus child pointers (CHILD: for output o,
 // child_a[o] = next_a[a] and child_b[o] = next_b[b] at the A/B positions a, b reached before
-// o, so [child[o], child[o+1]) is the operand's child range under o, empty when absent).
+// o, so [child[o], child[o+1]) is the operand's child range under o, empty when absent; a
+// null next_a / next_b makes the child pointer the position itself).
 template <Op OP, int IPT, bool VALUES, bool CHILD>
 __global__ __launch_bounds__(kBlock) void csr_write_kernel(
     const int *__restrict__ pa, const int *__restrict__ ca, const float *__restrict__ va,
@@ -445,8 +446,10 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
         if (CHILD) {
 #pragma unroll
             for (int s = 0; s < kSteps; ++s) {
-                ca_v[s] = next_a[sp.a0 + static_cast<int>(lo.pos[s] & 0xffffu)];
-                cb_v[s] = next_b[sp.b0 + static_cast<int>(lo.pos[s] >> 16)];
+                const int pa_s = sp.a0 + static_cast<int>(lo.pos[s] & 0xffffu);
+                const int pb_s = sp.b0 + static_cast<int>(lo.pos[s] >> 16);
+                ca_v[s] = next_a ? next_a[pa_s] : pa_s;
+                cb_v[s] = next_b ? next_b[pb_s] : pb_s;
             }
         }
         int o = offset, r = lo.first_row;
@@ -483,8 +486,8 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
         if (t == num_tiles - 1 && tid == 0) {
             *length = static_cast<unsigned>(base);
             if (CHILD) {
-                child_a[base] = next_a[nnz_a];
-                child_b[base] = next_b[nnz_b];
+                child_a[base] = next_a ? next_a[nnz_a] : nnz_a;
+                child_b[base] = next_b ? next_b[nnz_b] : nnz_b;
             }
         }
         __syncthreads();  // staged outputs consumed

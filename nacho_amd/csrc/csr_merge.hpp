@@ -10,7 +10,7 @@ namespace csr {
 
 // One operand level: `pos` has rows + 1 entries (pos[0] == 0) indexing `crd`/`val`
 // (`len` entries).  `next` (optional) is the offsets array of the level below, indexed by
-// this level's positions (len + 1 entries).
+// this level's positions (len + 1 entries); when null, child pointers are the positions.
 struct LevelOperand {
     const int *pos;
     const int *crd;

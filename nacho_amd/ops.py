@@ -15,7 +15,7 @@ import ctypes
 import torch
 
 from . import _device, _lib
-from .tensors import COO3_gpu, COO_gpu, CSF3_gpu, CSR64_gpu, CSR_gpu
+from .tensors import COO3_gpu, COO_gpu, CSF3_gpu, CSR64_gpu, CSR_gpu, DCSR_gpu
 
 _I32, _I64, _F32 = torch.int32, torch.int64, torch.float32
 
@@ -63,6 +63,18 @@ def _coo3_desc(t: COO3_gpu) -> _lib.Coo3Desc:
                          _p(t.dim_k_indices), _p(t.values), n)
 
 
+def _dcsr_desc(t: DCSR_gpu) -> _lib.DcsrDesc:
+    rows, cols = (int(x) for x in t.shape)
+    ni, nj = t.dim_i_indices.numel(), t.dim_j_indices.numel()
+    if t.dim_j_offsets.numel() != ni + 1:
+        raise ValueError(f"DCSR_gpu: dim_j_offsets has {t.dim_j_offsets.numel()} entries, "
+                         f"expected stored rows + 1 = {ni + 1}")
+    if t.values.numel() != nj:
+        raise ValueError("DCSR_gpu: dim_j_indices and values differ in length")
+    return _lib.DcsrDesc(rows, cols, ni, _p(t.dim_i_indices), _p(t.dim_j_offsets), nj,
+                         _p(t.dim_j_indices), _p(t.values), nj)
+
+
 def _csf3_desc(t: CSF3_gpu) -> _lib.Csf3Desc:
     si, sj, sk = (int(x) for x in t.shape)
     ni, nj, nk = t.dim_i_indices.numel(), t.dim_j_indices.numel(), t.dim_k_indices.numel()
@@ -108,6 +120,15 @@ def _adopt_coo3(z: _lib.Coo3Desc, device, stream) -> COO3_gpu:
                               _device.adopt(z.dim_k_indices, n, _I32, device, stream),
                               _device.adopt(z.values, n, _F32, device, stream)),
                              [z.dim_i_size, z.dim_j_size, z.dim_k_size], device)
+
+
+def _adopt_dcsr(z: _lib.DcsrDesc, device, stream) -> DCSR_gpu:
+    ni, nj = z.dim_i_length, z.dim_j_length
+    return DCSR_gpu._trusted((_device.adopt(z.dim_i_indices, ni, _I32, device, stream),
+                              _device.adopt(z.dim_j_offsets, ni + 1, _I32, device, stream),
+                              _device.adopt(z.dim_j_indices, nj, _I32, device, stream),
+                              _device.adopt(z.values, nj, _F32, device, stream)),
+                             [z.dim_i_size, z.dim_j_size], device)
 
 
 def _adopt_csf3(z: _lib.Csf3Desc, device, stream) -> CSF3_gpu:
@@ -176,6 +197,31 @@ def gpu_coo3d_add_f32(a: COO3_gpu, b: COO3_gpu, num_blocks: int = 256,
     """Z = a + b over COO3 (union of (i, j, k)).  compiler.cpp:138."""
     return _call("nacho_gpu_coo3d_add_f32", a, b, COO3_gpu, _coo3_desc, _lib.Coo3Desc,
                  _adopt_coo3, num_blocks, threads_per_block)
+
+
+def gpu_dcsr_add_f32(a: DCSR_gpu, b: DCSR_gpu, num_blocks: int = 256,
+                     threads_per_block: int = 256) -> DCSR_gpu:
+    """Z = a + b over DCSR (union of row ids, then of each row's columns).
+    compiler.cpp:124."""
+    return _call("nacho_gpu_dcsr_add_f32", a, b, DCSR_gpu, _dcsr_desc, _lib.DcsrDesc,
+                 _adopt_dcsr, num_blocks, threads_per_block)
+
+
+def gpu_dcsr_mul_f32(a: DCSR_gpu, b: DCSR_gpu, num_blocks: int = 256,
+                     threads_per_block: int = 256) -> DCSR_gpu:
+    """Z = a * b over DCSR: rows stored in both operands, each with the intersection of its
+    columns (kept when that is empty).  compiler.cpp:126."""
+    return _call("nacho_gpu_dcsr_mul_f32", a, b, DCSR_gpu, _dcsr_desc, _lib.DcsrDesc,
+                 _adopt_dcsr, num_blocks, threads_per_block)
+
+
+def gpu_dcsr_mul_without_recursive_partitioning_f32(
+        a: DCSR_gpu, b: DCSR_gpu, num_blocks: int = 256,
+        threads_per_block: int = 256) -> DCSR_gpu:
+    """The same product as gpu_dcsr_mul_f32 (the reference variant differs only in how it
+    partitions work).  compiler.cpp:128-133."""
+    return _call("nacho_gpu_dcsr_mul_without_recursive_partitioning_f32", a, b, DCSR_gpu,
+                 _dcsr_desc, _lib.DcsrDesc, _adopt_dcsr, num_blocks, threads_per_block)
 
 
 def gpu_csf_add_f32(a: CSF3_gpu, b: CSF3_gpu, num_blocks: int = 256,

@@ -8,6 +8,7 @@ those names, argument orders and field names for the GPU target:
     CSR_gpu(dim_j_offsets, dim_j_indices, values, shape)
     COO_gpu(dim_i_indices, dim_j_indices, values, shape)
     COO3_gpu(dim_i_indices, dim_j_indices, dim_k_indices, values, shape)
+    DCSR_gpu(dim_i_indices, dim_j_offsets, dim_j_indices, values, shape)
     CSF3_gpu(dim_i_indices, dim_j_offsets, dim_j_indices, dim_k_offsets, dim_k_indices,
              values, shape)
 
@@ -127,6 +128,15 @@ COO3_gpu = _make(
      ("values", _F32)],
     3,
     "COO order-3 tensor (reference class COO3_gpu).",
+)
+
+DCSR_gpu = _make(
+    "DCSR_gpu",
+    [("dim_i_indices", _I32), ("dim_j_offsets", _I32), ("dim_j_indices", _I32),
+     ("values", _F32)],
+    2,
+    "DCSR matrix {i, j: Compressed_unique}: only rows with entries are stored "
+    "(reference class DCSR_gpu).",
 )
 
 CSF3_gpu = _make(

@@ -28,6 +28,10 @@
  *     operands without empty fibres, which is what to_csf3 builds).  Serial restatement of
  *     the lattice; the reference's nested partitioning (partition.cpp:286-461) only splits
  *     this work among threads.
+ *   - dcsr_union / dcsr_intersect: the two-level lattice of dcsr_add / dcsr_mul
+ *     (compiler.cpp:124-133): i over A_i ∪ B_i (add) or A_i ∩ B_i (mul), j over the union /
+ *     intersection of the two fibres; a row id is emitted at every i lattice point, with its
+ *     fibre, even when a product fibre is empty.  Serial restatement of the lattice.
  *   - spgemm: the reference has no CPU SpGEMM (compiler.cpp:145-148 is GPU-only).  This is
  *     the ESC semantics of its GPU path (stitch_and_generate_gpu.cpp:14-138, 257-366) run
  *     row-parallel on the CPU: per row, expand a_ij * b_jk, sort by k, and sum runs.
@@ -631,6 +635,95 @@ int oracle_csf3_union(const int32_t *a_ci, int a_ni, const int32_t *a_pj, const 
     *o_ni = (int)o.ni;
     *o_nj = (int)o.nj;
     *o_nk = (int)o.nk;
+    return ORC_OK;
+}
+
+/* ---------------------------------------------------------------------------------- */
+/* DCSR union / intersection                                                             */
+
+/* Z = A (+|*) B over DCSR (i and j both compressed).  Follows the generated loop nest of
+ * dcsr_add / dcsr_mul (compiler.cpp:124-133): the i level co-iterates the two row-id lists
+ * (union for add; for mul only the ids present in both), and at every such i lattice point
+ * the j level merges the two fibres (union / intersection, compute.cpp:1169-1198), appends
+ * the fibre and counts the row id whether or not the fibre is empty (compute.cpp:945-990).
+ * Values: a + b or a copy (add), a * b (mul), one float32 operation each.  Inputs:
+ * (crd_i[ni], pos_j[ni+1], crd_j[nj], val[nj]) per operand.  Outputs are malloc'd. */
+int oracle_dcsr_binary(int intersect, const int32_t *a_ci, int a_ni, const int32_t *a_pj,
+                       const int32_t *a_cj, const float *a_v, const int32_t *b_ci, int b_ni,
+                       const int32_t *b_pj, const int32_t *b_cj, const float *b_v,
+                       int32_t **o_ci, int32_t **o_pj, int32_t **o_cj, float **o_v,
+                       int *o_ni, int *o_nj) {
+    const int a_nj = a_pj[a_ni], b_nj = b_pj[b_ni];
+    const size_t ci_cap = (size_t)a_ni + b_ni + 1, cj_cap = (size_t)a_nj + b_nj + 1;
+    int32_t *ci = (int32_t *)malloc(sizeof(int32_t) * ci_cap);
+    int32_t *pj = (int32_t *)malloc(sizeof(int32_t) * (ci_cap + 1));
+    int32_t *cj = (int32_t *)malloc(sizeof(int32_t) * cj_cap);
+    float *v = (float *)malloc(sizeof(float) * cj_cap);
+    if (!ci || !pj || !cj || !v) {
+        free(ci);
+        free(pj);
+        free(cj);
+        free(v);
+        return ORC_ENOMEM;
+    }
+    long ni = 0, nj = 0;
+    pj[0] = 0;
+    int ia = 0, ib = 0;
+    while (intersect ? (ia < a_ni && ib < b_ni) : (ia < a_ni || ib < b_ni)) {
+        int ha = ia < a_ni, hb = ib < b_ni;
+        int i;
+        if (ha && hb) {
+            i = a_ci[ia] < b_ci[ib] ? a_ci[ia] : b_ci[ib];
+            ha = a_ci[ia] == i;
+            hb = b_ci[ib] == i;
+        } else {
+            i = ha ? a_ci[ia] : b_ci[ib];
+        }
+        if (!intersect || (ha && hb)) {
+            int x = ha ? a_pj[ia] : 0, xe = ha ? a_pj[ia + 1] : 0;
+            int y = hb ? b_pj[ib] : 0, ye = hb ? b_pj[ib + 1] : 0;
+            while (x < xe && y < ye) {
+                if (a_cj[x] == b_cj[y]) {
+                    cj[nj] = a_cj[x];
+                    v[nj++] = intersect ? a_v[x] * b_v[y] : a_v[x] + b_v[y];
+                    ++x;
+                    ++y;
+                } else if (a_cj[x] < b_cj[y]) {
+                    if (!intersect) {
+                        cj[nj] = a_cj[x];
+                        v[nj++] = a_v[x];
+                    }
+                    ++x;
+                } else {
+                    if (!intersect) {
+                        cj[nj] = b_cj[y];
+                        v[nj++] = b_v[y];
+                    }
+                    ++y;
+                }
+            }
+            if (!intersect) {
+                for (; x < xe; ++x) {
+                    cj[nj] = a_cj[x];
+                    v[nj++] = a_v[x];
+                }
+                for (; y < ye; ++y) {
+                    cj[nj] = b_cj[y];
+                    v[nj++] = b_v[y];
+                }
+            }
+            ci[ni++] = i;
+            pj[ni] = (int32_t)nj;
+        }
+        ia += ha;
+        ib += hb;
+    }
+    *o_ci = ci;
+    *o_pj = pj;
+    *o_cj = cj;
+    *o_v = v;
+    *o_ni = (int)ni;
+    *o_nj = (int)nj;
     return ORC_OK;
 }
 

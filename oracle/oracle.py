@@ -13,7 +13,8 @@ only as the checker.  Two independent kinds of reference live here:
 Parity status of each function (how it is pinned) is recorded in the test modules and in
 the repository's design notes: csr/coo/coo3/csf union and intersection are pinned by the
 closed forms, by scipy, by brute force on tiny inputs and by the reference's own smoke
-cases (tests/smoke.py semantics); spgemm is pinned by a float64 scipy product.
+cases (tests/smoke.py semantics); dcsr union / intersection by the DCSR closed form over the
+expanded CSR matrices; spgemm is pinned by a float64 scipy product.
 """
 
 from __future__ import annotations
@@ -64,6 +65,11 @@ def load() -> ctypes.CDLL:
             [_i32p, ctypes.c_int, _i32p, _i32p, ctypes.c_int, _i32p, _i32p, _f32p, ctypes.c_int]
             * 2 + [ctypes.POINTER(_i32p)] * 5 + [ctypes.POINTER(_f32p)]
             + [ctypes.POINTER(ctypes.c_int)] * 3)
+        lib.oracle_dcsr_binary.restype = ctypes.c_int
+        lib.oracle_dcsr_binary.argtypes = (
+            [ctypes.c_int] + [_i32p, ctypes.c_int, _i32p, _i32p, _f32p] * 2
+            + [ctypes.POINTER(_i32p)] * 3 + [ctypes.POINTER(_f32p)]
+            + [ctypes.POINTER(ctypes.c_int)] * 2)
         lib.oracle_spgemm.restype = ctypes.c_int
         lib.oracle_spgemm.argtypes = [
             ctypes.c_int, ctypes.c_int, ctypes.c_int, _i32p, _i32p, _f32p, _i32p, _i32p, _f32p,
@@ -189,6 +195,36 @@ def port_csf3_union(a_levels, a_val, b_levels, b_val, timing=None):
     return levels, _take(oval, nk, np.float32)
 
 
+def port_dcsr_binary(op, a_levels, a_val, b_levels, b_val, timing=None):
+    """levels = (crd_i, pos_j, crd_j).  op = "add" | "mul".  Returns (levels, val).  If
+    `timing` is a dict, timing["seconds"] receives the duration of the C call alone."""
+    import time
+
+    lib = load()
+    ka = [_as(x, np.int32) for x in a_levels] + [_as(a_val, np.float32), len(a_levels[0])]
+    kb = [_as(x, np.int32) for x in b_levels] + [_as(b_val, np.float32), len(b_levels[0])]
+
+    def args(k):
+        ci, pj, cj, v, ni = k
+        return [_ptr(ci, ctypes.c_int32), ni, _ptr(pj, ctypes.c_int32),
+                _ptr(cj, ctypes.c_int32), _ptr(v, ctypes.c_float)]
+
+    outs = [_i32p() for _ in range(3)]
+    oval = _f32p()
+    ni, nj = ctypes.c_int(), ctypes.c_int()
+    t0 = time.perf_counter()
+    rc = lib.oracle_dcsr_binary(1 if op == "mul" else 0, *args(ka), *args(kb),
+                                *[ctypes.byref(o) for o in outs], ctypes.byref(oval),
+                                ctypes.byref(ni), ctypes.byref(nj))
+    if timing is not None:
+        timing["seconds"] = time.perf_counter() - t0
+    if rc != 0:
+        raise RuntimeError(f"oracle_dcsr_binary failed ({rc})")
+    levels = (_take(outs[0], ni.value, np.int32), _take(outs[1], ni.value + 1, np.int32),
+              _take(outs[2], nj.value, np.int32))
+    return levels, _take(oval, nj.value, np.float32)
+
+
 def port_spgemm(rows, inner, cols, pa, ca, va, pb, cb, vb, nthreads=0):
     """ESC semantics on the CPU: returns (pos int64, crd int32, val float32)."""
     lib = load()
@@ -273,6 +309,25 @@ def closed_coo_binary(op, shape, a_crd, va, b_crd, vb):
         crd.append((rest % (int(n) + 1)).astype(np.int32))
         rest //= (int(n) + 1)
     return tuple(reversed(crd)), val
+
+
+def closed_dcsr_binary(op, rows, cols, a_levels, a_val, b_levels, b_val):
+    """DCSR result from the mathematics: the stored row ids are the union (add) or the
+    intersection (mul) of the operands' row ids; each row's entries are the CSR union /
+    intersection of the expanded matrices (closed_csr_binary)."""
+    def expand(levels):
+        ci, pj, _ = (np.asarray(x, np.int64) for x in levels)
+        pos = np.zeros(int(rows) + 1, np.int64)
+        pos[ci + 1] = np.diff(pj)
+        return np.cumsum(pos)
+
+    pos, crd, val = closed_csr_binary(op, rows, cols, expand(a_levels), a_levels[2], a_val,
+                                      expand(b_levels), b_levels[2], b_val)
+    ra, rb = np.asarray(a_levels[0], np.int64), np.asarray(b_levels[0], np.int64)
+    ids = np.union1d(ra, rb) if op == "add" else np.intersect1d(ra, rb)
+    pos = np.asarray(pos, np.int64)
+    pj = np.append(pos[ids], pos[-1]) if len(ids) else np.array([pos[-1]], np.int64)
+    return (ids.astype(np.int32), pj.astype(np.int32), crd), val
 
 
 def closed_spgemm_f64(rows, inner, cols, pa, ca, va, pb, cb, vb):

@@ -99,3 +99,37 @@ def test_struct_layouts_match_the_header():
     assert _lib.CsrDesc.dim_j_indices.offset == 24
     assert ctypes.sizeof(_lib.CsrDesc) == 48
     assert ctypes.sizeof(_lib.Csr64Desc) == 48
+
+
+def test_every_descriptor_layout_matches_the_c_compiler(tmp_path):
+    """Field offsets and sizes of every ctypes descriptor equal what gcc computes from
+    include/nacho_hip.h."""
+    import shutil
+    import subprocess
+
+    from nacho_amd import _lib
+
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    pairs = {"nacho_csr": _lib.CsrDesc, "nacho_csr64": _lib.Csr64Desc,
+             "nacho_coo": _lib.CooDesc, "nacho_coo3": _lib.Coo3Desc,
+             "nacho_dcsr": _lib.DcsrDesc, "nacho_csf3": _lib.Csf3Desc}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "nacho_hip.h"',
+             "int main(void) {"]
+    for cname, desc in pairs.items():
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for field, _ in desc._fields_:
+            lines.append(f'printf("{cname} {field} %zu\\n", offsetof({cname}, {field}));')
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    include = Path(__file__).resolve().parent.parent / "include"
+    subprocess.run([gcc, f"-I{include}", str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout
+    for line in out.splitlines():
+        cname, field, value = line.split()
+        desc = pairs[cname]
+        got = ctypes.sizeof(desc) if field == "size" else getattr(desc, field).offset
+        assert got == int(value), f"{cname}.{field}: ctypes {got}, C {value}"
