@@ -1,6 +1,7 @@
 """Benchmark of the nacho GPU path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2|c3|c4|c5|c5coo|c2coo]
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+                    [--workload c2|c3|c4|c5|c5coo|c2coo|c2dcsr|c3dcsr]
 
 A step is one call of the hot path over one batch of synthetic input, with the operands
 already resident in HBM: `nacho_amd.gpu_csr_add_f32(A, B)` for the default workload (C2:
@@ -26,9 +27,9 @@ time, P = number of intermediate products; its roofline bytes are
 4*(n+1) + 8*nnzA + 8*P (B's gathered entries) + 8*(n+1) + 8*nnzC, and its CPU baseline is
 the row-parallel C SpGEMM of oracle/ on a random row sample.
 
-Workloads c5 (csf_add), c5coo (coo3d_add) and c2coo (coo_add) report GB/s of algorithmic
-bytes: CSF3 counts every level array of A, B and C once; COO3 16 bytes and COO 12 bytes per
-entry of A, B and C.
+Workloads c5 (csf_add), c5coo (coo3d_add), c2coo (coo_add), c2dcsr (dcsr_add) and c3dcsr
+(dcsr_mul) report GB/s of algorithmic bytes: CSF3 and DCSR count every level array of A, B
+and C once; COO3 16 bytes and COO 12 bytes per entry of A, B and C.
 """
 
 from __future__ import annotations
@@ -67,9 +68,16 @@ WORKLOADS = {
     "c2coo": dict(op="coo_add", kernel="coo_partition_kernel + coo_count_kernel + "
                                       "coo_write_kernel (packed 64-bit keys)",
                   desc="C2 as COO: coo_add f32 of the C2 operands' (i, j) tuples"),
-    "c4": dict(op="spgemm", kernel="expand_kernel + sort_tiles_kernel + level_merge_kernel + "
-                                 "compress_{count,write}_kernel (one call's device "
-                                 "pipeline, host planning gaps excluded)",
+    "c2dcsr": dict(op="dcsr_add", kernel="two chained level merges (csr_partition_kernel + "
+                                        "csr_count_kernel + csr_write_kernel per level)",
+                   desc="C2 as DCSR: dcsr_add f32 of the C2 operands with empty rows "
+                        "dropped"),
+    "c3dcsr": dict(op="dcsr_mul", kernel="two chained level merges + row compaction",
+                   desc="C3 as DCSR: dcsr_mul f32 of the C3 operands with empty rows "
+                        "dropped"),
+    "c4": dict(op="spgemm", kernel="chunk_kernel<histogram, scatter> + dense/bitmap/sort "
+                                 "unit kernels + copy_units_kernel and the sizing kernels "
+                                 "(one call's device pipeline, host readback gaps excluded)",
                desc="C4 ESC SpGEMM C=A*A f32, R-MAT 2^20 (a,b,c,d)=(.57,.19,.19,.05), "
                     "8*2^20 draws deduplicated, no vertex permutation, values U[0.5,1.5], "
                     "seed 1; int64 result offsets"),
@@ -281,9 +289,21 @@ def csf_bytes(levels_list):
     return total
 
 
+def dcsr_levels(pos, crd):
+    """DCSR levels (crd_i, pos_j, crd_j) of a CSR matrix: empty rows dropped."""
+    import numpy as np
+
+    lengths = np.diff(np.asarray(pos, np.int64))
+    present = np.flatnonzero(lengths > 0)
+    pj = np.zeros(len(present) + 1, np.int64)
+    pj[1:] = np.cumsum(lengths[present])
+    return present.astype(np.int32), pj.astype(np.int32), np.asarray(crd, np.int32)
+
+
 def bench_tuple_workload(args, device, workload):
-    """c5 (csf_add), c5coo (coo3d_add), c2coo (coo_add): element-wise union of coordinate
-    tuples; one step = one call with operands resident in HBM."""
+    """c5 (csf_add), c5coo (coo3d_add), c2coo (coo_add), c2dcsr / c3dcsr (dcsr_add /
+    dcsr_mul): element-wise merges of coordinate trees or tuples; one step = one call with
+    operands resident in HBM."""
     import numpy as np
     import torch
 
@@ -293,7 +313,11 @@ def bench_tuple_workload(args, device, workload):
 
     spec = WORKLOADS[workload]
     t0 = time.perf_counter()
-    if workload == "c2coo":
+    if workload in ("c2dcsr", "c3dcsr"):
+        ops = synth.c2_operands() if workload == "c2dcsr" else synth.c3_operands()
+        ops_np = [(dcsr_levels(p, c), v) for p, c, v in ops]
+        shape = (len(ops[0][0]) - 1, len(ops[0][0]) - 1)
+    elif workload == "c2coo":
         (pa, ca, va), (pb, cb, vb) = synth.c2_operands()
         rows = len(pa) - 1
         ia = np.repeat(np.arange(rows, dtype=np.int32), np.diff(pa))
@@ -311,6 +335,8 @@ def bench_tuple_workload(args, device, workload):
         t = [torch.from_numpy(np.ascontiguousarray(c, dtype=np.int32)).to(device) for c in crd]
         v = torch.from_numpy(np.ascontiguousarray(val, dtype=np.float32)).to(device)
         dims = torch.tensor(list(shape), dtype=torch.int32)
+        if workload in ("c2dcsr", "c3dcsr"):
+            return nacho_amd.DCSR_gpu(t[0], t[1], t[2], v, dims)
         if workload == "c2coo":
             return nacho_amd.COO_gpu(t[0], t[1], v, dims)
         if workload == "c5coo":
@@ -321,7 +347,8 @@ def bench_tuple_workload(args, device, workload):
 
     copies = [tuple(upload(*o) for o in ops_np) for _ in range(ROTATE)]
     fn = {"c2coo": nacho_amd.gpu_coo_add_f32, "c5coo": nacho_amd.gpu_coo3d_add_f32,
-          "c5": nacho_amd.gpu_csf_add_f32}[workload]
+          "c5": nacho_amd.gpu_csf_add_f32, "c2dcsr": nacho_amd.gpu_dcsr_add_f32,
+          "c3dcsr": nacho_amd.gpu_dcsr_mul_f32}[workload]
     z = fn(*copies[0])
     torch.cuda.synchronize()
     nnz = [len(ops_np[0][1]), len(ops_np[1][1]), int(z.values.numel())]
@@ -330,6 +357,11 @@ def bench_tuple_workload(args, device, workload):
               z.dim_k_offsets.numel(), z.dim_k_indices.numel()]
         alg_bytes = csf_bytes([csf3_levels(np.stack(o[0], axis=1)) for o in ops_np])
         alg_bytes += 4 * (sum(lz) + lz[4])
+    elif workload in ("c2dcsr", "c3dcsr"):
+        # crd_i, pos_j, crd_j and values of A, B and C
+        alg_bytes = sum(4 * (len(o[0][0]) + len(o[0][1]) + 2 * len(o[0][2])) for o in ops_np)
+        alg_bytes += 4 * (z.dim_i_indices.numel() + z.dim_j_offsets.numel()
+                          + 2 * z.dim_j_indices.numel())
     else:
         alg_bytes = (12 if workload == "c2coo" else 16) * sum(nnz)
     del z
@@ -365,7 +397,11 @@ def bench_tuple_workload(args, device, workload):
         begin = time.perf_counter()
         while time.perf_counter() - begin < args.cpu_budget and len(times) < 20:
             t = {}
-            if workload == "c5":
+            if workload in ("c2dcsr", "c3dcsr"):
+                oracle.port_dcsr_binary("add" if workload == "c2dcsr" else "mul",
+                                        ops_np[0][0], ops_np[0][1], ops_np[1][0],
+                                        ops_np[1][1], timing=t)
+            elif workload == "c5":
                 oracle.port_csf3_union(csf3_levels(np.stack(ops_np[0][0], axis=1)), ops_np[0][1],
                                        csf3_levels(np.stack(ops_np[1][0], axis=1)), ops_np[1][1],
                                        timing=t)
@@ -374,7 +410,7 @@ def bench_tuple_workload(args, device, workload):
                                        ops_np[1][1], nthreads=cores, timing=t)
             times.append(t["seconds"])
         sec = sorted(times)[len(times) // 2]
-        serial = workload == "c5"
+        serial = workload in ("c5", "c2dcsr", "c3dcsr")
         cpu = {
             "value": round(alg_bytes / sec / 1e9, 3),
             "unit": "GB/s",
@@ -460,7 +496,7 @@ def main():
     if args.workload == "c4":
         print(json.dumps(bench_spgemm(args, device)), flush=True)
         return
-    if args.workload in ("c5", "c5coo", "c2coo"):
+    if args.workload in ("c5", "c5coo", "c2coo", "c2dcsr", "c3dcsr"):
         print(json.dumps(bench_tuple_workload(args, device, args.workload)), flush=True)
         return
 
