@@ -45,6 +45,8 @@ extern "C" {
 #define NACHO_ERR_MALFORMED_INPUT (-4)  /* validation found unsorted/duplicate/bad pos    */
 #define NACHO_ERR_NO_DEVICE (-5)        /* no HIP device visible                          */
 #define NACHO_ERR_INTERNAL (-6)         /* a kernel's bounded wait expired (library bug)  */
+#define NACHO_ERR_IO (-7)               /* a file could not be opened or read             */
+#define NACHO_ERR_UNSUPPORTED (-8)      /* a file format variant the reader does not take */
 
 /* ---- tensor descriptors (field order = the reference's generated structs) ---------- */
 
@@ -237,6 +239,46 @@ int nacho_gpu_spgemm_f32(const nacho_csr *a, const nacho_csr *b, nacho_csr *z,
 int nacho_gpu_spgemm64_f32(const nacho_csr *a, const nacho_csr *b, nacho_csr64 *z,
                            int32_t num_blocks, int32_t threads_per_block, void *stream,
                            const nacho_allocator *alloc);
+
+/* ---- file readers (host) ---------------------------------------------------------
+ * Matrix Market and FROSTT readers, replacing nacho.parse2D / nacho.parse3D_i32_f32
+ * (runtime/io/parse.h:28-263, registered at runtime/register_runtime.cpp:20-40).  Arrays are
+ * host memory allocated by the library; release each with nacho_host_free(). */
+
+/* Coordinates and values of a Matrix Market file, in file order (0-based). */
+typedef struct nacho_coo2d_host {
+    int32_t N;      /* rows    */
+    int32_t M;      /* columns */
+    int64_t nnz;    /* entries, including mirrored ones of symmetric files */
+    int32_t *row;
+    int32_t *col;
+    float *data;
+} nacho_coo2d_host;
+
+/* Coordinates and values of a FROSTT .tns file, in file order (0-based). */
+typedef struct nacho_coo3d_host {
+    int32_t N, M, K;
+    int64_t nnz;
+    int32_t *row;
+    int32_t *col;
+    int32_t *dep;
+    float *data;
+} nacho_coo3d_host;
+
+/* parse2D: a `coordinate real` Matrix Market file with general, symmetric or
+ * skew-symmetric symmetry.  Symmetric files get the mirror of every off-diagonal entry
+ * appended after the file's entries (negated when skew-symmetric), as the reference does.
+ * Values are read as double and rounded to float.  Returns NACHO_ERR_IO,
+ * NACHO_ERR_UNSUPPORTED (another field or symmetry) or NACHO_ERR_MALFORMED_INPUT where the
+ * reference terminates the process. */
+int nacho_parse2d(const char *path, nacho_coo2d_host *out);
+
+/* parse3D_i32_f32: "i j k value" lines (1-based) of a tensor of shape (N, M, K), read up
+ * to the first entry that does not parse; values are read as float. */
+int nacho_parse3d(const char *path, int32_t N, int32_t M, int32_t K, nacho_coo3d_host *out);
+
+/* Release an array returned by a reader. */
+void nacho_host_free(void *p);
 
 /* ---- diagnostics ------------------------------------------------------------------ */
 

@@ -1,9 +1,10 @@
 """nacho_amd — MI355X (gfx950) backend for nacho's GPU target.
 
 Python surface of the reference (`import nacho`; python/nacho/__init__.py) for the GPU
-target: the tensor classes, the `gpu_<kernel>_f32` entry points and the converters.  Every
-entry point runs hand-written HIP kernels from libnacho_hip.so through its C ABI
-(include/nacho_hip.h); nothing here computes on the CPU.
+target: the tensor classes, the `gpu_<kernel>_f32` entry points, the converters and the
+Matrix Market / FROSTT readers.  Every `gpu_` entry point runs hand-written HIP kernels from
+libnacho_hip.so through its C ABI (include/nacho_hip.h); nothing here computes on the CPU
+except the file readers (host C++ in the same library).
 """
 
 from .convert import to_coo, to_coo3, to_csf3, to_csr, to_dcsr  # noqa: F401
@@ -23,6 +24,7 @@ from .ops import (  # noqa: F401
     release_cached_memory,
     set_kernel_timing,
 )
+from .io import COO2D, COO3D_parsed, parse2D, parse3D_i32_f32  # noqa: F401
 from .tensors import COO3_gpu, COO_gpu, CSF3_gpu, CSR64_gpu, CSR_gpu, DCSR_gpu  # noqa: F401
 
 __version__ = "0.1.0"

@@ -101,6 +101,30 @@ class Csf3Desc(ctypes.Structure):
     ]
 
 
+class Coo2dHost(ctypes.Structure):
+    _fields_ = [
+        ("N", ctypes.c_int32),
+        ("M", ctypes.c_int32),
+        ("nnz", ctypes.c_int64),
+        ("row", ctypes.c_void_p),
+        ("col", ctypes.c_void_p),
+        ("data", ctypes.c_void_p),
+    ]
+
+
+class Coo3dHost(ctypes.Structure):
+    _fields_ = [
+        ("N", ctypes.c_int32),
+        ("M", ctypes.c_int32),
+        ("K", ctypes.c_int32),
+        ("nnz", ctypes.c_int64),
+        ("row", ctypes.c_void_p),
+        ("col", ctypes.c_void_p),
+        ("dep", ctypes.c_void_p),
+        ("data", ctypes.c_void_p),
+    ]
+
+
 class Allocator(ctypes.Structure):
     _fields_ = [
         ("ctx", ctypes.c_void_p),
@@ -146,6 +170,13 @@ def load() -> ctypes.CDLL:
         fn.argtypes = [ctypes.POINTER(operand), ctypes.POINTER(operand), ctypes.POINTER(result),
                        ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p,
                        ctypes.POINTER(Allocator)]
+    lib.nacho_parse2d.restype = ctypes.c_int
+    lib.nacho_parse2d.argtypes = [ctypes.c_char_p, ctypes.POINTER(Coo2dHost)]
+    lib.nacho_parse3d.restype = ctypes.c_int
+    lib.nacho_parse3d.argtypes = [ctypes.c_char_p, ctypes.c_int32, ctypes.c_int32,
+                                  ctypes.c_int32, ctypes.POINTER(Coo3dHost)]
+    lib.nacho_host_free.restype = None
+    lib.nacho_host_free.argtypes = [ctypes.c_void_p]
     lib.nacho_free.restype = ctypes.c_int
     lib.nacho_free.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
     lib.nacho_release_cached_memory.restype = ctypes.c_int

@@ -1,6 +1,7 @@
-"""Build the gfx950 shared library `nacho_amd/libnacho_hip.so` from `nacho_amd/csrc/*.hip`.
+"""Build the gfx950 shared library `nacho_amd/libnacho_hip.so` from `nacho_amd/csrc/*.hip`
+(device code, hipcc for gfx950 only) and `nacho_amd/csrc/*.cpp` (host-only code, g++).
 
-Every source is compiled by hipcc for gfx950 only, in parallel, then linked into one
+Every source is compiled in parallel, then linked into one
 shared library exporting the C ABI declared in `include/nacho_hip.h`.  The library is built
 in-tree so that it travels with the repository to the GPU machine.
 
@@ -51,16 +52,26 @@ def hipcc() -> str:
     return path
 
 
+# Host-only sources (no device code): compiled by the host C++ compiler.
+HOST_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Wall", f"-I{REPO_DIR / 'include'}"]
+
+
 def sources() -> list[Path]:
-    return sorted(CSRC_DIR.glob("*.hip"))
+    return sorted(CSRC_DIR.glob("*.hip")) + sorted(CSRC_DIR.glob("*.cpp"))
 
 
 def _compile(src: Path) -> Path:
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [hipcc(), *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
+    if src.suffix == ".cpp":
+        cxx = shutil.which("g++") or shutil.which("c++")
+        if cxx is None:
+            raise RuntimeError("no host C++ compiler (g++) for the host-only sources")
+        cmd = [cxx, *HOST_FLAGS, "-c", str(src), "-o", str(obj)]
+    else:
+        cmd = [hipcc(), *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
-        raise RuntimeError(f"hipcc failed on {src.name}:\n{proc.stdout}\n{proc.stderr}")
+        raise RuntimeError(f"compile failed on {src.name}:\n{proc.stdout}\n{proc.stderr}")
     return obj
 
 

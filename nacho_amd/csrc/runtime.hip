@@ -251,6 +251,8 @@ const char *nacho_error_string(int code) {
         case NACHO_ERR_MALFORMED_INPUT: return "nacho: malformed sparse operand";
         case NACHO_ERR_NO_DEVICE: return "nacho: no HIP device";
         case NACHO_ERR_INTERNAL: return "nacho: internal error (kernel wait bound expired)";
+        case NACHO_ERR_IO: return "nacho: file could not be opened or read";
+        case NACHO_ERR_UNSUPPORTED: return "nacho: unsupported file format variant";
         default: break;
     }
     if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));

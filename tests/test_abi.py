@@ -114,7 +114,8 @@ def test_every_descriptor_layout_matches_the_c_compiler(tmp_path):
         pytest.skip("gcc not available")
     pairs = {"nacho_csr": _lib.CsrDesc, "nacho_csr64": _lib.Csr64Desc,
              "nacho_coo": _lib.CooDesc, "nacho_coo3": _lib.Coo3Desc,
-             "nacho_dcsr": _lib.DcsrDesc, "nacho_csf3": _lib.Csf3Desc}
+             "nacho_dcsr": _lib.DcsrDesc, "nacho_csf3": _lib.Csf3Desc,
+             "nacho_coo2d_host": _lib.Coo2dHost, "nacho_coo3d_host": _lib.Coo3dHost}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "nacho_hip.h"',
              "int main(void) {"]
     for cname, desc in pairs.items():
