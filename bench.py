@@ -1,7 +1,7 @@
 """Benchmark of the nacho GPU path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--workload c2|c3|c4|c5|c5coo|c2coo|c2dcsr|c3dcsr]
+                    [--workload c2|c3|c4|c5|c5coo|c2coo|c2dcsr|c3dcsr|c2add3]
 
 A step is one call of the hot path over one batch of synthetic input, with the operands
 already resident in HBM: `nacho_amd.gpu_csr_add_f32(A, B)` for the default workload (C2:
@@ -68,6 +68,10 @@ WORKLOADS = {
     "c2coo": dict(op="coo_add", kernel="coo_partition_kernel + coo_count_kernel + "
                                       "coo_write_kernel (packed 64-bit keys)",
                   desc="C2 as COO: coo_add f32 of the C2 operands' (i, j) tuples"),
+    "c2add3": dict(op="add3", kernel="two level merges (csr_partition_kernel + "
+                                    "csr_count_kernel + csr_write_kernel, twice)",
+                   desc="csr_add_3 f32: three C2 operands (Zipf(1.6) rows, 16.7M nnz each, "
+                        "seeds 1, 2, 4)"),
     "c2dcsr": dict(op="dcsr_add", kernel="two chained level merges (csr_partition_kernel + "
                                         "csr_count_kernel + csr_write_kernel per level)",
                    desc="C2 as DCSR: dcsr_add f32 of the C2 operands with empty rows "
@@ -93,6 +97,8 @@ def make_operands(workload):
 
     if workload == "c2":
         return synth.c2_operands()
+    if workload == "c2add3":
+        return tuple(synth.zipf_csr(synth.C2_ROWS, s) for s in (1, 2, 4))
     return synth.c3_operands()
 
 
@@ -107,17 +113,23 @@ def traffic_from_profiles(workload, family="csr_merge"):
         return None
 
 
-def cpu_baseline(workload, op, a, b, rows, bytes_per_call, budget_s):
+def cpu_baseline(workload, op, operands, rows, bytes_per_call, budget_s):
     """Time the oracle's C restatement of the reference CPU kernel on this host."""
     from oracle import oracle
 
     cores = len(os.sched_getaffinity(0))
     cores = max(1, min(cores, 64))
+    if op == "add3":
+        cores = 1  # the three-way restatement is serial
     times = []
     start = time.perf_counter()
     while time.perf_counter() - start < budget_s and len(times) < 50:
         t = {}
-        oracle.port_csr_binary(op, rows, *a, *b, nthreads=cores, timing=t)
+        if op == "add3":
+            oracle.port_csr_add3(rows, *operands, timing=t)
+        else:
+            oracle.port_csr_binary(op, rows, *operands[0], *operands[1], nthreads=cores,
+                                   timing=t)
         times.append(t["seconds"])
     times.sort()
     trimmed = times[1:-1] if len(times) > 4 else times
@@ -505,23 +517,27 @@ def main():
 
     spec = WORKLOADS[args.workload]
     t0 = time.perf_counter()
-    a_np, b_np = make_operands(args.workload)
+    operands_np = make_operands(args.workload)
+    a_np, b_np = operands_np[0], operands_np[1]
     rows = len(a_np[0]) - 1
-    log(f"generated {args.workload}: rows={rows} nnzA={len(a_np[1])} nnzB={len(b_np[1])} "
-        f"in {time.perf_counter() - t0:.1f}s")
+    log(f"generated {args.workload}: rows={rows} "
+        f"nnz={[len(o[1]) for o in operands_np]} in {time.perf_counter() - t0:.1f}s")
 
     def upload(t):
         pos, crd, val = (torch.from_numpy(x).to(device) for x in t)
         return nacho_amd.CSR_gpu(pos, crd, val, torch.tensor([rows, rows], dtype=torch.int32))
 
-    copies = [(upload(a_np), upload(b_np)) for _ in range(ROTATE)]
-    fn = nacho_amd.gpu_csr_add_f32 if spec["op"] == "add" else nacho_amd.gpu_csr_mul_f32
+    copies = [tuple(upload(o) for o in operands_np) for _ in range(ROTATE)]
+    fn = {"add": nacho_amd.gpu_csr_add_f32, "mul": nacho_amd.gpu_csr_mul_f32,
+          "add3": nacho_amd.gpu_csr_add_3_f32}[spec["op"]]
 
     z = fn(*copies[0])
     torch.cuda.synchronize()
     nnz_c = int(z.dim_j_indices.numel())
     del z
     alg_bytes = synth.csr_bytes(rows, len(a_np[1]), len(b_np[1]), nnz_c)
+    if spec["op"] == "add3":  # the third operand's offsets and entries
+        alg_bytes += 4 * (rows + 1) + 8 * len(operands_np[2][1])
     log(f"nnzC={nnz_c} algorithmic bytes/call={alg_bytes}")
 
     # warmup, then per-launch kernel durations (HIP events on the launch stream)
@@ -553,7 +569,7 @@ def main():
 
     cpu = None
     if args.cpu_budget > 0:
-        cpu = cpu_baseline(args.workload, spec["op"], a_np, b_np, rows, alg_bytes,
+        cpu = cpu_baseline(args.workload, spec["op"], operands_np, rows, alg_bytes,
                            args.cpu_budget)
         log(f"cpu baseline {cpu['value']} GB/s on {cpu['cores']} threads")
 
@@ -573,6 +589,7 @@ def main():
         "config": {
             "workload": spec["desc"],
             "rows": rows,
+            "nnz_operands": [len(o[1]) for o in operands_np],
             "nnz_a": len(a_np[1]),
             "nnz_b": len(b_np[1]),
             "nnz_c": nnz_c,

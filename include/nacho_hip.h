@@ -173,6 +173,13 @@ int nacho_gpu_csr_add_f32(const nacho_csr *a, const nacho_csr *b, nacho_csr *z,
                           int32_t num_blocks, int32_t threads_per_block, void *stream,
                           const nacho_allocator *alloc);
 
+/* Z = a + b + c over CSR (union of three; a value is the sum of the present operands in
+ * the order (a + b) + c, one float32 add per extra operand).  Replaces
+ * csr_add_3::csr_add_3_gpu_i32_f32 (compiler.cpp:114). */
+int nacho_gpu_csr_add_3_f32(const nacho_csr *a, const nacho_csr *b, const nacho_csr *c,
+                            nacho_csr *z, int32_t num_blocks, int32_t threads_per_block,
+                            void *stream, const nacho_allocator *alloc);
+
 /* Z = a * b elementwise over CSR (intersection).  Replaces csr_mul::csr_mul_gpu_i32_f32
  * (compiler.cpp:116), including its empty-result early exit
  * (stitch_and_generate.cpp:168-220): an empty product returns zeroed offsets and NULL

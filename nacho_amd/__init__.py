@@ -13,6 +13,7 @@ from .ops import (  # noqa: F401
     gpu_coo_add_f32,
     gpu_coo_mul_f32,
     gpu_csf_add_f32,
+    gpu_csr_add_3_f32,
     gpu_csr_add_f32,
     gpu_csr_mul_f32,
     gpu_dcsr_add_f32,

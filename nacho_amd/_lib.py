@@ -149,6 +149,11 @@ ENTRY_POINTS = {
     "nacho_gpu_spgemm64_f32": (CsrDesc, Csr64Desc),
 }
 
+# three-operand entry points (a, b, c, z, ...)
+ENTRY_POINTS_3 = {
+    "nacho_gpu_csr_add_3_f32": (CsrDesc, CsrDesc),
+}
+
 _lib = None
 
 
@@ -170,6 +175,14 @@ def load() -> ctypes.CDLL:
         fn.argtypes = [ctypes.POINTER(operand), ctypes.POINTER(operand), ctypes.POINTER(result),
                        ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p,
                        ctypes.POINTER(Allocator)]
+    for name, (operand, result) in ENTRY_POINTS_3.items():
+        fn = getattr(lib, name, None)
+        if fn is None:
+            continue
+        fn.restype = ctypes.c_int
+        fn.argtypes = [ctypes.POINTER(operand)] * 3 + [
+            ctypes.POINTER(result), ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p,
+            ctypes.POINTER(Allocator)]
     lib.nacho_parse2d.restype = ctypes.c_int
     lib.nacho_parse2d.argtypes = [ctypes.c_char_p, ctypes.POINTER(Coo2dHost)]
     lib.nacho_parse3d.restype = ctypes.c_int

@@ -171,6 +171,29 @@ def gpu_csr_add_f32(a: CSR_gpu, b: CSR_gpu, num_blocks: int = 256,
                  num_blocks, threads_per_block)
 
 
+def gpu_csr_add_3_f32(a: CSR_gpu, b: CSR_gpu, c: CSR_gpu, num_blocks: int = 256,
+                      threads_per_block: int = 256) -> CSR_gpu:
+    """Z = a + b + c (sorted union of three; values (a + b) + c over the present operands).
+    compiler.cpp:114."""
+    entry = "nacho_gpu_csr_add_3_f32"
+    for name, t in (("a", a), ("b", b), ("c", c)):
+        if not isinstance(t, CSR_gpu):
+            raise TypeError(f"{entry}: operand {name} must be CSR_gpu, got {type(t).__name__}")
+    device = _same_device(a, b, c)
+    lib = _lib.load()
+    fn = getattr(lib, entry, None)
+    if fn is None:
+        raise RuntimeError(f"{entry} is not exported by {_lib.LIBRARY_PATH.name}")
+    da, db, dc = _csr_desc(a), _csr_desc(b), _csr_desc(c)
+    z = _lib.CsrDesc()
+    with torch.cuda.device(device):
+        stream = _device.current_stream(device)
+        rc = fn(ctypes.byref(da), ctypes.byref(db), ctypes.byref(dc), ctypes.byref(z),
+                int(num_blocks), int(threads_per_block), ctypes.c_void_p(stream), None)
+        _lib.check(rc, entry)
+        return _adopt_csr(z, device, stream)
+
+
 def gpu_csr_mul_f32(a: CSR_gpu, b: CSR_gpu, num_blocks: int = 256,
                     threads_per_block: int = 256) -> CSR_gpu:
     """Z = a * b elementwise (sorted intersection per row).  compiler.cpp:116."""

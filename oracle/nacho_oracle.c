@@ -28,6 +28,8 @@
  *     operands without empty fibres, which is what to_csf3 builds).  Serial restatement of
  *     the lattice; the reference's nested partitioning (partition.cpp:286-461) only splits
  *     this work among threads.
+ *   - csr_add3: the three-way union lattice of csr_add_3 (compiler.cpp:114), row by row,
+ *     values evaluated as (a + b) + c with absent operands removed.
  *   - dcsr_union / dcsr_intersect: the two-level lattice of dcsr_add / dcsr_mul
  *     (compiler.cpp:124-133): i over A_i ∪ B_i (add) or A_i ∩ B_i (mul), j over the union /
  *     intersection of the two fibres; a row id is emitted at every i lattice point, with its
@@ -635,6 +637,65 @@ int oracle_csf3_union(const int32_t *a_ci, int a_ni, const int32_t *a_pj, const 
     *o_ni = (int)o.ni;
     *o_nj = (int)o.nj;
     *o_nk = (int)o.nk;
+    return ORC_OK;
+}
+
+/* ---------------------------------------------------------------------------------- */
+/* CSR three-way union (csr_add_3)                                                       */
+
+/* Z = A + B + C over CSR (compiler.cpp:114).  Per row, the lattice of a + b + c: every
+ * coordinate of the three rows' union in ascending order, valued by the expression with the
+ * absent operands removed, evaluated as written ((a + b) + c, compute.cpp:413-491):
+ * (a + b) + c, a + b, a + c, b + c or a copy.  Serial.  Outputs are malloc'd. */
+int oracle_csr_add3(int rows, const int32_t *pa, const int32_t *ca, const float *va,
+                    const int32_t *pb, const int32_t *cb, const float *vb, const int32_t *pc,
+                    const int32_t *cc, const float *vc, int32_t **o_pos, int32_t **o_crd,
+                    float **o_val, int *o_nnz) {
+    const size_t cap = (size_t)pa[rows] + pb[rows] + pc[rows] + 1;
+    int32_t *pos = (int32_t *)malloc(sizeof(int32_t) * ((size_t)rows + 1));
+    int32_t *crd = (int32_t *)malloc(sizeof(int32_t) * cap);
+    float *val = (float *)malloc(sizeof(float) * cap);
+    if (!pos || !crd || !val) {
+        free(pos);
+        free(crd);
+        free(val);
+        return ORC_ENOMEM;
+    }
+    long n = 0;
+    pos[0] = 0;
+    for (int r = 0; r < rows; ++r) {
+        int x = pa[r], y = pb[r], z = pc[r];
+        const int xe = pa[r + 1], ye = pb[r + 1], ze = pc[r + 1];
+        while (x < xe || y < ye || z < ze) {
+            int j = INT32_MAX;
+            if (x < xe && ca[x] < j) j = ca[x];
+            if (y < ye && cb[y] < j) j = cb[y];
+            if (z < ze && cc[z] < j) j = cc[z];
+            const int ha = x < xe && ca[x] == j, hb = y < ye && cb[y] == j,
+                      hc = z < ze && cc[z] == j;
+            float v;
+            if (ha && hb) {
+                v = va[x] + vb[y];
+                if (hc) v = v + vc[z];
+            } else if (ha) {
+                v = hc ? va[x] + vc[z] : va[x];
+            } else if (hb) {
+                v = hc ? vb[y] + vc[z] : vb[y];
+            } else {
+                v = vc[z];
+            }
+            crd[n] = j;
+            val[n++] = v;
+            x += ha;
+            y += hb;
+            z += hc;
+        }
+        pos[r + 1] = (int32_t)n;
+    }
+    *o_pos = pos;
+    *o_crd = crd;
+    *o_val = val;
+    *o_nnz = (int)n;
     return ORC_OK;
 }
 

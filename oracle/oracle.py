@@ -14,7 +14,8 @@ Parity status of each function (how it is pinned) is recorded in the test module
 the repository's design notes: csr/coo/coo3/csf union and intersection are pinned by the
 closed forms, by scipy, by brute force on tiny inputs and by the reference's own smoke
 cases (tests/smoke.py semantics); dcsr union / intersection by the DCSR closed form over the
-expanded CSR matrices; spgemm is pinned by a float64 scipy product.
+expanded CSR matrices; csr_add3 by the three-way closed form; spgemm is pinned by a
+float64 scipy product.
 """
 
 from __future__ import annotations
@@ -65,6 +66,11 @@ def load() -> ctypes.CDLL:
             [_i32p, ctypes.c_int, _i32p, _i32p, ctypes.c_int, _i32p, _i32p, _f32p, ctypes.c_int]
             * 2 + [ctypes.POINTER(_i32p)] * 5 + [ctypes.POINTER(_f32p)]
             + [ctypes.POINTER(ctypes.c_int)] * 3)
+        lib.oracle_csr_add3.restype = ctypes.c_int
+        lib.oracle_csr_add3.argtypes = (
+            [ctypes.c_int] + [_i32p, _i32p, _f32p] * 3
+            + [ctypes.POINTER(_i32p), ctypes.POINTER(_i32p), ctypes.POINTER(_f32p),
+               ctypes.POINTER(ctypes.c_int)])
         lib.oracle_dcsr_binary.restype = ctypes.c_int
         lib.oracle_dcsr_binary.argtypes = (
             [ctypes.c_int] + [_i32p, ctypes.c_int, _i32p, _i32p, _f32p] * 2
@@ -195,6 +201,32 @@ def port_csf3_union(a_levels, a_val, b_levels, b_val, timing=None):
     return levels, _take(oval, nk, np.float32)
 
 
+def port_csr_add3(rows, a, b, c, timing=None):
+    """a, b, c = (pos, crd, val).  Returns (pos int32, crd int32, val float32).  If `timing`
+    is a dict, timing["seconds"] receives the duration of the C call alone."""
+    import time
+
+    lib = load()
+    keep = []
+    for t in (a, b, c):
+        keep += [_as(t[0], np.int32), _as(t[1], np.int32), _as(t[2], np.float32)]
+    args = []
+    for i in range(0, 9, 3):
+        args += [_ptr(keep[i], ctypes.c_int32), _ptr(keep[i + 1], ctypes.c_int32),
+                 _ptr(keep[i + 2], ctypes.c_float)]
+    opos, ocrd, oval, onnz = _i32p(), _i32p(), _f32p(), ctypes.c_int()
+    t0 = time.perf_counter()
+    rc = lib.oracle_csr_add3(int(rows), *args, ctypes.byref(opos), ctypes.byref(ocrd),
+                             ctypes.byref(oval), ctypes.byref(onnz))
+    if timing is not None:
+        timing["seconds"] = time.perf_counter() - t0
+    if rc != 0:
+        raise RuntimeError(f"oracle_csr_add3 failed ({rc})")
+    n = onnz.value
+    return (_take(opos, rows + 1, np.int32), _take(ocrd, n, np.int32),
+            _take(oval, n, np.float32))
+
+
 def port_dcsr_binary(op, a_levels, a_val, b_levels, b_val, timing=None):
     """levels = (crd_i, pos_j, crd_j).  op = "add" | "mul".  Returns (levels, val).  If
     `timing` is a dict, timing["seconds"] receives the duration of the C call alone."""
@@ -309,6 +341,21 @@ def closed_coo_binary(op, shape, a_crd, va, b_crd, vb):
         crd.append((rest % (int(n) + 1)).astype(np.int32))
         rest //= (int(n) + 1)
     return tuple(reversed(crd)), val
+
+
+def closed_csr_add3(rows, cols, a, b, c):
+    """Union of the three (row, col) key sets; each value the sum of the present operands
+    in the order (a + b) + c, in float32."""
+    width = int(cols) + 1
+    keys_of = [(_rows_of(t[0]) * width + np.asarray(t[1], np.int64)) for t in (a, b, c)]
+    keys = np.union1d(np.union1d(keys_of[0], keys_of[1]), keys_of[2])
+    hits = [_lookup(k, np.asarray(t[2], np.float32), keys) for k, t in zip(keys_of, (a, b, c))]
+    (ha, xa), (hb, xb), (hc, xc) = hits
+    ab = np.where(ha & hb, xa + xb, np.where(ha, xa, xb)).astype(np.float32)
+    val = np.where(ha | hb, np.where(hc, ab + xc, ab), xc).astype(np.float32)
+    pos = np.zeros(int(rows) + 1, np.int64)
+    np.add.at(pos, keys // width + 1, 1)
+    return np.cumsum(pos).astype(np.int32), (keys % width).astype(np.int32), val
 
 
 def closed_dcsr_binary(op, rows, cols, a_levels, a_val, b_levels, b_val):
