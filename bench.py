@@ -1,7 +1,7 @@
 """Benchmark of the nacho GPU path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--workload c2|c3|c4|c5|c5coo|c2coo|c2dcsr|c3dcsr|c2add3]
+                    [--workload c2|c3|c4|c5|c5coo|c2coo|c2dcsr|c3dcsr|c2add3|c4sssmm]
 
 A step is one call of the hot path over one batch of synthetic input, with the operands
 already resident in HBM: `nacho_amd.gpu_csr_add_f32(A, B)` for the default workload (C2:
@@ -79,6 +79,10 @@ WORKLOADS = {
     "c3dcsr": dict(op="dcsr_mul", kernel="two chained level merges + row compaction",
                    desc="C3 as DCSR: dcsr_mul f32 of the C3 operands with empty rows "
                         "dropped"),
+    "c4sssmm": dict(op="sssmm", kernel="hash tables + probe_kernel + output (one call's "
+                                       "device pipeline, host readback gaps excluded)",
+                    desc="sssmm f32: A * A masked by A on the C4 operand (R-MAT 2^20); "
+                         "GFLOP/s = 3 FLOP (two multiplies, one add) per term"),
     "c4": dict(op="spgemm", kernel="chunk_kernel<histogram, scatter> + dense/bitmap/sort "
                                  "unit kernels + copy_units_kernel and the sizing kernels "
                                  "(one call's device pipeline, host readback gaps excluded)",
@@ -285,6 +289,146 @@ def bench_spgemm(args, device):
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
             "traffic": traffic_from_profiles("c4", "spgemm"),
+            "kernel_avg_us": round(kernel_avg_ms * 1e3, 2),
+        },
+        "cpu_baseline": cpu,
+        "gpu_over_cpu": round(value / cpu["value"], 1) if cpu else None,
+    }
+
+
+def sssmm_cpu_baseline(pos, crd, budget_s):
+    """The oracle's row-parallel masked SpGEMM (A, A, A) on a uniform random row sample sized
+    to take about `budget_s`; unit values, so the result values count the terms."""
+    import numpy as np
+
+    from oracle import oracle
+
+    n = len(pos) - 1
+    cores = max(1, min(len(os.sched_getaffinity(0)), 64))
+    ones = np.ones(len(crd), np.float32)
+    rng = np.random.default_rng(98)
+    a = (pos, crd, ones)
+
+    def run(frac):
+        rows = np.sort(rng.choice(n, size=max(1, int(n * frac)), replace=False)).astype(np.int32)
+        t0 = time.perf_counter()
+        _, _, v = oracle.port_sssmm(n, n, a, a, a, row_list=rows, nthreads=cores)
+        return float(np.sum(v, dtype=np.float64)), time.perf_counter() - t0, len(rows)
+
+    _, s_small, _ = run(1 / 512)
+    frac = min(1.0, max(1 / 512, (budget_s / 2) / max(s_small, 1e-6) / 512))
+    samples = [run(frac) for _ in range(2)]
+    terms = sum(x[0] for x in samples)
+    sec = sum(x[1] for x in samples)
+    return {
+        "value": round(3 * terms / sec / 1e9, 3),
+        "unit": "GFLOP/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"2 runs of the row-parallel C masked SpGEMM (oracle/nacho_oracle.c, dense "
+                  f"mask marker, float64 sums) on uniform random samples of {samples[0][2]} "
+                  f"rows ({frac:.4f} of rows; {int(terms)} terms in {sec:.1f} s)",
+    }
+
+
+def bench_sssmm(args, device):
+    """c4sssmm: the masked product A * A masked by A on the C4 operand (the reference's
+    sssmm benchmark runs A, A, A for square matrices, benchmarks/sssmm.py:13-15)."""
+    import numpy as np
+    import torch
+
+    import nacho_amd
+    from nacho_amd import synth
+
+    spec = WORKLOADS["c4sssmm"]
+    t0 = time.perf_counter()
+    pos, crd, val = synth.c4_operand()
+    n = len(pos) - 1
+    lens = np.diff(pos.astype(np.int64))
+    colcnt = np.bincount(crd, minlength=n).astype(np.int64)
+    rows = np.repeat(np.arange(n), lens)
+    la, lb = lens[rows], colcnt[crd]
+    probes = int(np.where((la > 0) & (lb > 0), np.minimum(la, lb), 0).sum())
+    log(f"generated c4sssmm: n={n} nnz={len(crd)} probes={probes} "
+        f"in {time.perf_counter() - t0:.1f}s")
+
+    def upload(values):
+        t = (torch.from_numpy(x).to(device) for x in (pos, crd, values))
+        return nacho_amd.CSR_gpu(*t, torch.tensor([n, n], dtype=torch.int32))
+
+    ones = upload(np.ones(len(crd), np.float32))
+    zc = nacho_amd.gpu_sssmm_f32(ones, ones, ones)
+    terms = int(zc.values.double().sum().item())  # unit values: each entry counts its terms
+    del zc, ones
+    copies = [upload(val) for _ in range(2)]
+    fn = nacho_amd.gpu_sssmm_f32
+    z = fn(copies[0], copies[0], copies[0])
+    torch.cuda.synchronize()
+    nnz_z = int(z.dim_j_indices.numel())
+    del z
+    flops = 3 * terms
+    operand = 4 * (n + 1) + 8 * len(crd)
+    alg_bytes = 3 * operand + 4 * (n + 1) + 8 * nnz_z + 8 * probes
+    log(f"nnzZ={nnz_z} terms={terms} flops/call={flops} algorithmic bytes/call={alg_bytes}")
+
+    nacho_amd.set_kernel_timing(True)
+    for i in range(args.warmup):
+        fn(*(copies[i % 2],) * 3)
+    torch.cuda.synchronize()
+    kernel_ms = []
+    for i in range(args.steps):
+        fn(*(copies[i % 2],) * 3)
+        kernel_ms.append(nacho_amd.last_kernel_ms())
+    nacho_amd.set_kernel_timing(False)
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    for i in range(args.steps):
+        fn(*(copies[i % 2],) * 3)
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - start) * 1e3 / args.steps
+    value = flops / (ms_per_step * 1e-3) / 1e9
+    kernel_avg_ms = sum(kernel_ms) / len(kernel_ms)
+    achieved = alg_bytes / (kernel_avg_ms * 1e-3) / 1e9
+    log(f"pipeline avg {kernel_avg_ms:.3f} ms -> {achieved:.0f} GB/s; call {ms_per_step:.3f} ms "
+        f"-> {value:.1f} GFLOP/s")
+
+    cpu = None
+    if args.cpu_budget > 0:
+        cpu = sssmm_cpu_baseline(pos, crd, args.cpu_budget)
+        log(f"cpu baseline {cpu['value']} GFLOP/s on {cpu['cores']} threads")
+    nacho_amd.release_cached_memory()
+    return {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded generators in nacho_amd/synth.py)",
+        "config": {
+            "workload": spec["desc"],
+            "rows": n,
+            "nnz_a": len(crd),
+            "probes": probes,
+            "terms": terms,
+            "nnz_z": nnz_z,
+            "flops_per_step": flops,
+            "algorithmic_bytes_per_step": alg_bytes,
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": spec["kernel"],
+            "achieved": round(achieved, 2),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4),
+            "traffic": None,
             "kernel_avg_us": round(kernel_avg_ms * 1e3, 2),
         },
         "cpu_baseline": cpu,
@@ -507,6 +651,9 @@ def main():
 
     if args.workload == "c4":
         print(json.dumps(bench_spgemm(args, device)), flush=True)
+        return
+    if args.workload == "c4sssmm":
+        print(json.dumps(bench_sssmm(args, device)), flush=True)
         return
     if args.workload in ("c5", "c5coo", "c2coo", "c2dcsr", "c3dcsr"):
         print(json.dumps(bench_tuple_workload(args, device, args.workload)), flush=True)

@@ -233,6 +233,14 @@ int nacho_gpu_dcsr_mul_without_recursive_partitioning_f32(
     const nacho_dcsr *a, const nacho_dcsr *b, nacho_dcsr *z, int32_t num_blocks,
     int32_t threads_per_block, void *stream, const nacho_allocator *alloc);
 
+/* Masked SpGEMM: Z_ik = sum_j a_ij * b_jk * c_ik for the (i, k) stored in c that at least
+ * one product a_ij * b_jk reaches (Z's pattern = c's pattern intersected with a*b's).  Each
+ * term is ((a * b) * c) in float32; an entry's terms are summed in float64 and rounded
+ * once.  Replaces sssmm::sssmm_gpu_i32_f32 (compiler.cpp:150-153, GPU-only). */
+int nacho_gpu_sssmm_f32(const nacho_csr *a, const nacho_csr *b, const nacho_csr *c,
+                        nacho_csr *z, int32_t num_blocks, int32_t threads_per_block,
+                        void *stream, const nacho_allocator *alloc);
+
 /* Z_ik = sum_j a_ij * b_jk over CSR operands (ESC SpGEMM), int32 result.  Replaces
  * spgemm::spgemm_gpu_i32_f32 (compiler.cpp:145-148).  Fails with NACHO_ERR_INDEX_OVERFLOW
  * when nnz(Z) does not fit int32; use nacho_gpu_spgemm64_f32 then. */

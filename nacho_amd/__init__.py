@@ -20,6 +20,7 @@ from .ops import (  # noqa: F401
     gpu_dcsr_mul_f32,
     gpu_dcsr_mul_without_recursive_partitioning_f32,
     gpu_spgemm64_f32,
+    gpu_sssmm_f32,
     gpu_spgemm_f32,
     last_kernel_ms,
     release_cached_memory,

@@ -152,6 +152,7 @@ ENTRY_POINTS = {
 # three-operand entry points (a, b, c, z, ...)
 ENTRY_POINTS_3 = {
     "nacho_gpu_csr_add_3_f32": (CsrDesc, CsrDesc),
+    "nacho_gpu_sssmm_f32": (CsrDesc, CsrDesc),
 }
 
 _lib = None

@@ -60,6 +60,40 @@ __device__ __forceinline__ T block_exclusive_sum(T v, T *s_wave, T &total) {
     return before + incl - v;
 }
 
+// Last index x in [lo, hi] with a[x] <= q (a non-decreasing, a[lo] <= q).
+template <typename T>
+__device__ __forceinline__ int64_t last_le(const T *__restrict__ a, int64_t lo, int64_t hi,
+                                           int64_t q) {
+    while (lo < hi) {
+        const int64_t mid = (lo + hi + 1) >> 1;
+        if (static_cast<int64_t>(a[mid]) <= q) {
+            lo = mid;
+        } else {
+            hi = mid - 1;
+        }
+    }
+    return lo;
+}
+
+// Exclusive max over the workgroup (values >= 0, identity 0).  Ends synchronised.
+__device__ __forceinline__ int block_exclusive_max(int v, int *s_wave) {
+    const int l = lane();
+    const int w = threadIdx.x / kWave;
+    int incl = v;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+        const int n = __shfl_up(incl, o, kWave);
+        if (l >= o) incl = max(incl, n);
+    }
+    if (l == kWave - 1) s_wave[w] = incl;
+    int excl = __shfl_up(incl, 1, kWave);
+    if (l == 0) excl = 0;
+    __syncthreads();
+    for (int i = 0; i < w; ++i) excl = max(excl, s_wave[i]);
+    __syncthreads();
+    return excl;
+}
+
 // ---- decoupled look-back ------------------------------------------------------------
 // One 64-bit status word per tile: state in the high half (0 = not yet published,
 // 1 = tile aggregate, 2 = inclusive prefix), 32-bit value in the low half.  Word and state

@@ -74,39 +74,8 @@ static_assert(kChunk == kBlock * kPer, "chunk decode assumes kPer products per l
 constexpr int kPadded = kTile + kTile / 16;
 __device__ __forceinline__ int pad(int i) { return i + (i >> 4); }
 
-// Last index x in [lo, hi] with a[x] <= q (a non-decreasing, a[lo] <= q).
-template <typename T>
-__device__ __forceinline__ int64_t last_le(const T *__restrict__ a, int64_t lo, int64_t hi,
-                                           int64_t q) {
-    while (lo < hi) {
-        const int64_t mid = (lo + hi + 1) >> 1;
-        if (static_cast<int64_t>(a[mid]) <= q) {
-            lo = mid;
-        } else {
-            hi = mid - 1;
-        }
-    }
-    return lo;
-}
-
-// Exclusive max over the workgroup (values >= 0, identity 0).  Ends synchronised.
-__device__ __forceinline__ int block_exclusive_max(int v, int *s_wave) {
-    const int l = dev::lane();
-    const int w = threadIdx.x / dev::kWave;
-    int incl = v;
-#pragma unroll
-    for (int o = 1; o < dev::kWave; o <<= 1) {
-        const int n = __shfl_up(incl, o, dev::kWave);
-        if (l >= o) incl = max(incl, n);
-    }
-    if (l == dev::kWave - 1) s_wave[w] = incl;
-    int excl = __shfl_up(incl, 1, dev::kWave);
-    if (l == 0) excl = 0;
-    __syncthreads();
-    for (int i = 0; i < w; ++i) excl = max(excl, s_wave[i]);
-    __syncthreads();
-    return excl;
-}
+using dev::block_exclusive_max;
+using dev::last_le;
 
 // ---- 1-2: sizes and segments -----------------------------------------------------------
 

@@ -171,11 +171,7 @@ def gpu_csr_add_f32(a: CSR_gpu, b: CSR_gpu, num_blocks: int = 256,
                  num_blocks, threads_per_block)
 
 
-def gpu_csr_add_3_f32(a: CSR_gpu, b: CSR_gpu, c: CSR_gpu, num_blocks: int = 256,
-                      threads_per_block: int = 256) -> CSR_gpu:
-    """Z = a + b + c (sorted union of three; values (a + b) + c over the present operands).
-    compiler.cpp:114."""
-    entry = "nacho_gpu_csr_add_3_f32"
+def _call3(entry, a, b, c, num_blocks, threads_per_block) -> CSR_gpu:
     for name, t in (("a", a), ("b", b), ("c", c)):
         if not isinstance(t, CSR_gpu):
             raise TypeError(f"{entry}: operand {name} must be CSR_gpu, got {type(t).__name__}")
@@ -192,6 +188,20 @@ def gpu_csr_add_3_f32(a: CSR_gpu, b: CSR_gpu, c: CSR_gpu, num_blocks: int = 256,
                 int(num_blocks), int(threads_per_block), ctypes.c_void_p(stream), None)
         _lib.check(rc, entry)
         return _adopt_csr(z, device, stream)
+
+
+def gpu_csr_add_3_f32(a: CSR_gpu, b: CSR_gpu, c: CSR_gpu, num_blocks: int = 256,
+                      threads_per_block: int = 256) -> CSR_gpu:
+    """Z = a + b + c (sorted union of three; values (a + b) + c over the present operands).
+    compiler.cpp:114."""
+    return _call3("nacho_gpu_csr_add_3_f32", a, b, c, num_blocks, threads_per_block)
+
+
+def gpu_sssmm_f32(a: CSR_gpu, b: CSR_gpu, c: CSR_gpu, num_blocks: int = 256,
+                  threads_per_block: int = 256) -> CSR_gpu:
+    """Masked SpGEMM Z_ik = sum_j a_ij b_jk c_ik over the entries of c that a product reaches.
+    compiler.cpp:150-153."""
+    return _call3("nacho_gpu_sssmm_f32", a, b, c, num_blocks, threads_per_block)
 
 
 def gpu_csr_mul_f32(a: CSR_gpu, b: CSR_gpu, num_blocks: int = 256,

@@ -34,6 +34,8 @@
  *     (compiler.cpp:124-133): i over A_i ∪ B_i (add) or A_i ∩ B_i (mul), j over the union /
  *     intersection of the two fibres; a row id is emitted at every i lattice point, with its
  *     fibre, even when a product fibre is empty.  Serial restatement of the lattice.
+ *   - sssmm: masked SpGEMM (GPU-only in the reference, compiler.cpp:150-153), row by row
+ *     with a dense mask marker; products in ascending j, summed in float64.
  *   - spgemm: the reference has no CPU SpGEMM (compiler.cpp:145-148 is GPU-only).  This is
  *     the ESC semantics of its GPU path (stitch_and_generate_gpu.cpp:14-138, 257-366) run
  *     row-parallel on the CPU: per row, expand a_ij * b_jk, sort by k, and sum runs.
@@ -966,3 +968,161 @@ int oracle_spgemm(int rows, int inner, int cols, const int32_t *pa, const int32_
     *out_nnz = total;
     return ORC_OK;
 }
+
+/* ---------------------------------------------------------------------------------- */
+/* Masked SpGEMM (sssmm)                                                                 */
+
+/* Z_ik = sum_j a_ij * b_jk * c_ik for the (i, k) stored in C that at least one product
+ * reaches (compiler.cpp:150-153; GPU-only in the reference, whose benchmark checks the
+ * structure against cuSPARSE A*B followed by csr_mul with C, benchmarks/sssmm.py:46-51).
+ * Row by row: the row's mask entries are marked in a dense array over k; every product
+ * a_ij * b_jk (j ascending) that lands on a marked k adds (a_ij * b_jk) * c_ik, each product
+ * rounded to float32 as written, to a float64 accumulator; the reached entries are emitted
+ * in C's order with the sum rounded to float32. */
+typedef struct {
+    int rows, cols;
+    const int32_t *pa, *ca, *pb, *cb, *pc, *cc;
+    const float *va, *vb, *vc;
+    const int32_t *row_list; /* rows to compute (NULL = all) */
+    int n_list;
+    int phase;
+    int64_t *row_nnz;
+    int64_t *pz;
+    int32_t *cz;
+    float *vz;
+    int next;
+    int failed;
+} ms_job;
+
+static void ms_row(ms_job *J, int32_t *mark, double *acc, char *hit, int r) {
+    const int c0 = J->pc[r], c1 = J->pc[r + 1];
+    for (int q = c0; q < c1; ++q) {
+        mark[J->cc[q]] = q - c0 + 1;
+        acc[q - c0] = 0.0;
+        hit[q - c0] = 0;
+    }
+    for (int p = J->pa[r]; p < J->pa[r + 1]; ++p) {
+        const int j = J->ca[p];
+        const float a = J->va[p];
+        for (int q = J->pb[j]; q < J->pb[j + 1]; ++q) {
+            const int m = mark[J->cb[q]];
+            if (m) {
+                const float ab = a * J->vb[q];
+                acc[m - 1] += (double)(ab * J->vc[c0 + m - 1]);
+                hit[m - 1] = 1;
+            }
+        }
+    }
+    int64_t n = 0;
+    int64_t off = J->phase == 1 ? J->pz[r] : 0;
+    for (int q = c0; q < c1; ++q) {
+        mark[J->cc[q]] = 0;
+        if (hit[q - c0]) {
+            if (J->phase == 1) {
+                J->cz[off] = J->cc[q];
+                J->vz[off] = (float)acc[q - c0];
+                ++off;
+            }
+            ++n;
+        }
+    }
+    if (J->phase == 0) J->row_nnz[r] = n;
+}
+
+static void ms_task(int t, void *arg) {
+    ms_job *J = (ms_job *)arg;
+    (void)t;
+    int max_c = 1;
+    for (int r = 0; r < J->rows; ++r) {
+        const int len = J->pc[r + 1] - J->pc[r];
+        if (len > max_c) max_c = len;
+    }
+    int32_t *mark = (int32_t *)calloc((size_t)J->cols + 1, sizeof(int32_t));
+    double *acc = (double *)malloc(sizeof(double) * (size_t)max_c);
+    char *hit = (char *)malloc((size_t)max_c);
+    if (!mark || !acc || !hit) {
+        __atomic_store_n(&J->failed, 1, __ATOMIC_RELAXED);
+    } else {
+        const int n = J->row_list ? J->n_list : J->rows;
+        for (;;) {
+            const int x0 = __atomic_fetch_add(&J->next, SP_CHUNK, __ATOMIC_RELAXED);
+            if (x0 >= n) break;
+            const int x1 = x0 + SP_CHUNK < n ? x0 + SP_CHUNK : n;
+            for (int x = x0; x < x1; ++x) ms_row(J, mark, acc, hit, J->row_list ? J->row_list[x] : x);
+        }
+    }
+    free(mark);
+    free(acc);
+    free(hit);
+}
+
+/* Z = (A B) masked by C, valued as above (rows x cols).  `row_list` (n_list rows, may be
+ * NULL for all rows) restricts the work to those rows; the other rows of Z are empty.
+ * Returns 0 or an error. */
+int oracle_sssmm(int rows, int cols, const int32_t *pa, const int32_t *ca, const float *va,
+                 const int32_t *pb, const int32_t *cb, const float *vb, const int32_t *pc,
+                 const int32_t *cc, const float *vc, const int32_t *row_list, int n_list,
+                 int nthreads, int32_t **out_pos, int32_t **out_crd, float **out_val,
+                 int *out_nnz) {
+    ms_job J;
+    memset(&J, 0, sizeof(J));
+    J.rows = rows;
+    J.cols = cols;
+    J.pa = pa;
+    J.ca = ca;
+    J.va = va;
+    J.pb = pb;
+    J.cb = cb;
+    J.vb = vb;
+    J.pc = pc;
+    J.cc = cc;
+    J.vc = vc;
+    J.row_list = row_list;
+    J.n_list = n_list;
+    const int nt = nthreads > 0 ? nthreads : oracle_default_threads();
+    J.row_nnz = (int64_t *)calloc((size_t)rows + 1, sizeof(int64_t));
+    J.pz = (int64_t *)malloc(sizeof(int64_t) * ((size_t)rows + 1));
+    int32_t *pos = (int32_t *)malloc(sizeof(int32_t) * ((size_t)rows + 1));
+    if (!J.row_nnz || !J.pz || !pos) {
+        free(J.row_nnz);
+        free(J.pz);
+        free(pos);
+        return ORC_ENOMEM;
+    }
+    J.phase = 0;
+    parallel_for(nt, ms_task, &J);
+    int64_t total = 0;
+    for (int r = 0; r < rows; ++r) {
+        J.pz[r] = total;
+        total += J.row_nnz[r];
+    }
+    J.pz[rows] = total;
+    J.cz = (int32_t *)malloc(sizeof(int32_t) * (size_t)(total > 0 ? total : 1));
+    J.vz = (float *)malloc(sizeof(float) * (size_t)(total > 0 ? total : 1));
+    if (J.failed || !J.cz || !J.vz || total > INT32_MAX) {
+        free(J.row_nnz);
+        free(J.pz);
+        free(pos);
+        free(J.cz);
+        free(J.vz);
+        return J.failed || !J.cz || !J.vz ? ORC_ENOMEM : ORC_EOVERFLOW;
+    }
+    J.phase = 1;
+    J.next = 0;
+    parallel_for(nt, ms_task, &J);
+    for (int r = 0; r <= rows; ++r) pos[r] = (int32_t)J.pz[r];
+    free(J.row_nnz);
+    free(J.pz);
+    if (J.failed) {
+        free(pos);
+        free(J.cz);
+        free(J.vz);
+        return ORC_ENOMEM;
+    }
+    *out_pos = pos;
+    *out_crd = J.cz;
+    *out_val = J.vz;
+    *out_nnz = (int)total;
+    return ORC_OK;
+}
+

@@ -14,8 +14,8 @@ Parity status of each function (how it is pinned) is recorded in the test module
 the repository's design notes: csr/coo/coo3/csf union and intersection are pinned by the
 closed forms, by scipy, by brute force on tiny inputs and by the reference's own smoke
 cases (tests/smoke.py semantics); dcsr union / intersection by the DCSR closed form over the
-expanded CSR matrices; csr_add3 by the three-way closed form; spgemm is pinned by a
-float64 scipy product.
+expanded CSR matrices; csr_add3 by the three-way closed form; spgemm and sssmm are
+pinned by float64 scipy products.
 """
 
 from __future__ import annotations
@@ -71,6 +71,11 @@ def load() -> ctypes.CDLL:
             [ctypes.c_int] + [_i32p, _i32p, _f32p] * 3
             + [ctypes.POINTER(_i32p), ctypes.POINTER(_i32p), ctypes.POINTER(_f32p),
                ctypes.POINTER(ctypes.c_int)])
+        lib.oracle_sssmm.restype = ctypes.c_int
+        lib.oracle_sssmm.argtypes = (
+            [ctypes.c_int, ctypes.c_int] + [_i32p, _i32p, _f32p] * 3
+            + [_i32p, ctypes.c_int, ctypes.c_int, ctypes.POINTER(_i32p), ctypes.POINTER(_i32p),
+               ctypes.POINTER(_f32p), ctypes.POINTER(ctypes.c_int)])
         lib.oracle_dcsr_binary.restype = ctypes.c_int
         lib.oracle_dcsr_binary.argtypes = (
             [ctypes.c_int] + [_i32p, ctypes.c_int, _i32p, _i32p, _f32p] * 2
@@ -257,6 +262,37 @@ def port_dcsr_binary(op, a_levels, a_val, b_levels, b_val, timing=None):
     return levels, _take(oval, nj.value, np.float32)
 
 
+def port_sssmm(rows, cols, a, b, c, row_list=None, nthreads=0, timing=None):
+    """Masked SpGEMM: a, b, c = (pos, crd, val); Z has C's pattern restricted to the entries
+    some product reaches.  `row_list` restricts the work to those rows.  Returns
+    (pos int32, crd int32, val float32)."""
+    import time
+
+    lib = load()
+    keep = []
+    for t in (a, b, c):
+        keep += [_as(t[0], np.int32), _as(t[1], np.int32), _as(t[2], np.float32)]
+    args = []
+    for i in range(0, 9, 3):
+        args += [_ptr(keep[i], ctypes.c_int32), _ptr(keep[i + 1], ctypes.c_int32),
+                 _ptr(keep[i + 2], ctypes.c_float)]
+    rl = None if row_list is None else _as(row_list, np.int32)
+    opos, ocrd, oval, onnz = _i32p(), _i32p(), _f32p(), ctypes.c_int()
+    t0 = time.perf_counter()
+    rc = lib.oracle_sssmm(int(rows), int(cols), *args,
+                          None if rl is None else _ptr(rl, ctypes.c_int32),
+                          0 if row_list is None else len(row_list), int(nthreads),
+                          ctypes.byref(opos), ctypes.byref(ocrd), ctypes.byref(oval),
+                          ctypes.byref(onnz))
+    if timing is not None:
+        timing["seconds"] = time.perf_counter() - t0
+    if rc != 0:
+        raise RuntimeError(f"oracle_sssmm failed ({rc})")
+    n = onnz.value
+    return (_take(opos, rows + 1, np.int32), _take(ocrd, n, np.int32),
+            _take(oval, n, np.float32))
+
+
 def port_spgemm(rows, inner, cols, pa, ca, va, pb, cb, vb, nthreads=0):
     """ESC semantics on the CPU: returns (pos int64, crd int32, val float32)."""
     lib = load()
@@ -356,6 +392,33 @@ def closed_csr_add3(rows, cols, a, b, c):
     pos = np.zeros(int(rows) + 1, np.int64)
     np.add.at(pos, keys // width + 1, 1)
     return np.cumsum(pos).astype(np.int32), (keys % width).astype(np.int32), val
+
+
+def closed_sssmm_f64(rows, inner, cols, a, b, c):
+    """Masked product from scipy: structure = pattern(A) pattern(B) intersected with
+    pattern(C) (0/1 patterns, so cancellation keeps entries); values c_ik * (A B)_ik in
+    float64."""
+    import scipy.sparse as sp
+
+    def mat(t, shape, ones=False):
+        v = np.ones(len(t[1])) if ones else np.asarray(t[2], np.float64)
+        return sp.csr_matrix((v, np.asarray(t[1]), np.asarray(t[0])), shape=shape)
+
+    pat = (mat(a, (rows, inner), True) @ mat(b, (inner, cols), True)).tocsr()
+    cpat = mat(c, (rows, cols), True)
+    keep = pat.multiply(cpat).tocsr()
+    keep.eliminate_zeros()
+    keep.sort_indices()
+    prod = (mat(a, (rows, inner)) @ mat(b, (inner, cols))).multiply(mat(c, (rows, cols)))
+    prod = sp.csr_matrix(prod)
+    width = cols + 1
+    kk = _rows_of(keep.indptr) * width + keep.indices
+    prod.sort_indices()
+    kp = _rows_of(prod.indptr) * width + prod.indices
+    vals = np.zeros(keep.nnz, np.float64)
+    hit, v = _lookup(kp, prod.data, kk) if len(kp) else (np.zeros(keep.nnz, bool), vals)
+    vals[hit] = np.asarray(prod.data, np.float64)[np.searchsorted(kp, kk[hit])]
+    return keep.indptr.astype(np.int32), keep.indices.astype(np.int32), vals
 
 
 def closed_dcsr_binary(op, rows, cols, a_levels, a_val, b_levels, b_val):
