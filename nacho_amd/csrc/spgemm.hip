@@ -744,7 +744,6 @@ __global__ __launch_bounds__(kBlock) void bitmap_unit_kernel(
     int64_t *__restrict__ unit_nnz, int *__restrict__ row_unit, int *__restrict__ row_local) {
     constexpr int kWaves = kBlock / dev::kWave;
     __shared__ double s_acc[kTile];
-    __shared__ float s_val[kTile];
     __shared__ unsigned short s_col[kTile];  // column offset inside its bucket's window
     __shared__ unsigned s_bits[kWaves][kBitmapWords];
     __shared__ int s_pre[kWaves][kBitmapWords];
@@ -769,12 +768,11 @@ __global__ __launch_bounds__(kBlock) void bitmap_unit_kernel(
         s_sid[ord] = static_cast<int>(s);
     }
     if (threadIdx.x == 0) s_x0[n_buckets] = n;
-    // the unit's products, staged once (bucket = column >> shift, so the window offset is
-    // the column's low bits)
+    // the unit's columns, staged once (bucket = column >> shift, so the window offset is
+    // the column's low bits); values are read from the product buffer when accumulated
     const int low = (1 << shift) - 1;
     for (int q = threadIdx.x; q < n; q += kBlock) {
         s_col[q] = static_cast<unsigned short>(key[start + q] & low);
-        s_val[q] = val[start + q];
     }
     __syncthreads();
     const int w = threadIdx.x / dev::kWave, l = dev::lane();
@@ -822,7 +820,7 @@ __global__ __launch_bounds__(kBlock) void bitmap_unit_kernel(
             const int c = s_col[x];
             const int wd = c >> 5;
             const int r = pre[wd] + __popc(bm[wd] & ((1u << (c & 31)) - 1u));
-            atomicAdd(&s_acc[x0 + r], static_cast<double>(s_val[x]));
+            atomicAdd(&s_acc[x0 + r], static_cast<double>(val[start + x]));
         }
         wave_sync();
         const int64_t out = start + s_out[o];
