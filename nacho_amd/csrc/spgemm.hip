@@ -853,10 +853,14 @@ __global__ __launch_bounds__(kBlock) void bitmap_unit_kernel(
 
 // ---- 5c: dense units -------------------------------------------------------------------
 
-// One workgroup per dense unit (from the dense list).  The segment's column range
-// [bucket << shift, (bucket + 1) << shift) is accumulated kDenseCols columns at a time in an
-// LDS float64 array (plus a bitmap of touched columns), then compacted in column order.
-__global__ __launch_bounds__(kBlock) void dense_unit_kernel(
+// One workgroup of kDenseBlock threads per dense unit (from the dense list): the 64 KB
+// accumulator allows two resident workgroups per CU, so the workgroup is wide.  The
+// segment's column range [bucket << shift, (bucket + 1) << shift) is accumulated kDenseCols
+// columns at a time in an LDS float64 array (plus a bitmap of touched columns), then
+// compacted in column order, 16 columns per lane.
+constexpr int kDenseBlock = 512;
+
+__global__ __launch_bounds__(kDenseBlock) void dense_unit_kernel(
     const int *__restrict__ dense_list, const int *__restrict__ unit_seg,
     const int64_t *__restrict__ unit_start,
     const int64_t *__restrict__ seg_len, const int64_t *__restrict__ seg_prefix,
@@ -866,8 +870,8 @@ __global__ __launch_bounds__(kBlock) void dense_unit_kernel(
     int *__restrict__ row_local) {
     __shared__ double s_acc[kDenseCols];
     __shared__ unsigned s_bits[kDenseCols / 32];
-    __shared__ int s_wave[kBlock / dev::kWave];
-    static_assert(kDenseCols / 32 == kBlock, "one bitmap word per lane");
+    __shared__ int s_wave[kDenseBlock / dev::kWave];
+    static_assert(kDenseCols / 16 == kDenseBlock, "16 bitmap bits per lane");
     const int64_t u = dense_list[blockIdx.x];
     const int s = unit_seg[u];
     const int64_t len = seg_len[s];
@@ -882,10 +886,10 @@ __global__ __launch_bounds__(kBlock) void dense_unit_kernel(
     }
     int64_t written = 0;
     for (int64_t w0 = c_lo; w0 < c_hi; w0 += kDenseCols) {
-        for (int i = threadIdx.x; i < kDenseCols; i += kBlock) s_acc[i] = 0.0;
-        s_bits[threadIdx.x] = 0u;
+        for (int i = threadIdx.x; i < kDenseCols; i += kDenseBlock) s_acc[i] = 0.0;
+        if (threadIdx.x < kDenseCols / 32) s_bits[threadIdx.x] = 0u;
         __syncthreads();
-        for (int64_t x = threadIdx.x; x < len; x += kBlock) {
+        for (int64_t x = threadIdx.x; x < len; x += kDenseBlock) {
             const int64_t c = key[start + x] - w0;
             if (c >= 0 && c < kDenseCols) {
                 atomicAdd(&s_acc[c], static_cast<double>(val[start + x]));
@@ -893,14 +897,15 @@ __global__ __launch_bounds__(kBlock) void dense_unit_kernel(
             }
         }
         __syncthreads();
-        const unsigned word = s_bits[threadIdx.x];
+        const unsigned half = (s_bits[threadIdx.x >> 1] >> ((threadIdx.x & 1) * 16)) & 0xffffu;
         int total = 0;
-        int rank = dev::block_exclusive_sum<kBlock>(static_cast<int>(__popc(word)), s_wave, total);
-        unsigned m = word;
+        int rank = dev::block_exclusive_sum<kDenseBlock>(static_cast<int>(__popc(half)), s_wave,
+                                                         total);
+        unsigned m = half;
         while (m) {
             const int bit = __ffs(m) - 1;
             m &= m - 1;
-            const int c = threadIdx.x * 32 + bit;
+            const int c = threadIdx.x * 16 + bit;
             ukey[start + written + rank] = static_cast<int>(w0 + c);
             uval[start + written + rank] = static_cast<float>(s_acc[c]);
             ++rank;
@@ -1122,7 +1127,7 @@ int multiply(Call &call, const nacho_csr *a, const nacho_csr *b, Product *z) {
             NACHO_TRY_HIP(hipGetLastError());
         }
         if (n_kind[0] > 0) {
-            dense_unit_kernel<<<static_cast<unsigned>(n_kind[0]), kBlock, 0, st>>>(
+            dense_unit_kernel<<<static_cast<unsigned>(n_kind[0]), kDenseBlock, 0, st>>>(
                 dense_list, unit_seg, unit_start, seg_len, seg_prefix, seg_row, row_off, shift,
                 cols, key, val, ukey, uval, unit_nnz, row_unit, row_local);
             NACHO_TRY_HIP(hipGetLastError());
