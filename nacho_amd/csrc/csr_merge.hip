@@ -42,6 +42,7 @@
 #include "csr_merge.hpp"
 #include "device_utils.hpp"
 #include "runtime.hpp"
+#include "scan.hpp"
 
 namespace nacho {
 namespace csr {
@@ -388,7 +389,12 @@ __global__ __launch_bounds__(kBlock) void csr_count_kernel(
 // child_a[o] = next_a[a] and child_b[o] = next_b[b] at the A/B positions a, b reached before
 // o, so [child[o], child[o+1]) is the operand's child range under o, empty when absent; a
 // null next_a / next_b makes the child pointer the position itself).
-template <Op OP, int IPT, bool VALUES, bool CHILD>
+//
+// SPREAD (intersection only, no count pass): a tile's outputs go to cc/vc at the tile's own
+// start position in A (spread_by_a) or B, whose range holds every pair the tile can emit;
+// row ends write pos in those coordinates, and tile_count[t] receives the tile's length.
+// csr_compact_kernel then moves each tile to its final offset and corrects its rows' pos.
+template <Op OP, int IPT, bool VALUES, bool CHILD, bool SPREAD>
 __global__ __launch_bounds__(kBlock) void csr_write_kernel(
     const int *__restrict__ pa, const int *__restrict__ ca, const float *__restrict__ va,
     const int *__restrict__ pb, const int *__restrict__ cb, const float *__restrict__ vb,
@@ -397,8 +403,9 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
     const unsigned *__restrict__ chunk_count, int rows, int *__restrict__ pc,
     int *__restrict__ cc, float *__restrict__ vc, const int *__restrict__ next_a,
     const int *__restrict__ next_b, int *__restrict__ child_a, int *__restrict__ child_b,
-    unsigned *__restrict__ length) {
+    unsigned *__restrict__ length, int spread_by_a, int64_t *__restrict__ tile_count) {
     static_assert(!(VALUES && CHILD), "a level carries values or child pointers, not both");
+    static_assert(!SPREAD || (OP == Op::Intersect && !CHILD), "spread output: intersection");
     constexpr int kCap = kBlock * IPT + 2;
     constexpr int kLoads = (kCap + kBlock - 1) / kBlock;
     constexpr int kSteps = IPT + 1;
@@ -415,13 +422,15 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
     stage_splits(s_split, split_r, split_a, split_b, t0, t1);
 
     // Offset of this chunk: the counts of every earlier chunk.
-    int before = 0;
-    for (int i = tid; i < static_cast<int>(blockIdx.x); i += kBlock) before += chunk_count[i];
     int base = 0;
-    {
+    if (!SPREAD) {
+        int before = 0;
+        for (int i = tid; i < static_cast<int>(blockIdx.x); i += kBlock) before += chunk_count[i];
         int total = 0;
         (void)dev::block_exclusive_sum<kBlock>(before, s_wave, total);
         base = total;
+    } else {
+        __syncthreads();  // the staged splits
     }
     if (blockIdx.x == 0 && tid == 0) pc[0] = 0;
 
@@ -436,6 +445,7 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
         const TileSplit nsp2 = lds_split(s_split, t + 2 < t1 ? t + 2 - t0 : t + 1 < t1 ? t + 1 - t0 : t - t0);
         LaneOut<kSteps> lo;
         walk_lane<OP, VALUES, CHILD, IPT>(lo, sp, t, s_crd, s_val, s_row, tid);
+        if (SPREAD) base = spread_by_a ? sp.a0 : sp.b0;
 
         int tile_total = 0;
         const int offset =
@@ -482,8 +492,9 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
                 }
             }
         }
+        if (SPREAD && tid == 0) tile_count[t] = tile_total;
         base += tile_total;
-        if (t == num_tiles - 1 && tid == 0) {
+        if (!SPREAD && t == num_tiles - 1 && tid == 0) {
             *length = static_cast<unsigned>(base);
             if (CHILD) {
                 child_a[base] = next_a ? next_a[nnz_a] : nnz_a;
@@ -497,6 +508,30 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
         }
         sp = nsp;
         nsp = nsp2;
+    }
+}
+
+// Moves each tile's outputs from its spread position (csr_write_kernel<SPREAD>) to its final
+// offset tile_off[t] and shifts the pos entries of the rows ending in the tile (rows
+// [split_r[t], split_r[t + 1]), every remaining row for the last tile) by the same amount.
+// One workgroup per tile.
+__global__ __launch_bounds__(kBlock) void csr_compact_kernel(
+    const int *__restrict__ split_r, const int *__restrict__ split_a,
+    const int *__restrict__ split_b, int num_tiles, int rows, int spread_by_a,
+    const int64_t *__restrict__ tile_count, const int64_t *__restrict__ tile_off,
+    const int *__restrict__ tmp_crd, const float *__restrict__ tmp_val, int *__restrict__ pc,
+    int *__restrict__ cc, float *__restrict__ vc) {
+    const int t = blockIdx.x;
+    const int from = spread_by_a ? split_a[t] : split_b[t];
+    const int to = static_cast<int>(tile_off[t]);
+    const int n = static_cast<int>(tile_count[t]);
+    for (int q = threadIdx.x; q < n; q += kBlock) {
+        cc[to + q] = tmp_crd[from + q];
+        vc[to + q] = tmp_val[from + q];
+    }
+    const int r_end = t + 1 < num_tiles ? split_r[t + 1] : rows;
+    for (int r = split_r[t] + static_cast<int>(threadIdx.x); r < r_end; r += kBlock) {
+        pc[r + 1] += to - from;
     }
 }
 
@@ -517,9 +552,9 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
     // Grid: as many workgroups as stay resident, each owning a contiguous chunk of tiles.
     int resident = 0;
     const void *probe = values ? reinterpret_cast<const void *>(
-                                     csr_write_kernel<Op::Union, kItemsPerLane, true, false>)
+                                     csr_write_kernel<Op::Union, kItemsPerLane, true, false, false>)
                                : reinterpret_cast<const void *>(
-                                     csr_write_kernel<Op::Union, kItemsPerLane, false, true>);
+                                     csr_write_kernel<Op::Union, kItemsPerLane, false, true, false>);
     NACHO_TRY(resident_grid(probe, kBlock, &resident));
     int chunk = (num_tiles + resident - 1) / resident;
     if (chunk > kMaxChunk) chunk = kMaxChunk;  // more workgroups than resident: still correct
@@ -528,28 +563,55 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
     unsigned *length = counts + grid;
 
     const hipStream_t s = call.stream();
+    if (intersect) {
+        // One walk: each tile writes its pairs at its own position in the smaller operand's
+        // range of a scratch buffer, then one compaction moves them into place.
+        if (!values || child) return NACHO_ERR_INVALID_ARGUMENT;
+        const int by_a = A.len <= B.len ? 1 : 0;
+        const size_t cap = static_cast<size_t>(by_a ? A.len : B.len);
+        int *tmp_crd = nullptr;
+        float *tmp_val = nullptr;
+        int64_t *tile_count = nullptr, *tile_off = nullptr;
+        NACHO_TRY(call.scratch_n(cap, &tmp_crd));
+        NACHO_TRY(call.scratch_n(cap, &tmp_val));
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(num_tiles) + 1, &tile_count));
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(num_tiles) + 1, &tile_off));
+        NACHO_TRY(call.timer_start(kernel_name));  // the whole device pipeline of this level
+        csr_partition_kernel<<<ceil_div(static_cast<size_t>(num_tiles) + 1, 256), 256, 0, s>>>(
+            A.pos, A.crd, B.pos, B.crd, rows, static_cast<int>(total), num_tiles, split_r,
+            split_a, split_b);
+        NACHO_TRY_HIP(hipGetLastError());
+        csr_write_kernel<Op::Intersect, kItemsPerLane, true, false, true>
+            <<<grid, kBlock, 0, s>>>(A.pos, A.crd, A.val, B.pos, B.crd, B.val, A.len, B.len,
+                                     num_tiles, chunk, split_r, split_a, split_b, nullptr, rows,
+                                     Z.pos, tmp_crd, tmp_val, nullptr, nullptr, nullptr,
+                                     nullptr, nullptr, by_a, tile_count);
+        NACHO_TRY_HIP(hipGetLastError());
+        NACHO_TRY(scan::exclusive_scan_i64(call, tile_count, num_tiles, tile_off));
+        csr_compact_kernel<<<num_tiles, kBlock, 0, s>>>(split_r, split_a, split_b, num_tiles,
+                                                        rows, by_a, tile_count, tile_off,
+                                                        tmp_crd, tmp_val, Z.pos, Z.crd, Z.val);
+        NACHO_TRY_HIP(hipGetLastError());
+        NACHO_TRY(call.timer_stop());
+        int64_t len = 0;
+        NACHO_TRY(call.read_back(&len, tile_off + num_tiles, sizeof(len)));
+        *out_len = len;
+        return NACHO_OK;
+    }
     NACHO_TRY(call.timer_start(kernel_name));  // the whole device pipeline of this level
     csr_partition_kernel<<<ceil_div(static_cast<size_t>(num_tiles) + 1, 256), 256, 0, s>>>(
         A.pos, A.crd, B.pos, B.crd, rows, static_cast<int>(total), num_tiles, split_r, split_a,
         split_b);
     NACHO_TRY_HIP(hipGetLastError());
-    if (intersect) {
-        csr_count_kernel<Op::Intersect, kItemsPerLane><<<grid, kBlock, 0, s>>>(
-            A.pos, A.crd, B.pos, B.crd, num_tiles, chunk, split_r, split_a, split_b, counts);
-    } else {
-        csr_count_kernel<Op::Union, kItemsPerLane><<<grid, kBlock, 0, s>>>(
-            A.pos, A.crd, B.pos, B.crd, num_tiles, chunk, split_r, split_a, split_b, counts);
-    }
+    csr_count_kernel<Op::Union, kItemsPerLane><<<grid, kBlock, 0, s>>>(
+        A.pos, A.crd, B.pos, B.crd, num_tiles, chunk, split_r, split_a, split_b, counts);
     NACHO_TRY_HIP(hipGetLastError());
 #define NACHO_WRITE_LAUNCH(OPV, VAL, CHD)                                                        \
-    csr_write_kernel<OPV, kItemsPerLane, VAL, CHD><<<grid, kBlock, 0, s>>>(                      \
+    csr_write_kernel<OPV, kItemsPerLane, VAL, CHD, false><<<grid, kBlock, 0, s>>>(               \
         A.pos, A.crd, A.val, B.pos, B.crd, B.val, A.len, B.len, num_tiles, chunk, split_r,      \
         split_a, split_b, counts, rows, Z.pos, Z.crd, Z.val, A.next, B.next, Z.child_a,         \
-        Z.child_b, length)
-    if (intersect) {
-        if (!values || child) return NACHO_ERR_INVALID_ARGUMENT;
-        NACHO_WRITE_LAUNCH(Op::Intersect, true, false);
-    } else if (values) {
+        Z.child_b, length, 0, nullptr)
+    if (values) {
         if (child) return NACHO_ERR_INVALID_ARGUMENT;
         NACHO_WRITE_LAUNCH(Op::Union, true, false);
     } else if (child) {
