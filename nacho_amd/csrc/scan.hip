@@ -15,6 +15,7 @@ namespace scan {
 constexpr int kBlock = 256;
 constexpr int kPerThread = 16;
 constexpr int kChunk = kBlock * kPerThread;
+constexpr int64_t kSmall = 8 * kChunk;  // scanned by one workgroup in one launch
 
 __global__ __launch_bounds__(kBlock) void block_sums_kernel(const int64_t *__restrict__ in,
                                                             int64_t n,
@@ -32,18 +33,19 @@ __global__ __launch_bounds__(kBlock) void block_sums_kernel(const int64_t *__res
     if (threadIdx.x == 0) sums[blockIdx.x] = total;
 }
 
-// One workgroup: exclusive scan of the block sums in place; total to *grand.
-__global__ __launch_bounds__(kBlock) void scan_sums_kernel(int64_t *__restrict__ sums, int64_t nb,
-                                                           int64_t *__restrict__ grand) {
+// One workgroup: exclusive scan of in[0, n) into out (in == out allowed), chunk by chunk with
+// a running carry; the total goes to *grand.
+__device__ __forceinline__ void scan_one_workgroup(const int64_t *in, int64_t n, int64_t *out,
+                                                   int64_t *grand) {
     __shared__ int64_t s_wave[kBlock / dev::kWave];
     int64_t carry = 0;
-    for (int64_t start = 0; start < nb; start += kChunk) {
+    for (int64_t start = 0; start < n; start += kChunk) {
         int64_t v[kPerThread];
         int64_t mine = 0;
 #pragma unroll
         for (int j = 0; j < kPerThread; ++j) {
             const int64_t i = start + static_cast<int64_t>(threadIdx.x) * kPerThread + j;
-            v[j] = i < nb ? sums[i] : 0;
+            v[j] = i < n ? in[i] : 0;
             mine += v[j];
         }
         int64_t total = 0;
@@ -51,12 +53,24 @@ __global__ __launch_bounds__(kBlock) void scan_sums_kernel(int64_t *__restrict__
 #pragma unroll
         for (int j = 0; j < kPerThread; ++j) {
             const int64_t i = start + static_cast<int64_t>(threadIdx.x) * kPerThread + j;
-            if (i < nb) sums[i] = run;
+            if (i < n) out[i] = run;
             run += v[j];
         }
         carry += total;
     }
     if (threadIdx.x == 0) *grand = carry;
+}
+
+// Exclusive scan of the block sums in place; total to *grand.
+__global__ __launch_bounds__(kBlock) void scan_sums_kernel(int64_t *sums, int64_t nb,
+                                                           int64_t *__restrict__ grand) {
+    scan_one_workgroup(sums, nb, sums, grand);
+}
+
+// Short inputs in one launch: out[0, n) and out[n] = total.
+__global__ __launch_bounds__(kBlock) void scan_small_kernel(const int64_t *in, int64_t n,
+                                                            int64_t *out) {
+    scan_one_workgroup(in, n, out, out + n);
 }
 
 __global__ __launch_bounds__(kBlock) void scan_blocks_kernel(const int64_t *__restrict__ in,
@@ -90,6 +104,11 @@ __global__ void copy_total_kernel(const int64_t *__restrict__ grand, int64_t *__
 
 int exclusive_scan_i64(Call &call, const int64_t *in, int64_t n, int64_t *out) {
     const hipStream_t s = call.stream();
+    if (n <= kSmall) {  // one workgroup, one launch: launch latency dominates short scans
+        scan_small_kernel<<<1, kBlock, 0, s>>>(in, n, out);
+        NACHO_TRY_HIP(hipGetLastError());
+        return NACHO_OK;
+    }
     const int64_t nb = n > 0 ? (n + kChunk - 1) / kChunk : 0;
     int64_t *sums = nullptr;
     NACHO_TRY(call.scratch_n(static_cast<size_t>(nb) + 2, &sums));
