@@ -35,11 +35,13 @@ __global__ __launch_bounds__(kBlock) void block_sums_kernel(const int64_t *__res
 
 // One workgroup: exclusive scan of in[0, n) into out (in == out allowed), chunk by chunk with
 // a running carry; the total goes to *grand.
+template <int BLOCK>
 __device__ __forceinline__ void scan_one_workgroup(const int64_t *in, int64_t n, int64_t *out,
                                                    int64_t *grand) {
-    __shared__ int64_t s_wave[kBlock / dev::kWave];
+    constexpr int kStep = BLOCK * kPerThread;
+    __shared__ int64_t s_wave[BLOCK / dev::kWave];
     int64_t carry = 0;
-    for (int64_t start = 0; start < n; start += kChunk) {
+    for (int64_t start = 0; start < n; start += kStep) {
         int64_t v[kPerThread];
         int64_t mine = 0;
 #pragma unroll
@@ -49,7 +51,7 @@ __device__ __forceinline__ void scan_one_workgroup(const int64_t *in, int64_t n,
             mine += v[j];
         }
         int64_t total = 0;
-        int64_t run = carry + dev::block_exclusive_sum<kBlock>(mine, s_wave, total);
+        int64_t run = carry + dev::block_exclusive_sum<BLOCK>(mine, s_wave, total);
 #pragma unroll
         for (int j = 0; j < kPerThread; ++j) {
             const int64_t i = start + static_cast<int64_t>(threadIdx.x) * kPerThread + j;
@@ -64,13 +66,14 @@ __device__ __forceinline__ void scan_one_workgroup(const int64_t *in, int64_t n,
 // Exclusive scan of the block sums in place; total to *grand.
 __global__ __launch_bounds__(kBlock) void scan_sums_kernel(int64_t *sums, int64_t nb,
                                                            int64_t *__restrict__ grand) {
-    scan_one_workgroup(sums, nb, sums, grand);
+    scan_one_workgroup<kBlock>(sums, nb, sums, grand);
 }
 
-// Short inputs in one launch: out[0, n) and out[n] = total.
-__global__ __launch_bounds__(kBlock) void scan_small_kernel(const int64_t *in, int64_t n,
-                                                            int64_t *out) {
-    scan_one_workgroup(in, n, out, out + n);
+// Short inputs in one launch of one wide workgroup: out[0, n) and out[n] = total.
+constexpr int kSmallBlock = 1024;
+__global__ __launch_bounds__(kSmallBlock) void scan_small_kernel(const int64_t *in, int64_t n,
+                                                                 int64_t *out) {
+    scan_one_workgroup<kSmallBlock>(in, n, out, out + n);
 }
 
 __global__ __launch_bounds__(kBlock) void scan_blocks_kernel(const int64_t *__restrict__ in,
@@ -105,7 +108,7 @@ __global__ void copy_total_kernel(const int64_t *__restrict__ grand, int64_t *__
 int exclusive_scan_i64(Call &call, const int64_t *in, int64_t n, int64_t *out) {
     const hipStream_t s = call.stream();
     if (n <= kSmall) {  // one workgroup, one launch: launch latency dominates short scans
-        scan_small_kernel<<<1, kBlock, 0, s>>>(in, n, out);
+        scan_small_kernel<<<1, kSmallBlock, 0, s>>>(in, n, out);
         NACHO_TRY_HIP(hipGetLastError());
         return NACHO_OK;
     }
