@@ -42,7 +42,6 @@
 #include "csr_merge.hpp"
 #include "device_utils.hpp"
 #include "runtime.hpp"
-#include "scan.hpp"
 
 namespace nacho {
 namespace csr {
@@ -392,8 +391,9 @@ __global__ __launch_bounds__(kBlock) void csr_count_kernel(
 //
 // SPREAD (intersection only, no count pass): a tile's outputs go to cc/vc at the tile's own
 // start position in A (spread_by_a) or B, whose range holds every pair the tile can emit;
-// row ends write pos in those coordinates, and tile_count[t] receives the tile's length.
-// csr_compact_kernel then moves each tile to its final offset and corrects its rows' pos.
+// row ends write pos in those coordinates, tile_count[t] receives the tile's length and
+// chunk_total[w] the sum over workgroup w's chunk.  csr_compact_kernel then moves each tile
+// to its final offset and corrects its rows' pos.
 template <Op OP, int IPT, bool VALUES, bool CHILD, bool SPREAD>
 __global__ __launch_bounds__(kBlock) void csr_write_kernel(
     const int *__restrict__ pa, const int *__restrict__ ca, const float *__restrict__ va,
@@ -403,7 +403,8 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
     const unsigned *__restrict__ chunk_count, int rows, int *__restrict__ pc,
     int *__restrict__ cc, float *__restrict__ vc, const int *__restrict__ next_a,
     const int *__restrict__ next_b, int *__restrict__ child_a, int *__restrict__ child_b,
-    unsigned *__restrict__ length, int spread_by_a, int64_t *__restrict__ tile_count) {
+    unsigned *__restrict__ length, int spread_by_a, int64_t *__restrict__ tile_count,
+    int64_t *__restrict__ chunk_total) {
     static_assert(!(VALUES && CHILD), "a level carries values or child pointers, not both");
     static_assert(!SPREAD || (OP == Op::Intersect && !CHILD), "spread output: intersection");
     constexpr int kCap = kBlock * IPT + 2;
@@ -440,6 +441,7 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
     stage_tile<VALUES, kLoads>(st, sp, s_crd, s_val, s_row, tid);
     __syncthreads();
     TileSplit nsp = lds_split(s_split, t0 + 1 < t1 ? 1 : 0);
+    int64_t spread_sum = 0;
     for (int t = t0; t < t1; ++t) {
         fetch_tile<VALUES, kLoads>(st, nsp, pa, ca, va, pb, cb, vb, tid);
         const TileSplit nsp2 = lds_split(s_split, t + 2 < t1 ? t + 2 - t0 : t + 1 < t1 ? t + 1 - t0 : t - t0);
@@ -492,7 +494,11 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
                 }
             }
         }
-        if (SPREAD && tid == 0) tile_count[t] = tile_total;
+        if (SPREAD && tid == 0) {
+            tile_count[t] = tile_total;
+            spread_sum += tile_total;
+            if (t + 1 == t1) chunk_total[blockIdx.x] = spread_sum;
+        }
         base += tile_total;
         if (!SPREAD && t == num_tiles - 1 && tid == 0) {
             *length = static_cast<unsigned>(base);
@@ -512,19 +518,28 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
 }
 
 // Moves each tile's outputs from its spread position (csr_write_kernel<SPREAD>) to its final
-// offset tile_off[t] and shifts the pos entries of the rows ending in the tile (rows
+// offset and shifts the pos entries of the rows ending in the tile (rows
 // [split_r[t], split_r[t + 1]), every remaining row for the last tile) by the same amount.
-// One workgroup per tile.
+// The offset is the sum of the earlier chunks' totals and of the earlier tiles of its own
+// chunk (`chunk` tiles per chunk).  One workgroup per tile; the last one stores the length.
 __global__ __launch_bounds__(kBlock) void csr_compact_kernel(
     const int *__restrict__ split_r, const int *__restrict__ split_a,
-    const int *__restrict__ split_b, int num_tiles, int rows, int spread_by_a,
-    const int64_t *__restrict__ tile_count, const int64_t *__restrict__ tile_off,
+    const int *__restrict__ split_b, int num_tiles, int chunk, int rows, int spread_by_a,
+    const int64_t *__restrict__ tile_count, const int64_t *__restrict__ chunk_total,
     const int *__restrict__ tmp_crd, const float *__restrict__ tmp_val, int *__restrict__ pc,
-    int *__restrict__ cc, float *__restrict__ vc) {
+    int *__restrict__ cc, float *__restrict__ vc, int64_t *__restrict__ length) {
+    __shared__ int64_t s_wave[kBlock / dev::kWave];
     const int t = blockIdx.x;
+    const int c = t / chunk;
+    int64_t before = 0;
+    for (int i = threadIdx.x; i < c; i += kBlock) before += chunk_total[i];
+    for (int i = c * chunk + static_cast<int>(threadIdx.x); i < t; i += kBlock) before += tile_count[i];
+    int64_t to64 = 0;
+    (void)dev::block_exclusive_sum<kBlock>(before, s_wave, to64);
     const int from = spread_by_a ? split_a[t] : split_b[t];
-    const int to = static_cast<int>(tile_off[t]);
+    const int to = static_cast<int>(to64);
     const int n = static_cast<int>(tile_count[t]);
+    if (t == num_tiles - 1 && threadIdx.x == 0) *length = to64 + n;
     for (int q = threadIdx.x; q < n; q += kBlock) {
         cc[to + q] = tmp_crd[from + q];
         vc[to + q] = tmp_val[from + q];
@@ -571,11 +586,12 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
         const size_t cap = static_cast<size_t>(by_a ? A.len : B.len);
         int *tmp_crd = nullptr;
         float *tmp_val = nullptr;
-        int64_t *tile_count = nullptr, *tile_off = nullptr;
+        int64_t *tile_count = nullptr, *chunk_total = nullptr;
         NACHO_TRY(call.scratch_n(cap, &tmp_crd));
         NACHO_TRY(call.scratch_n(cap, &tmp_val));
-        NACHO_TRY(call.scratch_n(static_cast<size_t>(num_tiles) + 1, &tile_count));
-        NACHO_TRY(call.scratch_n(static_cast<size_t>(num_tiles) + 1, &tile_off));
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(num_tiles), &tile_count));
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(grid) + 1, &chunk_total));
+        int64_t *len_dev = chunk_total + grid;
         NACHO_TRY(call.timer_start(kernel_name));  // the whole device pipeline of this level
         csr_partition_kernel<<<ceil_div(static_cast<size_t>(num_tiles) + 1, 256), 256, 0, s>>>(
             A.pos, A.crd, B.pos, B.crd, rows, static_cast<int>(total), num_tiles, split_r,
@@ -585,16 +601,15 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
             <<<grid, kBlock, 0, s>>>(A.pos, A.crd, A.val, B.pos, B.crd, B.val, A.len, B.len,
                                      num_tiles, chunk, split_r, split_a, split_b, nullptr, rows,
                                      Z.pos, tmp_crd, tmp_val, nullptr, nullptr, nullptr,
-                                     nullptr, nullptr, by_a, tile_count);
+                                     nullptr, nullptr, by_a, tile_count, chunk_total);
         NACHO_TRY_HIP(hipGetLastError());
-        NACHO_TRY(scan::exclusive_scan_i64(call, tile_count, num_tiles, tile_off));
-        csr_compact_kernel<<<num_tiles, kBlock, 0, s>>>(split_r, split_a, split_b, num_tiles,
-                                                        rows, by_a, tile_count, tile_off,
-                                                        tmp_crd, tmp_val, Z.pos, Z.crd, Z.val);
+        csr_compact_kernel<<<num_tiles, kBlock, 0, s>>>(
+            split_r, split_a, split_b, num_tiles, chunk, rows, by_a, tile_count, chunk_total,
+            tmp_crd, tmp_val, Z.pos, Z.crd, Z.val, len_dev);
         NACHO_TRY_HIP(hipGetLastError());
         NACHO_TRY(call.timer_stop());
         int64_t len = 0;
-        NACHO_TRY(call.read_back(&len, tile_off + num_tiles, sizeof(len)));
+        NACHO_TRY(call.read_back(&len, len_dev, sizeof(len)));
         *out_len = len;
         return NACHO_OK;
     }
@@ -610,7 +625,7 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
     csr_write_kernel<OPV, kItemsPerLane, VAL, CHD, false><<<grid, kBlock, 0, s>>>(               \
         A.pos, A.crd, A.val, B.pos, B.crd, B.val, A.len, B.len, num_tiles, chunk, split_r,      \
         split_a, split_b, counts, rows, Z.pos, Z.crd, Z.val, A.next, B.next, Z.child_a,         \
-        Z.child_b, length, 0, nullptr)
+        Z.child_b, length, 0, nullptr, nullptr)
     if (values) {
         if (child) return NACHO_ERR_INVALID_ARGUMENT;
         NACHO_WRITE_LAUNCH(Op::Union, true, false);
