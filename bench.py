@@ -1,7 +1,7 @@
 """Benchmark of the nacho GPU path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--workload c2|c3|c4|c5|c5coo|c2coo|c2dcsr|c3dcsr|c2add3|c4sssmm]
+                    [--workload c2|c3|c4|c5|c5coo|c2coo|c3coo|c2dcsr|c3dcsr|c2add3|c4sssmm]
 
 A step is one call of the hot path over one batch of synthetic input, with the operands
 already resident in HBM: `nacho_amd.gpu_csr_add_f32(A, B)` for the default workload (C2:
@@ -27,8 +27,8 @@ time, P = number of intermediate products; its roofline bytes are
 4*(n+1) + 8*nnzA + 8*P (B's gathered entries) + 8*(n+1) + 8*nnzC, and its CPU baseline is
 the row-parallel C SpGEMM of oracle/ on a random row sample.
 
-Workloads c5 (csf_add), c5coo (coo3d_add), c2coo (coo_add), c2dcsr (dcsr_add) and c3dcsr
-(dcsr_mul) report GB/s of algorithmic bytes: CSF3 and DCSR count every level array of A, B
+Workloads c5 (csf_add), c5coo (coo3d_add), c2coo (coo_add), c3coo (coo_mul), c2dcsr
+(dcsr_add) and c3dcsr (dcsr_mul) report GB/s of algorithmic bytes: CSF3 and DCSR count every level array of A, B
 and C once; COO3 16 bytes and COO 12 bytes per entry of A, B and C.
 """
 
@@ -65,6 +65,9 @@ WORKLOADS = {
     "c5coo": dict(op="coo3d_add", kernel="coo_partition_kernel + coo_count_kernel + "
                                          "coo_write_kernel (packed 64-bit keys)",
                   desc="C5 as COO3: coo3d_add f32 of the same (i, j, k) tuples"),
+    "c3coo": dict(op="coo_mul", kernel="coo_partition_kernel + coo_write_kernel (spread) + "
+                                      "coo_compact_kernel (packed 64-bit keys)",
+                  desc="C3 as COO: coo_mul f32 of the C3 operands' (i, j) tuples"),
     "c2coo": dict(op="coo_add", kernel="coo_partition_kernel + coo_count_kernel + "
                                       "coo_write_kernel (packed 64-bit keys)",
                   desc="C2 as COO: coo_add f32 of the C2 operands' (i, j) tuples"),
@@ -473,8 +476,9 @@ def bench_tuple_workload(args, device, workload):
         ops = synth.c2_operands() if workload == "c2dcsr" else synth.c3_operands()
         ops_np = [(dcsr_levels(p, c), v) for p, c, v in ops]
         shape = (len(ops[0][0]) - 1, len(ops[0][0]) - 1)
-    elif workload == "c2coo":
-        (pa, ca, va), (pb, cb, vb) = synth.c2_operands()
+    elif workload in ("c2coo", "c3coo"):
+        ops = synth.c2_operands() if workload == "c2coo" else synth.c3_operands()
+        (pa, ca, va), (pb, cb, vb) = ops
         rows = len(pa) - 1
         ia = np.repeat(np.arange(rows, dtype=np.int32), np.diff(pa))
         ib = np.repeat(np.arange(rows, dtype=np.int32), np.diff(pb))
@@ -493,7 +497,7 @@ def bench_tuple_workload(args, device, workload):
         dims = torch.tensor(list(shape), dtype=torch.int32)
         if workload in ("c2dcsr", "c3dcsr"):
             return nacho_amd.DCSR_gpu(t[0], t[1], t[2], v, dims)
-        if workload == "c2coo":
+        if workload in ("c2coo", "c3coo"):
             return nacho_amd.COO_gpu(t[0], t[1], v, dims)
         if workload == "c5coo":
             return nacho_amd.COO3_gpu(t[0], t[1], t[2], v, dims)
@@ -502,7 +506,8 @@ def bench_tuple_workload(args, device, workload):
         return nacho_amd.CSF3_gpu(*lv, v, dims)
 
     copies = [tuple(upload(*o) for o in ops_np) for _ in range(ROTATE)]
-    fn = {"c2coo": nacho_amd.gpu_coo_add_f32, "c5coo": nacho_amd.gpu_coo3d_add_f32,
+    fn = {"c2coo": nacho_amd.gpu_coo_add_f32, "c3coo": nacho_amd.gpu_coo_mul_f32,
+          "c5coo": nacho_amd.gpu_coo3d_add_f32,
           "c5": nacho_amd.gpu_csf_add_f32, "c2dcsr": nacho_amd.gpu_dcsr_add_f32,
           "c3dcsr": nacho_amd.gpu_dcsr_mul_f32}[workload]
     z = fn(*copies[0])
@@ -519,7 +524,7 @@ def bench_tuple_workload(args, device, workload):
         alg_bytes += 4 * (z.dim_i_indices.numel() + z.dim_j_offsets.numel()
                           + 2 * z.dim_j_indices.numel())
     else:
-        alg_bytes = (12 if workload == "c2coo" else 16) * sum(nnz)
+        alg_bytes = (12 if workload in ("c2coo", "c3coo") else 16) * sum(nnz)
     del z
     log(f"nnzC={nnz[2]} algorithmic bytes/call={alg_bytes}")
 
@@ -562,8 +567,9 @@ def bench_tuple_workload(args, device, workload):
                                        csf3_levels(np.stack(ops_np[1][0], axis=1)), ops_np[1][1],
                                        timing=t)
             else:
-                oracle.port_coo_binary("add", ops_np[0][0], ops_np[0][1], ops_np[1][0],
-                                       ops_np[1][1], nthreads=cores, timing=t)
+                oracle.port_coo_binary("mul" if workload == "c3coo" else "add", ops_np[0][0],
+                                       ops_np[0][1], ops_np[1][0], ops_np[1][1],
+                                       nthreads=cores, timing=t)
             times.append(t["seconds"])
         sec = sorted(times)[len(times) // 2]
         serial = workload in ("c5", "c2dcsr", "c3dcsr")
@@ -655,7 +661,7 @@ def main():
     if args.workload == "c4sssmm":
         print(json.dumps(bench_sssmm(args, device)), flush=True)
         return
-    if args.workload in ("c5", "c5coo", "c2coo", "c2dcsr", "c3dcsr"):
+    if args.workload in ("c5", "c5coo", "c2coo", "c3coo", "c2dcsr", "c3dcsr"):
         print(json.dumps(bench_tuple_workload(args, device, args.workload)), flush=True)
         return
 

@@ -295,12 +295,18 @@ __global__ __launch_bounds__(kBlock) void coo_count_kernel(Codec codec, Coords c
     if (tid == 0) chunk_count[blockIdx.x] = total;
 }
 
-template <Op OP, typename Codec>
+// SPREAD (intersection only, no count pass): a tile's outputs go to zi/zj/zk/zv at the
+// tile's own start position in A (spread_by_a) or B, whose range holds every pair the tile
+// can emit; tile_count[t] receives the tile's length and chunk_total[w] the sum over
+// workgroup w's chunk.  coo_compact_kernel then moves each tile to its final offset.
+template <Op OP, typename Codec, bool SPREAD>
 __global__ __launch_bounds__(kBlock) void coo_write_kernel(
     Codec codec, Coords ca, const float *__restrict__ va, Coords cb, const float *__restrict__ vb,
     int num_tiles, int chunk, const int *__restrict__ split_a, const int *__restrict__ split_b,
     const unsigned *__restrict__ chunk_count, int *__restrict__ zi, int *__restrict__ zj,
-    int *__restrict__ zk, float *__restrict__ zv, unsigned *__restrict__ length) {
+    int *__restrict__ zk, float *__restrict__ zv, unsigned *__restrict__ length,
+    int spread_by_a, int64_t *__restrict__ tile_count, int64_t *__restrict__ chunk_total) {
+    static_assert(!SPREAD || OP == Op::Intersect, "spread output: intersection");
     using Key = typename Codec::Key;
     constexpr int kCap = kTile + 2;
     constexpr int kLoads = (kCap + kBlock - 1) / kBlock;
@@ -313,20 +319,26 @@ __global__ __launch_bounds__(kBlock) void coo_write_kernel(
     const int t0 = blockIdx.x * chunk, t1 = min(t0 + chunk, num_tiles);
     if (t0 >= t1) return;
     stage_splits(s_split, split_a, split_b, t0, t1);
-    int before = 0;
-    for (int i = tid; i < static_cast<int>(blockIdx.x); i += kBlock) before += chunk_count[i];
     int base = 0;
-    (void)dev::block_exclusive_sum<kBlock>(before, s_wave, base);
+    if (!SPREAD) {
+        int before = 0;
+        for (int i = tid; i < static_cast<int>(blockIdx.x); i += kBlock) before += chunk_count[i];
+        (void)dev::block_exclusive_sum<kBlock>(before, s_wave, base);
+    } else {
+        __syncthreads();  // the staged splits
+    }
 
     StagedKeys<Key, kLoads> st;
     fetch_keys<true>(st, codec, s_split, 0, ca, va, cb, vb, tid);
     stage_keys<true>(st, s_split, 0, s_key, s_val, tid);
     __syncthreads();
+    int64_t spread_sum = 0;
     for (int t = t0; t < t1; ++t) {
         const int i = t - t0;
         if (t + 1 < t1) fetch_keys<true>(st, codec, s_split, i + 1, ca, va, cb, vb, tid);
         KeyLaneOut<OP, true, Key, kSteps> lo;
         walk_keys<OP, true, Key>(lo, s_split, i, t, s_key, s_val, tid);
+        if (SPREAD) base = spread_by_a ? s_split[2 * i] : s_split[2 * i + 1];
         int tile_total = 0;
         const int offset =
             dev::block_exclusive_sum<kBlock>(static_cast<int>(__popc(lo.valid)), s_wave, tile_total);
@@ -352,13 +364,48 @@ __global__ __launch_bounds__(kBlock) void coo_write_kernel(
                 zv[base + q] = s_val[q];
             }
         }
+        if (SPREAD && tid == 0) {
+            tile_count[t] = tile_total;
+            spread_sum += tile_total;
+            if (t + 1 == t1) chunk_total[blockIdx.x] = spread_sum;
+        }
         base += tile_total;
-        if (t == num_tiles - 1 && tid == 0) *length = static_cast<unsigned>(base);
+        if (!SPREAD && t == num_tiles - 1 && tid == 0) *length = static_cast<unsigned>(base);
         __syncthreads();
         if (t + 1 < t1) {
             stage_keys<true>(st, s_split, i + 1, s_key, s_val, tid);
             __syncthreads();
         }
+    }
+}
+
+// Moves each tile's outputs from its spread position (coo_write_kernel<SPREAD>) to its final
+// offset: the sum of the earlier chunks' totals and of the earlier tiles of its own chunk
+// (`chunk` tiles per chunk).  One workgroup per tile; the last one stores the length.
+__global__ __launch_bounds__(kBlock) void coo_compact_kernel(
+    const int *__restrict__ split_a, const int *__restrict__ split_b, int num_tiles, int chunk,
+    int spread_by_a, int arity, const int64_t *__restrict__ tile_count,
+    const int64_t *__restrict__ chunk_total, const int *__restrict__ ti,
+    const int *__restrict__ tj, const int *__restrict__ tk, const float *__restrict__ tv,
+    int *__restrict__ zi, int *__restrict__ zj, int *__restrict__ zk, float *__restrict__ zv,
+    int64_t *__restrict__ length) {
+    __shared__ int64_t s_wave[kBlock / dev::kWave];
+    const int t = blockIdx.x;
+    const int c = t / chunk;
+    int64_t before = 0;
+    for (int i = threadIdx.x; i < c; i += kBlock) before += chunk_total[i];
+    for (int i = c * chunk + static_cast<int>(threadIdx.x); i < t; i += kBlock) before += tile_count[i];
+    int64_t to64 = 0;
+    (void)dev::block_exclusive_sum<kBlock>(before, s_wave, to64);
+    const int from = spread_by_a ? split_a[t] : split_b[t];
+    const int to = static_cast<int>(to64);
+    const int n = static_cast<int>(tile_count[t]);
+    if (t == num_tiles - 1 && threadIdx.x == 0) *length = to64 + n;
+    for (int q = threadIdx.x; q < n; q += kBlock) {
+        zi[to + q] = ti[from + q];
+        zj[to + q] = tj[from + q];
+        if (arity == 3) zk[to + q] = tk[from + q];
+        zv[to + q] = tv[from + q];
     }
 }
 
@@ -403,13 +450,46 @@ int coo_binary(int arity, const int32_t extents[3], Coords ca, const float *va, 
     unsigned *counts = nullptr;
     auto launch = [&](auto codec) -> int {
         using Codec = decltype(codec);
+        constexpr bool kSpread = OP == Op::Intersect;
         int resident = 0;
-        NACHO_TRY(resident_grid(reinterpret_cast<const void *>(coo_write_kernel<OP, Codec>),
-                                kBlock, &resident));
+        NACHO_TRY(resident_grid(
+            reinterpret_cast<const void *>(coo_write_kernel<OP, Codec, kSpread>), kBlock,
+            &resident));
         int chunk = (num_tiles + resident - 1) / resident;
         if (chunk > kMaxChunk) chunk = kMaxChunk;
         const int grid = (num_tiles + chunk - 1) / chunk;
         NACHO_TRY(call.scratch_n(static_cast<size_t>(grid) + 4, &counts));
+        if (kSpread) {
+            // One walk: each tile writes its pairs at its own position in the smaller
+            // operand's range of scratch arrays, then one compaction moves them into place.
+            const int by_a = nnz_a <= nnz_b ? 1 : 0;
+            int32_t *t[3] = {nullptr, nullptr, nullptr};
+            float *tv = nullptr;
+            int64_t *tile_count = nullptr, *chunk_total = nullptr;
+            for (int d = 0; d < arity; ++d) NACHO_TRY(call.scratch_n(static_cast<size_t>(cap), &t[d]));
+            NACHO_TRY(call.scratch_n(static_cast<size_t>(cap), &tv));
+            NACHO_TRY(call.scratch_n(static_cast<size_t>(num_tiles), &tile_count));
+            NACHO_TRY(call.scratch_n(static_cast<size_t>(grid) + 1, &chunk_total));
+            int64_t *len_dev = chunk_total + grid;
+            NACHO_TRY(call.timer_start(kernel_name));
+            coo_partition_kernel<Codec><<<part_grid, 256, 0, s>>>(codec, ca, nnz_a, cb, nnz_b,
+                                                                  num_tiles, split_a, split_b);
+            NACHO_TRY_HIP(hipGetLastError());
+            coo_write_kernel<OP, Codec, kSpread><<<grid, kBlock, 0, s>>>(
+                codec, ca, va, cb, vb, num_tiles, chunk, split_a, split_b, nullptr, t[0], t[1],
+                t[2], tv, nullptr, by_a, tile_count, chunk_total);
+            NACHO_TRY_HIP(hipGetLastError());
+            coo_compact_kernel<<<num_tiles, kBlock, 0, s>>>(
+                split_a, split_b, num_tiles, chunk, by_a, arity, tile_count, chunk_total, t[0],
+                t[1], t[2], tv, z[0], z[1], z[2], zv, len_dev);
+            NACHO_TRY_HIP(hipGetLastError());
+            NACHO_TRY(call.timer_stop());
+            int64_t len = 0;
+            NACHO_TRY(call.read_back(&len, len_dev, sizeof(len)));
+            if (len > INT_MAX) return NACHO_ERR_INDEX_OVERFLOW;
+            *out_nnz = static_cast<int32_t>(len);
+            return NACHO_OK;
+        }
         NACHO_TRY(call.timer_start(kernel_name));
         coo_partition_kernel<Codec><<<part_grid, 256, 0, s>>>(codec, ca, nnz_a, cb, nnz_b, num_tiles,
                                                               split_a, split_b);
@@ -417,9 +497,9 @@ int coo_binary(int arity, const int32_t extents[3], Coords ca, const float *va, 
         coo_count_kernel<OP, Codec><<<grid, kBlock, 0, s>>>(codec, ca, cb, num_tiles, chunk, split_a,
                                                             split_b, counts);
         NACHO_TRY_HIP(hipGetLastError());
-        coo_write_kernel<OP, Codec><<<grid, kBlock, 0, s>>>(codec, ca, va, cb, vb, num_tiles, chunk,
-                                                            split_a, split_b, counts, z[0], z[1],
-                                                            z[2], zv, counts + grid);
+        coo_write_kernel<OP, Codec, false><<<grid, kBlock, 0, s>>>(
+            codec, ca, va, cb, vb, num_tiles, chunk, split_a, split_b, counts, z[0], z[1], z[2],
+            zv, counts + grid, 0, nullptr, nullptr);
         NACHO_TRY_HIP(hipGetLastError());
         NACHO_TRY(call.timer_stop());
         unsigned len = 0;
