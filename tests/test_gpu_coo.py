@@ -101,3 +101,32 @@ def test_c5_coo3_reduced(gpu):
     tb = tuple(bc[:, d] for d in range(3))
     got = run("add", synth.C5_SHAPE, ta, av, tb, bv, gpu)
     assert_coo_equal(got, oracle.port_coo_binary("add", ta, av, tb, bv, nthreads=16), "C5 2M")
+
+
+def _coo_of(csr):
+    pos, crd, val = csr
+    rows = np.repeat(np.arange(len(pos) - 1, dtype=np.int32), np.diff(pos))
+    return (rows, crd), val
+
+
+@pytest.mark.parametrize("op", ["add", "mul"])
+def test_c2_c3_full_size(gpu, op):
+    """C2 (coo_add) and C3 (coo_mul) operands as COO at their full size (16.7M nnz each)."""
+    from nacho_amd import synth
+
+    ops = synth.c2_operands() if op == "add" else synth.c3_operands()
+    (ta, va), (tb, vb) = (_coo_of(t) for t in ops)
+    shape = (synth.C2_ROWS, synth.C2_ROWS)
+    got = run(op, shape, ta, va, tb, vb, gpu)
+    assert_coo_equal(got, oracle.port_coo_binary(op, ta, va, tb, vb, nthreads=16), f"C{op}")
+
+
+def test_c5_coo3_full_size(gpu):
+    """The C5 configuration at its full size (20M draws per operand)."""
+    from nacho_amd import synth
+
+    (ac, av), (bc, bv) = synth.c5_operands()
+    ta = tuple(ac[:, d] for d in range(3))
+    tb = tuple(bc[:, d] for d in range(3))
+    got = run("add", synth.C5_SHAPE, ta, av, tb, bv, gpu)
+    assert_coo_equal(got, oracle.port_coo_binary("add", ta, av, tb, bv, nthreads=16), "C5")

@@ -74,3 +74,11 @@ def test_c5_reduced(gpu):
 
     (ac, av), (bc, bv) = (synth.zipf3_coords(2_000_000, synth.C5_SHAPE, s) for s in (1, 2))
     assert_csf_equal(run(synth.C5_SHAPE, ac, av, bc, bv, gpu), want(ac, av, bc, bv), "C5 2M")
+
+
+def test_c5_full_size(gpu):
+    """The C5 configuration at its full size (20M draws per operand)."""
+    from nacho_amd import synth
+
+    (ac, av), (bc, bv) = synth.c5_operands()
+    assert_csf_equal(run(synth.C5_SHAPE, ac, av, bc, bv, gpu), want(ac, av, bc, bv), "C5 full")
