@@ -222,7 +222,6 @@ __device__ __forceinline__ void walk_lane(LaneOut<IPT + 1> &out, const TileSplit
                                           const unsigned *s_row, int tid) {
     constexpr int kSteps = IPT + 1;
     constexpr int kMax = INT_MAX;  // head sentinel: row exhausted on that side
-    constexpr int kCapIdx = kBlock * IPT + 1;  // last index of the staged arrays
     const int r0 = sp.r0, a0 = sp.a0, b0 = sp.b0, r1 = sp.r1, a1 = sp.a1, b1 = sp.b1;
     const int na = a1 - a0, nr = r1 - r0 + 1;
     auto A = [&](int x) { return s_crd[x - a0]; };
@@ -265,11 +264,19 @@ __device__ __forceinline__ void walk_lane(LaneOut<IPT + 1> &out, const TileSplit
         b = D - slo;
     }
     out.first_row = r0 + k;
-    int aE = k < nr - 1 ? row_a(k + 1) : a1;
-    int bE = k < nr - 1 ? row_b(k + 1) : b1;
-    int last_a = a > row_a(k) ? A(a - 1) : -1;  // previous A of this row inside the tile
-    int xa = a < aE ? A(a) : kMax;
-    int xb = b < bE ? B(b) : kMax;
+    // From here positions are indices into the staged arrays: A's entries at [0, na), B's at
+    // [na, na + nb).  A tile holds at most kTile + 1 entries (the pair rule adds one), so
+    // every index read below, one past a row's last entry included, is < kCap.
+    const int nb = b1 - b0;
+    auto end_a = [&](int kk) { return kk < nr - 1 ? static_cast<int>(s_row[kk + 1] & 0xffffu) : na; };
+    auto end_b = [&](int kk) {
+        return na + (kk < nr - 1 ? static_cast<int>(s_row[kk + 1] >> 16) : nb);
+    };
+    int ia = a - a0, ib = na + b - b0;
+    int iae = end_a(k), ibe = end_b(k);
+    int last_a = ia > static_cast<int>(s_row[k] & 0xffffu) ? s_crd[ia - 1] : -1;
+    int xa = ia < iae ? s_crd[ia] : kMax;
+    int xb = ib < ibe ? s_crd[ib] : kMax;
     unsigned valid = 0, row_ends = 0;
 #pragma unroll
     for (int s = 0; s < kSteps; ++s) {
@@ -280,33 +287,32 @@ __device__ __forceinline__ void walk_lane(LaneOut<IPT + 1> &out, const TileSplit
             if (xa == kMax && xb == kMax) {  // row end
                 row_ends |= 1u << s;
                 ++k;
-                aE = k < nr - 1 ? row_a(k + 1) : a1;
-                bE = k < nr - 1 ? row_b(k + 1) : b1;
+                iae = end_a(k);
+                ibe = end_b(k);
                 last_a = -1;
-                xa = a < aE ? A(a) : kMax;
-                xb = b < bE ? B(b) : kMax;
+                xa = ia < iae ? s_crd[ia] : kMax;
+                xb = ib < ibe ? s_crd[ib] : kMax;
             } else {
                 const bool take_a = xa <= xb;
                 const bool pair = take_a && xa == xb;
-                if (CHILD) out.pos[s] = static_cast<unsigned>(a - a0) | (static_cast<unsigned>(b - b0) << 16);
-                out.crd[s] = take_a ? xa : xb;
+                if (CHILD) out.pos[s] = static_cast<unsigned>(ia) | (static_cast<unsigned>(ib - na) << 16);
+                out.crd[s] = min(xa, xb);
                 if (VALUES) {
-                    const float own = s_val[take_a ? a - a0 : na + b - b0];
+                    const float own = s_val[take_a ? ia : ib];
                     if (OP == Op::Union) {
-                        out.val[s] = pair ? own + s_val[na + b - b0] : own;
+                        out.val[s] = pair ? own + s_val[ib] : own;
                     } else {
-                        out.val[s] = own * s_val[na + b - b0];
+                        out.val[s] = own * s_val[ib];
                     }
                 }
                 const bool emit = (OP == Op::Union) ? (take_a || last_a != xb) : pair;
                 valid |= static_cast<unsigned>(emit) << s;
                 if (take_a) last_a = xa;
-                a += take_a;
-                b += !take_a;
-                const int np = take_a ? a : b;  // reload the head that advanced
-                const bool in = np < (take_a ? aE : bE);
-                // always read (the index stays inside the staged tile), then mask
-                const int h0 = s_crd[min(take_a ? np - a0 : na + np - b0, kCapIdx)];
+                ia += take_a;
+                ib += !take_a;
+                const int np = take_a ? ia : ib;  // reload the head that advanced
+                const bool in = np < (take_a ? iae : ibe);
+                const int h0 = s_crd[np];  // always read (np < kCap), then mask
                 const int h = in ? h0 : kMax;
                 xa = take_a ? h : xa;
                 xb = take_a ? xb : h;
@@ -458,6 +464,7 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
         if (CHILD) {
 #pragma unroll
             for (int s = 0; s < kSteps; ++s) {
+                // pos is 0 for steps that emitted nothing: (a0, b0), inside both operands
                 const int pa_s = sp.a0 + static_cast<int>(lo.pos[s] & 0xffffu);
                 const int pb_s = sp.b0 + static_cast<int>(lo.pos[s] >> 16);
                 ca_v[s] = next_a ? next_a[pa_s] : pa_s;
