@@ -135,3 +135,69 @@ def test_every_descriptor_layout_matches_the_c_compiler(tmp_path):
         desc = pairs[cname]
         got = ctypes.sizeof(desc) if field == "size" else getattr(desc, field).offset
         assert got == int(value), f"{cname}.{field}: ctypes {got}, C {value}"
+
+
+def test_cpp_shim_matches_the_generated_signatures(tmp_path):
+    """include/nacho_hip.hpp compiles as C++17, its format templates have the C descriptors'
+    layout field by field, every generated-style entry point links against the library, and
+    a failing call (mismatched shapes, rejected before any HIP call) throws."""
+    import shutil
+
+    from nacho_amd import _lib
+
+    gxx = shutil.which("g++")
+    if gxx is None:
+        pytest.skip("g++ not available")
+    pairs = {  # shim format -> (C descriptor, {shim field: C field})
+        "nacho_hip::csr_ij<int32_t, float>": ("nacho_csr", {}),
+        "nacho_hip::csr_jk<int32_t, float>": ("nacho_csr", {
+            "dim_j_size": "dim_i_size", "dim_k_size": "dim_j_size",
+            "dim_k_offsets": "dim_j_offsets", "dim_k_length": "dim_j_length",
+            "dim_k_indices": "dim_j_indices"}),
+        "nacho_hip::csr_ik<int32_t, float>": ("nacho_csr", {
+            "dim_k_size": "dim_j_size", "dim_k_offsets": "dim_j_offsets",
+            "dim_k_length": "dim_j_length", "dim_k_indices": "dim_j_indices"}),
+        "nacho_hip::dcsr_ij<int32_t, float>": ("nacho_dcsr", {}),
+        "nacho_hip::csf3_ijk<int32_t, float>": ("nacho_csf3", {}),
+        "nacho_hip::coo_ij<int32_t, float>": ("nacho_coo", {}),
+        "nacho_hip::coo3_ijk<int32_t, float>": ("nacho_coo3", {}),
+    }
+    descs = {"nacho_csr": _lib.CsrDesc, "nacho_dcsr": _lib.DcsrDesc,
+             "nacho_csf3": _lib.Csf3Desc, "nacho_coo": _lib.CooDesc, "nacho_coo3": _lib.Coo3Desc}
+    lines = ["#include <cstddef>", "#include <cstdio>", '#include "nacho_hip.hpp"',
+             "int main() {", "int bad = 0;"]
+    for shim, (cname, rename) in pairs.items():
+        inverse = {v: k for k, v in rename.items()}
+        lines.append(f"{{ using F = {shim}; static_assert(sizeof(F) == sizeof({cname}), \"size\");")
+        for field, _ in descs[cname]._fields_:
+            sf = inverse.get(field, field)
+            lines.append(f"if (offsetof(F, {sf}) != offsetof({cname}, {field})) "
+                         f"{{ std::printf(\"{shim}.{sf}\\n\"); ++bad; }}")
+        lines.append("}")
+    lines += [
+        "void *fns[] = {",
+        "  (void *)&csr_add::csr_add_gpu_i32_f32, (void *)&csr_mul::csr_mul_gpu_i32_f32,",
+        "  (void *)&csr_add_3::csr_add_3_gpu_i32_f32, (void *)&coo_add::coo_add_gpu_i32_f32,",
+        "  (void *)&coo_mul::coo_mul_gpu_i32_f32, (void *)&coo3d_add::coo3d_add_gpu_i32_f32,",
+        "  (void *)&dcsr_add::dcsr_add_gpu_i32_f32, (void *)&dcsr_mul::dcsr_mul_gpu_i32_f32,",
+        "  (void *)&dcsr_mul_without_recursive_partitioning::"
+        "dcsr_mul_without_recursive_partitioning_gpu_i32_f32,",
+        "  (void *)&csf_add::csf_add_gpu_i32_f32, (void *)&spgemm::spgemm_gpu_i32_f32,",
+        "  (void *)&sssmm::sssmm_gpu_i32_f32};",
+        "for (void *f : fns) bad += f == nullptr;",
+        "csr_add::a_tensor_format<int32_t, float> a{4, 4, nullptr, 0, nullptr, nullptr, 0};",
+        "csr_add::b_tensor_format<int32_t, float> b{5, 4, nullptr, 0, nullptr, nullptr, 0};",
+        "try { (void)csr_add::csr_add_gpu_i32_f32(a, b, 256, 256); ++bad; std::printf(\"no throw\\n\"); }",
+        "catch (const std::runtime_error &e) { std::printf(\"threw: %s\\n\", e.what()); }",
+        "return bad; }",
+    ]
+    src = tmp_path / "shim.cpp"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "shim"
+    include = REPO / "include"
+    libdir = _lib.LIBRARY_PATH.parent
+    subprocess.run([gxx, "-std=c++17", f"-I{include}", str(src), "-o", str(exe),
+                    f"-L{libdir}", "-lnacho_hip", f"-Wl,-rpath,{libdir}"], check=True)
+    run = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert run.returncode == 0, run.stdout + run.stderr
+    assert "threw: csr_add: " in run.stdout
