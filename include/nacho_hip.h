@@ -21,6 +21,12 @@
  * `alloc` (or by the library's caching device allocator when `alloc` is NULL, in which case
  * the caller releases them with nacho_free()).  A result array of length 0 is a NULL pointer.
  *
+ * Ordering: an entry point returns once the result lengths are known; the last kernels that
+ * fill the result arrays may still be running on `stream`.  Work the caller queues on the
+ * same stream sees complete results; other streams must wait for `stream` (an event), and
+ * host reads must synchronise it, as with any stream-ordered library.  The reference's
+ * generated entry point likewise returns after launching its write pass.
+ *
  * Input contract (the reference's, made explicit): pos[0] == 0, pos non-decreasing,
  * pos[rows] == length of the coordinate array, coordinates strictly increasing within
  * each fibre (sorted, no duplicates), COO/COO3 coordinates sorted lexicographically and
@@ -144,7 +150,10 @@ typedef struct nacho_csf3 {
 /* ---- allocation ------------------------------------------------------------------- */
 
 /* Caller-supplied device allocator, used for results and scratch.  `allocate` returns NULL
- * on failure.  `stream` is the hipStream_t the call runs on.  Replaces the generated code's
+ * on failure.  `stream` is the hipStream_t the call runs on.  `release` is called for
+ * scratch buffers when the entry point returns, possibly while kernels queued on `stream`
+ * still use them: it must be stream-ordered (reuse only by work queued later on `stream`,
+ * or after synchronising it), like hipFreeAsync or torch's caching allocator.  Replaces the generated code's
  * cudaMallocAsync/cudaFreeAsync on stream 0 (stitch_and_generate_gpu.cpp:187-196) and the
  * Python deleter of runtime/nacho_nb.h:50-58. */
 typedef struct nacho_allocator {

@@ -112,9 +112,11 @@ template <typename Codec>
 __global__ __launch_bounds__(256) void coo_partition_kernel(Codec codec, Coords ca, int nnz_a,
                                                             Coords cb, int nnz_b, int num_tiles,
                                                             int *__restrict__ split_a,
-                                                            int *__restrict__ split_b) {
+                                                            int *__restrict__ split_b,
+                                                            unsigned long long *__restrict__ done) {
     const int t = blockIdx.x * blockDim.x + threadIdx.x;
     if (t > num_tiles) return;
+    if (t == 0) *done = 0ull;  // accumulator of the kernel that totals the length
     const int total = nnz_a + nnz_b;
     const long long d64 = static_cast<long long>(t) * kTile;
     const int diag = d64 > total ? total : static_cast<int>(d64);
@@ -256,7 +258,9 @@ __global__ __launch_bounds__(kBlock) void coo_count_kernel(Codec codec, Coords c
                                                           int num_tiles, int chunk,
                                                           const int *__restrict__ split_a,
                                                           const int *__restrict__ split_b,
-                                                          unsigned *__restrict__ chunk_count) {
+                                                          unsigned *__restrict__ chunk_count,
+                                                          unsigned long long *__restrict__ done,
+                                                          int64_t *__restrict__ length_out) {
     using Key = typename Codec::Key;
     constexpr int kCap = kTile + 2;
     constexpr int kLoads = (kCap + kBlock - 1) / kBlock;
@@ -266,7 +270,10 @@ __global__ __launch_bounds__(kBlock) void coo_count_kernel(Codec codec, Coords c
     const int tid = threadIdx.x;
     const int t0 = blockIdx.x * chunk, t1 = min(t0 + chunk, num_tiles);
     if (t0 >= t1) {
-        if (tid == 0) chunk_count[blockIdx.x] = 0u;
+        if (tid == 0) {
+            chunk_count[blockIdx.x] = 0u;
+            dev::add_to_total(0u, done, length_out);
+        }
         return;
     }
     stage_splits(s_split, split_a, split_b, t0, t1);
@@ -292,20 +299,27 @@ __global__ __launch_bounds__(kBlock) void coo_count_kernel(Codec codec, Coords c
             __syncthreads();
         }
     }
-    if (tid == 0) chunk_count[blockIdx.x] = total;
+    if (tid == 0) {
+        chunk_count[blockIdx.x] = total;
+        // The last workgroup to finish stores the result length (the sum of every chunk).
+        dev::add_to_total(total, done, length_out);
+    }
 }
 
 // SPREAD (intersection only, no count pass): a tile's outputs go to zi/zj/zk/zv at the
 // tile's own start position in A (spread_by_a) or B, whose range holds every pair the tile
-// can emit; tile_count[t] receives the tile's length and chunk_total[w] the sum over
-// workgroup w's chunk.  coo_compact_kernel then moves each tile to its final offset.
+// can emit; tile_count[t] receives the tile's length, chunk_total[w] the sum over
+// workgroup w's chunk, and the last workgroup to finish stores the sum of all chunks, the
+// result length, to `length_out`.  coo_compact_kernel then moves each tile to its final
+// offset.
 template <Op OP, typename Codec, bool SPREAD>
 __global__ __launch_bounds__(kBlock) void coo_write_kernel(
     Codec codec, Coords ca, const float *__restrict__ va, Coords cb, const float *__restrict__ vb,
     int num_tiles, int chunk, const int *__restrict__ split_a, const int *__restrict__ split_b,
     const unsigned *__restrict__ chunk_count, int *__restrict__ zi, int *__restrict__ zj,
     int *__restrict__ zk, float *__restrict__ zv, unsigned *__restrict__ length,
-    int spread_by_a, int64_t *__restrict__ tile_count, int64_t *__restrict__ chunk_total) {
+    int spread_by_a, int64_t *__restrict__ tile_count, int64_t *__restrict__ chunk_total,
+    unsigned long long *__restrict__ done, int64_t *__restrict__ length_out) {
     static_assert(!SPREAD || OP == Op::Intersect, "spread output: intersection");
     using Key = typename Codec::Key;
     constexpr int kCap = kTile + 2;
@@ -317,7 +331,15 @@ __global__ __launch_bounds__(kBlock) void coo_write_kernel(
     __shared__ int s_split[2 * (kMaxChunk + 1)];
     const int tid = threadIdx.x;
     const int t0 = blockIdx.x * chunk, t1 = min(t0 + chunk, num_tiles);
-    if (t0 >= t1) return;
+    if (t0 >= t1) {
+        if (SPREAD) {
+            if (tid == 0) {
+                chunk_total[blockIdx.x] = 0;
+                dev::add_to_total(0u, done, length_out);
+            }
+        }
+        return;
+    }
     stage_splits(s_split, split_a, split_b, t0, t1);
     int base = 0;
     if (!SPREAD) {
@@ -377,6 +399,8 @@ __global__ __launch_bounds__(kBlock) void coo_write_kernel(
             __syncthreads();
         }
     }
+    // Spread output: the last workgroup to finish stores the result length.
+    if (SPREAD && tid == 0) dev::add_to_total(static_cast<uint32_t>(spread_sum), done, length_out);
 }
 
 // Moves each tile's outputs from its spread position (coo_write_kernel<SPREAD>) to its final
@@ -458,7 +482,14 @@ int coo_binary(int arity, const int32_t extents[3], Coords ca, const float *va, 
         int chunk = (num_tiles + resident - 1) / resident;
         if (chunk > kMaxChunk) chunk = kMaxChunk;
         const int grid = (num_tiles + chunk - 1) / chunk;
-        NACHO_TRY(call.scratch_n(static_cast<size_t>(grid) + 4, &counts));
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(grid) + 6, &counts));
+        // 64-bit accumulator of the length total (an 8-byte aligned slot after the counts).
+    unsigned long long *done =
+        reinterpret_cast<unsigned long long *>(counts + ((grid + 2) & ~1));
+        // The result length goes straight to a pinned host word as soon as the kernel that
+        // totals it ends; the host waits for that kernel only, not for the writes after it.
+        int64_t *length_out = nullptr;
+        NACHO_TRY(call.length_word(&length_out));
         if (kSpread) {
             // One walk: each tile writes its pairs at its own position in the smaller
             // operand's range of scratch arrays, then one compaction moves them into place.
@@ -473,38 +504,43 @@ int coo_binary(int arity, const int32_t extents[3], Coords ca, const float *va, 
             int64_t *len_dev = chunk_total + grid;
             NACHO_TRY(call.timer_start(kernel_name));
             coo_partition_kernel<Codec><<<part_grid, 256, 0, s>>>(codec, ca, nnz_a, cb, nnz_b,
-                                                                  num_tiles, split_a, split_b);
+                                                                  num_tiles, split_a, split_b,
+                                                                  done);
             NACHO_TRY_HIP(hipGetLastError());
             coo_write_kernel<OP, Codec, kSpread><<<grid, kBlock, 0, s>>>(
                 codec, ca, va, cb, vb, num_tiles, chunk, split_a, split_b, nullptr, t[0], t[1],
-                t[2], tv, nullptr, by_a, tile_count, chunk_total);
+                t[2], tv, nullptr, by_a, tile_count, chunk_total, done, length_out);
             NACHO_TRY_HIP(hipGetLastError());
+            NACHO_TRY(call.mark_length());
             coo_compact_kernel<<<num_tiles, kBlock, 0, s>>>(
                 split_a, split_b, num_tiles, chunk, by_a, arity, tile_count, chunk_total, t[0],
                 t[1], t[2], tv, z[0], z[1], z[2], zv, len_dev);
             NACHO_TRY_HIP(hipGetLastError());
             NACHO_TRY(call.timer_stop());
             int64_t len = 0;
-            NACHO_TRY(call.read_back(&len, len_dev, sizeof(len)));
+            NACHO_TRY(call.wait_length(&len));
             if (len > INT_MAX) return NACHO_ERR_INDEX_OVERFLOW;
             *out_nnz = static_cast<int32_t>(len);
             return NACHO_OK;
         }
         NACHO_TRY(call.timer_start(kernel_name));
         coo_partition_kernel<Codec><<<part_grid, 256, 0, s>>>(codec, ca, nnz_a, cb, nnz_b, num_tiles,
-                                                              split_a, split_b);
+                                                              split_a, split_b, done);
         NACHO_TRY_HIP(hipGetLastError());
         coo_count_kernel<OP, Codec><<<grid, kBlock, 0, s>>>(codec, ca, cb, num_tiles, chunk, split_a,
-                                                            split_b, counts);
+                                                            split_b, counts, done, length_out);
         NACHO_TRY_HIP(hipGetLastError());
+        NACHO_TRY(call.mark_length());
         coo_write_kernel<OP, Codec, false><<<grid, kBlock, 0, s>>>(
             codec, ca, va, cb, vb, num_tiles, chunk, split_a, split_b, counts, z[0], z[1], z[2],
-            zv, counts + grid, 0, nullptr, nullptr);
+            zv, counts + grid, 0, nullptr, nullptr, nullptr, nullptr);
         NACHO_TRY_HIP(hipGetLastError());
         NACHO_TRY(call.timer_stop());
-        unsigned len = 0;
-        NACHO_TRY(call.read_back(&len, counts + grid, sizeof(len)));
-        return static_cast<int>(len) < 0 ? NACHO_ERR_INDEX_OVERFLOW : (*out_nnz = static_cast<int32_t>(len), NACHO_OK);
+        int64_t len = 0;
+        NACHO_TRY(call.wait_length(&len));
+        if (len > INT_MAX) return NACHO_ERR_INDEX_OVERFLOW;
+        *out_nnz = static_cast<int32_t>(len);
+        return NACHO_OK;
     };
     if (arity == 2) {
         PackedCodec c{2, 32, 0, 0xffffffffull, 0ull};

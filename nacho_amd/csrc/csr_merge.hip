@@ -75,12 +75,14 @@ __device__ __forceinline__ void merge_split(ReadA A, ReadB B, int aS, int aE, in
 }
 
 // One thread per tile boundary t in [0, num_tiles]: split of diagonal min(t*TILE, total).
+// Thread 0 also zeroes the ticket counter that the next kernel's length total uses.
 __global__ __launch_bounds__(256) void csr_partition_kernel(
     const int *__restrict__ pa, const int *__restrict__ ca, const int *__restrict__ pb,
     const int *__restrict__ cb, int rows, int total, int num_tiles, int *__restrict__ split_r,
-    int *__restrict__ split_a, int *__restrict__ split_b) {
+    int *__restrict__ split_a, int *__restrict__ split_b, unsigned long long *__restrict__ done) {
     const int t = blockIdx.x * blockDim.x + threadIdx.x;
     if (t > num_tiles) return;
+    if (t == 0) *done = 0ull;  // accumulator of the kernel that totals the length
     const long long d64 = static_cast<long long>(t) * kTile;
     const int diag = d64 > total ? total : static_cast<int>(d64);
 
@@ -343,13 +345,15 @@ __device__ __forceinline__ T block_sum(T v, T *s_wave) {
     return all;
 }
 
-// Output count of each chunk (coordinates and row offsets only).
+// Output count of each chunk (coordinates and row offsets only), and their sum, the result
+// length, stored to `length_out` by the last workgroup.
 template <Op OP, int IPT>
 __global__ __launch_bounds__(kBlock) void csr_count_kernel(
     const int *__restrict__ pa, const int *__restrict__ ca, const int *__restrict__ pb,
     const int *__restrict__ cb, int num_tiles, int chunk, const int *__restrict__ split_r,
     const int *__restrict__ split_a, const int *__restrict__ split_b,
-    unsigned *__restrict__ chunk_count) {
+    unsigned *__restrict__ chunk_count, unsigned long long *__restrict__ done,
+    int64_t *__restrict__ length_out) {
     constexpr int kCap = kBlock * IPT + 2;
     constexpr int kLoads = (kCap + kBlock - 1) / kBlock;
     static_assert(kCap < 65536, "row offsets are packed in 16 bits");
@@ -362,7 +366,10 @@ __global__ __launch_bounds__(kBlock) void csr_count_kernel(
     int t0, t1;
     chunk_range(num_tiles, chunk, t0, t1);
     if (t0 >= t1) {
-        if (tid == 0) chunk_count[blockIdx.x] = 0u;
+        if (tid == 0) {
+            chunk_count[blockIdx.x] = 0u;
+            dev::add_to_total(0u, done, length_out);
+        }
         return;
     }
     stage_splits(s_split, split_r, split_a, split_b, t0, t1);
@@ -387,7 +394,11 @@ __global__ __launch_bounds__(kBlock) void csr_count_kernel(
         sp = nsp;
         nsp = nsp2;
     }
-    if (tid == 0) chunk_count[blockIdx.x] = total;
+    if (tid == 0) {
+        chunk_count[blockIdx.x] = total;
+        // The last workgroup to finish stores the result length (the sum of every chunk).
+        dev::add_to_total(total, done, length_out);
+    }
 }
 
 // Writes the result: crd/val (VALUES) or crd plus child pointers (CHILD: for output o,
@@ -398,8 +409,9 @@ __global__ __launch_bounds__(kBlock) void csr_count_kernel(
 // SPREAD (intersection only, no count pass): a tile's outputs go to cc/vc at the tile's own
 // start position in A (spread_by_a) or B, whose range holds every pair the tile can emit;
 // row ends write pos in those coordinates, tile_count[t] receives the tile's length and
-// chunk_total[w] the sum over workgroup w's chunk.  csr_compact_kernel then moves each tile
-// to its final offset and corrects its rows' pos.
+// chunk_total[w] the sum over workgroup w's chunk, and the last workgroup to finish stores
+// the sum of all chunks, the result length, to `length_out`.  csr_compact_kernel then moves
+// each tile to its final offset and corrects its rows' pos.
 template <Op OP, int IPT, bool VALUES, bool CHILD, bool SPREAD>
 __global__ __launch_bounds__(kBlock) void csr_write_kernel(
     const int *__restrict__ pa, const int *__restrict__ ca, const float *__restrict__ va,
@@ -410,7 +422,8 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
     int *__restrict__ cc, float *__restrict__ vc, const int *__restrict__ next_a,
     const int *__restrict__ next_b, int *__restrict__ child_a, int *__restrict__ child_b,
     unsigned *__restrict__ length, int spread_by_a, int64_t *__restrict__ tile_count,
-    int64_t *__restrict__ chunk_total) {
+    int64_t *__restrict__ chunk_total, unsigned long long *__restrict__ done,
+    int64_t *__restrict__ length_out) {
     static_assert(!(VALUES && CHILD), "a level carries values or child pointers, not both");
     static_assert(!SPREAD || (OP == Op::Intersect && !CHILD), "spread output: intersection");
     constexpr int kCap = kBlock * IPT + 2;
@@ -425,7 +438,15 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
     const int tid = threadIdx.x;
     int t0, t1;
     chunk_range(num_tiles, chunk, t0, t1);
-    if (t0 >= t1) return;
+    if (t0 >= t1) {
+        if (SPREAD) {
+            if (tid == 0) {
+                chunk_total[blockIdx.x] = 0;
+                dev::add_to_total(0u, done, length_out);
+            }
+        }
+        return;
+    }
     stage_splits(s_split, split_r, split_a, split_b, t0, t1);
 
     // Offset of this chunk: the counts of every earlier chunk.
@@ -522,6 +543,8 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
         sp = nsp;
         nsp = nsp2;
     }
+    // Spread output: the last workgroup to finish stores the result length.
+    if (SPREAD && tid == 0) dev::add_to_total(static_cast<uint32_t>(spread_sum), done, length_out);
 }
 
 // Moves each tile's outputs from its spread position (csr_write_kernel<SPREAD>) to its final
@@ -581,8 +604,15 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
     int chunk = (num_tiles + resident - 1) / resident;
     if (chunk > kMaxChunk) chunk = kMaxChunk;  // more workgroups than resident: still correct
     const int grid = (num_tiles + chunk - 1) / chunk;
-    NACHO_TRY(call.scratch_n(static_cast<size_t>(grid) + 4, &counts));
+    NACHO_TRY(call.scratch_n(static_cast<size_t>(grid) + 6, &counts));
     unsigned *length = counts + grid;
+    // 64-bit accumulator of the length total (an 8-byte aligned slot after the counts).
+    unsigned long long *done =
+        reinterpret_cast<unsigned long long *>(counts + ((grid + 2) & ~1));
+    // The result length goes straight to a pinned host word as soon as the kernel that
+    // totals it ends; the host waits for that kernel only, not for the writes after it.
+    int64_t *length_out = nullptr;
+    NACHO_TRY(call.length_word(&length_out));
 
     const hipStream_t s = call.stream();
     if (intersect) {
@@ -602,37 +632,41 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
         NACHO_TRY(call.timer_start(kernel_name));  // the whole device pipeline of this level
         csr_partition_kernel<<<ceil_div(static_cast<size_t>(num_tiles) + 1, 256), 256, 0, s>>>(
             A.pos, A.crd, B.pos, B.crd, rows, static_cast<int>(total), num_tiles, split_r,
-            split_a, split_b);
+            split_a, split_b, done);
         NACHO_TRY_HIP(hipGetLastError());
         csr_write_kernel<Op::Intersect, kItemsPerLane, true, false, true>
             <<<grid, kBlock, 0, s>>>(A.pos, A.crd, A.val, B.pos, B.crd, B.val, A.len, B.len,
                                      num_tiles, chunk, split_r, split_a, split_b, nullptr, rows,
                                      Z.pos, tmp_crd, tmp_val, nullptr, nullptr, nullptr,
-                                     nullptr, nullptr, by_a, tile_count, chunk_total);
+                                     nullptr, nullptr, by_a, tile_count, chunk_total, done,
+                                     length_out);
         NACHO_TRY_HIP(hipGetLastError());
+        NACHO_TRY(call.mark_length());
         csr_compact_kernel<<<num_tiles, kBlock, 0, s>>>(
             split_r, split_a, split_b, num_tiles, chunk, rows, by_a, tile_count, chunk_total,
             tmp_crd, tmp_val, Z.pos, Z.crd, Z.val, len_dev);
         NACHO_TRY_HIP(hipGetLastError());
         NACHO_TRY(call.timer_stop());
         int64_t len = 0;
-        NACHO_TRY(call.read_back(&len, len_dev, sizeof(len)));
+        NACHO_TRY(call.wait_length(&len));
         *out_len = len;
         return NACHO_OK;
     }
     NACHO_TRY(call.timer_start(kernel_name));  // the whole device pipeline of this level
     csr_partition_kernel<<<ceil_div(static_cast<size_t>(num_tiles) + 1, 256), 256, 0, s>>>(
         A.pos, A.crd, B.pos, B.crd, rows, static_cast<int>(total), num_tiles, split_r, split_a,
-        split_b);
+        split_b, done);
     NACHO_TRY_HIP(hipGetLastError());
     csr_count_kernel<Op::Union, kItemsPerLane><<<grid, kBlock, 0, s>>>(
-        A.pos, A.crd, B.pos, B.crd, num_tiles, chunk, split_r, split_a, split_b, counts);
+        A.pos, A.crd, B.pos, B.crd, num_tiles, chunk, split_r, split_a, split_b, counts, done,
+        length_out);
     NACHO_TRY_HIP(hipGetLastError());
+    NACHO_TRY(call.mark_length());
 #define NACHO_WRITE_LAUNCH(OPV, VAL, CHD)                                                        \
     csr_write_kernel<OPV, kItemsPerLane, VAL, CHD, false><<<grid, kBlock, 0, s>>>(               \
         A.pos, A.crd, A.val, B.pos, B.crd, B.val, A.len, B.len, num_tiles, chunk, split_r,      \
         split_a, split_b, counts, rows, Z.pos, Z.crd, Z.val, A.next, B.next, Z.child_a,         \
-        Z.child_b, length, 0, nullptr, nullptr)
+        Z.child_b, length, 0, nullptr, nullptr, nullptr, nullptr)
     if (values) {
         if (child) return NACHO_ERR_INVALID_ARGUMENT;
         NACHO_WRITE_LAUNCH(Op::Union, true, false);
@@ -645,8 +679,8 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
     NACHO_TRY_HIP(hipGetLastError());
     NACHO_TRY(call.timer_stop());
 
-    unsigned len = 0;
-    if (num_tiles > 0) NACHO_TRY(call.read_back(&len, length, sizeof(len)));
+    int64_t len = 0;
+    NACHO_TRY(call.wait_length(&len));
     *out_len = len;
     return NACHO_OK;
 }

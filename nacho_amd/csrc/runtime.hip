@@ -111,6 +111,12 @@ thread_local const char *t_last_name = "";
 // Pinned host word for length readbacks, one per host thread.
 thread_local void *t_pinned = nullptr;
 
+// Coherent pinned word that kernels store a length into (early readback), its device
+// address, and the event marking the kernel that stores it; one of each per host thread.
+thread_local volatile int64_t *t_len_host = nullptr;
+thread_local int64_t *t_len_dev = nullptr;
+thread_local hipEvent_t t_ev_len = nullptr;
+
 }  // namespace
 
 Call::Call(void *stream, const nacho_allocator *alloc)
@@ -177,6 +183,38 @@ int Call::read_back(void *host, const void *device, size_t bytes) {
     NACHO_TRY_HIP(hipMemcpyAsync(t_pinned, device, bytes, hipMemcpyDeviceToHost, stream_));
     NACHO_TRY_HIP(hipStreamSynchronize(stream_));
     std::memcpy(host, t_pinned, bytes);
+    return collect_timer();
+}
+
+int Call::length_word(int64_t **dev) {
+    if (!t_len_host) {
+        void *h = nullptr;
+        NACHO_TRY_HIP(hipHostMalloc(&h, 64, hipHostMallocMapped | hipHostMallocCoherent |
+                                                hipHostMallocPortable));
+        void *d = nullptr;
+        const hipError_t e = hipHostGetDevicePointer(&d, h, 0);
+        if (e != hipSuccess) {
+            (void)hipHostFree(h);
+            return static_cast<int>(e);
+        }
+        t_len_host = static_cast<volatile int64_t *>(h);
+        t_len_dev = static_cast<int64_t *>(d);
+    }
+    *t_len_host = -1;  // a kernel that did not store would show as an impossible length
+    *dev = t_len_dev;
+    return NACHO_OK;
+}
+
+int Call::mark_length() {
+    if (!t_ev_len) NACHO_TRY_HIP(hipEventCreateWithFlags(&t_ev_len, hipEventDisableTiming));
+    NACHO_TRY_HIP(hipEventRecord(t_ev_len, stream_));
+    return NACHO_OK;
+}
+
+int Call::wait_length(int64_t *len) {
+    NACHO_TRY_HIP(hipEventSynchronize(t_ev_len));
+    *len = *t_len_host;
+    if (*len < 0) return NACHO_ERR_INTERNAL;
     return collect_timer();
 }
 

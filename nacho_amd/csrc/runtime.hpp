@@ -68,6 +68,16 @@ class Call {
     // Copy `bytes` from device to a host variable and wait for the stream.
     int read_back(void *host, const void *device, size_t bytes);
 
+    // Early length readback.  A kernel stores a result length straight into this host
+    // thread's pinned, device-visible word (`*dev` receives its device address); the host
+    // records an event right after that kernel (mark_length), keeps launching the rest of
+    // the pipeline, and wait_length waits only for the event, so the call returns while
+    // the remaining kernels still run, stream-ordered, like the reference's generated entry
+    // point, which returns after launching its write pass.
+    int length_word(int64_t **dev);
+    int mark_length();
+    int wait_length(int64_t *len);
+
     // Kernel timing hook (see nacho_set_kernel_timing): intervals between timer_start and
     // timer_stop are summed over the call and reported when the call ends.  An interval is
     // collected at the next read_back (which synchronises the stream).
