@@ -6,10 +6,12 @@
 A step is one call of the hot path over one batch of synthetic input, with the operands
 already resident in HBM: `nacho_amd.gpu_csr_add_f32(A, B)` for the default workload (C2:
 two 2^20 x 2^20 CSR matrices with rescaled Zipf(1.6) row lengths, 16.7M nonzeros each).
-A call includes result allocation from the device pool, both kernels and the explicit
-readback of the result length, exactly what a caller of the entry point waits for.  Steps
-rotate over several independent copies of the operands so that no step re-reads inputs
-still resident in the 256 MB Infinity Cache.
+A call includes result allocation from the device pool, the kernels and the readback of
+the result length; it returns once the length is known, while its last kernel (the write
+pass) still runs on the stream, so one call's write pass overlaps the next call's host
+work.  The timed region ends with a device synchronize, so every step's kernels are inside
+it.  Steps rotate over several independent copies of the operands so that no step re-reads
+inputs still resident in the 256 MB Infinity Cache.
 
 Prints ONE JSON line:
   value            whole-job throughput: algorithmic bytes per step / wall time per step
