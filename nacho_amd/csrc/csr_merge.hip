@@ -218,10 +218,19 @@ struct LaneOut {
     int first_row;
 };
 
-template <Op OP, bool VALUES, bool CHILD, int IPT>
+// Where a lane's walk starts: its first row k (tile-local) and its A and B heads as indices
+// into the staged arrays (ia in [0, na], ib in [na, na + nb]), packed k | ia << 16 and ib.
+// The count kernel finds them by searching and stores them; the write kernel of the same
+// tiles loads them instead of searching again.
+struct LaneStart {
+    unsigned k_ia;
+    unsigned ib;
+};
+
+template <Op OP, bool VALUES, bool CHILD, int IPT, bool GIVEN = false>
 __device__ __forceinline__ void walk_lane(LaneOut<IPT + 1> &out, const TileSplit &sp, int tile,
                                           const int *s_crd, const float *s_val,
-                                          const unsigned *s_row, int tid) {
+                                          const unsigned *s_row, int tid, LaneStart &start) {
     constexpr int kSteps = IPT + 1;
     constexpr int kMax = INT_MAX;  // head sentinel: row exhausted on that side
     const int r0 = sp.r0, a0 = sp.a0, b0 = sp.b0, r1 = sp.r1, a1 = sp.a1, b1 = sp.b1;
@@ -238,7 +247,11 @@ __device__ __forceinline__ void walk_lane(LaneOut<IPT + 1> &out, const TileSplit
     const int steps = tid == kBlock - 1 ? tile_end - g_lo
                                         : min(tile_lo + (tid + 1) * IPT, tile_end) - g_lo;
     int k = 0, a = a0, b = b0;
-    if (tid > 0 && g_lo < tile_end) {
+    if (GIVEN) {
+        k = static_cast<int>(start.k_ia & 0xffffu);
+        a = a0 + static_cast<int>(start.k_ia >> 16);
+        b = b0 + static_cast<int>(start.ib) - na;
+    } else if (tid > 0 && g_lo < tile_end) {
         int lo = 0, hi = nr - 1;  // row of item g_lo
         while (lo < hi) {
             const int mid = (lo + hi + 1) >> 1;
@@ -275,6 +288,10 @@ __device__ __forceinline__ void walk_lane(LaneOut<IPT + 1> &out, const TileSplit
         return na + (kk < nr - 1 ? static_cast<int>(s_row[kk + 1] >> 16) : nb);
     };
     int ia = a - a0, ib = na + b - b0;
+    if (!GIVEN) {
+        start.k_ia = static_cast<unsigned>(k) | (static_cast<unsigned>(ia) << 16);
+        start.ib = static_cast<unsigned>(ib);
+    }
     int iae = end_a(k), ibe = end_b(k);
     int last_a = ia > static_cast<int>(s_row[k] & 0xffffu) ? s_crd[ia - 1] : -1;
     int xa = ia < iae ? s_crd[ia] : kMax;
@@ -346,14 +363,15 @@ __device__ __forceinline__ T block_sum(T v, T *s_wave) {
 }
 
 // Output count of each chunk (coordinates and row offsets only), and their sum, the result
-// length, stored to `length_out` by the last workgroup.
+// length, stored to `length_out` by the last workgroup.  Every lane's walk start (found by
+// its search) goes to starts[tile * kBlock + lane] for the write kernel.
 template <Op OP, int IPT>
 __global__ __launch_bounds__(kBlock) void csr_count_kernel(
     const int *__restrict__ pa, const int *__restrict__ ca, const int *__restrict__ pb,
     const int *__restrict__ cb, int num_tiles, int chunk, const int *__restrict__ split_r,
     const int *__restrict__ split_a, const int *__restrict__ split_b,
     unsigned *__restrict__ chunk_count, unsigned long long *__restrict__ done,
-    int64_t *__restrict__ length_out) {
+    int64_t *__restrict__ length_out, uint2 *__restrict__ starts) {
     constexpr int kCap = kBlock * IPT + 2;
     constexpr int kLoads = (kCap + kBlock - 1) / kBlock;
     static_assert(kCap < 65536, "row offsets are packed in 16 bits");
@@ -385,7 +403,9 @@ __global__ __launch_bounds__(kBlock) void csr_count_kernel(
         fetch_tile<false, kLoads>(st, nsp, pa, ca, nullptr, pb, cb, nullptr, tid);
         const TileSplit nsp2 = lds_split(s_split, t + 2 < t1 ? t + 2 - t0 : t + 1 < t1 ? t + 1 - t0 : t - t0);
         LaneOut<IPT + 1> lo;
-        walk_lane<OP, false, false, IPT>(lo, sp, t, s_crd, nullptr, s_row, tid);
+        LaneStart start;
+        walk_lane<OP, false, false, IPT>(lo, sp, t, s_crd, nullptr, s_row, tid, start);
+        starts[static_cast<size_t>(t) * kBlock + tid] = make_uint2(start.k_ia, start.ib);
         total += block_sum<kBlock / dev::kWave>(static_cast<unsigned>(__popc(lo.valid)), s_wave);
         if (t + 1 < t1) {
             stage_tile<false, kLoads>(st, nsp, s_crd, nullptr, s_row, tid);
@@ -423,7 +443,7 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
     const int *__restrict__ next_b, int *__restrict__ child_a, int *__restrict__ child_b,
     unsigned *__restrict__ length, int spread_by_a, int64_t *__restrict__ tile_count,
     int64_t *__restrict__ chunk_total, unsigned long long *__restrict__ done,
-    int64_t *__restrict__ length_out) {
+    int64_t *__restrict__ length_out, const uint2 *__restrict__ starts) {
     static_assert(!(VALUES && CHILD), "a level carries values or child pointers, not both");
     static_assert(!SPREAD || (OP == Op::Intersect && !CHILD), "spread output: intersection");
     constexpr int kCap = kBlock * IPT + 2;
@@ -469,11 +489,24 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
     __syncthreads();
     TileSplit nsp = lds_split(s_split, t0 + 1 < t1 ? 1 : 0);
     int64_t spread_sum = 0;
+    // A union's lane starts come from its count kernel (loaded one tile ahead); the spread
+    // intersection has no count pass and searches.
+    constexpr bool kGiven = !SPREAD;
+    LaneStart cur{0u, 0u}, nxt{0u, 0u};
+    if (kGiven) {
+        const uint2 v = starts[static_cast<size_t>(t0) * kBlock + tid];
+        cur = LaneStart{v.x, v.y};
+    }
     for (int t = t0; t < t1; ++t) {
         fetch_tile<VALUES, kLoads>(st, nsp, pa, ca, va, pb, cb, vb, tid);
+        if (kGiven && t + 1 < t1) {
+            const uint2 v = starts[static_cast<size_t>(t + 1) * kBlock + tid];
+            nxt = LaneStart{v.x, v.y};
+        }
         const TileSplit nsp2 = lds_split(s_split, t + 2 < t1 ? t + 2 - t0 : t + 1 < t1 ? t + 1 - t0 : t - t0);
         LaneOut<kSteps> lo;
-        walk_lane<OP, VALUES, CHILD, IPT>(lo, sp, t, s_crd, s_val, s_row, tid);
+        walk_lane<OP, VALUES, CHILD, IPT, kGiven>(lo, sp, t, s_crd, s_val, s_row, tid, cur);
+        cur = nxt;
         if (SPREAD) base = spread_by_a ? sp.a0 : sp.b0;
 
         int tile_total = 0;
@@ -639,7 +672,7 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
                                      num_tiles, chunk, split_r, split_a, split_b, nullptr, rows,
                                      Z.pos, tmp_crd, tmp_val, nullptr, nullptr, nullptr,
                                      nullptr, nullptr, by_a, tile_count, chunk_total, done,
-                                     length_out);
+                                     length_out, nullptr);
         NACHO_TRY_HIP(hipGetLastError());
         NACHO_TRY(call.mark_length());
         csr_compact_kernel<<<num_tiles, kBlock, 0, s>>>(
@@ -652,6 +685,8 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
         *out_len = len;
         return NACHO_OK;
     }
+    uint2 *starts = nullptr;  // every lane's walk start, from the count kernel to the write
+    NACHO_TRY(call.scratch_n(static_cast<size_t>(num_tiles) * kBlock, &starts));
     NACHO_TRY(call.timer_start(kernel_name));  // the whole device pipeline of this level
     csr_partition_kernel<<<ceil_div(static_cast<size_t>(num_tiles) + 1, 256), 256, 0, s>>>(
         A.pos, A.crd, B.pos, B.crd, rows, static_cast<int>(total), num_tiles, split_r, split_a,
@@ -659,14 +694,14 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
     NACHO_TRY_HIP(hipGetLastError());
     csr_count_kernel<Op::Union, kItemsPerLane><<<grid, kBlock, 0, s>>>(
         A.pos, A.crd, B.pos, B.crd, num_tiles, chunk, split_r, split_a, split_b, counts, done,
-        length_out);
+        length_out, starts);
     NACHO_TRY_HIP(hipGetLastError());
     NACHO_TRY(call.mark_length());
 #define NACHO_WRITE_LAUNCH(OPV, VAL, CHD)                                                        \
     csr_write_kernel<OPV, kItemsPerLane, VAL, CHD, false><<<grid, kBlock, 0, s>>>(               \
         A.pos, A.crd, A.val, B.pos, B.crd, B.val, A.len, B.len, num_tiles, chunk, split_r,      \
         split_a, split_b, counts, rows, Z.pos, Z.crd, Z.val, A.next, B.next, Z.child_a,         \
-        Z.child_b, length, 0, nullptr, nullptr, nullptr, nullptr)
+        Z.child_b, length, 0, nullptr, nullptr, nullptr, nullptr, starts)
     if (values) {
         if (child) return NACHO_ERR_INVALID_ARGUMENT;
         NACHO_WRITE_LAUNCH(Op::Union, true, false);
