@@ -186,9 +186,20 @@ __device__ __forceinline__ void fetch_tile(Staged<LOADS> &st, const TileSplit &s
 
 // LDS layout of a staged tile: s_crd = A's crd range then B's; s_val likewise; s_row[k] =
 // (max(posA[r0+k], a0) - a0) | (max(posB[r0+k], b0) - b0) << 16.
-template <bool VALUES, int LOADS>
+//
+// Row-start bins (when s_bin is given): row k >= 1 of the tile starts at item
+// x_k = (a0 + b0 + r0 - tile_lo) + ra_k + rb_k + k counted from the tile's lane grid
+// tile_lo = tile * kBlock * IPT, so it is the row of every lane L >= ceil(x_k / IPT) until a
+// later row starts.  It is recorded as atomicMax(s_bin[L], tag << 16 | k) for that first L
+// (if L < kBlock); after a barrier, lane_first_row turns the bins into each lane's first row
+// with one workgroup max-scan, replacing a per-lane binary search over the tile's rows.  The
+// tag (distinct per staged tile of a workgroup, increasing) makes stale entries of earlier
+// tiles lose every max and read as "no row", so the bins are never cleared.
+template <bool VALUES, int LOADS, int IPT = 0>
 __device__ __forceinline__ void stage_tile(const Staged<LOADS> &st, const TileSplit &sp,
-                                           int *s_crd, float *s_val, unsigned *s_row, int tid) {
+                                           int *s_crd, float *s_val, unsigned *s_row, int tid,
+                                           unsigned *s_bin = nullptr, unsigned tag = 0,
+                                           int tile_lo = 0) {
     const int nab = (sp.a1 - sp.a0) + (sp.b1 - sp.b0), nr = sp.r1 - sp.r0 + 1;
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
@@ -201,8 +212,23 @@ __device__ __forceinline__ void stage_tile(const Staged<LOADS> &st, const TileSp
             const unsigned ra = static_cast<unsigned>(max(st.pa[j], sp.a0) - sp.a0);
             const unsigned rb = static_cast<unsigned>(max(st.pb[j], sp.b0) - sp.b0);
             s_row[k] = ra | (rb << 16);
+            if (IPT > 0 && k > 0) {
+                const int x = (sp.a0 + sp.b0 + sp.r0 - tile_lo) + static_cast<int>(ra + rb) + k;
+                const int lane = max(1, (x + IPT - 1) / IPT);
+                if (lane < kBlock) atomicMax(&s_bin[lane], (tag << 16) | static_cast<unsigned>(k));
+            }
         }
     }
+}
+
+// This lane's first row (tile-local) from the row-start bins of the tile staged with `tag`
+// (see stage_tile): the largest row recorded at or before this lane.  Call after the barrier
+// that ends the staging; ends synchronised.
+__device__ __forceinline__ int lane_first_row(const unsigned *s_bin, unsigned tag, int *s_wave,
+                                              int tid) {
+    const unsigned v = s_bin[tid];
+    const int mine = (v >> 16) == tag ? static_cast<int>(v & 0xffffu) : 0;
+    return max(mine, dev::block_exclusive_max(mine, s_wave));
 }
 
 // ---- one lane's walk -------------------------------------------------------------------
@@ -227,7 +253,12 @@ struct LaneStart {
     unsigned ib;
 };
 
-template <Op OP, bool VALUES, bool CHILD, int IPT, bool GIVEN = false>
+// How a lane finds its start: search for its row and its split in the row; take the row
+// (start.k_ia's low half, from the tile's row-start bins) and search in the row only; or take
+// the whole start.  The search modes return the start found in `start`.
+enum class Start { Search, RowGiven, Given };
+
+template <Op OP, bool VALUES, bool CHILD, int IPT, Start MODE = Start::Search>
 __device__ __forceinline__ void walk_lane(LaneOut<IPT + 1> &out, const TileSplit &sp, int tile,
                                           const int *s_crd, const float *s_val,
                                           const unsigned *s_row, int tid, LaneStart &start) {
@@ -247,21 +278,25 @@ __device__ __forceinline__ void walk_lane(LaneOut<IPT + 1> &out, const TileSplit
     const int steps = tid == kBlock - 1 ? tile_end - g_lo
                                         : min(tile_lo + (tid + 1) * IPT, tile_end) - g_lo;
     int k = 0, a = a0, b = b0;
-    if (GIVEN) {
+    if (MODE == Start::Given) {
         k = static_cast<int>(start.k_ia & 0xffffu);
         a = a0 + static_cast<int>(start.k_ia >> 16);
         b = b0 + static_cast<int>(start.ib) - na;
     } else if (tid > 0 && g_lo < tile_end) {
-        int lo = 0, hi = nr - 1;  // row of item g_lo
-        while (lo < hi) {
-            const int mid = (lo + hi + 1) >> 1;
-            if (row_a(mid) + row_b(mid) + r0 + mid <= g_lo) {
-                lo = mid;
-            } else {
-                hi = mid - 1;
+        if (MODE == Start::RowGiven) {
+            k = static_cast<int>(start.k_ia & 0xffffu);
+        } else {
+            int lo = 0, hi = nr - 1;  // row of item g_lo
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (row_a(mid) + row_b(mid) + r0 + mid <= g_lo) {
+                    lo = mid;
+                } else {
+                    hi = mid - 1;
+                }
             }
+            k = lo;
         }
-        k = lo;
         const int aS = row_a(k), bS = row_b(k);
         const int aE = k < nr - 1 ? row_a(k + 1) : a1;
         const int bE = k < nr - 1 ? row_b(k + 1) : b1;
@@ -288,7 +323,7 @@ __device__ __forceinline__ void walk_lane(LaneOut<IPT + 1> &out, const TileSplit
         return na + (kk < nr - 1 ? static_cast<int>(s_row[kk + 1] >> 16) : nb);
     };
     int ia = a - a0, ib = na + b - b0;
-    if (!GIVEN) {
+    if (MODE != Start::Given) {
         start.k_ia = static_cast<unsigned>(k) | (static_cast<unsigned>(ia) << 16);
         start.ib = static_cast<unsigned>(ib);
     }
@@ -366,7 +401,8 @@ __device__ __forceinline__ T block_sum(T v, T *s_wave) {
 // length, stored to `length_out` by the last workgroup.  Every lane's walk start (found by
 // its search) goes to starts[tile * kBlock + lane] for the write kernel.
 template <Op OP, int IPT>
-__global__ __launch_bounds__(kBlock) void csr_count_kernel(
+// (At most 128 VGPRs: four waves per SIMD, which its LDS use also allows.)
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) void csr_count_kernel(
     const int *__restrict__ pa, const int *__restrict__ ca, const int *__restrict__ pb,
     const int *__restrict__ cb, int num_tiles, int chunk, const int *__restrict__ split_r,
     const int *__restrict__ split_a, const int *__restrict__ split_b,
@@ -378,6 +414,8 @@ __global__ __launch_bounds__(kBlock) void csr_count_kernel(
     __shared__ int s_crd[kCap];
     __shared__ unsigned s_row[kCap];
     __shared__ unsigned s_wave[kBlock / dev::kWave];
+    __shared__ int s_wmax[kBlock / dev::kWave];
+    __shared__ unsigned s_bin[kBlock];  // row-start bins (see stage_tile)
     __shared__ int s_split[3 * (kMaxChunk + 1)];
 
     const int tid = threadIdx.x;
@@ -390,26 +428,31 @@ __global__ __launch_bounds__(kBlock) void csr_count_kernel(
         }
         return;
     }
+    s_bin[tid] = 0u;
     stage_splits(s_split, split_r, split_a, split_b, t0, t1);
     __syncthreads();
     TileSplit sp = lds_split(s_split, 0);
     Staged<kLoads> st;
     fetch_tile<false, kLoads>(st, sp, pa, ca, nullptr, pb, cb, nullptr, tid);
-    stage_tile<false, kLoads>(st, sp, s_crd, nullptr, s_row, tid);
+    stage_tile<false, kLoads, IPT>(st, sp, s_crd, nullptr, s_row, tid, s_bin, 1u, t0 * kBlock * IPT);
     __syncthreads();
+    LaneStart start{static_cast<unsigned>(lane_first_row(s_bin, 1u, s_wmax, tid)), 0u};
     TileSplit nsp = lds_split(s_split, t0 + 1 < t1 ? 1 : 0);
     unsigned total = 0;
     for (int t = t0; t < t1; ++t) {
         fetch_tile<false, kLoads>(st, nsp, pa, ca, nullptr, pb, cb, nullptr, tid);
         const TileSplit nsp2 = lds_split(s_split, t + 2 < t1 ? t + 2 - t0 : t + 1 < t1 ? t + 1 - t0 : t - t0);
         LaneOut<IPT + 1> lo;
-        LaneStart start;
-        walk_lane<OP, false, false, IPT>(lo, sp, t, s_crd, nullptr, s_row, tid, start);
+        walk_lane<OP, false, false, IPT, Start::RowGiven>(lo, sp, t, s_crd, nullptr, s_row, tid,
+                                                          start);
         starts[static_cast<size_t>(t) * kBlock + tid] = make_uint2(start.k_ia, start.ib);
         total += block_sum<kBlock / dev::kWave>(static_cast<unsigned>(__popc(lo.valid)), s_wave);
         if (t + 1 < t1) {
-            stage_tile<false, kLoads>(st, nsp, s_crd, nullptr, s_row, tid);
+            const unsigned tag = static_cast<unsigned>(t + 2 - t0);
+            stage_tile<false, kLoads, IPT>(st, nsp, s_crd, nullptr, s_row, tid, s_bin, tag,
+                                           (t + 1) * kBlock * IPT);
             __syncthreads();
+            start = LaneStart{static_cast<unsigned>(lane_first_row(s_bin, tag, s_wmax, tid)), 0u};
         }
         sp = nsp;
         nsp = nsp2;
@@ -454,6 +497,8 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
     __shared__ unsigned s_row[kCap];
     __shared__ int s_wave[kBlock / dev::kWave];
     __shared__ int s_split[3 * (kMaxChunk + 1)];
+    __shared__ unsigned s_bin[SPREAD ? kBlock : 1];  // row-start bins (see stage_tile)
+    __shared__ int s_wmax[kBlock / dev::kWave];
 
     const int tid = threadIdx.x;
     int t0, t1;
@@ -467,6 +512,7 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
         }
         return;
     }
+    if (SPREAD) s_bin[tid] = 0u;
     stage_splits(s_split, split_r, split_a, split_b, t0, t1);
 
     // Offset of this chunk: the counts of every earlier chunk.
@@ -485,17 +531,23 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
     TileSplit sp = lds_split(s_split, 0);  // (the exclusive sum above ended with a barrier)
     Staged<kLoads> st;
     fetch_tile<VALUES, kLoads>(st, sp, pa, ca, va, pb, cb, vb, tid);
-    stage_tile<VALUES, kLoads>(st, sp, s_crd, s_val, s_row, tid);
+    // A union's lane starts come from its count kernel (loaded one tile ahead); the spread
+    // intersection has no count pass: its lanes take their row from the row-start bins and
+    // search only inside it.
+    constexpr bool kGiven = !SPREAD;
+    constexpr Start kMode = SPREAD ? Start::RowGiven : Start::Given;
+    constexpr int kBinIpt = SPREAD ? IPT : 0;  // stage_tile fills the bins only when spread
+    stage_tile<VALUES, kLoads, kBinIpt>(st, sp, s_crd, s_val, s_row, tid, s_bin, 1u,
+                                        t0 * kBlock * IPT);
     __syncthreads();
     TileSplit nsp = lds_split(s_split, t0 + 1 < t1 ? 1 : 0);
     int64_t spread_sum = 0;
-    // A union's lane starts come from its count kernel (loaded one tile ahead); the spread
-    // intersection has no count pass and searches.
-    constexpr bool kGiven = !SPREAD;
     LaneStart cur{0u, 0u}, nxt{0u, 0u};
     if (kGiven) {
         const uint2 v = starts[static_cast<size_t>(t0) * kBlock + tid];
         cur = LaneStart{v.x, v.y};
+    } else {
+        cur = LaneStart{static_cast<unsigned>(lane_first_row(s_bin, 1u, s_wmax, tid)), 0u};
     }
     for (int t = t0; t < t1; ++t) {
         fetch_tile<VALUES, kLoads>(st, nsp, pa, ca, va, pb, cb, vb, tid);
@@ -505,8 +557,8 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
         }
         const TileSplit nsp2 = lds_split(s_split, t + 2 < t1 ? t + 2 - t0 : t + 1 < t1 ? t + 1 - t0 : t - t0);
         LaneOut<kSteps> lo;
-        walk_lane<OP, VALUES, CHILD, IPT, kGiven>(lo, sp, t, s_crd, s_val, s_row, tid, cur);
-        cur = nxt;
+        walk_lane<OP, VALUES, CHILD, IPT, kMode>(lo, sp, t, s_crd, s_val, s_row, tid, cur);
+        if (kGiven) cur = nxt;
         if (SPREAD) base = spread_by_a ? sp.a0 : sp.b0;
 
         int tile_total = 0;
@@ -570,8 +622,14 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
         }
         __syncthreads();  // staged outputs consumed
         if (t + 1 < t1) {
-            stage_tile<VALUES, kLoads>(st, nsp, s_crd, s_val, s_row, tid);
+            const unsigned tag = static_cast<unsigned>(t + 2 - t0);
+            stage_tile<VALUES, kLoads, kBinIpt>(st, nsp, s_crd, s_val, s_row, tid, s_bin, tag,
+                                                (t + 1) * kBlock * IPT);
             __syncthreads();
+            if (!kGiven) {
+                cur = LaneStart{static_cast<unsigned>(lane_first_row(s_bin, tag, s_wmax, tid)),
+                                0u};
+            }
         }
         sp = nsp;
         nsp = nsp2;
