@@ -223,12 +223,13 @@ __device__ __forceinline__ void stage_tile(const Staged<LOADS> &st, const TileSp
 
 // This lane's first row (tile-local) from the row-start bins of the tile staged with `tag`
 // (see stage_tile): the largest row recorded at or before this lane.  Call after the barrier
-// that ends the staging; ends synchronised.
+// that ends the staging.  One barrier inside; `s_wave` must not be written again before the
+// caller's next barrier.
 __device__ __forceinline__ int lane_first_row(const unsigned *s_bin, unsigned tag, int *s_wave,
                                               int tid) {
     const unsigned v = s_bin[tid];
     const int mine = (v >> 16) == tag ? static_cast<int>(v & 0xffffu) : 0;
-    return max(mine, dev::block_exclusive_max(mine, s_wave));
+    return max(mine, dev::block_exclusive_max<false>(mine, s_wave));
 }
 
 // ---- one lane's walk -------------------------------------------------------------------
@@ -438,7 +439,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
     __syncthreads();
     LaneStart start{static_cast<unsigned>(lane_first_row(s_bin, 1u, s_wmax, tid)), 0u};
     TileSplit nsp = lds_split(s_split, t0 + 1 < t1 ? 1 : 0);
-    unsigned total = 0;
+    unsigned mine = 0;  // this lane's outputs over the chunk
     for (int t = t0; t < t1; ++t) {
         fetch_tile<false, kLoads>(st, nsp, pa, ca, nullptr, pb, cb, nullptr, tid);
         const TileSplit nsp2 = lds_split(s_split, t + 2 < t1 ? t + 2 - t0 : t + 1 < t1 ? t + 1 - t0 : t - t0);
@@ -446,8 +447,9 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
         walk_lane<OP, false, false, IPT, Start::RowGiven>(lo, sp, t, s_crd, nullptr, s_row, tid,
                                                           start);
         starts[static_cast<size_t>(t) * kBlock + tid] = make_uint2(start.k_ia, start.ib);
-        total += block_sum<kBlock / dev::kWave>(static_cast<unsigned>(__popc(lo.valid)), s_wave);
+        mine += static_cast<unsigned>(__popc(lo.valid));  // summed over the chunk at the end
         if (t + 1 < t1) {
+            __syncthreads();  // every lane is done reading this tile's LDS
             const unsigned tag = static_cast<unsigned>(t + 2 - t0);
             stage_tile<false, kLoads, IPT>(st, nsp, s_crd, nullptr, s_row, tid, s_bin, tag,
                                            (t + 1) * kBlock * IPT);
@@ -457,6 +459,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
         sp = nsp;
         nsp = nsp2;
     }
+    const unsigned total = block_sum<kBlock / dev::kWave>(mine, s_wave);
     if (tid == 0) {
         chunk_count[blockIdx.x] = total;
         // The last workgroup to finish stores the result length (the sum of every chunk).

@@ -74,7 +74,10 @@ __device__ __forceinline__ int64_t last_le(const T *__restrict__ a, int64_t lo, 
     return lo;
 }
 
-// Exclusive max over the workgroup (values >= 0, identity 0).  Ends synchronised.
+// Exclusive max over the workgroup (values >= 0, identity 0).  Ends synchronised, unless
+// SYNC_END is false: then `s_wave` must not be written again before the caller's next
+// barrier.
+template <bool SYNC_END = true>
 __device__ __forceinline__ int block_exclusive_max(int v, int *s_wave) {
     const int l = lane();
     const int w = threadIdx.x / kWave;
@@ -89,7 +92,7 @@ __device__ __forceinline__ int block_exclusive_max(int v, int *s_wave) {
     if (l == 0) excl = 0;
     __syncthreads();
     for (int i = 0; i < w; ++i) excl = max(excl, s_wave[i]);
-    __syncthreads();
+    if (SYNC_END) __syncthreads();
     return excl;
 }
 
