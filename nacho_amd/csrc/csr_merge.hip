@@ -565,9 +565,10 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
         if (SPREAD) base = spread_by_a ? sp.a0 : sp.b0;
 
         int tile_total = 0;
-        const int offset =
-            dev::block_exclusive_sum<kBlock>(static_cast<int>(__popc(lo.valid)), s_wave, tile_total);
-        // (the scan's barriers also mean every lane is done reading this tile's LDS inputs)
+        // (the scan's barrier also means every lane is done reading this tile's LDS inputs;
+        // s_wave is next written after this tile's later barriers)
+        const int offset = dev::block_exclusive_sum<kBlock, int, false>(
+            static_cast<int>(__popc(lo.valid)), s_wave, tile_total);
 
         int ca_v[kSteps], cb_v[kSteps];
         if (CHILD) {

@@ -38,8 +38,10 @@ __device__ __forceinline__ T wave_sum(T v) {
 }
 
 // Exclusive prefix sum over a workgroup of BLOCK threads; `total` receives the sum of all.
-// `s_wave` holds BLOCK/64 entries.  Ends with the workgroup synchronised and `s_wave` free.
-template <int BLOCK, typename T>
+// `s_wave` holds BLOCK/64 entries.  Ends with the workgroup synchronised and `s_wave` free,
+// unless SYNC_END is false: then `s_wave` must not be written again before the caller's next
+// barrier.
+template <int BLOCK, typename T, bool SYNC_END = true>
 __device__ __forceinline__ T block_exclusive_sum(T v, T *s_wave, T &total) {
     static_assert(BLOCK % kWave == 0, "workgroup must be whole wavefronts");
     constexpr int kWaves = BLOCK / kWave;
@@ -54,7 +56,7 @@ __device__ __forceinline__ T block_exclusive_sum(T v, T *s_wave, T &total) {
         before += (i < w) ? x : T(0);
         all += x;
     }
-    __syncthreads();
+    if (SYNC_END) __syncthreads();
     total = all;
     return before + incl - v;
 }
