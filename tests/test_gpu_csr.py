@@ -168,6 +168,28 @@ def test_deterministic_and_stream(gpu):
     assert_csr_equal(second, first, "repeat")
 
 
+def test_results_are_stream_ordered(gpu):
+    """A call returns once the result length is known, while its write pass may still run:
+    work queued behind it on the same stream, with no host synchronisation in between, sees
+    the complete result."""
+    import nacho_amd
+    from nacho_amd import synth
+
+    a = synth.zipf_csr(1 << 16, 31)
+    b = synth.zipf_csr(1 << 16, 32)
+    want = oracle.port_csr_binary("add", 1 << 16, *a, *b, nthreads=4)
+    ga, gb = to_gpu(a, 1 << 16, 1 << 16, gpu), to_gpu(b, 1 << 16, 1 << 16, gpu)
+    side = torch.cuda.Stream(device=gpu)
+    side.wait_stream(torch.cuda.current_stream(gpu))
+    with torch.cuda.stream(side):
+        z = nacho_amd.gpu_csr_add_f32(ga, gb)
+        # queued on `side` right behind the call's kernels
+        copies = [t.clone() for t in (z.dim_j_offsets, z.dim_j_indices, z.values)]
+    side.synchronize()
+    got = tuple(t.cpu().numpy() for t in copies)
+    assert_csr_equal(got, want, "stream-ordered")
+
+
 def test_caller_allocator_through_c_abi(gpu):
     """Call the C entry point directly with a caller-supplied allocator (torch tensors)."""
     from nacho_amd import _lib
