@@ -190,6 +190,44 @@ def test_results_are_stream_ordered(gpu):
     assert_csr_equal(got, want, "stream-ordered")
 
 
+def test_concurrent_host_threads(gpu):
+    """Two host threads call csr_add / csr_mul at the same time on their own streams (the
+    ctypes call releases the GIL): per-thread readback words and events and the shared
+    caching allocator keep every result exact."""
+    import threading
+
+    import nacho_amd
+    from nacho_amd import synth
+
+    a = synth.zipf_csr(1 << 15, 41)
+    b = synth.zipf_csr(1 << 15, 42)
+    want = {op: oracle.port_csr_binary(op, 1 << 15, *a, *b, nthreads=4) for op in ("add", "mul")}
+    ga, gb = to_gpu(a, 1 << 15, 1 << 15, gpu), to_gpu(b, 1 << 15, 1 << 15, gpu)
+    torch.cuda.synchronize(gpu)
+    got, errors = {}, []
+
+    def work(op):
+        try:
+            fn = nacho_amd.gpu_csr_add_f32 if op == "add" else nacho_amd.gpu_csr_mul_f32
+            stream = torch.cuda.Stream(device=gpu)
+            with torch.cuda.stream(stream):
+                outs = [fn(ga, gb) for _ in range(6)]
+                host = [from_gpu(z) for z in outs]
+            got[op] = host
+        except Exception as e:  # reported below
+            errors.append(repr(e))
+
+    threads = [threading.Thread(target=work, args=(op,)) for op in ("add", "mul")]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    for op in ("add", "mul"):
+        for i, z in enumerate(got[op]):
+            assert_csr_equal(z, want[op], f"{op} #{i}")
+
+
 def test_caller_allocator_through_c_abi(gpu):
     """Call the C entry point directly with a caller-supplied allocator (torch tensors)."""
     from nacho_amd import _lib
