@@ -73,8 +73,8 @@ WORKLOADS = {
     "c2coo": dict(op="coo_add", kernel="coo_partition_kernel + coo_count_kernel + "
                                       "coo_write_kernel (packed 64-bit keys)",
                   desc="C2 as COO: coo_add f32 of the C2 operands' (i, j) tuples"),
-    "c2add3": dict(op="add3", kernel="two level merges (csr_partition_kernel + "
-                                    "csr_count_kernel + csr_write_kernel, twice)",
+    "c2add3": dict(op="add3", kernel="fused three-way merge (csr3_partition_kernel + "
+                                    "csr3_count_kernel + csr3_write_kernel)",
                    desc="csr_add_3 f32: three C2 operands (Zipf(1.6) rows, 16.7M nnz each, "
                         "seeds 1, 2, 4)"),
     "c2dcsr": dict(op="dcsr_add", kernel="two chained level merges (csr_partition_kernel + "

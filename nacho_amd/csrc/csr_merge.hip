@@ -838,87 +838,10 @@ int csr_binary(bool intersect, const nacho_csr *a, const nacho_csr *b, nacho_csr
     return NACHO_OK;
 }
 
-// Z = A + B + C (csr_add_3): the union of three CSR matrices, valued by the reference's
-// lattice for (a + b) + c: a sum of the present operands in that order, one float32 add per
-// extra operand (compute.cpp:413-491 with absent operands removed).  Computed as two level
-// merges, (A + B) into scratch memory and then (A + B) + C into the result: the first merge
-// makes every a + b and copy, the second adds c where present.
-int csr_add3(const nacho_csr *a, const nacho_csr *b, const nacho_csr *c, nacho_csr *z,
-             int32_t num_blocks, int32_t threads_per_block, void *stream,
-             const nacho_allocator *alloc) {
-    if (!z) return NACHO_ERR_INVALID_ARGUMENT;
-    *z = nacho_csr{};
-    NACHO_TRY(check_launch_hints(num_blocks, threads_per_block));
-    if (bad_csr(a) || bad_csr(b) || bad_csr(c)) return NACHO_ERR_INVALID_ARGUMENT;
-    if (a->dim_i_size != b->dim_i_size || a->dim_j_size != b->dim_j_size ||
-        a->dim_i_size != c->dim_i_size || a->dim_j_size != c->dim_j_size) {
-        return NACHO_ERR_INVALID_ARGUMENT;
-    }
-    const int rows = a->dim_i_size;
-    const long long cap_ab = static_cast<long long>(a->dim_j_length) + b->dim_j_length;
-    const long long cap = cap_ab + c->dim_j_length;
-    if (cap + rows > static_cast<long long>(INT_MAX) - 2 * kTile) return NACHO_ERR_INDEX_OVERFLOW;
-
-    Call call(stream, alloc);
-    int *pm = nullptr, *cm = nullptr;
-    float *vm = nullptr;
-    NACHO_TRY(call.scratch_n(static_cast<size_t>(rows) + 1, &pm));
-    NACHO_TRY(call.scratch_n(static_cast<size_t>(cap_ab), &cm));
-    NACHO_TRY(call.scratch_n(static_cast<size_t>(cap_ab), &vm));
-    long long nm = 0;
-    {
-        const LevelOperand A{a->dim_j_offsets, a->dim_j_indices, a->values, a->dim_j_length,
-                             nullptr};
-        const LevelOperand B{b->dim_j_offsets, b->dim_j_indices, b->values, b->dim_j_length,
-                             nullptr};
-        const LevelResult M{pm, cm, vm, nullptr, nullptr};
-        NACHO_TRY(merge_level(call, false, true, false, rows, A, B, M, &nm,
-                              "csr_add_3: two level merges"));
-    }
-    if (nm > cap_ab) return NACHO_ERR_MALFORMED_INPUT;
-    int *pz = nullptr, *cz = nullptr;
-    float *vz = nullptr;
-    const long long cap_z = nm + c->dim_j_length;
-    NACHO_TRY(call.result_n(static_cast<size_t>(rows) + 1, &pz));
-    NACHO_TRY(call.result_n(static_cast<size_t>(cap_z), &cz));
-    NACHO_TRY(call.result_n(static_cast<size_t>(cap_z), &vz));
-    long long nz = 0;
-    {
-        const LevelOperand M{pm, cm, vm, static_cast<int>(nm), nullptr};
-        const LevelOperand C{c->dim_j_offsets, c->dim_j_indices, c->values, c->dim_j_length,
-                             nullptr};
-        const LevelResult Z{pz, cz, vz, nullptr, nullptr};
-        NACHO_TRY(merge_level(call, false, true, false, rows, M, C, Z, &nz,
-                              "csr_add_3: two level merges"));
-    }
-    if (nz > cap_z) return NACHO_ERR_MALFORMED_INPUT;
-    if (nz == 0) {
-        call.drop_result(cz);
-        call.drop_result(vz);
-        cz = nullptr;
-        vz = nullptr;
-    }
-    z->dim_i_size = rows;
-    z->dim_j_size = a->dim_j_size;
-    z->dim_j_offsets = pz;
-    z->dim_j_length = static_cast<int32_t>(nz);
-    z->dim_j_indices = cz;
-    z->values = vz;
-    z->nnz = static_cast<int32_t>(nz);
-    call.commit();
-    return NACHO_OK;
-}
-
 }  // namespace csr
 }  // namespace nacho
 
 extern "C" {
-
-int nacho_gpu_csr_add_3_f32(const nacho_csr *a, const nacho_csr *b, const nacho_csr *c,
-                            nacho_csr *z, int32_t num_blocks, int32_t threads_per_block,
-                            void *stream, const nacho_allocator *alloc) {
-    return nacho::csr::csr_add3(a, b, c, z, num_blocks, threads_per_block, stream, alloc);
-}
 
 int nacho_gpu_csr_add_f32(const nacho_csr *a, const nacho_csr *b, nacho_csr *z,
                           int32_t num_blocks, int32_t threads_per_block, void *stream,

@@ -50,3 +50,28 @@ def test_c2_triple(gpu):
     rows = synth.C2_ROWS
     ops = [synth.zipf_csr(rows, s) for s in (1, 2, 4)]
     assert_csr_equal(run(rows, rows, ops, gpu), oracle.port_csr_add3(rows, *ops), "C2 triple")
+
+
+@pytest.mark.parametrize("pattern", ["same", "strided", "dense_rows"])
+def test_key_groups_across_tiles(gpu, pattern):
+    """Long rows where most keys occur in two or three operands, so that tile and lane
+    boundaries fall inside key groups (a group must still produce one entry)."""
+    rng = np.random.default_rng(7)
+    if pattern == "same":  # one row, every key in all three operands
+        rows, cols = 1, 40000
+        keys = [np.arange(cols)] * 3
+        ops = [csr_from_rows(rows, cols, [k.tolist()], rng.standard_normal(len(k)).tolist())
+               for k in keys]
+    elif pattern == "strided":  # A: even keys, B: multiples of 3, C: every key
+        rows, cols = 2, 30011
+        ops = []
+        for step in (2, 3, 1):
+            k = np.arange(0, cols, step)
+            ops.append(csr_from_rows(rows, cols, [k.tolist(), k[: len(k) // 2].tolist()],
+                                     rng.standard_normal(len(k) + len(k) // 2).tolist()))
+    else:  # many short dense rows with full overlap, and empty rows between
+        rows, cols = 5000, 7
+        lists = [[list(range(cols)) if r % 3 else [] for r in range(rows)] for _ in range(3)]
+        ops = [csr_from_rows(rows, cols, l, rng.standard_normal(sum(map(len, l))).tolist())
+               for l in lists]
+    assert_csr_equal(run(rows, cols, ops, gpu), oracle.port_csr_add3(rows, *ops), pattern)
