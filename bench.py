@@ -88,7 +88,7 @@ WORKLOADS = {
                                        "device pipeline, host readback gaps excluded)",
                     desc="sssmm f32: A * A masked by A on the C4 operand (R-MAT 2^20); "
                          "GFLOP/s = 3 FLOP (two multiplies, one add) per term"),
-    "c4": dict(op="spgemm", kernel="chunk_kernel<histogram, scatter> + dense/bitmap/sort "
+    "c4": dict(op="spgemm", kernel="long_hist_kernel + chunk_kernel (scatter) + dense/bitmap/sort "
                                  "unit kernels + copy_units_kernel and the sizing kernels "
                                  "(one call's device pipeline, host readback gaps excluded)",
                desc="C4 ESC SpGEMM C=A*A f32, R-MAT 2^20 (a,b,c,d)=(.57,.19,.19,.05), "
@@ -433,7 +433,7 @@ def bench_sssmm(args, device):
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": None,
+            "traffic": traffic_from_profiles("c4sssmm", "sssmm"),
             "kernel_avg_us": round(kernel_avg_ms * 1e3, 2),
         },
         "cpu_baseline": cpu,
