@@ -22,8 +22,9 @@
 //    emits (its value is the sum of the group's present values, in the order (a + b) + c,
 //    the others are peeked at their heads); later items of the group are skipped by
 //    comparing with the previous item's key, so groups may straddle lanes.  The count
-//    kernel totals the result length for the early readback; the write kernel stages its
-//    outputs in LDS and stores them coalesced.
+//    kernel totals the result length for the early readback and stores every lane's start;
+//    the write kernel walks from those starts, stages its outputs in LDS and stores them
+//    coalesced.
 // Every value is the reference's float32 sum in operand order, so results are bit-exact.
 #include <hip/hip_runtime.h>
 

@@ -92,6 +92,27 @@ def test_invalid_arguments_rejected_without_a_device(lib):
     assert z.dim_j_offsets is None and z.nnz == 0
 
 
+def test_csr_add_3_arguments_rejected_without_a_device(lib):
+    """The fused three-way union checks its third operand like the other two, and refuses
+    a total item count past int32 before any allocation."""
+    from nacho_amd import _lib
+
+    z = _lib.CsrDesc()
+    good = _lib.CsrDesc(4, 4, ctypes.c_void_p(0x1000), 0, None, None, 0)
+    other = _lib.CsrDesc(4, 5, ctypes.c_void_p(0x1000), 0, None, None, 0)
+    fn = lib.nacho_gpu_csr_add_3_f32
+    r = ctypes.byref
+    assert fn(r(good), r(good), None, r(z), 256, 256, None, None) == -1
+    assert fn(r(good), r(good), r(other), r(z), 256, 256, None, None) == -1
+    assert fn(r(good), r(good), r(good), None, 256, 256, None, None) == -1
+    assert fn(r(good), r(good), r(good), r(z), 256, 0, None, None) == -1
+    third = 2**30  # three operands of 2^30 entries: 3 * 2^30 items overflow int32
+    huge = _lib.CsrDesc(4, 4, ctypes.c_void_p(0x1000), third, ctypes.c_void_p(0x2000),
+                        ctypes.c_void_p(0x3000), third)
+    assert fn(r(huge), r(huge), r(huge), r(z), 256, 256, None, None) == -2
+    assert z.dim_j_offsets is None and z.nnz == 0
+
+
 def test_struct_layouts_match_the_header():
     """ctypes mirrors of the descriptors have the C layout (offsets of pointer fields)."""
     from nacho_amd import _lib
