@@ -145,20 +145,30 @@ __global__ void run_row_starts_kernel(const int *__restrict__ pos_b, int rows_b,
     }
 }
 
-// Run q (numbered by the exclusive scan run_idx of the flags): its bucket and its first B
-// entry; run_start[total runs] = nnz_b closes the last run.  B row k's runs are
+// Run q (numbered by the exclusive scan run_idx of the flags): its bucket (run[q].x) and
+// its first B entry; run_start[total runs] = nnz_b closes the last run.  B row k's runs are
 // [run_idx[pos_b[k]], run_idx[pos_b[k + 1]]).
 __global__ void runs_kernel(const int *__restrict__ crd_b, int64_t nnz_b, int shift,
                             const int64_t *__restrict__ flag, const int64_t *__restrict__ run_idx,
-                            int *__restrict__ run_bkt, int *__restrict__ run_start) {
+                            int2 *__restrict__ run, int *__restrict__ run_start) {
     for (int64_t p = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; p < nnz_b;
          p += static_cast<int64_t>(gridDim.x) * blockDim.x) {
         if (flag[p]) {
             const int64_t q = run_idx[p];
-            run_bkt[q] = crd_b[p] >> shift;
+            run[q].x = crd_b[p] >> shift;
             run_start[q] = static_cast<int>(p);
         }
         if (p == 0) run_start[run_idx[nnz_b]] = static_cast<int>(nnz_b);
+    }
+}
+
+// run[q].y = the length of run q (runs numbered below run_idx[nnz_b]).
+__global__ void run_lengths_kernel(const int64_t *__restrict__ run_idx, int64_t nnz_b,
+                                   const int *__restrict__ run_start, int2 *__restrict__ run) {
+    const int64_t n_runs = run_idx[nnz_b];
+    for (int64_t q = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; q < n_runs;
+         q += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        run[q].y = run_start[q + 1] - run_start[q];
     }
 }
 
@@ -189,8 +199,8 @@ __global__ __launch_bounds__(kBlock) void long_hist_kernel(
     const int *__restrict__ pos_a, const int *__restrict__ crd_a,
     const int64_t *__restrict__ blk_off, const int *__restrict__ blk_row, int rows,
     const int *__restrict__ pos_b, const int64_t *__restrict__ run_idx,
-    const int *__restrict__ run_bkt, const int *__restrict__ run_start, int nb,
-    const int64_t *__restrict__ seg_prefix, int64_t *__restrict__ seg_len) {
+    const int2 *__restrict__ run, int nb, const int64_t *__restrict__ seg_prefix,
+    int64_t *__restrict__ seg_len) {
     __shared__ int s_hist[kMaxBuckets];
     const int64_t n_blk = blk_off[rows];
     for (int64_t blk = blockIdx.x; blk < n_blk; blk += gridDim.x) {
@@ -201,10 +211,21 @@ __global__ __launch_bounds__(kBlock) void long_hist_kernel(
         const int p = pos_a[i] + static_cast<int>(blk - first) * kBlock + threadIdx.x;
         if (p < pos_a[i + 1]) {
             const int k = crd_a[p];
-            const int64_t q1 = run_idx[pos_b[k + 1]];
-            for (int64_t q = run_idx[pos_b[k]]; q < q1; ++q) {
-                const int b = run_bkt[q];
-                if (b < nb) atomicAdd(&s_hist[b], run_start[q + 1] - run_start[q]);
+            const int64_t q0 = run_idx[pos_b[k]];
+            const int n_runs = static_cast<int>(run_idx[pos_b[k + 1]] - q0);
+            const int2 *r = run + q0;
+            // four runs per iteration, so that four loads are in flight
+            int j = 0;
+            for (; j + 4 <= n_runs; j += 4) {
+                const int2 x0 = r[j], x1 = r[j + 1], x2 = r[j + 2], x3 = r[j + 3];
+                if (x0.x < nb) atomicAdd(&s_hist[x0.x], x0.y);
+                if (x1.x < nb) atomicAdd(&s_hist[x1.x], x1.y);
+                if (x2.x < nb) atomicAdd(&s_hist[x2.x], x2.y);
+                if (x3.x < nb) atomicAdd(&s_hist[x3.x], x3.y);
+            }
+            for (; j < n_runs; ++j) {
+                const int2 x = r[j];
+                if (x.x < nb) atomicAdd(&s_hist[x.x], x.y);
             }
         }
         __syncthreads();
@@ -1144,10 +1165,11 @@ int multiply(Call &call, const nacho_csr *a, const nacho_csr *b, Product *z) {
         const int64_t nnz_b = b->dim_j_length;
         const int rows_b = b->dim_i_size;
         int64_t *flag = nullptr, *run_idx = nullptr;
-        int *run_bkt = nullptr, *run_start = nullptr;
+        int2 *run = nullptr;
+        int *run_start = nullptr;
         NACHO_TRY(call.scratch_n(static_cast<size_t>(nnz_b) + 1, &flag));
         NACHO_TRY(call.scratch_n(static_cast<size_t>(nnz_b) + 1, &run_idx));
-        NACHO_TRY(call.scratch_n(static_cast<size_t>(nnz_b), &run_bkt));
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(nnz_b), &run));
         NACHO_TRY(call.scratch_n(static_cast<size_t>(nnz_b) + 1, &run_start));
         run_flags_kernel<<<grid_for(nnz_b, 256), 256, 0, st>>>(b->dim_j_indices, nnz_b, shift,
                                                                flag);
@@ -1159,7 +1181,9 @@ int multiply(Call &call, const nacho_csr *a, const nacho_csr *b, Product *z) {
         }
         NACHO_TRY(scan::exclusive_scan_i64(call, flag, nnz_b, run_idx));
         runs_kernel<<<grid_for(nnz_b, 256), 256, 0, st>>>(b->dim_j_indices, nnz_b, shift, flag,
-                                                          run_idx, run_bkt, run_start);
+                                                          run_idx, run, run_start);
+        NACHO_TRY_HIP(hipGetLastError());
+        run_lengths_kernel<<<grid_for(nnz_b, 256), 256, 0, st>>>(run_idx, nnz_b, run_start, run);
         NACHO_TRY_HIP(hipGetLastError());
         int64_t *nblk = nullptr, *blk_off = nullptr;
         int *blk_row = nullptr;
@@ -1175,7 +1199,7 @@ int multiply(Call &call, const nacho_csr *a, const nacho_csr *b, Product *z) {
         NACHO_TRY_HIP(hipGetLastError());
         long_hist_kernel<<<kHistGrid, kBlock, 0, st>>>(
             a->dim_j_offsets, a->dim_j_indices, blk_off, blk_row, rows, b->dim_j_offsets,
-            run_idx, run_bkt, run_start, nb, seg_prefix, seg_len);
+            run_idx, run, nb, seg_prefix, seg_len);
         NACHO_TRY_HIP(hipGetLastError());
         NACHO_TRY(scan::exclusive_scan_i64(call, seg_len, n_seg, seg_off));
         chunk_kernel<<<chunks, kBlock, 0, st>>>(
