@@ -711,11 +711,25 @@ __global__ __launch_bounds__(kBlock) void sort_unit_kernel(
     const int64_t start = unit_start[u];
     const int n = static_cast<int>(unit_start[u + 1] - start);
     const int64_t s_end = u + 1 < n_units ? unit_seg[u + 1] : n_seg;
-    for (int q = threadIdx.x; q < kTile; q += kBlock) {
-        s_mark[pad(q)] = 0;
-        if (q < n) {  // coalesced staging of the raw columns and values
-            s_key[pad(q)] = static_cast<K>(static_cast<uint32_t>(key[start + q]));
-            s_val[pad(q)] = val[start + q];
+    {
+        // coalesced staging of the raw columns and values: every load issued first (clamped
+        // to the unit), then the LDS stores
+        int kk[kPer];
+        float vv[kPer];
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int64_t q = start + max(0, min(static_cast<int>(threadIdx.x) + j * kBlock, n - 1));
+            kk[j] = n > 0 ? key[q] : 0;
+            vv[j] = n > 0 ? val[q] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int q = threadIdx.x + j * kBlock;
+            s_mark[pad(q)] = 0;
+            if (q < n) {
+                s_key[pad(q)] = static_cast<K>(static_cast<uint32_t>(kk[j]));
+                s_val[pad(q)] = vv[j];
+            }
         }
     }
     __syncthreads();
@@ -842,10 +856,11 @@ __device__ __forceinline__ void mark_bucket(unsigned *bm, const unsigned short *
 
 // One workgroup per bitmap unit; one wavefront per bucket at a time.  A bucket's distinct
 // columns are the set bits of its 8192-bit window bitmap; the rank of a column (prefix
-// popcount) indexes its float64 accumulator, and reading the bits in order emits the
-// distinct columns sorted.  Pass A counts each bucket's distinct columns (for the output
-// offsets inside the unit); pass B accumulates and writes.  Accumulators of a bucket live
-// in its own product range of the unit.
+// popcount) indexes its float64 accumulator, and reading the bits in order lists the
+// distinct columns sorted.  Accumulators and the listed columns of a bucket live in its own
+// product range of the unit; once every bucket is done, a scan of their counts gives the
+// output offsets and the workgroup stores the unit's entries with consecutive lanes on
+// consecutive outputs.
 __global__ __launch_bounds__(kBlock) void bitmap_unit_kernel(
     const int *__restrict__ bitmap_list, const int *__restrict__ unit_seg,
     const int64_t *__restrict__ unit_start, int64_t n_units, int64_t n_seg,
@@ -883,34 +898,24 @@ __global__ __launch_bounds__(kBlock) void bitmap_unit_kernel(
     // the unit's columns, staged once (bucket = column >> shift, so the window offset is
     // the column's low bits); values are read from the product buffer when accumulated
     const int low = (1 << shift) - 1;
-    for (int q = threadIdx.x; q < n; q += kBlock) {
-        s_col[q] = static_cast<unsigned short>(key[start + q] & low);
+    for (int q0 = threadIdx.x; q0 < n; q0 += 4 * kBlock) {
+        int kv[4];  // four loads in flight (clamped to the unit)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) kv[j] = key[start + min(q0 + j * kBlock, n - 1)];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (q0 + j * kBlock < n) s_col[q0 + j * kBlock] = static_cast<unsigned short>(kv[j] & low);
+        }
     }
     __syncthreads();
     const int w = threadIdx.x / dev::kWave, l = dev::lane();
     unsigned *bm = s_bits[w];
     int *pre = s_pre[w];
-    // pass A: distinct columns per bucket
-    for (int o = w; o < n_buckets; o += kWaves) {
-        mark_bucket(bm, s_col, s_x0[o], s_x0[o + 1]);
-        int c = 0;
-#pragma unroll
-        for (int i = 0; i < kBitmapWords / dev::kWave; ++i) c += __popc(bm[l + i * dev::kWave]);
-        c = dev::wave_sum(c);
-        if (l == 0) s_out[o] = c;
-        wave_sync();
-    }
-    __syncthreads();
-    // output offset of each bucket inside the unit
-    int total = 0;
-    const int cnt = static_cast<int>(threadIdx.x) < n_buckets ? s_out[threadIdx.x] : 0;
-    const int off = dev::block_exclusive_sum<kBlock>(cnt, s_wave, total);
-    if (static_cast<int>(threadIdx.x) < n_buckets) s_out[threadIdx.x] = off;
-    __syncthreads();
-    // pass B: accumulate by rank, emit in column order
+    // accumulate each bucket by rank; its distinct columns (window offsets, in order) and
+    // their sums are left in its own product range, s_col / s_acc[x0 + rank]
     constexpr int kWordsPerLane = kBitmapWords / dev::kWave;
     for (int o = w; o < n_buckets; o += kWaves) {
-        const int x0 = s_x0[o], x1 = s_x0[o + 1], base = s_base[o];
+        const int x0 = s_x0[o], x1 = s_x0[o + 1];
         for (int x = x0 + l; x < x1; x += dev::kWave) s_acc[x] = 0.0;
         mark_bucket(bm, s_col, x0, x1);
         // exclusive popcount prefix per word; lane l owns words [l*4, l*4 + 4)
@@ -921,21 +926,30 @@ __global__ __launch_bounds__(kBlock) void bitmap_unit_kernel(
             pc[i] = __popc(bm[l * kWordsPerLane + i]);
             mine += pc[i];
         }
-        int run = dev::wave_inclusive_sum(mine) - mine;
+        const int incl = dev::wave_inclusive_sum(mine);
+        int run = incl - mine;
 #pragma unroll
         for (int i = 0; i < kWordsPerLane; ++i) {
             pre[l * kWordsPerLane + i] = run;
             run += pc[i];
         }
         wave_sync();
-        for (int x = x0 + l; x < x1; x += dev::kWave) {
-            const int c = s_col[x];
-            const int wd = c >> 5;
-            const int r = pre[wd] + __popc(bm[wd] & ((1u << (c & 31)) - 1u));
-            atomicAdd(&s_acc[x0 + r], static_cast<double>(val[start + x]));
+        for (int xb = x0 + l; xb < x1; xb += 4 * dev::kWave) {
+            float vv[4];  // four value loads in flight (clamped to the bucket)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) vv[j] = val[start + min(xb + j * dev::kWave, x1 - 1)];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int x = xb + j * dev::kWave;
+                if (x < x1) {
+                    const int c = s_col[x];
+                    const int wd = c >> 5;
+                    const int r = pre[wd] + __popc(bm[wd] & ((1u << (c & 31)) - 1u));
+                    atomicAdd(&s_acc[x0 + r], static_cast<double>(vv[j]));
+                }
+            }
         }
-        wave_sync();
-        const int64_t out = start + s_out[o];
+        wave_sync();  // every column of the bucket is read: its slots take the output columns
 #pragma unroll
         for (int i = 0; i < kWordsPerLane; ++i) {
             const int wd = l * kWordsPerLane + i;
@@ -944,12 +958,28 @@ __global__ __launch_bounds__(kBlock) void bitmap_unit_kernel(
             while (m) {
                 const int bit = __ffs(m) - 1;
                 m &= m - 1u;
-                ukey[out + r] = base + wd * 32 + bit;
-                uval[out + r] = static_cast<float>(s_acc[x0 + r]);
+                s_col[x0 + r] = static_cast<unsigned short>(wd * 32 + bit);
                 ++r;
             }
         }
+        if (l == dev::kWave - 1) s_out[o] = incl;  // the bucket's distinct columns
         wave_sync();
+    }
+    __syncthreads();
+    // output offset of each bucket inside the unit
+    int total = 0;
+    const int cnt = static_cast<int>(threadIdx.x) < n_buckets ? s_out[threadIdx.x] : 0;
+    const int off = dev::block_exclusive_sum<kBlock>(cnt, s_wave, total);
+    if (static_cast<int>(threadIdx.x) < n_buckets) s_out[threadIdx.x] = off;
+    __syncthreads();
+    // the unit's entries, consecutive lanes on consecutive outputs: output i belongs to the
+    // last bucket whose offset is at most i
+    for (int i = threadIdx.x; i < total; i += kBlock) {
+        int o = 0;
+        for (int b = 1; b < n_buckets; ++b) o += s_out[b] <= i ? 1 : 0;
+        const int x = s_x0[o] + (i - s_out[o]);
+        ukey[start + i] = s_base[o] + s_col[x];
+        uval[start + i] = static_cast<float>(s_acc[x]);
     }
     // rows starting in this unit, and the unit's count
     if (static_cast<int>(threadIdx.x) < n_buckets) {
@@ -1001,11 +1031,23 @@ __global__ __launch_bounds__(kDenseBlock) void dense_unit_kernel(
         for (int i = threadIdx.x; i < kDenseCols; i += kDenseBlock) s_acc[i] = 0.0;
         if (threadIdx.x < kDenseCols / 32) s_bits[threadIdx.x] = 0u;
         __syncthreads();
-        for (int64_t x = threadIdx.x; x < len; x += kDenseBlock) {
-            const int64_t c = key[start + x] - w0;
-            if (c >= 0 && c < kDenseCols) {
-                atomicAdd(&s_acc[c], static_cast<double>(val[start + x]));
-                atomicOr(&s_bits[c >> 5], 1u << (c & 31));
+        // four products per iteration, their loads issued first (clamped to the segment)
+        for (int64_t x0 = threadIdx.x; x0 < len; x0 += 4 * kDenseBlock) {
+            int kk[4];
+            float vv[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int64_t x = min(x0 + q * kDenseBlock, len - 1);
+                kk[q] = key[start + x];
+                vv[q] = val[start + x];
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int64_t c = kk[q] - w0;
+                if (x0 + q * kDenseBlock < len && c >= 0 && c < kDenseCols) {
+                    atomicAdd(&s_acc[c], static_cast<double>(vv[q]));
+                    atomicOr(&s_bits[c >> 5], 1u << (c & 31));
+                }
             }
         }
         __syncthreads();
