@@ -185,18 +185,19 @@ int dcsr_binary(bool intersect, const nacho_dcsr *a, const nacho_dcsr *b, nacho_
             NACHO_TRY_HIP(hipGetLastError());
         }
         NACHO_TRY(scan::exclusive_scan_i64(call, keep, nu, keep_off));
-        NACHO_TRY(call.timer_stop());
-        int64_t kept = 0;
-        NACHO_TRY(call.read_back(&kept, keep_off + nu, sizeof(kept)));
-        ni = kept;
-        NACHO_TRY(call.result_n(static_cast<size_t>(ni), &crd_i));
-        NACHO_TRY(call.result_n(static_cast<size_t>(ni) + 1, &pos_j));
-        NACHO_TRY(call.timer_start(name));
+        // The kept rows are compacted into arrays sized for all nu rows, so the compaction
+        // follows the scan on the stream without a host round trip; the count is read once,
+        // at the end.
+        NACHO_TRY(call.result_n(static_cast<size_t>(nu), &crd_i));
+        NACHO_TRY(call.result_n(static_cast<size_t>(nu) + 1, &pos_j));
         compact_rows_kernel<<<grid_for(nu + 1), kBlock, 0, s>>>(keep_off, crd_u, pos_u,
                                                                 static_cast<int>(nu), crd_i,
                                                                 pos_j);
         NACHO_TRY_HIP(hipGetLastError());
         NACHO_TRY(call.timer_stop());
+        int64_t kept = 0;
+        NACHO_TRY(call.read_back(&kept, keep_off + nu, sizeof(kept)));
+        ni = kept;
         NACHO_TRY(call.collect_timer());
     }
     if (ni == 0 && crd_i) {
