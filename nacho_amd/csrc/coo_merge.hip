@@ -108,8 +108,10 @@ __device__ __forceinline__ void merge_split(ReadA A, ReadB B, int aS, int aE, in
     if (a > aS && b < bE && A(a - 1) == B(b)) ++b;
 }
 
+constexpr int kPartBlock = 64;
+
 template <typename Codec>
-__global__ __launch_bounds__(256) void coo_partition_kernel(Codec codec, Coords ca, int nnz_a,
+__global__ __launch_bounds__(kPartBlock) void coo_partition_kernel(Codec codec, Coords ca, int nnz_a,
                                                             Coords cb, int nnz_b, int num_tiles,
                                                             int *__restrict__ split_a,
                                                             int *__restrict__ split_b,
@@ -468,7 +470,9 @@ int coo_binary(int arity, const int32_t extents[3], Coords ca, const float *va, 
     NACHO_TRY(call.result_n(static_cast<size_t>(cap), &zv));
 
     const hipStream_t s = call.stream();
-    const unsigned part_grid = ceil_div(static_cast<size_t>(num_tiles) + 1, 256);
+    // one thread per boundary in 64-thread workgroups, so the dependent searches spread
+    // over every CU
+    const unsigned part_grid = ceil_div(static_cast<size_t>(num_tiles) + 1, kPartBlock);
     const int bi = bits_for_extent(extents[0]), bj = bits_for_extent(extents[1]);
     const int bk = arity == 3 ? bits_for_extent(extents[2]) : 0;
     unsigned *counts = nullptr;
@@ -503,7 +507,7 @@ int coo_binary(int arity, const int32_t extents[3], Coords ca, const float *va, 
             NACHO_TRY(call.scratch_n(static_cast<size_t>(grid) + 1, &chunk_total));
             int64_t *len_dev = chunk_total + grid;
             NACHO_TRY(call.timer_start(kernel_name));
-            coo_partition_kernel<Codec><<<part_grid, 256, 0, s>>>(codec, ca, nnz_a, cb, nnz_b,
+            coo_partition_kernel<Codec><<<part_grid, kPartBlock, 0, s>>>(codec, ca, nnz_a, cb, nnz_b,
                                                                   num_tiles, split_a, split_b,
                                                                   done);
             NACHO_TRY_HIP(hipGetLastError());
@@ -524,7 +528,7 @@ int coo_binary(int arity, const int32_t extents[3], Coords ca, const float *va, 
             return NACHO_OK;
         }
         NACHO_TRY(call.timer_start(kernel_name));
-        coo_partition_kernel<Codec><<<part_grid, 256, 0, s>>>(codec, ca, nnz_a, cb, nnz_b, num_tiles,
+        coo_partition_kernel<Codec><<<part_grid, kPartBlock, 0, s>>>(codec, ca, nnz_a, cb, nnz_b, num_tiles,
                                                               split_a, split_b, done);
         NACHO_TRY_HIP(hipGetLastError());
         coo_count_kernel<OP, Codec><<<grid, kBlock, 0, s>>>(codec, ca, cb, num_tiles, chunk, split_a,

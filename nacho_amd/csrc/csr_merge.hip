@@ -51,6 +51,7 @@ enum class Op { Union, Intersect };
 constexpr int kBlock = 256;
 constexpr int kItemsPerLane = 15;  // odd: lanes' LDS walks spread over banks
 constexpr int kTile = kBlock * kItemsPerLane;
+constexpr int kPartBlock = 64;  // threads per workgroup of the partition kernel
 
 
 // Merge-path split of the merged order of A[aS, aE) and B[bS, bE) (ties: A first) at the
@@ -76,7 +77,9 @@ __device__ __forceinline__ void merge_split(ReadA A, ReadB B, int aS, int aE, in
 
 // One thread per tile boundary t in [0, num_tiles]: split of diagonal min(t*TILE, total).
 // Thread 0 also zeroes the ticket counter that the next kernel's length total uses.
-__global__ __launch_bounds__(256) void csr_partition_kernel(
+// (Launched in kPartBlock-thread workgroups: the few thousand boundaries then spread over
+// every CU instead of a few dozen.)
+__global__ __launch_bounds__(kPartBlock) void csr_partition_kernel(
     const int *__restrict__ pa, const int *__restrict__ ca, const int *__restrict__ pb,
     const int *__restrict__ cb, int rows, int total, int num_tiles, int *__restrict__ split_r,
     int *__restrict__ split_a, int *__restrict__ split_b, unsigned long long *__restrict__ done) {
@@ -725,7 +728,7 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
         NACHO_TRY(call.scratch_n(static_cast<size_t>(grid) + 1, &chunk_total));
         int64_t *len_dev = chunk_total + grid;
         NACHO_TRY(call.timer_start(kernel_name));  // the whole device pipeline of this level
-        csr_partition_kernel<<<ceil_div(static_cast<size_t>(num_tiles) + 1, 256), 256, 0, s>>>(
+        csr_partition_kernel<<<ceil_div(static_cast<size_t>(num_tiles) + 1, kPartBlock), kPartBlock, 0, s>>>(
             A.pos, A.crd, B.pos, B.crd, rows, static_cast<int>(total), num_tiles, split_r,
             split_a, split_b, done);
         NACHO_TRY_HIP(hipGetLastError());
@@ -750,7 +753,7 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
     uint2 *starts = nullptr;  // every lane's walk start, from the count kernel to the write
     NACHO_TRY(call.scratch_n(static_cast<size_t>(num_tiles) * kBlock, &starts));
     NACHO_TRY(call.timer_start(kernel_name));  // the whole device pipeline of this level
-    csr_partition_kernel<<<ceil_div(static_cast<size_t>(num_tiles) + 1, 256), 256, 0, s>>>(
+    csr_partition_kernel<<<ceil_div(static_cast<size_t>(num_tiles) + 1, kPartBlock), kPartBlock, 0, s>>>(
         A.pos, A.crd, B.pos, B.crd, rows, static_cast<int>(total), num_tiles, split_r, split_a,
         split_b, done);
     NACHO_TRY_HIP(hipGetLastError());

@@ -46,6 +46,7 @@ constexpr int kCap = kTile + 3;          // a split takes at most two more group
 constexpr int kLoads = (kCap + kBlock - 1) / kBlock;
 constexpr int kSteps = kIpt + 2;         // a lane's range plus the group rule's two items
 constexpr int kMaxChunk = 64;
+constexpr int kPartBlock = 64;           // partition workgroups: boundaries over every CU
 constexpr int kMax = INT_MAX;            // head sentinel: that operand's row is exhausted
 static_assert(kCap < 65536, "tile-local offsets are packed in 16 bits");
 
@@ -99,7 +100,7 @@ __device__ __forceinline__ void split3(RA A, RB B, RC C, int aS, int aE, int bS,
 // One thread per tile boundary t in [0, num_tiles]: the split (row, a, b, c) of diagonal
 // min(t * kTile, total), moved past the rest of a key group it would cut.  Thread 0 also
 // zeroes the accumulator of the count kernel's length total.
-__global__ __launch_bounds__(256) void csr3_partition_kernel(
+__global__ __launch_bounds__(kPartBlock) void csr3_partition_kernel(
     const int *__restrict__ pa, const int *__restrict__ ca, const int *__restrict__ pb,
     const int *__restrict__ cb, const int *__restrict__ pc, const int *__restrict__ cc,
     int rows, int total, int num_tiles, int *__restrict__ split,
@@ -551,7 +552,8 @@ int csr_add3_fused(const nacho_csr *a, const nacho_csr *b, const nacho_csr *c, n
 
     const hipStream_t s = call.stream();
     NACHO_TRY(call.timer_start("csr_add_3: fused three-way merge"));
-    csr3_partition_kernel<<<ceil_div(static_cast<size_t>(num_tiles) + 1, 256), 256, 0, s>>>(
+    csr3_partition_kernel<<<ceil_div(static_cast<size_t>(num_tiles) + 1, kPartBlock), kPartBlock,
+                            0, s>>>(
         a->dim_j_offsets, a->dim_j_indices, b->dim_j_offsets, b->dim_j_indices,
         c->dim_j_offsets, c->dim_j_indices, rows, static_cast<int>(total), num_tiles, split,
         done);
