@@ -1,9 +1,13 @@
 /*
  * nacho_hip.h — C ABI of the MI355X (gfx950) backend for nacho's GPU target.
  *
- * Every declared GPU kernel of the reference gets one extern "C" entry point here.  The
- * reference binds `namespace <k> { Z_tensor_format <k>_gpu_i32_f32(a, b, num_blocks,
- * threads_per_block); }` (entry point printed at src/backend/stitch_and_generate.cpp:299-301,
+ * Each GPU kernel that the reference declares for the operations this backend covers
+ * (csr_add, csr_add_3, csr_mul, coo_add, coo_mul, coo3d_add, csf_add, dcsr_add, dcsr_mul,
+ * dcsr_mul_without_recursive_partitioning, spgemm, sssmm: compiler.cpp:112-153) gets one
+ * extern "C" entry point here.  The reference's coo_csr_add, inner_prod and inner_prod_coo
+ * declarations (compiler.cpp:122, 141, 143) have none.  The reference binds
+ * `namespace <k> { Z_tensor_format <k>_gpu_i32_f32(a, b, num_blocks, threads_per_block); }`
+ * (entry point printed at src/backend/stitch_and_generate.cpp:299-301,
  * called from the wrapper written by src/backend/generate_bindings.cpp:288-314).  These
  * functions replace those generated entry points: same operands, same meaning of every
  * field, same launch-geometry arguments, plus an explicit stream and an optional allocator.
@@ -30,8 +34,9 @@
  * Input contract (the reference's, made explicit): pos[0] == 0, pos non-decreasing,
  * pos[rows] == length of the coordinate array, coordinates strictly increasing within
  * each fibre (sorted, no duplicates), COO/COO3 coordinates sorted lexicographically and
- * distinct.  As in the reference, the device does not check it: host-side shape and pointer
- * checks return NACHO_ERR_INVALID_ARGUMENT, but operand contents are trusted.
+ * distinct.  As in the reference, the entry points do not check it on the device: host-side
+ * shape and pointer checks return NACHO_ERR_INVALID_ARGUMENT, operand contents are trusted,
+ * and nacho_validate_csr() checks a CSR operand on request.
  */
 #ifndef NACHO_HIP_H
 #define NACHO_HIP_H
@@ -48,9 +53,10 @@ extern "C" {
 #define NACHO_ERR_INVALID_ARGUMENT (-1) /* null pointer, negative size, shape mismatch   */
 #define NACHO_ERR_INDEX_OVERFLOW (-2)   /* result or work count does not fit int32        */
 #define NACHO_ERR_OUT_OF_MEMORY (-3)    /* the allocator returned NULL                    */
-#define NACHO_ERR_MALFORMED_INPUT (-4)  /* validation found unsorted/duplicate/bad pos    */
+#define NACHO_ERR_MALFORMED_INPUT (-4)  /* nacho_validate_* found unsorted/duplicate/bad
+                                           pos, or a reader found a malformed file     */
 #define NACHO_ERR_NO_DEVICE (-5)        /* no HIP device visible                          */
-#define NACHO_ERR_INTERNAL (-6)         /* a kernel's bounded wait expired (library bug)  */
+#define NACHO_ERR_INTERNAL (-6)         /* a kernel did not publish a result length       */
 #define NACHO_ERR_IO (-7)               /* a file could not be opened or read             */
 #define NACHO_ERR_UNSUPPORTED (-8)      /* a file format variant the reader does not take */
 
@@ -170,6 +176,15 @@ int nacho_free(void *ptr, void *stream);
  * stream-ordered).  This returns every cached, unused buffer to the driver. */
 int nacho_release_cached_memory(void);
 
+/* Note that work queued on `stream` uses the buffer `ptr` (a buffer the default allocator
+ * returned, not yet released).  When the buffer is released on its own stream, an event is
+ * also recorded on `stream`, and the buffer is reused only by work ordered after it: a
+ * consumer on another stream may drop its reference before its reads finish.  The
+ * counterpart of torch's Tensor.record_stream for this library's buffers; the reference,
+ * which runs everything on stream 0, has none.  NACHO_ERR_INVALID_ARGUMENT if `ptr` is not
+ * a live buffer of the default allocator. */
+int nacho_record_stream(void *ptr, void *stream);
+
 /* ---- entry points ------------------------------------------------------------------
  * `num_blocks` / `threads_per_block` are the reference's launch arguments
  * (generate_bindings.cpp:292-325, default 256/256).  They are accepted and validated
@@ -263,6 +278,16 @@ int nacho_gpu_spgemm_f32(const nacho_csr *a, const nacho_csr *b, nacho_csr *z,
 int nacho_gpu_spgemm64_f32(const nacho_csr *a, const nacho_csr *b, nacho_csr64 *z,
                            int32_t num_blocks, int32_t threads_per_block, void *stream,
                            const nacho_allocator *alloc);
+
+/* ---- input validation ------------------------------------------------------------
+ * The entry points trust operand contents, as the reference's generated code does.  This
+ * checks a CSR operand against the input contract on the device: pos[0] == 0, pos
+ * non-decreasing, pos[rows] == dim_j_length, 0 <= crd < dim_j_size, crd strictly
+ * increasing within each row.  Returns NACHO_OK, NACHO_ERR_MALFORMED_INPUT, or
+ * NACHO_ERR_INVALID_ARGUMENT for host-visible faults (null pointers, negative sizes).
+ * Synchronises `stream`.  No counterpart in the reference (its generated code checks
+ * nothing). */
+int nacho_validate_csr(const nacho_csr *t, void *stream);
 
 /* ---- file readers (host) ---------------------------------------------------------
  * Matrix Market and FROSTT readers, replacing nacho.parse2D / nacho.parse3D_i32_f32

@@ -25,7 +25,10 @@ from .ops import (  # noqa: F401
     last_kernel_ms,
     release_cached_memory,
     set_kernel_timing,
+    set_validation,
+    validate_csr,
 )
+from ._device import record_stream  # noqa: F401
 from .io import COO2D, COO3D_parsed, parse2D, parse3D_i32_f32  # noqa: F401
 from .tensors import COO3_gpu, COO_gpu, CSF3_gpu, CSR64_gpu, CSR_gpu, DCSR_gpu  # noqa: F401
 

@@ -1,9 +1,12 @@
 """Device plumbing between torch and the C ABI: streams, and adopting result buffers.
 
 Result buffers come back from libnacho_hip.so as raw device pointers owned by the caller
-(allocated from the device's stream-ordered pool).  `adopt` wraps one in a torch tensor
-without copying; when the last tensor referencing it is collected the buffer is released
-with `nacho_free` on the stream it was produced on.  This is the counterpart of the
+(allocated by the library's caching allocator over hipMalloc).  `adopt` wraps one in a torch
+tensor without copying; when the last tensor referencing it is collected the buffer is
+released with `nacho_free` on the stream it was produced on.  Work on another stream that
+reads a result must be announced with `record_stream` (torch's own `Tensor.record_stream`
+only tracks torch's allocator): the library then orders the buffer's reuse after that
+stream's work at release time.  This is the counterpart of the
 reference's `adopt_gpu` capsule (runtime/nacho_nb.h:50-58).  A zero-length result is a
 NULL pointer and becomes an empty tensor (runtime/nacho_nb.h:37-39).
 """
@@ -136,6 +139,19 @@ def adopt(ptr: int | None, count: int, dtype: torch.dtype, device: torch.device,
     if tensor.data_ptr() != ptr or tensor.numel() != count or tensor.dtype != dtype:
         raise RuntimeError("torch did not adopt the device buffer in place")
     return tensor
+
+
+def record_stream(t: torch.Tensor, stream) -> None:
+    """Mark the library-allocated buffer under `t` as used by `stream` (a torch.cuda.Stream
+    or a raw hipStream_t), so that its reuse after release waits for work queued on that
+    stream until then."""
+    if t.numel() == 0:
+        return
+    raw = stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream)
+    rc = _lib.load().nacho_record_stream(ctypes.c_void_p(t.data_ptr()), ctypes.c_void_p(raw))
+    if rc != 0:
+        raise ValueError("record_stream: the tensor does not start a buffer that libnacho_hip "
+                         f"allocated ({_lib.error_string(rc)})")
 
 
 def adoption_route() -> str | None:

@@ -205,9 +205,10 @@ def load() -> ctypes.CDLL:
     lib.nacho_last_kernel_ms.argtypes = []
     lib.nacho_last_kernel_name.restype = ctypes.c_char_p
     lib.nacho_last_kernel_name.argtypes = []
-    if hasattr(lib, "nacho_validate_csr"):
-        lib.nacho_validate_csr.restype = ctypes.c_int
-        lib.nacho_validate_csr.argtypes = [ctypes.POINTER(CsrDesc), ctypes.c_void_p]
+    lib.nacho_validate_csr.restype = ctypes.c_int
+    lib.nacho_validate_csr.argtypes = [ctypes.POINTER(CsrDesc), ctypes.c_void_p]
+    lib.nacho_record_stream.restype = ctypes.c_int
+    lib.nacho_record_stream.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
     _lib = lib
     return lib
 

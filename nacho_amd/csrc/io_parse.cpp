@@ -16,6 +16,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <new>
 #include <string>
 #include <vector>
 
@@ -108,13 +109,22 @@ T *to_malloc(const std::vector<T> &v) {
 
 }  // namespace
 
-extern "C" {
+namespace {
 
-void nacho_host_free(void *p) { std::free(p); }
+// The readers are called through ctypes and C: a C++ exception must not leave them.
+// std::bad_alloc becomes NACHO_ERR_OUT_OF_MEMORY, anything else NACHO_ERR_MALFORMED_INPUT.
+template <typename F>
+int guarded(F &&body) {
+    try {
+        return body();
+    } catch (const std::bad_alloc &) {
+        return NACHO_ERR_OUT_OF_MEMORY;
+    } catch (...) {
+        return NACHO_ERR_MALFORMED_INPUT;
+    }
+}
 
-int nacho_parse2d(const char *path, nacho_coo2d_host *out) {
-    if (!path || !out) return NACHO_ERR_INVALID_ARGUMENT;
-    *out = nacho_coo2d_host{};
+int parse2d(const char *path, nacho_coo2d_host *out) {
     std::string text;
     if (!read_file(path, &text)) return NACHO_ERR_IO;
     Cursor c{text.c_str()};
@@ -138,9 +148,13 @@ int nacho_parse2d(const char *path, nacho_coo2d_host *out) {
     const bool symm = symmetry == "symmetric" || skew;
     std::vector<int32_t> row, col;
     std::vector<float> val;
-    row.reserve(nnz);
-    col.reserve(nnz);
-    val.reserve(nnz);
+    // Every entry takes at least 6 characters ("1 1 0\n"), so a header that claims more
+    // entries than the text can hold does not get to size the buffers.
+    const uint64_t room = static_cast<uint64_t>(text.size() / 6);
+    const size_t expect = static_cast<size_t>(nnz < room ? nnz : room);
+    row.reserve(expect);
+    col.reserve(expect);
+    val.reserve(expect);
     uint64_t mirrored = 0;
     for (uint64_t e = 0; e < nnz; ++e) {
         uint64_t i = 0, j = 0;
@@ -178,9 +192,7 @@ int nacho_parse2d(const char *path, nacho_coo2d_host *out) {
     return NACHO_OK;
 }
 
-int nacho_parse3d(const char *path, int32_t n, int32_t m, int32_t k, nacho_coo3d_host *out) {
-    if (!path || !out) return NACHO_ERR_INVALID_ARGUMENT;
-    *out = nacho_coo3d_host{};
+int parse3d(const char *path, int32_t n, int32_t m, int32_t k, nacho_coo3d_host *out) {
     std::string text;
     if (!read_file(path, &text)) return NACHO_ERR_IO;
     Cursor c{text.c_str()};
@@ -219,6 +231,24 @@ int nacho_parse3d(const char *path, int32_t n, int32_t m, int32_t k, nacho_coo3d
     out->K = k;
     out->nnz = static_cast<int64_t>(ci.size());
     return NACHO_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+void nacho_host_free(void *p) { std::free(p); }
+
+int nacho_parse2d(const char *path, nacho_coo2d_host *out) {
+    if (!path || !out) return NACHO_ERR_INVALID_ARGUMENT;
+    *out = nacho_coo2d_host{};
+    return guarded([&] { return parse2d(path, out); });
+}
+
+int nacho_parse3d(const char *path, int32_t n, int32_t m, int32_t k, nacho_coo3d_host *out) {
+    if (!path || !out) return NACHO_ERR_INVALID_ARGUMENT;
+    *out = nacho_coo3d_host{};
+    return guarded([&] { return parse3d(path, n, m, k, out); });
 }
 
 }  // extern "C"

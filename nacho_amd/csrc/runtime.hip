@@ -18,21 +18,71 @@ namespace {
 // Result and scratch buffers are recycled instead of going back to the driver: every call
 // of an entry point allocates a handful of buffers, and driver allocation (or the
 // stream-ordered pool) costs tens of microseconds each.  Blocks are binned by size class
-// (powers of two split into 4 sub-classes, minimum 512 B).  A block freed on stream S is
-// reused immediately by a later allocation on S (stream order makes that safe); before a
-// block is reused on another stream, S is synchronised.  When the
-// driver runs out of memory the cache is emptied (after a device synchronise) and the
-// allocation retried.
+// (powers of two split into 4 sub-classes, minimum 512 B).
+//
+// Ordering.  A block freed on stream S is reused at once by a later allocation on S (stream
+// order makes that safe).  A release records one event on S (shared by every block released
+// in the same batch), and an event on each other stream that nacho_record_stream named for
+// the block; an allocation that takes the block makes its own stream wait for those events
+// (hipStreamWaitEvent, outside the cache lock) unless they all sit on its own stream.  The
+// host never blocks on a stream for reuse.  When the driver runs out of memory the cache is
+// emptied (after a device synchronise) and the allocation retried.
+
+// A pooled event shared by the blocks of one release batch.
+struct SharedEvent {
+    hipEvent_t event;
+    hipStream_t stream;  // where it was recorded
+    int refs;
+};
+
 struct Block {
     void *ptr;
     size_t size;  // rounded size class
     int device;
-    hipStream_t stream;  // stream of the last use (allocation or free)
+    hipStream_t stream;                  // stream of the last allocation or release
+    std::vector<hipStream_t> used_on;    // other streams named by nacho_record_stream
+    std::vector<SharedEvent *> pending;  // events to wait for before reuse (free blocks)
 };
 
 std::mutex g_cache_mutex;
 std::unordered_map<void *, Block> g_live;              // allocated blocks by pointer
 std::map<std::pair<int, size_t>, std::vector<Block>> g_free;  // (device, size) -> free
+std::vector<hipEvent_t> g_event_pool;  // idle events (created with timing disabled)
+
+// An idle event, or a new one (nullptr if creation fails).  Caller holds g_cache_mutex.
+hipEvent_t take_event_locked() {
+    if (!g_event_pool.empty()) {
+        hipEvent_t e = g_event_pool.back();
+        g_event_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    return e;
+}
+
+// Event recorded on `stream` now, shared with refcount `refs` (nullptr if recording fails:
+// the caller then falls back to host synchronisation).  Caller holds g_cache_mutex.
+SharedEvent *record_shared_locked(hipStream_t stream, int refs) {
+    hipEvent_t e = take_event_locked();
+    if (!e) return nullptr;
+    if (hipEventRecord(e, stream) != hipSuccess) {
+        (void)hipGetLastError();
+        g_event_pool.push_back(e);
+        return nullptr;
+    }
+    return new SharedEvent{e, stream, refs};
+}
+
+void drop_shared_locked(SharedEvent *s) {
+    if (--s->refs == 0) {
+        g_event_pool.push_back(s->event);
+        delete s;
+    }
+}
 
 size_t size_class(size_t bytes) {
     if (bytes <= 512) return 512;
@@ -47,33 +97,68 @@ size_t size_class(size_t bytes) {
 void release_cached_blocks_locked() {
     (void)hipDeviceSynchronize();
     for (auto &bin : g_free) {
-        for (Block &b : bin.second) (void)hipFree(b.ptr);
+        for (Block &b : bin.second) {
+            for (SharedEvent *e : b.pending) drop_shared_locked(e);
+            (void)hipFree(b.ptr);
+        }
     }
     g_free.clear();
+    for (hipEvent_t e : g_event_pool) (void)hipEventDestroy(e);
+    g_event_pool.clear();
+}
+
+// Make `stream` wait for the events a reused block carries (outside the cache lock), then
+// return the events.  An event recorded on `stream` itself needs no wait.  If the runtime
+// refuses a device-side wait, the host waits for the event instead.
+void wait_pending(std::vector<SharedEvent *> &pending, hipStream_t stream) {
+    for (SharedEvent *e : pending) {
+        if (e->stream == stream) continue;
+        if (hipStreamWaitEvent(stream, e->event, 0) != hipSuccess) {
+            (void)hipGetLastError();
+            if (hipEventSynchronize(e->event) != hipSuccess) {
+                (void)hipGetLastError();
+                (void)hipDeviceSynchronize();
+            }
+        }
+    }
+    if (pending.empty()) return;
+    std::lock_guard<std::mutex> lock(g_cache_mutex);
+    for (SharedEvent *e : pending) drop_shared_locked(e);
+    pending.clear();
 }
 
 void *default_allocate(size_t bytes, hipStream_t stream) {
     int device = 0;
     if (hipGetDevice(&device) != hipSuccess) return nullptr;
     const size_t size = size_class(bytes);
-    std::lock_guard<std::mutex> lock(g_cache_mutex);
-    auto it = g_free.find({device, size});
-    if (it != g_free.end() && !it->second.empty()) {
-        std::vector<Block> &bin = it->second;
-        size_t pick = bin.size() - 1;
-        for (size_t i = bin.size(); i-- > 0;) {
-            if (bin[i].stream == stream) {
-                pick = i;
-                break;
+    std::vector<SharedEvent *> pending;
+    void *reused = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_cache_mutex);
+        auto it = g_free.find({device, size});
+        if (it != g_free.end() && !it->second.empty()) {
+            std::vector<Block> &bin = it->second;
+            size_t pick = bin.size() - 1;
+            for (size_t i = bin.size(); i-- > 0;) {
+                if (bin[i].stream == stream) {
+                    pick = i;
+                    break;
+                }
             }
+            Block b = std::move(bin[pick]);
+            bin.erase(bin.begin() + static_cast<std::ptrdiff_t>(pick));
+            pending.swap(b.pending);
+            b.stream = stream;
+            b.used_on.clear();
+            reused = b.ptr;
+            g_live[b.ptr] = std::move(b);
         }
-        Block b = bin[pick];
-        bin.erase(bin.begin() + static_cast<std::ptrdiff_t>(pick));
-        if (b.stream != stream) (void)hipStreamSynchronize(b.stream);
-        b.stream = stream;
-        g_live[b.ptr] = b;
-        return b.ptr;
     }
+    if (reused) {
+        wait_pending(pending, stream);
+        return reused;
+    }
+    std::lock_guard<std::mutex> lock(g_cache_mutex);
     void *ptr = nullptr;
     hipError_t err = hipMalloc(&ptr, size);
     if (err != hipSuccess) {
@@ -85,19 +170,57 @@ void *default_allocate(size_t bytes, hipStream_t stream) {
             return nullptr;
         }
     }
-    g_live[ptr] = Block{ptr, size, device, stream};
+    g_live[ptr] = Block{ptr, size, device, stream, {}, {}};
     return ptr;
 }
 
-void default_release(void *ptr, hipStream_t stream) {
-    if (!ptr) return;
+// Return blocks to the cache, stream-ordered on `stream`: one event recorded on `stream` is
+// shared by the whole batch, plus one per other stream named by nacho_record_stream.  If an
+// event cannot be recorded, the host synchronises that stream instead (rare fallback).
+// Pointers the cache does not own are ignored.
+void release_batch(void *const *ptrs, size_t n, hipStream_t stream) {
+    std::lock_guard<std::mutex> lock(g_cache_mutex);
+    int owned = 0;
+    for (size_t i = 0; i < n; ++i) owned += (ptrs[i] && g_live.count(ptrs[i])) ? 1 : 0;
+    if (owned == 0) return;
+    SharedEvent *freed = record_shared_locked(stream, owned);
+    if (!freed) (void)hipStreamSynchronize(stream);
+    for (size_t i = 0; i < n; ++i) {
+        if (!ptrs[i]) continue;
+        auto it = g_live.find(ptrs[i]);
+        if (it == g_live.end()) continue;
+        Block b = std::move(it->second);
+        g_live.erase(it);
+        b.stream = stream;
+        if (freed) b.pending.push_back(freed);
+        for (hipStream_t u : b.used_on) {
+            if (u == stream) continue;
+            SharedEvent *e = record_shared_locked(u, 1);
+            if (e) {
+                b.pending.push_back(e);
+            } else {
+                (void)hipStreamSynchronize(u);
+            }
+        }
+        b.used_on.clear();
+        g_free[{b.device, b.size}].push_back(std::move(b));
+    }
+}
+
+void default_release(void *ptr, hipStream_t stream) { release_batch(&ptr, 1, stream); }
+
+// Note that `stream` also uses a live block (the block's own stream is implied).
+int record_stream(void *ptr, hipStream_t stream) {
     std::lock_guard<std::mutex> lock(g_cache_mutex);
     auto it = g_live.find(ptr);
-    if (it == g_live.end()) return;  // not ours: ignore rather than corrupt the cache
-    Block b = it->second;
-    g_live.erase(it);
-    b.stream = stream;
-    g_free[{b.device, b.size}].push_back(b);
+    if (it == g_live.end()) return NACHO_ERR_INVALID_ARGUMENT;
+    Block &b = it->second;
+    if (stream == b.stream) return NACHO_OK;
+    for (hipStream_t u : b.used_on) {
+        if (u == stream) return NACHO_OK;
+    }
+    b.used_on.push_back(stream);
+    return NACHO_OK;
 }
 
 // Kernel timing state (per host thread).
@@ -126,9 +249,11 @@ Call::Call(void *stream, const nacho_allocator *alloc)
 
 Call::~Call() {
     if (timed_) t_last_ms = timed_ms_;
-    for (void *p : scratch_) release(p);
-    if (!committed_) {
-        for (void *p : results_) release(p);
+    if (!committed_) scratch_.insert(scratch_.end(), results_.begin(), results_.end());
+    if (alloc_) {
+        for (void *p : scratch_) release(p);
+    } else if (!scratch_.empty()) {
+        release_batch(scratch_.data(), scratch_.size(), stream_);  // one event for the batch
     }
 }
 
@@ -274,6 +399,11 @@ int nacho_free(void *ptr, void *stream) {
     return NACHO_OK;
 }
 
+int nacho_record_stream(void *ptr, void *stream) {
+    if (!ptr) return NACHO_ERR_INVALID_ARGUMENT;
+    return nacho::record_stream(ptr, static_cast<hipStream_t>(stream));
+}
+
 int nacho_release_cached_memory(void) {
     std::lock_guard<std::mutex> lock(nacho::g_cache_mutex);
     nacho::release_cached_blocks_locked();
@@ -288,7 +418,7 @@ const char *nacho_error_string(int code) {
         case NACHO_ERR_OUT_OF_MEMORY: return "nacho: device allocation failed";
         case NACHO_ERR_MALFORMED_INPUT: return "nacho: malformed sparse operand";
         case NACHO_ERR_NO_DEVICE: return "nacho: no HIP device";
-        case NACHO_ERR_INTERNAL: return "nacho: internal error (kernel wait bound expired)";
+        case NACHO_ERR_INTERNAL: return "nacho: internal error (a kernel did not publish its result length)";
         case NACHO_ERR_IO: return "nacho: file could not be opened or read";
         case NACHO_ERR_UNSUPPORTED: return "nacho: unsupported file format variant";
         default: break;

@@ -1,7 +1,8 @@
 // Thin HIP runtime shared by every entry point of the gfx950 backend: error plumbing,
-// stream-ordered allocation through the caller's allocator (or the device's default memory
-// pool), scratch that is released on every exit path, the pinned host word used to read
-// result lengths back, and the optional kernel timing hook.
+// stream-ordered allocation through the caller's allocator (or the library's caching
+// allocator over hipMalloc, with event-ordered reuse across streams), scratch that is
+// released on every exit path, the pinned host word used to read result lengths back, and
+// the optional kernel timing hook.
 //
 // It stands where the reference's generated entry points use cudaMallocAsync /
 // cudaFreeAsync / cudaMemsetAsync / cudaMemcpyAsync on stream 0

@@ -408,6 +408,13 @@ int multiply(const nacho_csr *a, const nacho_csr *b, const nacho_csr *c, nacho_c
     int64_t sizes[2] = {0, 0};
     NACHO_TRY(call.read_back(&sizes[0], toff_b + cols, sizeof(int64_t)));
     NACHO_TRY(call.read_back(&sizes[1], toff_a + rows, sizeof(int64_t)));
+    // A table's mask is kept in 31 bits (bit 31 flags the walked side), so no table may
+    // exceed 2^31 slots.  Table sizes are powers of two, so a larger one (2^32 slots or
+    // more, for a row or column of more than 2^30 entries) would make its side's total at
+    // least 2^32.
+    if (sizes[0] >= (int64_t{1} << 32) || sizes[1] >= (int64_t{1} << 32)) {
+        return NACHO_ERR_INDEX_OVERFLOW;
+    }
     NACHO_TRY(call.timer_start(name));
 
     // tables and B's columns

@@ -89,32 +89,58 @@ def parse3D_i32_f32(filename: str, N: int, M: int, K: int) -> COO3D_parsed:  # n
 
 
 def parse_matrix(path, return_coo: bool = False, device="cuda") -> torch.Tensor:
-    """A .mtx file as a torch sparse tensor, CSR unless return_coo
-    (benchmarks/common/parser.py:87-99; here the argument is the file's path)."""
-    coo = parse2D(str(path))
-    row = coo.row.to(dtype=torch.long, device=device)
-    col = coo.col.to(dtype=torch.long, device=device)
-    values = coo.data.to(dtype=torch.float32, device=device)
-    tensor = torch.sparse_coo_tensor(torch.stack([row, col], dim=0), values, (coo.N, coo.M))
-    return tensor if return_coo else tensor.to_sparse_csr()
+    """A .mtx file as a torch sparse tensor (CSR, or coalesced COO when return_coo): the
+    operand builder of the reference's matrix benchmarks (benchmarks/common/parser.py:87-99),
+    which takes a matrix name where this takes the file's path.
+
+    Entries are ordered by one int64 key row * columns + column on the host; entries that
+    share a key (possible in general files) are summed in file order."""
+    m = parse2D(str(path))
+    key = m.row.to(torch.int64) * int(m.M) + m.col.to(torch.int64)
+    key, order = torch.sort(key, stable=True)
+    uniq, slot = torch.unique_consecutive(key, return_inverse=True)
+    vals = torch.zeros(uniq.numel(), dtype=torch.float32).index_add_(0, slot, m.data[order])
+    rows, cols = uniq // int(m.M), uniq % int(m.M)
+    if return_coo:
+        out = torch.sparse_coo_tensor(torch.stack((rows, cols)), vals, (m.N, m.M),
+                                      is_coalesced=True)
+        return out.to(device)
+    crow = torch.zeros(int(m.N) + 1, dtype=torch.int64)
+    torch.cumsum(torch.bincount(rows, minlength=int(m.N)), 0, out=crow[1:])
+    return torch.sparse_csr_tensor(crow, cols, vals, (m.N, m.M)).to(device)
 
 
 def load_frostt(path, dims):
-    """A .tns file as (coordinates shaped (nnz, 3), values) (benchmarks/common/frostt.py:11-24;
-    here the argument is the file's path)."""
-    parsed = parse3D_i32_f32(str(path), *dims)
-    coordinates = np.stack([parsed.row.numpy(), parsed.col.numpy(), parsed.dep.numpy()], axis=1)
-    return coordinates, parsed.data.numpy()
+    """A .tns file as (int32 coordinates of shape (nnz, 3), float32 values): the loader of
+    the reference's tensor benchmarks (benchmarks/common/frostt.py:11-24), which takes a
+    tensor name where this takes the file's path."""
+    t = parse3D_i32_f32(str(path), *dims)
+    return np.column_stack((t.row.numpy(), t.col.numpy(), t.dep.numpy())), t.data.numpy()
 
 
 def shift_coordinates(coordinates, values, shape):
-    """A second operand from the first: every coordinate advanced by one and clamped to the
-    extent, duplicates summed, lexicographically sorted (benchmarks/common/frostt.py:27-44)."""
-    coordinates = np.asarray(coordinates)
-    shifted = np.minimum(coordinates + 1, np.array(shape, dtype=coordinates.dtype) - 1)
-    order = np.lexsort((shifted[:, 2], shifted[:, 1], shifted[:, 0]))
-    shifted, ordered = shifted[order], np.asarray(values)[order]
-    starts = np.ones(len(shifted), dtype=bool)
-    starts[1:] = np.any(shifted[1:] != shifted[:-1], axis=1)
-    run_starts = np.flatnonzero(starts)
-    return shifted[run_starts], np.add.reduceat(ordered, run_starts) if len(run_starts) else ordered
+    """The second operand of the reference's tensor benchmarks
+    (benchmarks/common/frostt.py:27-44): every coordinate moved one step along each mode,
+    stopping at the last index, then entries that land on the same coordinate summed (in
+    their sorted order), lexicographically sorted.
+
+    Coordinates become one int64 key (mode 0 most significant) when the shape allows it,
+    else a three-column lexicographic sort gives the same order."""
+    c = np.asarray(coordinates)
+    ext = np.asarray(shape, dtype=np.int64)
+    moved = np.minimum(c.astype(np.int64) + 1, ext - 1)
+    if int(ext[0]) * int(ext[1]) * int(ext[2]) < (1 << 62):
+        key = (moved[:, 0] * ext[1] + moved[:, 1]) * ext[2] + moved[:, 2]
+        order = np.argsort(key, kind="stable")
+        key = key[order]
+        head = np.ones(len(key), dtype=bool)
+        head[1:] = key[1:] != key[:-1]
+    else:
+        order = np.lexsort((moved[:, 2], moved[:, 1], moved[:, 0]))
+        m = moved[order]
+        head = np.ones(len(m), dtype=bool)
+        head[1:] = (m[1:] != m[:-1]).any(axis=1)
+    first = np.flatnonzero(head)
+    ordered = np.asarray(values)[order]
+    summed = np.add.reduceat(ordered, first) if len(first) else ordered
+    return moved[order][first].astype(c.dtype), summed

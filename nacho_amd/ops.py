@@ -142,6 +142,42 @@ def _adopt_csf3(z: _lib.Csf3Desc, device, stream) -> CSF3_gpu:
                              [z.dim_i_size, z.dim_j_size, z.dim_k_size], device)
 
 
+# ---- input validation ----------------------------------------------------------------
+
+_VALIDATE = False
+
+
+def set_validation(enable: bool) -> None:
+    """Validation mode: when enabled, every `gpu_` entry point first checks its CSR operands
+    on the device (nacho_validate_csr) and raises ValueError for a malformed one.  Off by
+    default: like the reference's generated code, the kernels trust operand contents."""
+    global _VALIDATE
+    _VALIDATE = bool(enable)
+
+
+def validate_csr(t: CSR_gpu) -> None:
+    """Check a CSR operand against the input contract (pos[0] == 0, pos non-decreasing,
+    pos[rows] == nnz, 0 <= crd < columns, crd strictly increasing per row); raises
+    ValueError if it is malformed."""
+    if not isinstance(t, CSR_gpu):
+        raise TypeError(f"validate_csr: expected CSR_gpu, got {type(t).__name__}")
+    desc = _csr_desc(t)
+    with torch.cuda.device(t.device):
+        rc = _lib.load().nacho_validate_csr(ctypes.byref(desc),
+                                            ctypes.c_void_p(_device.current_stream(t.device)))
+    if rc == -4:  # NACHO_ERR_MALFORMED_INPUT
+        raise ValueError("CSR operand violates the input contract (offsets, column range or "
+                         "per-row order)")
+    _lib.check(rc, "nacho_validate_csr")
+
+
+def _maybe_validate(*operands):
+    if _VALIDATE:
+        for t in operands:
+            if isinstance(t, CSR_gpu):
+                validate_csr(t)
+
+
 # ---- generic call --------------------------------------------------------------------
 
 def _call(entry, a, b, cls, desc_fn, result_desc, adopt_fn, num_blocks, threads_per_block):
@@ -149,6 +185,7 @@ def _call(entry, a, b, cls, desc_fn, result_desc, adopt_fn, num_blocks, threads_
         if not isinstance(t, cls):
             raise TypeError(f"{entry}: operand {name} must be {cls.__name__}, "
                             f"got {type(t).__name__}")
+    _maybe_validate(a, b)
     device = _same_device(a, b)
     lib = _lib.load()
     fn = getattr(lib, entry, None)
@@ -175,6 +212,7 @@ def _call3(entry, a, b, c, num_blocks, threads_per_block) -> CSR_gpu:
     for name, t in (("a", a), ("b", b), ("c", c)):
         if not isinstance(t, CSR_gpu):
             raise TypeError(f"{entry}: operand {name} must be CSR_gpu, got {type(t).__name__}")
+    _maybe_validate(a, b, c)
     device = _same_device(a, b, c)
     lib = _lib.load()
     fn = getattr(lib, entry, None)

@@ -75,6 +75,20 @@ class _GpuTensor:
     def device(self) -> torch.device:
         return self._device
 
+    def record_stream(self, stream) -> None:
+        """Mark every buffer as used by `stream` (a torch.cuda.Stream), like torch's
+        Tensor.record_stream: a buffer the library allocated is then reused, after it is
+        released, only by work ordered after `stream`'s work queued until the release.
+        Buffers torch allocated are passed to torch's own record_stream."""
+        for name, _ in self._fields:
+            buf = getattr(self, "_" + name)
+            if buf.numel() == 0:
+                continue
+            try:
+                _device.record_stream(buf, stream)
+            except ValueError:
+                buf.record_stream(stream)
+
     def __setattr__(self, name, value):
         raise AttributeError(f"{type(self).__name__} fields are read-only")
 

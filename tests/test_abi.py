@@ -222,3 +222,72 @@ def test_cpp_shim_matches_the_generated_signatures(tmp_path):
     run = subprocess.run([str(exe)], capture_output=True, text=True)
     assert run.returncode == 0, run.stdout + run.stderr
     assert "threw: csr_add: " in run.stdout
+
+
+class _CountingAllocator:
+    """A caller allocator that hands out fake device addresses and returns NULL from the
+    `fail_at`-th request on; it records every pointer handed out and every release."""
+
+    def __init__(self, fail_at):
+        from nacho_amd import _lib
+
+        self.fail_at = fail_at
+        self.handed, self.released, self.requests = [], [], 0
+        self._next = 0x10000000
+
+        def allocate(ctx, nbytes, stream):
+            self.requests += 1
+            if self.requests >= self.fail_at:
+                return None
+            p = self._next
+            self._next += (nbytes + 0xFFF) & ~0xFFF or 0x1000
+            self.handed.append(p)
+            return p
+
+        def release(ctx, ptr, stream):
+            self.released.append(ptr)
+
+        self.struct = _lib.Allocator(None, _lib.Allocator._fields_[1][1](allocate),
+                                     _lib.Allocator._fields_[2][1](release))
+
+
+@pytest.mark.parametrize("entry", ["nacho_gpu_csr_add_f32", "nacho_gpu_csr_mul_f32"])
+@pytest.mark.parametrize("fail_at", [1, 2, 3])
+def test_allocator_failure_releases_everything(lib, entry, fail_at):
+    """The caller's allocator returning NULL gives NACHO_ERR_OUT_OF_MEMORY, a zeroed result
+    and a release of every buffer the call had obtained (the result arrays are the first
+    three requests, before any HIP call)."""
+    from nacho_amd import _lib
+
+    alloc = _CountingAllocator(fail_at)
+    a = _lib.CsrDesc(8, 8, ctypes.c_void_p(0x1000), 5, ctypes.c_void_p(0x2000),
+                     ctypes.c_void_p(0x3000), 5)
+    z = _lib.CsrDesc()
+    rc = getattr(lib, entry)(ctypes.byref(a), ctypes.byref(a), ctypes.byref(z), 256, 256, None,
+                             ctypes.byref(alloc.struct))
+    assert rc == -3, _lib.error_string(rc)
+    assert alloc.requests == fail_at
+    assert sorted(alloc.handed) == sorted(alloc.released)
+    assert z.dim_j_offsets is None and z.dim_j_indices is None and z.values is None
+    assert z.nnz == 0 and z.dim_j_length == 0
+
+
+def test_validate_csr_rejects_host_visible_faults(lib):
+    """nacho_validate_csr refuses null pointers, negative sizes and nnz != dim_j_length
+    before touching the device."""
+    from nacho_amd import _lib
+
+    r = ctypes.byref
+    fn = lib.nacho_validate_csr
+    assert fn(None, None) == -1
+    assert fn(r(_lib.CsrDesc(4, 4, None, 0, None, None, 0)), None) == -1
+    assert fn(r(_lib.CsrDesc(-1, 4, ctypes.c_void_p(0x1000), 0, None, None, 0)), None) == -1
+    assert fn(r(_lib.CsrDesc(4, 4, ctypes.c_void_p(0x1000), 3, None, None, 3)), None) == -1
+    assert fn(r(_lib.CsrDesc(4, 4, ctypes.c_void_p(0x1000), 3, ctypes.c_void_p(0x2000), None,
+                             2)), None) == -1
+
+
+def test_record_stream_rejects_unknown_buffers(lib):
+    """nacho_record_stream only accepts live buffers of the library's allocator."""
+    assert lib.nacho_record_stream(None, None) == -1
+    assert lib.nacho_record_stream(ctypes.c_void_p(0x1234000), None) == -1

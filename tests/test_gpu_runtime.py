@@ -1,0 +1,115 @@
+"""GPU tests of the runtime around the kernels: input validation (nacho_validate_csr and the
+validation mode) and stream-ordered buffer reuse across streams (nacho_record_stream)."""
+
+import numpy as np
+import pytest
+import torch
+
+from tests.helpers import csr_from_rows, random_csr
+from tests.test_gpu_csr import to_gpu
+
+pytestmark = pytest.mark.gpu
+
+
+def _malformed_cases():
+    rows, cols = 4, 6
+    good = csr_from_rows(rows, cols, [[0, 2], [], [1, 3, 5], [4]])
+    cases = {"good": good}
+    pos, crd, val = (x.copy() for x in good)
+    crd[3], crd[4] = crd[4], crd[3]  # row 2 unsorted
+    cases["unsorted"] = (pos, crd, val)
+    pos, crd, val = (x.copy() for x in good)
+    crd[3] = crd[2]  # row 2: duplicate column
+    cases["duplicate"] = (pos, crd, val)
+    pos, crd, val = (x.copy() for x in good)
+    crd[0] = cols  # column out of range
+    cases["column_range"] = (pos, crd, val)
+    pos, crd, val = (x.copy() for x in good)
+    pos[2], pos[3] = 4, 2  # offsets decrease
+    cases["decreasing"] = (pos, crd, val)
+    pos, crd, val = (x.copy() for x in good)
+    pos[0] = 1
+    cases["first_offset"] = (pos, crd, val)
+    pos, crd, val = (x.copy() for x in good)
+    pos[4] = 5  # last offset short of nnz
+    cases["last_offset"] = (pos, crd, val)
+    pos, crd, val = (x.copy() for x in good)
+    pos[1] = 99  # an offset past nnz (reported, never used as an index)
+    cases["offset_past_end"] = (pos, crd, val)
+    return rows, cols, cases
+
+
+@pytest.mark.parametrize("case", ["good", "unsorted", "duplicate", "column_range", "decreasing",
+                                  "first_offset", "last_offset", "offset_past_end"])
+def test_validate_csr(gpu, case):
+    import nacho_amd
+
+    rows, cols, cases = _malformed_cases()
+    print(f"[gpu] validate_csr case={case}", flush=True)
+    t = to_gpu(cases[case], rows, cols, gpu)
+    if case == "good":
+        nacho_amd.validate_csr(t)
+    else:
+        with pytest.raises(ValueError, match="input contract"):
+            nacho_amd.validate_csr(t)
+
+
+def test_validate_csr_large_valid_operand(gpu):
+    import nacho_amd
+
+    rng = np.random.default_rng(5)
+    a = random_csr(rng, 20000, 30000, 0.002)
+    nacho_amd.validate_csr(to_gpu(a, 20000, 30000, gpu))
+
+
+def test_validation_mode_guards_the_entry_points(gpu):
+    import nacho_amd
+
+    rows, cols, cases = _malformed_cases()
+    good, bad = (to_gpu(cases[k], rows, cols, gpu) for k in ("good", "unsorted"))
+    nacho_amd.set_validation(True)
+    try:
+        with pytest.raises(ValueError):
+            nacho_amd.gpu_csr_add_f32(good, bad)
+        with pytest.raises(ValueError):
+            nacho_amd.gpu_csr_mul_f32(bad, good)
+        z = nacho_amd.gpu_csr_add_f32(good, good)
+        torch.cuda.synchronize()
+        assert z.dim_j_indices.numel() == cases["good"][1].size
+    finally:
+        nacho_amd.set_validation(False)
+
+
+def test_record_stream_orders_reuse_after_a_side_stream(gpu):
+    """A result read on a side stream (behind a long spin) and then dropped: with
+    record_stream, the next call on the main stream, which reuses the freed blocks and
+    writes different values into them, must not overwrite them before the side stream's
+    read."""
+    import nacho_amd
+
+    rng = np.random.default_rng(11)
+    rows, cols = 4000, 5000
+    a = random_csr(rng, rows, cols, 0.01)
+    b = random_csr(rng, rows, cols, 0.01)
+    na = (a[0], a[1], -a[2])
+    nb = (b[0], b[1], -b[2])
+    ga, gb, gna, gnb = (to_gpu(t, rows, cols, gpu) for t in (a, b, na, nb))
+    main = torch.cuda.current_stream(gpu)
+    side = torch.cuda.Stream(gpu)
+    for trial in range(3):
+        z = nacho_amd.gpu_csr_add_f32(ga, gb)
+        expected = z.values.clone()
+        ptr = z.values.data_ptr()
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            torch.cuda._sleep(20_000_000)
+            seen = z.values.clone()
+        z.record_stream(side)
+        del z
+        z2 = nacho_amd.gpu_csr_add_f32(gna, gnb)  # same sizes: reuses the freed blocks
+        reused = z2.values.data_ptr() == ptr
+        torch.cuda.synchronize()
+        print(f"[gpu] record_stream trial={trial} reused={reused}", flush=True)
+        assert torch.equal(seen, expected)
+        assert torch.equal(z2.values, -expected)
+        del z2

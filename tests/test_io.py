@@ -136,3 +136,34 @@ def test_parse_matrix_and_frostt_helpers(tmp_path):
         brute[key] = brute.get(key, 0.0) + x
     assert [tuple(x) for x in sc.tolist()] == sorted(brute)
     np.testing.assert_allclose(sv, [brute[k] for k in sorted(brute)], rtol=1e-6)
+
+
+def test_header_claiming_huge_nnz_is_an_error_not_a_crash(tmp_path):
+    """A header that claims 1e15 entries must not size the buffers from the header (which
+    would throw through the C ABI and end the process): the reader sizes by the file and
+    reports the missing entries as malformed input."""
+    text = "%%MatrixMarket matrix coordinate real general\n3 3 1000000000000000\n1 1 1.0\n"
+    f = write(tmp_path / "huge.mtx", text)
+    with pytest.raises(RuntimeError, match="malformed"):
+        nacho_amd.parse2D(f)
+    # the same through the C ABI, with the error code
+    from nacho_amd import _lib
+
+    out = _lib.Coo2dHost()
+    assert _lib.load().nacho_parse2d(f.encode(), ctypes.byref(out)) == -4
+    assert out.nnz == 0 and not out.row
+
+
+def test_parse_matrix_builds_csr_and_coo(tmp_path):
+    """parse_matrix (the benchmarks' operand builder) sorts entries by (row, column) and
+    sums duplicates in file order."""
+    text = ("%%MatrixMarket matrix coordinate real general\n3 4 5\n"
+            "3 2 1.0\n1 4 2.0\n1 1 3.0\n3 2 0.5\n2 3 -1.0\n")
+    f = write(tmp_path / "p.mtx", text)
+    csr = io.parse_matrix(f, device="cpu")
+    assert csr.crow_indices().tolist() == [0, 2, 3, 4]
+    assert csr.col_indices().tolist() == [0, 3, 2, 1]
+    assert csr.values().tolist() == [3.0, 2.0, -1.0, 1.5]
+    coo = io.parse_matrix(f, return_coo=True, device="cpu")
+    assert coo.is_coalesced()
+    np.testing.assert_array_equal(coo.to_dense().numpy(), csr.to_dense().numpy())
