@@ -1,7 +1,12 @@
 """Benchmark of the nacho GPU path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only]
                     [--workload c2|c3|c4|c5|c5coo|c2coo|c3coo|c2dcsr|c3dcsr|c2add3|c4sssmm]
+
+The default run prints the C2 csr_add line (the headline `value`) with a `workloads` list
+holding the other north-star configurations measured in the same run: C3 csr_mul, C5
+csf_add and coo3d_add, and C4 ESC SpGEMM (each with its call time, roofline and CPU
+baseline).  `--only` (or any --workload other than c2) prints one workload's line alone.
 
 A step is one call of the hot path over one batch of synthetic input, with the operands
 already resident in HBM: `nacho_amd.gpu_csr_add_f32(A, B)` for the default workload (C2:
@@ -101,6 +106,48 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def cpu_model():
+    """The host CPU's model name (first `model name` of /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
+
+
+def host_cores():
+    return max(1, min(len(os.sched_getaffinity(0)), 64))
+
+
+def compact(workload, line):
+    """The fields of one workload's line that go into the default run's `workloads` list."""
+    rec = {
+        "workload": workload,
+        "config": line["config"]["workload"],
+        "metric": "GFLOP/s" if line["unit"] == "GFLOP/s" else "effective HBM GB/s",
+        "value": line["value"],
+        "unit": line["unit"],
+        "ms_per_call": line["ms_per_step"],
+        "steps": line["steps"],
+        "roofline": line["roofline"],
+        "cpu_baseline": line["cpu_baseline"],
+    }
+    if line["unit"] == "GB/s":
+        rec["percent_of_peak_hbm"] = round(100.0 * line["value"] / PEAK_HBM_GBS, 2)
+    cpu = line["cpu_baseline"]
+    if cpu:
+        rec["gpu_over_cpu"] = round(line["value"] / cpu["value"], 1)
+    for key in ("products", "flops_per_step", "nnz_c", "algorithmic_bytes_per_step"):
+        if key in line["config"]:
+            rec[key] = line["config"][key]
+    return rec
+
+
 def make_operands(workload):
     from nacho_amd import synth
 
@@ -126,16 +173,13 @@ def cpu_baseline(workload, op, operands, rows, bytes_per_call, budget_s):
     """Time the oracle's C restatement of the reference CPU kernel on this host."""
     from oracle import oracle
 
-    cores = len(os.sched_getaffinity(0))
-    cores = max(1, min(cores, 64))
-    if op == "add3":
-        cores = 1  # the three-way restatement is serial
+    cores = host_cores()
     times = []
     start = time.perf_counter()
     while time.perf_counter() - start < budget_s and len(times) < 50:
         t = {}
         if op == "add3":
-            oracle.port_csr_add3(rows, *operands, timing=t)
+            oracle.port_csr_add3(rows, *operands, timing=t, nthreads=cores)
         else:
             oracle.port_csr_binary(op, rows, *operands[0], *operands[1], nthreads=cores,
                                    timing=t)
@@ -147,10 +191,11 @@ def cpu_baseline(workload, op, operands, rows, bytes_per_call, budget_s):
         "value": round(bytes_per_call / sec / 1e9, 3),
         "unit": "GB/s",
         "cores": cores,
+        "cpu_model": cpu_model(),
         "kind": "port",
         "sample": f"{len(times)} full {workload} calls of the C restatement "
-                  f"(oracle/nacho_oracle.c), mean of the middle {len(trimmed)}: "
-                  f"{sec * 1e3:.1f} ms/call",
+                  f"(oracle/nacho_oracle.c, one partition per thread), mean of the middle "
+                  f"{len(trimmed)}: {sec * 1e3:.1f} ms/call",
     }
 
 
@@ -170,7 +215,7 @@ def spgemm_cpu_baseline(pos, crd, val, budget_s):
     from oracle import oracle
 
     n = len(pos) - 1
-    cores = max(1, min(len(os.sched_getaffinity(0)), 64))
+    cores = host_cores()
     lens = np.diff(pos.astype(np.int64))
     rng = np.random.default_rng(99)
 
@@ -197,6 +242,7 @@ def spgemm_cpu_baseline(pos, crd, val, budget_s):
         "value": round(2 * prods / sec / 1e9, 3),
         "unit": "GFLOP/s",
         "cores": cores,
+        "cpu_model": cpu_model(),
         "kind": "port",
         "sample": f"2 runs of A[rows] @ A on uniform random samples of {samples[0][2]} rows "
                   f"({frac:.4f} of rows; {prods} products in {sec:.1f} s) with the "
@@ -309,7 +355,7 @@ def sssmm_cpu_baseline(pos, crd, budget_s):
     from oracle import oracle
 
     n = len(pos) - 1
-    cores = max(1, min(len(os.sched_getaffinity(0)), 64))
+    cores = host_cores()
     ones = np.ones(len(crd), np.float32)
     rng = np.random.default_rng(98)
     a = (pos, crd, ones)
@@ -329,6 +375,7 @@ def sssmm_cpu_baseline(pos, crd, budget_s):
         "value": round(3 * terms / sec / 1e9, 3),
         "unit": "GFLOP/s",
         "cores": cores,
+        "cpu_model": cpu_model(),
         "kind": "port",
         "sample": f"2 runs of the row-parallel C masked SpGEMM (oracle/nacho_oracle.c, dense "
                   f"mask marker, float64 sums) on uniform random samples of {samples[0][2]} "
@@ -555,33 +602,34 @@ def bench_tuple_workload(args, device, workload):
     if args.cpu_budget > 0:
         from oracle import oracle
 
-        cores = max(1, min(len(os.sched_getaffinity(0)), 64))
+        cores = host_cores()
         times = []
+        if workload == "c5":
+            levels = [csf3_levels(np.stack(o[0], axis=1)) for o in ops_np]
         begin = time.perf_counter()
         while time.perf_counter() - begin < args.cpu_budget and len(times) < 20:
             t = {}
             if workload in ("c2dcsr", "c3dcsr"):
                 oracle.port_dcsr_binary("add" if workload == "c2dcsr" else "mul",
                                         ops_np[0][0], ops_np[0][1], ops_np[1][0],
-                                        ops_np[1][1], timing=t)
+                                        ops_np[1][1], timing=t, nthreads=cores)
             elif workload == "c5":
-                oracle.port_csf3_union(csf3_levels(np.stack(ops_np[0][0], axis=1)), ops_np[0][1],
-                                       csf3_levels(np.stack(ops_np[1][0], axis=1)), ops_np[1][1],
-                                       timing=t)
+                oracle.port_csf3_union(levels[0], ops_np[0][1], levels[1], ops_np[1][1],
+                                       timing=t, nthreads=cores)
             else:
                 oracle.port_coo_binary("mul" if workload == "c3coo" else "add", ops_np[0][0],
                                        ops_np[0][1], ops_np[1][0], ops_np[1][1],
                                        nthreads=cores, timing=t)
             times.append(t["seconds"])
         sec = sorted(times)[len(times) // 2]
-        serial = workload in ("c5", "c2dcsr", "c3dcsr")
         cpu = {
             "value": round(alg_bytes / sec / 1e9, 3),
             "unit": "GB/s",
-            "cores": 1 if serial else cores,
+            "cores": cores,
+            "cpu_model": cpu_model(),
             "kind": "port",
             "sample": f"{len(times)} full {workload} calls of the C restatement "
-                      f"(oracle/nacho_oracle.c{', serial lattice' if serial else ''}), "
+                      f"(oracle/nacho_oracle.c, one partition per thread), "
                       f"median {sec * 1e3:.1f} ms/call",
         }
         log(f"cpu baseline {cpu['value']} GB/s on {cpu['cores']} threads")
@@ -622,60 +670,20 @@ def bench_tuple_workload(args, device, workload):
     }
 
 
-def main():
-    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c2")
-    ap.add_argument("--cpu-budget", type=float, default=12.0,
-                    help="seconds of CPU baseline timing (0 disables)")
-    ap.add_argument("--calibrate-copy", action="store_true",
-                    help="only run a 1 GiB device copy (rocprof counter calibration)")
-    args = ap.parse_args()
-
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU: this build has no multi-GPU path "
-              f"(--gpus {args.gpus} requested).", file=sys.stderr)
-        sys.exit(2)
-
+def bench_csr(args, device, workload):
+    """c2 (csr_add), c3 (csr_mul), c2add3 (csr_add_3): one step = one call with operands
+    resident in HBM, rotating over ROTATE copies."""
     import torch
-
-    if not torch.cuda.is_available():
-        print("bench.py needs a HIP device", file=sys.stderr)
-        sys.exit(1)
-    device = torch.device("cuda:0")
-
-    if args.calibrate_copy:
-        n = 1 << 28  # 1 GiB of float32
-        src = torch.ones(n, dtype=torch.float32, device=device)
-        dst = torch.empty_like(src)
-        for _ in range(5):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        print(json.dumps({"calibration": "copy", "bytes_read": 4 * n, "bytes_written": 4 * n,
-                          "launches": 5}))
-        return
-
-    if args.workload == "c4":
-        print(json.dumps(bench_spgemm(args, device)), flush=True)
-        return
-    if args.workload == "c4sssmm":
-        print(json.dumps(bench_sssmm(args, device)), flush=True)
-        return
-    if args.workload in ("c5", "c5coo", "c2coo", "c3coo", "c2dcsr", "c3dcsr"):
-        print(json.dumps(bench_tuple_workload(args, device, args.workload)), flush=True)
-        return
 
     import nacho_amd
     from nacho_amd import synth
 
-    spec = WORKLOADS[args.workload]
+    spec = WORKLOADS[workload]
     t0 = time.perf_counter()
-    operands_np = make_operands(args.workload)
+    operands_np = make_operands(workload)
     a_np, b_np = operands_np[0], operands_np[1]
     rows = len(a_np[0]) - 1
-    log(f"generated {args.workload}: rows={rows} "
+    log(f"generated {workload}: rows={rows} "
         f"nnz={[len(o[1]) for o in operands_np]} in {time.perf_counter() - t0:.1f}s")
 
     def upload(t):
@@ -724,7 +732,7 @@ def main():
 
     cpu = None
     if args.cpu_budget > 0:
-        cpu = cpu_baseline(args.workload, spec["op"], operands_np, rows, alg_bytes,
+        cpu = cpu_baseline(workload, spec["op"], operands_np, rows, alg_bytes,
                            args.cpu_budget)
         log(f"cpu baseline {cpu['value']} GB/s on {cpu['cores']} threads")
 
@@ -759,12 +767,85 @@ def main():
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": traffic_from_profiles(args.workload),
+            "traffic": traffic_from_profiles(workload),
             "kernel_avg_us": round(kernel_avg_ms * 1e3, 2),
         },
         "cpu_baseline": cpu,
     }
+    return line
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c2")
+    ap.add_argument("--only", action="store_true",
+                    help="measure --workload alone (no `workloads` list)")
+    ap.add_argument("--cpu-budget", type=float, default=12.0,
+                    help="seconds of CPU baseline timing (0 disables)")
+    ap.add_argument("--extra-cpu-budget", type=float, default=8.0,
+                    help="seconds of CPU baseline timing per listed workload")
+    ap.add_argument("--extra-steps", type=int, default=10,
+                    help="timed steps per listed workload (at most --steps)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a 1 GiB device copy (rocprof counter calibration)")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path "
+              f"(--gpus {args.gpus} requested).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(1)
+    device = torch.device("cuda:0")
+
+    if args.calibrate_copy:
+        n = 1 << 28  # 1 GiB of float32
+        src = torch.ones(n, dtype=torch.float32, device=device)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration": "copy", "bytes_read": 4 * n, "bytes_written": 4 * n,
+                          "launches": 5}))
+        return
+
+    line = run_workload(args, device, args.workload)
+    if args.workload == "c2" and not args.only:
+        # The other north-star configurations, measured in the same run: C3 csr_mul, C5 as
+        # CSF3 (csf_add) and as COO3 (coo3d_add), then C4 SpGEMM (its cached buffers are
+        # released at the end).
+        extra = argparse.Namespace(**vars(args))
+        extra.steps = max(1, min(args.steps, args.extra_steps))
+        extra.warmup = max(1, min(args.warmup, 3))
+        extra.cpu_budget = args.extra_cpu_budget if args.cpu_budget > 0 else 0.0
+        records = []
+        for w in ("c3", "c5", "c5coo", "c4"):
+            t0 = time.perf_counter()
+            records.append(compact(w, run_workload(extra, device, w)))
+            log(f"{w} done in {time.perf_counter() - t0:.1f}s")
+            import nacho_amd
+
+            nacho_amd.release_cached_memory()
+            torch.cuda.empty_cache()
+        line["workloads"] = records
     print(json.dumps(line), flush=True)
+
+
+def run_workload(args, device, workload):
+    if workload == "c4":
+        return bench_spgemm(args, device)
+    if workload == "c4sssmm":
+        return bench_sssmm(args, device)
+    if workload in ("c5", "c5coo", "c2coo", "c3coo", "c2dcsr", "c3dcsr"):
+        return bench_tuple_workload(args, device, workload)
+    return bench_csr(args, device, workload)
 
 
 if __name__ == "__main__":

@@ -1126,3 +1126,461 @@ int oracle_sssmm(int rows, int cols, const int32_t *pa, const int32_t *ca, const
     return ORC_OK;
 }
 
+
+/* ---------------------------------------------------------------------------------- */
+/* Thread-parallel restatements of the serial lattices above (CPU baselines)            */
+/*
+ * The reference's CPU target runs one partition per hardware thread: a partition pass, a
+ * count pass, a serial prefix of the counts, and a write pass (stitch_and_generate_cpu.cpp:
+ * 26-31, 138-154).  These follow that structure for CSF3 union, DCSR union / intersection
+ * and the three-way CSR union: the outermost level is cut into `nthreads` ranges of about
+ * equal nonzero count (ranges never split a coordinate present in both operands), each
+ * thread counts its range's outputs, a serial exclusive scan turns counts into offsets, and
+ * each thread writes its range at its offsets.  The results are identical to the serial
+ * functions' (tests/test_oracle_mt.py checks it).
+ */
+
+typedef struct {
+    int ia0, ia1, ib0, ib1; /* top-level ranges of A and B (or rows: ia only)          */
+    long n[3];              /* per-level output counts, then exclusive offsets          */
+} top_range;
+
+/* Cut the merged top-level id lists into `nt` ranges of about equal weight.  wa(i) / wb(i)
+ * give the weight of A's / B's i-th fibre (pos arrays of the level holding the nonzeros). */
+static void split_top(const int32_t *a_ci, int a_ni, const long *wa_pos, const int32_t *b_ci,
+                      int b_ni, const long *wb_pos, int nt, top_range *r) {
+    const long total = (a_ni ? wa_pos[a_ni] - wa_pos[0] : 0) +
+                       (b_ni ? wb_pos[b_ni] - wb_pos[0] : 0) + (long)a_ni + b_ni;
+    int ia = 0, ib = 0, t = 0;
+    long acc = 0;
+    r[0].ia0 = 0;
+    r[0].ib0 = 0;
+    while (ia < a_ni || ib < b_ni) {
+        int ha = ia < a_ni, hb = ib < b_ni;
+        if (ha && hb) {
+            const int i = a_ci[ia] < b_ci[ib] ? a_ci[ia] : b_ci[ib];
+            ha = a_ci[ia] == i;
+            hb = b_ci[ib] == i;
+        }
+        if (ha) acc += wa_pos[ia + 1] - wa_pos[ia] + 1;
+        if (hb) acc += wb_pos[ib + 1] - wb_pos[ib] + 1;
+        ia += ha;
+        ib += hb;
+        while (t + 1 < nt && acc * nt >= total * (long)(t + 1)) {
+            r[t].ia1 = ia;
+            r[t].ib1 = ib;
+            ++t;
+            r[t].ia0 = ia;
+            r[t].ib0 = ib;
+        }
+    }
+    for (; t < nt; ++t) {
+        r[t].ia1 = a_ni;
+        r[t].ib1 = b_ni;
+        if (t + 1 < nt) {
+            r[t + 1].ia0 = a_ni;
+            r[t + 1].ib0 = b_ni;
+        }
+    }
+}
+
+static void exclusive_offsets(top_range *r, int nt, int levels, long *totals) {
+    for (int d = 0; d < levels; ++d) {
+        long run = 0;
+        for (int t = 0; t < nt; ++t) {
+            const long c = r[t].n[d];
+            r[t].n[d] = run;
+            run += c;
+        }
+        totals[d] = run;
+    }
+}
+
+/* -- CSF3 union ----------------------------------------------------------------------- */
+
+typedef struct {
+    const int32_t *ci, *pj, *cj, *pk, *ck;
+    const float *v;
+    int ni;
+} csf_in;
+
+typedef struct {
+    const csf_in *A, *B;
+    top_range *r;
+    csf_out o; /* shared output arrays (write pass) */
+    int write;
+} csf_mt_job;
+
+/* The serial CSF3 union loop over one top-level range, counting (write == 0) or writing at
+ * the range's offsets. */
+static void csf_union_range(csf_mt_job *J, int t) {
+    const csf_in *A = J->A, *B = J->B;
+    top_range *rg = &J->r[t];
+    long ni = J->write ? rg->n[0] : 0, nj = J->write ? rg->n[1] : 0, nk = J->write ? rg->n[2] : 0;
+    csf_out *o = &J->o;
+    int ia = rg->ia0, ib = rg->ib0;
+    while (ia < rg->ia1 || ib < rg->ib1) {
+        int ha = ia < rg->ia1, hb = ib < rg->ib1, i;
+        if (ha && hb) {
+            i = A->ci[ia] < B->ci[ib] ? A->ci[ia] : B->ci[ib];
+            ha = A->ci[ia] == i;
+            hb = B->ci[ib] == i;
+        } else {
+            i = ha ? A->ci[ia] : B->ci[ib];
+        }
+        int ja = ha ? A->pj[ia] : 0, jae = ha ? A->pj[ia + 1] : 0;
+        int jb = hb ? B->pj[ib] : 0, jbe = hb ? B->pj[ib + 1] : 0;
+        while (ja < jae || jb < jbe) {
+            int ga = ja < jae, gb = jb < jbe, j;
+            if (ga && gb) {
+                j = A->cj[ja] < B->cj[jb] ? A->cj[ja] : B->cj[jb];
+                ga = A->cj[ja] == j;
+                gb = B->cj[jb] == j;
+            } else {
+                j = ga ? A->cj[ja] : B->cj[jb];
+            }
+            int x = ga ? A->pk[ja] : 0, xe = ga ? A->pk[ja + 1] : 0;
+            int y = gb ? B->pk[jb] : 0, ye = gb ? B->pk[jb + 1] : 0;
+            while (x < xe || y < ye) {
+                const int hx = x < xe, hy = y < ye;
+                const int k = (hx && (!hy || A->ck[x] <= B->ck[y])) ? A->ck[x] : B->ck[y];
+                const int ux = hx && A->ck[x] == k, uy = hy && B->ck[y] == k;
+                if (J->write) {
+                    o->ck[nk] = k;
+                    o->v[nk] = ux && uy ? A->v[x] + B->v[y] : (ux ? A->v[x] : B->v[y]);
+                }
+                ++nk;
+                x += ux;
+                y += uy;
+            }
+            if (J->write) {
+                o->cj[nj] = j;
+                o->pk[nj + 1] = (int32_t)nk;
+            }
+            ++nj;
+            ja += ga;
+            jb += gb;
+        }
+        if (J->write) {
+            o->ci[ni] = i;
+            o->pj[ni + 1] = (int32_t)nj;
+        }
+        ++ni;
+        ia += ha;
+        ib += hb;
+    }
+    if (!J->write) {
+        rg->n[0] = ni;
+        rg->n[1] = nj;
+        rg->n[2] = nk;
+    }
+}
+
+static void csf_union_task(int t, void *arg) { csf_union_range((csf_mt_job *)arg, t); }
+
+/* The same result as oracle_csf3_union, on `nthreads` threads (0: all online cores). */
+int oracle_csf3_union_mt(const int32_t *a_ci, int a_ni, const int32_t *a_pj,
+                         const int32_t *a_cj, int a_nj, const int32_t *a_pk,
+                         const int32_t *a_ck, const float *a_v, int a_nk, const int32_t *b_ci,
+                         int b_ni, const int32_t *b_pj, const int32_t *b_cj, int b_nj,
+                         const int32_t *b_pk, const int32_t *b_ck, const float *b_v, int b_nk,
+                         int nthreads, int32_t **o_ci, int32_t **o_pj, int32_t **o_cj,
+                         int32_t **o_pk, int32_t **o_ck, float **o_v, int *o_ni, int *o_nj,
+                         int *o_nk) {
+    (void)a_nj;
+    (void)b_nj;
+    (void)a_nk;
+    (void)b_nk;
+    const int nt = nthreads > 0 ? nthreads : oracle_default_threads();
+    const csf_in A = {a_ci, a_pj, a_cj, a_pk, a_ck, a_v, a_ni};
+    const csf_in B = {b_ci, b_pj, b_cj, b_pk, b_ck, b_v, b_ni};
+    /* weight of a top-level fibre: its k entries, from pos_k at the fibre's j range */
+    long *wa = (long *)malloc(sizeof(long) * ((size_t)a_ni + 1));
+    long *wb = (long *)malloc(sizeof(long) * ((size_t)b_ni + 1));
+    top_range *r = (top_range *)calloc((size_t)nt, sizeof(top_range));
+    if (!wa || !wb || !r) {
+        free(wa);
+        free(wb);
+        free(r);
+        return ORC_ENOMEM;
+    }
+    for (int i = 0; i <= a_ni; ++i) wa[i] = a_pk[a_pj[i]];
+    for (int i = 0; i <= b_ni; ++i) wb[i] = b_pk[b_pj[i]];
+    split_top(a_ci, a_ni, wa, b_ci, b_ni, wb, nt, r);
+    free(wa);
+    free(wb);
+    csf_mt_job J;
+    memset(&J, 0, sizeof(J));
+    J.A = &A;
+    J.B = &B;
+    J.r = r;
+    parallel_for(nt, csf_union_task, &J);
+    long tot[3];
+    exclusive_offsets(r, nt, 3, tot);
+    J.o.ci = (int32_t *)malloc(sizeof(int32_t) * ((size_t)tot[0] + 1));
+    J.o.pj = (int32_t *)malloc(sizeof(int32_t) * ((size_t)tot[0] + 1));
+    J.o.cj = (int32_t *)malloc(sizeof(int32_t) * ((size_t)tot[1] + 1));
+    J.o.pk = (int32_t *)malloc(sizeof(int32_t) * ((size_t)tot[1] + 1));
+    J.o.ck = (int32_t *)malloc(sizeof(int32_t) * ((size_t)tot[2] + 1));
+    J.o.v = (float *)malloc(sizeof(float) * ((size_t)tot[2] + 1));
+    if (!J.o.ci || !J.o.pj || !J.o.cj || !J.o.pk || !J.o.ck || !J.o.v) {
+        free(J.o.ci);
+        free(J.o.pj);
+        free(J.o.cj);
+        free(J.o.pk);
+        free(J.o.ck);
+        free(J.o.v);
+        free(r);
+        return ORC_ENOMEM;
+    }
+    J.o.pj[0] = 0;
+    J.o.pk[0] = 0;
+    J.write = 1;
+    parallel_for(nt, csf_union_task, &J);
+    free(r);
+    *o_ci = J.o.ci;
+    *o_pj = J.o.pj;
+    *o_cj = J.o.cj;
+    *o_pk = J.o.pk;
+    *o_ck = J.o.ck;
+    *o_v = J.o.v;
+    *o_ni = (int)tot[0];
+    *o_nj = (int)tot[1];
+    *o_nk = (int)tot[2];
+    return ORC_OK;
+}
+
+/* -- DCSR union / intersection --------------------------------------------------------- */
+
+typedef struct {
+    const int32_t *a_ci, *a_pj, *a_cj, *b_ci, *b_pj, *b_cj;
+    const float *a_v, *b_v;
+    int intersect, write;
+    top_range *r;
+    int32_t *ci, *pj, *cj;
+    float *v;
+} dcsr_mt_job;
+
+static void dcsr_range(dcsr_mt_job *J, int t) {
+    top_range *rg = &J->r[t];
+    long ni = J->write ? rg->n[0] : 0, nj = J->write ? rg->n[1] : 0;
+    int ia = rg->ia0, ib = rg->ib0;
+    const int X = J->intersect;
+    while (X ? (ia < rg->ia1 && ib < rg->ib1) : (ia < rg->ia1 || ib < rg->ib1)) {
+        int ha = ia < rg->ia1, hb = ib < rg->ib1, i;
+        if (ha && hb) {
+            i = J->a_ci[ia] < J->b_ci[ib] ? J->a_ci[ia] : J->b_ci[ib];
+            ha = J->a_ci[ia] == i;
+            hb = J->b_ci[ib] == i;
+        } else {
+            i = ha ? J->a_ci[ia] : J->b_ci[ib];
+        }
+        if (!X || (ha && hb)) {
+            int x = ha ? J->a_pj[ia] : 0, xe = ha ? J->a_pj[ia + 1] : 0;
+            int y = hb ? J->b_pj[ib] : 0, ye = hb ? J->b_pj[ib + 1] : 0;
+            while (X ? (x < xe && y < ye) : (x < xe || y < ye)) {
+                const int hx = x < xe, hy = y < ye;
+                const int j = (hx && (!hy || J->a_cj[x] <= J->b_cj[y])) ? J->a_cj[x] : J->b_cj[y];
+                const int ux = hx && J->a_cj[x] == j, uy = hy && J->b_cj[y] == j;
+                if (!X || (ux && uy)) {
+                    if (J->write) {
+                        J->cj[nj] = j;
+                        J->v[nj] = ux && uy ? (X ? J->a_v[x] * J->b_v[y] : J->a_v[x] + J->b_v[y])
+                                            : (ux ? J->a_v[x] : J->b_v[y]);
+                    }
+                    ++nj;
+                }
+                x += ux;
+                y += uy;
+            }
+            if (J->write) {
+                J->ci[ni] = i;
+                J->pj[ni + 1] = (int32_t)nj;
+            }
+            ++ni;
+        }
+        ia += ha;
+        ib += hb;
+    }
+    if (!J->write) {
+        rg->n[0] = ni;
+        rg->n[1] = nj;
+    }
+}
+
+static void dcsr_task(int t, void *arg) { dcsr_range((dcsr_mt_job *)arg, t); }
+
+/* The same result as oracle_dcsr_binary, on `nthreads` threads (0: all online cores). */
+int oracle_dcsr_binary_mt(int intersect, const int32_t *a_ci, int a_ni, const int32_t *a_pj,
+                          const int32_t *a_cj, const float *a_v, const int32_t *b_ci, int b_ni,
+                          const int32_t *b_pj, const int32_t *b_cj, const float *b_v,
+                          int nthreads, int32_t **o_ci, int32_t **o_pj, int32_t **o_cj,
+                          float **o_v, int *o_ni, int *o_nj) {
+    const int nt = nthreads > 0 ? nthreads : oracle_default_threads();
+    long *wa = (long *)malloc(sizeof(long) * ((size_t)a_ni + 1));
+    long *wb = (long *)malloc(sizeof(long) * ((size_t)b_ni + 1));
+    top_range *r = (top_range *)calloc((size_t)nt, sizeof(top_range));
+    if (!wa || !wb || !r) {
+        free(wa);
+        free(wb);
+        free(r);
+        return ORC_ENOMEM;
+    }
+    for (int i = 0; i <= a_ni; ++i) wa[i] = a_pj[i];
+    for (int i = 0; i <= b_ni; ++i) wb[i] = b_pj[i];
+    split_top(a_ci, a_ni, wa, b_ci, b_ni, wb, nt, r);
+    free(wa);
+    free(wb);
+    dcsr_mt_job J;
+    memset(&J, 0, sizeof(J));
+    J.a_ci = a_ci;
+    J.a_pj = a_pj;
+    J.a_cj = a_cj;
+    J.a_v = a_v;
+    J.b_ci = b_ci;
+    J.b_pj = b_pj;
+    J.b_cj = b_cj;
+    J.b_v = b_v;
+    J.intersect = intersect;
+    J.r = r;
+    parallel_for(nt, dcsr_task, &J);
+    long tot[2];
+    exclusive_offsets(r, nt, 2, tot);
+    J.ci = (int32_t *)malloc(sizeof(int32_t) * ((size_t)tot[0] + 1));
+    J.pj = (int32_t *)malloc(sizeof(int32_t) * ((size_t)tot[0] + 1));
+    J.cj = (int32_t *)malloc(sizeof(int32_t) * ((size_t)tot[1] + 1));
+    J.v = (float *)malloc(sizeof(float) * ((size_t)tot[1] + 1));
+    if (!J.ci || !J.pj || !J.cj || !J.v) {
+        free(J.ci);
+        free(J.pj);
+        free(J.cj);
+        free(J.v);
+        free(r);
+        return ORC_ENOMEM;
+    }
+    J.pj[0] = 0;
+    J.write = 1;
+    parallel_for(nt, dcsr_task, &J);
+    free(r);
+    *o_ci = J.ci;
+    *o_pj = J.pj;
+    *o_cj = J.cj;
+    *o_v = J.v;
+    *o_ni = (int)tot[0];
+    *o_nj = (int)tot[1];
+    return ORC_OK;
+}
+
+/* -- three-way CSR union --------------------------------------------------------------- */
+
+typedef struct {
+    int rows;
+    const int32_t *pa, *ca, *pb, *cb, *pc, *cc;
+    const float *va, *vb, *vc;
+    int write;
+    top_range *r; /* ia0/ia1 = row range */
+    int32_t *pos, *crd;
+    float *val;
+} add3_mt_job;
+
+static void add3_range(add3_mt_job *J, int t) {
+    top_range *rg = &J->r[t];
+    long n = J->write ? rg->n[0] : 0;
+    for (int row = rg->ia0; row < rg->ia1; ++row) {
+        int x = J->pa[row], y = J->pb[row], z = J->pc[row];
+        const int xe = J->pa[row + 1], ye = J->pb[row + 1], ze = J->pc[row + 1];
+        while (x < xe || y < ye || z < ze) {
+            int j = INT32_MAX;
+            if (x < xe && J->ca[x] < j) j = J->ca[x];
+            if (y < ye && J->cb[y] < j) j = J->cb[y];
+            if (z < ze && J->cc[z] < j) j = J->cc[z];
+            const int ha = x < xe && J->ca[x] == j, hb = y < ye && J->cb[y] == j,
+                      hc = z < ze && J->cc[z] == j;
+            if (J->write) {
+                float v;
+                if (ha && hb) {
+                    v = J->va[x] + J->vb[y];
+                    if (hc) v = v + J->vc[z];
+                } else if (ha) {
+                    v = hc ? J->va[x] + J->vc[z] : J->va[x];
+                } else if (hb) {
+                    v = hc ? J->vb[y] + J->vc[z] : J->vb[y];
+                } else {
+                    v = J->vc[z];
+                }
+                J->crd[n] = j;
+                J->val[n] = v;
+            }
+            ++n;
+            x += ha;
+            y += hb;
+            z += hc;
+        }
+        if (J->write) J->pos[row + 1] = (int32_t)n;
+    }
+    if (!J->write) rg->n[0] = n;
+}
+
+static void add3_task(int t, void *arg) { add3_range((add3_mt_job *)arg, t); }
+
+/* The same result as oracle_csr_add3, on `nthreads` threads (0: all online cores): rows cut
+ * into ranges of about equal (entries + rows). */
+int oracle_csr_add3_mt(int rows, const int32_t *pa, const int32_t *ca, const float *va,
+                       const int32_t *pb, const int32_t *cb, const float *vb, const int32_t *pc,
+                       const int32_t *cc, const float *vc, int nthreads, int32_t **o_pos,
+                       int32_t **o_crd, float **o_val, int *o_nnz) {
+    const int nt = nthreads > 0 ? nthreads : oracle_default_threads();
+    top_range *r = (top_range *)calloc((size_t)nt, sizeof(top_range));
+    if (!r) return ORC_ENOMEM;
+    const long total = (long)pa[rows] + pb[rows] + pc[rows] + rows;
+    for (int t = 0; t < nt; ++t) {
+        /* first row whose prefix weight reaches t * total / nt */
+        const long target = total * t / nt;
+        int lo = 0, hi = rows;
+        while (lo < hi) {
+            const int mid = (lo + hi) / 2;
+            if ((long)pa[mid] + pb[mid] + pc[mid] + mid < target) {
+                lo = mid + 1;
+            } else {
+                hi = mid;
+            }
+        }
+        r[t].ia0 = t == 0 ? 0 : lo;
+    }
+    for (int t = 0; t < nt; ++t) r[t].ia1 = t + 1 < nt ? r[t + 1].ia0 : rows;
+    add3_mt_job J;
+    memset(&J, 0, sizeof(J));
+    J.rows = rows;
+    J.pa = pa;
+    J.ca = ca;
+    J.va = va;
+    J.pb = pb;
+    J.cb = cb;
+    J.vb = vb;
+    J.pc = pc;
+    J.cc = cc;
+    J.vc = vc;
+    J.r = r;
+    parallel_for(nt, add3_task, &J);
+    long tot[1];
+    exclusive_offsets(r, nt, 1, tot);
+    J.pos = (int32_t *)malloc(sizeof(int32_t) * ((size_t)rows + 1));
+    J.crd = (int32_t *)malloc(sizeof(int32_t) * ((size_t)tot[0] + 1));
+    J.val = (float *)malloc(sizeof(float) * ((size_t)tot[0] + 1));
+    if (!J.pos || !J.crd || !J.val) {
+        free(J.pos);
+        free(J.crd);
+        free(J.val);
+        free(r);
+        return ORC_ENOMEM;
+    }
+    J.pos[0] = 0;
+    J.write = 1;
+    parallel_for(nt, add3_task, &J);
+    free(r);
+    *o_pos = J.pos;
+    *o_crd = J.crd;
+    *o_val = J.val;
+    *o_nnz = (int)tot[0];
+    return ORC_OK;
+}

@@ -81,6 +81,21 @@ def load() -> ctypes.CDLL:
             [ctypes.c_int] + [_i32p, ctypes.c_int, _i32p, _i32p, _f32p] * 2
             + [ctypes.POINTER(_i32p)] * 3 + [ctypes.POINTER(_f32p)]
             + [ctypes.POINTER(ctypes.c_int)] * 2)
+        lib.oracle_csf3_union_mt.restype = ctypes.c_int
+        lib.oracle_csf3_union_mt.argtypes = (
+            [_i32p, ctypes.c_int, _i32p, _i32p, ctypes.c_int, _i32p, _i32p, _f32p, ctypes.c_int]
+            * 2 + [ctypes.c_int] + [ctypes.POINTER(_i32p)] * 5 + [ctypes.POINTER(_f32p)]
+            + [ctypes.POINTER(ctypes.c_int)] * 3)
+        lib.oracle_csr_add3_mt.restype = ctypes.c_int
+        lib.oracle_csr_add3_mt.argtypes = (
+            [ctypes.c_int] + [_i32p, _i32p, _f32p] * 3 + [ctypes.c_int]
+            + [ctypes.POINTER(_i32p), ctypes.POINTER(_i32p), ctypes.POINTER(_f32p),
+               ctypes.POINTER(ctypes.c_int)])
+        lib.oracle_dcsr_binary_mt.restype = ctypes.c_int
+        lib.oracle_dcsr_binary_mt.argtypes = (
+            [ctypes.c_int] + [_i32p, ctypes.c_int, _i32p, _i32p, _f32p] * 2 + [ctypes.c_int]
+            + [ctypes.POINTER(_i32p)] * 3 + [ctypes.POINTER(_f32p)]
+            + [ctypes.POINTER(ctypes.c_int)] * 2)
         lib.oracle_spgemm.restype = ctypes.c_int
         lib.oracle_spgemm.argtypes = [
             ctypes.c_int, ctypes.c_int, ctypes.c_int, _i32p, _i32p, _f32p, _i32p, _i32p, _f32p,
@@ -169,9 +184,11 @@ def port_coo_binary(op, a_crd, va, b_crd, vb, nthreads=0, timing=None):
     return crd, _take(oval, n, np.float32)
 
 
-def port_csf3_union(a_levels, a_val, b_levels, b_val, timing=None):
+def port_csf3_union(a_levels, a_val, b_levels, b_val, timing=None, nthreads=None):
     """levels = (crd_i, pos_j, crd_j, pos_k, crd_k).  Returns (levels, val).  If `timing` is
-    a dict, timing["seconds"] receives the duration of the C call alone."""
+    a dict, timing["seconds"] receives the duration of the C call alone.  nthreads=None runs
+    the serial lattice (oracle_csf3_union); a count (0 = all cores) runs the range-parallel
+    restatement (oracle_csf3_union_mt), whose result is the same."""
     import time
 
     lib = load()
@@ -193,8 +210,13 @@ def port_csf3_union(a_levels, a_val, b_levels, b_val, timing=None):
     oval = _f32p()
     ns = [ctypes.c_int() for _ in range(3)]
     t0 = time.perf_counter()
-    rc = lib.oracle_csf3_union(*args(pa), *args(pb), *[ctypes.byref(o) for o in outs],
-                               ctypes.byref(oval), *[ctypes.byref(n) for n in ns])
+    if nthreads is None:
+        rc = lib.oracle_csf3_union(*args(pa), *args(pb), *[ctypes.byref(o) for o in outs],
+                                   ctypes.byref(oval), *[ctypes.byref(n) for n in ns])
+    else:
+        rc = lib.oracle_csf3_union_mt(*args(pa), *args(pb), int(nthreads),
+                                      *[ctypes.byref(o) for o in outs], ctypes.byref(oval),
+                                      *[ctypes.byref(n) for n in ns])
     if timing is not None:
         timing["seconds"] = time.perf_counter() - t0
     if rc != 0:
@@ -206,9 +228,10 @@ def port_csf3_union(a_levels, a_val, b_levels, b_val, timing=None):
     return levels, _take(oval, nk, np.float32)
 
 
-def port_csr_add3(rows, a, b, c, timing=None):
+def port_csr_add3(rows, a, b, c, timing=None, nthreads=None):
     """a, b, c = (pos, crd, val).  Returns (pos int32, crd int32, val float32).  If `timing`
-    is a dict, timing["seconds"] receives the duration of the C call alone."""
+    is a dict, timing["seconds"] receives the duration of the C call alone.  nthreads=None
+    runs the serial lattice; a count (0 = all cores) the row-range-parallel restatement."""
     import time
 
     lib = load()
@@ -221,8 +244,12 @@ def port_csr_add3(rows, a, b, c, timing=None):
                  _ptr(keep[i + 2], ctypes.c_float)]
     opos, ocrd, oval, onnz = _i32p(), _i32p(), _f32p(), ctypes.c_int()
     t0 = time.perf_counter()
-    rc = lib.oracle_csr_add3(int(rows), *args, ctypes.byref(opos), ctypes.byref(ocrd),
-                             ctypes.byref(oval), ctypes.byref(onnz))
+    if nthreads is None:
+        rc = lib.oracle_csr_add3(int(rows), *args, ctypes.byref(opos), ctypes.byref(ocrd),
+                                 ctypes.byref(oval), ctypes.byref(onnz))
+    else:
+        rc = lib.oracle_csr_add3_mt(int(rows), *args, int(nthreads), ctypes.byref(opos),
+                                    ctypes.byref(ocrd), ctypes.byref(oval), ctypes.byref(onnz))
     if timing is not None:
         timing["seconds"] = time.perf_counter() - t0
     if rc != 0:
@@ -232,9 +259,11 @@ def port_csr_add3(rows, a, b, c, timing=None):
             _take(oval, n, np.float32))
 
 
-def port_dcsr_binary(op, a_levels, a_val, b_levels, b_val, timing=None):
+def port_dcsr_binary(op, a_levels, a_val, b_levels, b_val, timing=None, nthreads=None):
     """levels = (crd_i, pos_j, crd_j).  op = "add" | "mul".  Returns (levels, val).  If
-    `timing` is a dict, timing["seconds"] receives the duration of the C call alone."""
+    `timing` is a dict, timing["seconds"] receives the duration of the C call alone.
+    nthreads=None runs the serial lattice; a count (0 = all cores) the range-parallel
+    restatement."""
     import time
 
     lib = load()
@@ -250,9 +279,14 @@ def port_dcsr_binary(op, a_levels, a_val, b_levels, b_val, timing=None):
     oval = _f32p()
     ni, nj = ctypes.c_int(), ctypes.c_int()
     t0 = time.perf_counter()
-    rc = lib.oracle_dcsr_binary(1 if op == "mul" else 0, *args(ka), *args(kb),
-                                *[ctypes.byref(o) for o in outs], ctypes.byref(oval),
-                                ctypes.byref(ni), ctypes.byref(nj))
+    if nthreads is None:
+        rc = lib.oracle_dcsr_binary(1 if op == "mul" else 0, *args(ka), *args(kb),
+                                    *[ctypes.byref(o) for o in outs], ctypes.byref(oval),
+                                    ctypes.byref(ni), ctypes.byref(nj))
+    else:
+        rc = lib.oracle_dcsr_binary_mt(1 if op == "mul" else 0, *args(ka), *args(kb),
+                                       int(nthreads), *[ctypes.byref(o) for o in outs],
+                                       ctypes.byref(oval), ctypes.byref(ni), ctypes.byref(nj))
     if timing is not None:
         timing["seconds"] = time.perf_counter() - t0
     if rc != 0:
