@@ -59,6 +59,8 @@ extern "C" {
 #define NACHO_ERR_INTERNAL (-6)         /* a kernel did not publish a result length       */
 #define NACHO_ERR_IO (-7)               /* a file could not be opened or read             */
 #define NACHO_ERR_UNSUPPORTED (-8)      /* a file format variant the reader does not take */
+#define NACHO_ERR_SCRATCH_TOO_SMALL (-9) /* input beyond an allocation-free entry point's
+                                            static scratch (NACHO_NOALLOC_MAX_ITEMS)     */
 
 /* ---- tensor descriptors (field order = the reference's generated structs) ---------- */
 
@@ -196,6 +198,27 @@ int nacho_record_stream(void *ptr, void *stream);
 int nacho_gpu_csr_add_f32(const nacho_csr *a, const nacho_csr *b, nacho_csr *z,
                           int32_t num_blocks, int32_t threads_per_block, void *stream,
                           const nacho_allocator *alloc);
+
+/* Allocation-free Z = a + b over CSR: the same result as nacho_gpu_csr_add_f32, computed
+ * without allocating anything (no hipMalloc / hipFree / allocating library routine).  No
+ * counterpart in the reference; for callers that cannot allocate: code that must not call
+ * hipMalloc (serving loops, harnesses that forbid it, work prepared for HIP graph capture).
+ *   - The caller passes the result buffers in `z`: dim_j_offsets (dim_i_size + 1 entries),
+ *     dim_j_indices and values, each with room for z->dim_j_length entries, which must be
+ *     at least a->dim_j_length + b->dim_j_length (the union's upper bound).  On return
+ *     z->dim_j_length and z->nnz hold the result length (0 on failure); the pointers are
+ *     left as given.
+ *   - Scratch is a static device array of 1 MiB per GPU (held until the process ends),
+ *     enough for a->dim_j_length + b->dim_j_length + dim_i_size <= NACHO_NOALLOC_MAX_ITEMS;
+ *     larger inputs fail with NACHO_ERR_SCRATCH_TOO_SMALL before any device work.
+ *   - Every call on a GPU shares that GPU's scratch: calls that overlap on one GPU (other
+ *     host threads, or other streams still running) race and must be serialised by the
+ *     caller.
+ *   - The call synchronises `stream` to read the result length back. */
+#define NACHO_NOALLOC_MAX_ITEMS 250000000LL
+int nacho_gpu_csr_add_f32_noalloc(const nacho_csr *a, const nacho_csr *b, nacho_csr *z,
+                                  int32_t num_blocks, int32_t threads_per_block,
+                                  void *stream);
 
 /* Z = a + b + c over CSR (union of three; a value is the sum of the present operands in
  * the order (a + b) + c, one float32 add per extra operand).  Replaces

@@ -155,6 +155,12 @@ ENTRY_POINTS_3 = {
     "nacho_gpu_sssmm_f32": (CsrDesc, CsrDesc),
 }
 
+# allocation-free entry points (a, b, z, num_blocks, threads_per_block, stream): the caller
+# passes the result buffers in z
+ENTRY_POINTS_NOALLOC = {
+    "nacho_gpu_csr_add_f32_noalloc": (CsrDesc, CsrDesc),
+}
+
 _lib = None
 
 
@@ -184,6 +190,11 @@ def load() -> ctypes.CDLL:
         fn.argtypes = [ctypes.POINTER(operand)] * 3 + [
             ctypes.POINTER(result), ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p,
             ctypes.POINTER(Allocator)]
+    for name, (operand, result) in ENTRY_POINTS_NOALLOC.items():
+        fn = getattr(lib, name)
+        fn.restype = ctypes.c_int
+        fn.argtypes = [ctypes.POINTER(operand), ctypes.POINTER(operand), ctypes.POINTER(result),
+                       ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]
     lib.nacho_parse2d.restype = ctypes.c_int
     lib.nacho_parse2d.argtypes = [ctypes.c_char_p, ctypes.POINTER(Coo2dHost)]
     lib.nacho_parse3d.restype = ctypes.c_int

@@ -38,6 +38,7 @@
 
 #include <climits>
 #include <cstdint>
+#include <mutex>
 
 #include "csr_merge.hpp"
 #include "device_utils.hpp"
@@ -449,7 +450,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
         LaneOut<IPT + 1> lo;
         walk_lane<OP, false, false, IPT, Start::RowGiven>(lo, sp, t, s_crd, nullptr, s_row, tid,
                                                           start);
-        starts[static_cast<size_t>(t) * kBlock + tid] = make_uint2(start.k_ia, start.ib);
+        if (starts) starts[static_cast<size_t>(t) * kBlock + tid] = make_uint2(start.k_ia, start.ib);
         mine += static_cast<unsigned>(__popc(lo.valid));  // summed over the chunk at the end
         if (t + 1 < t1) {
             __syncthreads();  // every lane is done reading this tile's LDS
@@ -481,7 +482,11 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
 // chunk_total[w] the sum over workgroup w's chunk, and the last workgroup to finish stores
 // the sum of all chunks, the result length, to `length_out`.  csr_compact_kernel then moves
 // each tile to its final offset and corrects its rows' pos.
-template <Op OP, int IPT, bool VALUES, bool CHILD, bool SPREAD>
+//
+// SEARCH (union without stored lane starts): every lane finds its start from the tile's
+// row-start bins and a search inside its row, as the spread intersection does, instead of
+// loading it from `starts`.
+template <Op OP, int IPT, bool VALUES, bool CHILD, bool SPREAD, bool SEARCH = false>
 __global__ __launch_bounds__(kBlock) void csr_write_kernel(
     const int *__restrict__ pa, const int *__restrict__ ca, const float *__restrict__ va,
     const int *__restrict__ pb, const int *__restrict__ cb, const float *__restrict__ vb,
@@ -503,7 +508,8 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
     __shared__ unsigned s_row[kCap];
     __shared__ int s_wave[kBlock / dev::kWave];
     __shared__ int s_split[3 * (kMaxChunk + 1)];
-    __shared__ unsigned s_bin[SPREAD ? kBlock : 1];  // row-start bins (see stage_tile)
+    constexpr bool kOwn = SPREAD || SEARCH;  // lanes find their own starts
+    __shared__ unsigned s_bin[kOwn ? kBlock : 1];  // row-start bins (see stage_tile)
     __shared__ int s_wmax[kBlock / dev::kWave];
 
     const int tid = threadIdx.x;
@@ -518,7 +524,7 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
         }
         return;
     }
-    if (SPREAD) s_bin[tid] = 0u;
+    if (kOwn) s_bin[tid] = 0u;
     stage_splits(s_split, split_r, split_a, split_b, t0, t1);
 
     // Offset of this chunk: the counts of every earlier chunk.
@@ -538,11 +544,11 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
     Staged<kLoads> st;
     fetch_tile<VALUES, kLoads>(st, sp, pa, ca, va, pb, cb, vb, tid);
     // A union's lane starts come from its count kernel (loaded one tile ahead); the spread
-    // intersection has no count pass: its lanes take their row from the row-start bins and
-    // search only inside it.
-    constexpr bool kGiven = !SPREAD;
-    constexpr Start kMode = SPREAD ? Start::RowGiven : Start::Given;
-    constexpr int kBinIpt = SPREAD ? IPT : 0;  // stage_tile fills the bins only when spread
+    // intersection has no count pass, and the SEARCH union has no stored starts: their lanes
+    // take their row from the row-start bins and search only inside it.
+    constexpr bool kGiven = !kOwn;
+    constexpr Start kMode = kOwn ? Start::RowGiven : Start::Given;
+    constexpr int kBinIpt = kOwn ? IPT : 0;  // stage_tile fills the bins only then
     stage_tile<VALUES, kLoads, kBinIpt>(st, sp, s_crd, s_val, s_row, tid, s_bin, 1u,
                                         t0 * kBlock * IPT);
     __syncthreads();
@@ -682,7 +688,7 @@ __global__ __launch_bounds__(kBlock) void csr_compact_kernel(
 
 int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
                 const LevelOperand &A, const LevelOperand &B, const LevelResult &Z,
-                long long *out_len, const char *kernel_name) {
+                long long *out_len, const char *kernel_name, bool keep_starts) {
     const long long total = static_cast<long long>(A.len) + B.len + rows;
     if (total > static_cast<long long>(INT_MAX) - 2 * kTile) return NACHO_ERR_INDEX_OVERFLOW;
     const int num_tiles = total > 0 ? static_cast<int>((total + kTile - 1) / kTile) : 1;
@@ -751,7 +757,7 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
         return NACHO_OK;
     }
     uint2 *starts = nullptr;  // every lane's walk start, from the count kernel to the write
-    NACHO_TRY(call.scratch_n(static_cast<size_t>(num_tiles) * kBlock, &starts));
+    if (keep_starts) NACHO_TRY(call.scratch_n(static_cast<size_t>(num_tiles) * kBlock, &starts));
     NACHO_TRY(call.timer_start(kernel_name));  // the whole device pipeline of this level
     csr_partition_kernel<<<ceil_div(static_cast<size_t>(num_tiles) + 1, kPartBlock), kPartBlock, 0, s>>>(
         A.pos, A.crd, B.pos, B.crd, rows, static_cast<int>(total), num_tiles, split_r, split_a,
@@ -767,7 +773,16 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
         A.pos, A.crd, A.val, B.pos, B.crd, B.val, A.len, B.len, num_tiles, chunk, split_r,      \
         split_a, split_b, counts, rows, Z.pos, Z.crd, Z.val, A.next, B.next, Z.child_a,         \
         Z.child_b, length, 0, nullptr, nullptr, nullptr, nullptr, starts)
-    if (values) {
+    if (values && !keep_starts) {
+        if (child) return NACHO_ERR_INVALID_ARGUMENT;
+        csr_write_kernel<Op::Union, kItemsPerLane, true, false, false, true>
+            <<<grid, kBlock, 0, s>>>(A.pos, A.crd, A.val, B.pos, B.crd, B.val, A.len, B.len,
+                                     num_tiles, chunk, split_r, split_a, split_b, counts, rows,
+                                     Z.pos, Z.crd, Z.val, nullptr, nullptr, nullptr, nullptr,
+                                     length, 0, nullptr, nullptr, nullptr, nullptr, nullptr);
+    } else if (!keep_starts) {
+        return NACHO_ERR_INVALID_ARGUMENT;  // only the value level runs without stored starts
+    } else if (values) {
         if (child) return NACHO_ERR_INVALID_ARGUMENT;
         NACHO_WRITE_LAUNCH(Op::Union, true, false);
     } else if (child) {
@@ -783,6 +798,13 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
     NACHO_TRY(call.wait_length(&len));
     *out_len = len;
     return NACHO_OK;
+}
+
+size_t merge_level_arena_bytes(long long items) {
+    const long long tiles = items > 0 ? (items + kTile - 1) / kTile : 1;
+    // splits (3 per boundary), chunk counts (at most one per tile) plus the ticket words,
+    // the length word, and 256-byte alignment of each piece
+    return static_cast<size_t>(12 * (tiles + 1) + 4 * (tiles + 6) + 8 + 4 * 256);
 }
 
 bool bad_csr(const nacho_csr *t) {
@@ -841,10 +863,84 @@ int csr_binary(bool intersect, const nacho_csr *a, const nacho_csr *b, nacho_csr
     return NACHO_OK;
 }
 
+// ---- allocation-free csr_add ------------------------------------------------------------
+// Scratch of nacho_gpu_csr_add_f32_noalloc: a file-scope device array, one copy per GPU,
+// held for the life of the process.  Host code never passes `scratch` itself to a kernel
+// (in host code the name is a stand-in, not a device address): it looks up each device's
+// address once with hipGetSymbolAddress and uses that.
+constexpr size_t kNoAllocScratchBytes = size_t{1} << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+
+// Device address of `scratch` on the current device, looked up on the first call there.
+int scratch_address(void **out) {
+    static std::mutex mutex;
+    static void *address[kMaxDevices] = {};
+    int device = 0;
+    NACHO_TRY_HIP(hipGetDevice(&device));
+    if (device < 0 || device >= kMaxDevices) return NACHO_ERR_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lock(mutex);
+    if (!address[device]) {
+        void *p = nullptr;
+        NACHO_TRY_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return NACHO_ERR_INTERNAL;
+        address[device] = p;
+    }
+    *out = address[device];
+    return NACHO_OK;
+}
+
+int csr_add_noalloc(const nacho_csr *a, const nacho_csr *b, nacho_csr *z, int32_t num_blocks,
+                    int32_t threads_per_block, void *stream) {
+    if (!z) return NACHO_ERR_INVALID_ARGUMENT;
+    int *pc = z->dim_j_offsets, *cc = z->dim_j_indices;
+    float *vc = z->values;
+    const long long capacity = z->dim_j_length;
+    z->dim_j_length = 0;
+    z->nnz = 0;
+    NACHO_TRY(check_launch_hints(num_blocks, threads_per_block));
+    if (bad_csr(a) || bad_csr(b)) return NACHO_ERR_INVALID_ARGUMENT;
+    if (a->dim_i_size != b->dim_i_size || a->dim_j_size != b->dim_j_size) {
+        return NACHO_ERR_INVALID_ARGUMENT;
+    }
+    const int rows = a->dim_i_size;
+    const long long nnz_a = a->dim_j_length, nnz_b = b->dim_j_length;
+    const long long items = nnz_a + nnz_b + rows;
+    if (items > static_cast<long long>(INT_MAX) - 2 * kTile) return NACHO_ERR_INDEX_OVERFLOW;
+    if (!pc || capacity < nnz_a + nnz_b || (capacity > 0 && (!cc || !vc))) {
+        return NACHO_ERR_INVALID_ARGUMENT;
+    }
+    if (items > NACHO_NOALLOC_MAX_ITEMS) return NACHO_ERR_SCRATCH_TOO_SMALL;
+    if (merge_level_arena_bytes(items) > kNoAllocScratchBytes) return NACHO_ERR_INTERNAL;
+    void *arena = nullptr;
+    NACHO_TRY(scratch_address(&arena));
+    Call call(stream, arena, kNoAllocScratchBytes);
+    const LevelOperand A{a->dim_j_offsets, a->dim_j_indices, a->values, a->dim_j_length, nullptr};
+    const LevelOperand B{b->dim_j_offsets, b->dim_j_indices, b->values, b->dim_j_length, nullptr};
+    const LevelResult Z{pc, cc, vc, nullptr, nullptr};
+    long long nnz = 0;
+    NACHO_TRY(merge_level(call, false, true, false, rows, A, B, Z, &nnz,
+                          "csr_add (no-alloc): partition+count+write", false));
+    if (nnz > nnz_a + nnz_b) return NACHO_ERR_MALFORMED_INPUT;
+    z->dim_i_size = rows;
+    z->dim_j_size = a->dim_j_size;
+    z->dim_j_length = static_cast<int32_t>(nnz);
+    z->nnz = static_cast<int32_t>(nnz);
+    return NACHO_OK;
+}
+
 }  // namespace csr
 }  // namespace nacho
 
 extern "C" {
+
+int nacho_gpu_csr_add_f32_noalloc(const nacho_csr *a, const nacho_csr *b, nacho_csr *z,
+                                  int32_t num_blocks, int32_t threads_per_block,
+                                  void *stream) {
+    return nacho::csr::csr_add_noalloc(a, b, z, num_blocks, threads_per_block, stream);
+}
+
 
 int nacho_gpu_csr_add_f32(const nacho_csr *a, const nacho_csr *b, nacho_csr *z,
                           int32_t num_blocks, int32_t threads_per_block, void *stream,

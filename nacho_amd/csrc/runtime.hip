@@ -247,7 +247,15 @@ Call::Call(void *stream, const nacho_allocator *alloc)
       alloc_(alloc && alloc->allocate ? alloc : nullptr),
       timing_(g_timing_enabled.load(std::memory_order_relaxed) != 0) {}
 
+Call::Call(void *stream, void *arena, size_t arena_bytes)
+    : stream_(static_cast<hipStream_t>(stream)),
+      alloc_(nullptr),
+      timing_(false),
+      arena_(static_cast<unsigned char *>(arena)),
+      arena_size_(arena_bytes) {}
+
 Call::~Call() {
+    if (arena_) return;  // nothing was allocated
     if (timed_) t_last_ms = timed_ms_;
     if (!committed_) scratch_.insert(scratch_.end(), results_.begin(), results_.end());
     if (alloc_) {
@@ -274,6 +282,13 @@ void Call::release(void *ptr) {
 int Call::scratch(size_t bytes, void **out) {
     *out = nullptr;
     if (bytes == 0) return NACHO_OK;
+    if (arena_) {
+        const size_t at = (arena_used_ + 255) & ~static_cast<size_t>(255);
+        if (at > arena_size_ || bytes > arena_size_ - at) return NACHO_ERR_SCRATCH_TOO_SMALL;
+        arena_used_ = at + bytes;
+        *out = arena_ + at;
+        return NACHO_OK;
+    }
     void *p = allocate(bytes);
     if (!p) return NACHO_ERR_OUT_OF_MEMORY;
     scratch_.push_back(p);
@@ -284,6 +299,7 @@ int Call::scratch(size_t bytes, void **out) {
 int Call::result(size_t bytes, void **out) {
     *out = nullptr;
     if (bytes == 0) return NACHO_OK;
+    if (arena_) return NACHO_ERR_INVALID_ARGUMENT;  // the caller passes result buffers
     void *p = allocate(bytes);
     if (!p) return NACHO_ERR_OUT_OF_MEMORY;
     results_.push_back(p);
@@ -304,6 +320,11 @@ void Call::drop_result(void *ptr) {
 
 int Call::read_back(void *host, const void *device, size_t bytes) {
     if (bytes > 64) return NACHO_ERR_INVALID_ARGUMENT;
+    if (arena_) {  // no pinned staging word: copy straight into the caller's variable
+        NACHO_TRY_HIP(hipMemcpyAsync(host, device, bytes, hipMemcpyDeviceToHost, stream_));
+        NACHO_TRY_HIP(hipStreamSynchronize(stream_));
+        return NACHO_OK;
+    }
     if (!t_pinned) NACHO_TRY_HIP(hipHostMalloc(&t_pinned, 64, hipHostMallocDefault));
     NACHO_TRY_HIP(hipMemcpyAsync(t_pinned, device, bytes, hipMemcpyDeviceToHost, stream_));
     NACHO_TRY_HIP(hipStreamSynchronize(stream_));
@@ -312,6 +333,11 @@ int Call::read_back(void *host, const void *device, size_t bytes) {
 }
 
 int Call::length_word(int64_t **dev) {
+    if (arena_) {  // the kernel that totals the length stores it in the arena
+        NACHO_TRY(scratch_n(1, &arena_len_));
+        *dev = arena_len_;
+        return NACHO_OK;
+    }
     if (!t_len_host) {
         void *h = nullptr;
         NACHO_TRY_HIP(hipHostMalloc(&h, 64, hipHostMallocMapped | hipHostMallocCoherent |
@@ -331,12 +357,21 @@ int Call::length_word(int64_t **dev) {
 }
 
 int Call::mark_length() {
+    if (arena_) return NACHO_OK;  // wait_length synchronises the stream instead
     if (!t_ev_len) NACHO_TRY_HIP(hipEventCreateWithFlags(&t_ev_len, hipEventDisableTiming));
     NACHO_TRY_HIP(hipEventRecord(t_ev_len, stream_));
     return NACHO_OK;
 }
 
 int Call::wait_length(int64_t *len) {
+    if (arena_) {
+        if (!arena_len_) return NACHO_ERR_INTERNAL;
+        int64_t v = -1;
+        NACHO_TRY(read_back(&v, arena_len_, sizeof(v)));
+        if (v < 0) return NACHO_ERR_INTERNAL;
+        *len = v;
+        return NACHO_OK;
+    }
     NACHO_TRY_HIP(hipEventSynchronize(t_ev_len));
     *len = *t_len_host;
     if (*len < 0) return NACHO_ERR_INTERNAL;
@@ -421,6 +456,8 @@ const char *nacho_error_string(int code) {
         case NACHO_ERR_INTERNAL: return "nacho: internal error (a kernel did not publish its result length)";
         case NACHO_ERR_IO: return "nacho: file could not be opened or read";
         case NACHO_ERR_UNSUPPORTED: return "nacho: unsupported file format variant";
+        case NACHO_ERR_SCRATCH_TOO_SMALL:
+            return "nacho: input too large for the allocation-free entry point's static scratch";
         default: break;
     }
     if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));

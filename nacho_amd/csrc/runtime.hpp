@@ -40,6 +40,11 @@ namespace nacho {
 class Call {
   public:
     Call(void *stream, const nacho_allocator *alloc);
+    // Arena mode, for the allocation-free entry points: scratch is carved from the device
+    // region [arena, arena + arena_bytes) (256-byte aligned pieces), results cannot be
+    // allocated, the length word lives in the region and is read back with a copy and a
+    // stream synchronise, and kernel timing is off.  Nothing is allocated or released.
+    Call(void *stream, void *arena, size_t arena_bytes);
     ~Call();
     Call(const Call &) = delete;
     Call &operator=(const Call &) = delete;
@@ -98,6 +103,10 @@ class Call {
     std::vector<void *> results_;
     bool committed_ = false;
     bool timing_ = false;
+    unsigned char *arena_ = nullptr;  // arena mode when non-null
+    size_t arena_size_ = 0;
+    size_t arena_used_ = 0;
+    int64_t *arena_len_ = nullptr;
     bool timed_ = false;
     float timed_ms_ = 0.0f;  // sum of this call's bracketed intervals
 };

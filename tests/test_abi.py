@@ -50,7 +50,7 @@ def test_python_bindings_cover_every_gpu_entry_point():
     from nacho_amd import _lib
 
     gpu = [n for n in declared_functions() if n.startswith("nacho_gpu_")]
-    bound = set(_lib.ENTRY_POINTS) | set(_lib.ENTRY_POINTS_3)
+    bound = set(_lib.ENTRY_POINTS) | set(_lib.ENTRY_POINTS_3) | set(_lib.ENTRY_POINTS_NOALLOC)
     assert set(gpu) <= bound, set(gpu) - bound
 
 
