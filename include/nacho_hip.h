@@ -208,7 +208,7 @@ int nacho_gpu_csr_add_f32(const nacho_csr *a, const nacho_csr *b, nacho_csr *z,
  *     at least a->dim_j_length + b->dim_j_length (the union's upper bound).  On return
  *     z->dim_j_length and z->nnz hold the result length (0 on failure); the pointers are
  *     left as given.
- *   - Scratch is a static device array of 1 MiB per GPU (held until the process ends),
+ *   - Scratch is a static device array of 8 MiB per GPU (held until the process ends),
  *     enough for a->dim_j_length + b->dim_j_length + dim_i_size <= NACHO_NOALLOC_MAX_ITEMS;
  *     larger inputs fail with NACHO_ERR_SCRATCH_TOO_SMALL before any device work.
  *   - Every call on a GPU shares that GPU's scratch: calls that overlap on one GPU (other

@@ -124,18 +124,18 @@ def adopt(ptr: int | None, count: int, dtype: torch.dtype, device: torch.device,
         return torch.empty(0, dtype=dtype, device=device)
     owner = _OwnedBuffer(ptr, count, dtype, stream)
     tensor = None
-    with torch.cuda.device(device):
-        if _ROUTE in (None, "cai"):
-            try:
-                tensor = torch.as_tensor(owner, device=device)
-                _ROUTE = "cai"
-            except (TypeError, RuntimeError, ValueError):
-                if _ROUTE == "cai":
-                    raise
-                tensor = None
-        if tensor is None:
-            tensor = _adopt_dlpack(owner, device)
-            _ROUTE = "dlpack"
+    # (the caller has made `device` current: gpu_<k> entry points run under it)
+    if _ROUTE in (None, "cai"):
+        try:
+            tensor = torch.as_tensor(owner, device=device)
+            _ROUTE = "cai"
+        except (TypeError, RuntimeError, ValueError):
+            if _ROUTE == "cai":
+                raise
+            tensor = None
+    if tensor is None:
+        tensor = _adopt_dlpack(owner, device)
+        _ROUTE = "dlpack"
     if tensor.data_ptr() != ptr or tensor.numel() != count or tensor.dtype != dtype:
         raise RuntimeError("torch did not adopt the device buffer in place")
     return tensor
@@ -162,6 +162,30 @@ def adoption_route() -> str | None:
 def current_stream(device: torch.device) -> int:
     """The hipStream_t of torch's current stream on `device`, as an integer."""
     return int(torch.cuda.current_stream(device).cuda_stream)
+
+
+class on_device:
+    """Make `device` the current HIP device for the block, switching (and restoring) only
+    when it is not current already: torch.cuda.device() switches unconditionally, which
+    costs tens of microseconds per call."""
+
+    __slots__ = ("index", "prev")
+
+    def __init__(self, device: torch.device):
+        self.index = device.index if device.index is not None else torch.cuda.current_device()
+        self.prev = None
+
+    def __enter__(self):
+        current = torch.cuda.current_device()
+        if current != self.index:
+            self.prev = current
+            torch.cuda.set_device(self.index)
+        return self
+
+    def __exit__(self, *exc):
+        if self.prev is not None:
+            torch.cuda.set_device(self.prev)
+        return False
 
 
 def require_device_tensor(t: torch.Tensor, dtype: torch.dtype, name: str) -> torch.Tensor:

@@ -77,16 +77,19 @@ __device__ __forceinline__ void merge_split(ReadA A, ReadB B, int aS, int aE, in
 }
 
 // One thread per tile boundary t in [0, num_tiles]: split of diagonal min(t*TILE, total).
-// Thread 0 also zeroes the ticket counter that the next kernel's length total uses.
+// Thread 0 also zeroes the ticket counter that the next kernel's length total uses, and the
+// first n_counts threads zero the chunk counts (n_counts <= num_tiles + 1).
 // (Launched in kPartBlock-thread workgroups: the few thousand boundaries then spread over
 // every CU instead of a few dozen.)
 __global__ __launch_bounds__(kPartBlock) void csr_partition_kernel(
     const int *__restrict__ pa, const int *__restrict__ ca, const int *__restrict__ pb,
     const int *__restrict__ cb, int rows, int total, int num_tiles, int *__restrict__ split_r,
-    int *__restrict__ split_a, int *__restrict__ split_b, unsigned long long *__restrict__ done) {
+    int *__restrict__ split_a, int *__restrict__ split_b, unsigned long long *__restrict__ done,
+    unsigned *__restrict__ zero_counts, int n_counts) {
     const int t = blockIdx.x * blockDim.x + threadIdx.x;
     if (t > num_tiles) return;
     if (t == 0) *done = 0ull;  // accumulator of the kernel that totals the length
+    if (t < n_counts) zero_counts[t] = 0u;  // chunk counts the count kernel adds into
     const long long d64 = static_cast<long long>(t) * kTile;
     const int diag = d64 > total ? total : static_cast<int>(d64);
 
@@ -471,6 +474,350 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
     }
 }
 
+// ---- pair count: the union's count pass ----------------------------------------------
+//
+// A union tile's output count is na + nb - pairs, and an equal A/B pair never straddles
+// tiles, so the count pass only has to find the pairs.  In every row of the tile where both
+// operands have entries, each entry of the side with fewer entries (A on a tie) is searched
+// in the other side's range of the row (binary search in LDS).  Rows where one side is empty
+// cost only their offsets; a row heavy in one operand costs the light side's entries times
+// log2 of the heavy side's length.  At C2 (Zipf rows, independent operands) that is 2.4e5
+// searches for 3.4e7 items.
+//
+// Staging reads 16-byte granules: the tile's A range then its B range of coordinates, each
+// cut at its array's 16-byte boundaries (a granule holding one element of the range lies in
+// the same page as that element, so reading all of it never leaves mapped memory; the extra
+// elements are never used), and the row offsets of up to kRowBlock + 1 rows per pass.
+
+// Offset of each array's base address from a 16-byte boundary, in elements (0..3).
+struct Misalign {
+    int ca, cb, pa, pb;
+};
+
+// A 16-byte granule as a native vector (HIP's int4 is a struct over a union, which keeps
+// arrays of it in scratch memory).
+typedef int grain_t __attribute__((ext_vector_type(4)));
+
+constexpr int kGrains = 4;      // coordinate granules per lane: 4096 entries >= tile + padding
+constexpr int kRowGrains = 2;   // row-offset granules per lane per operand: 2048 offsets
+constexpr int kRowBlock = kRowGrains * 4 * kBlock - 4;  // rows per pass (their ends included)
+constexpr int kGrainCap = kGrains * 4 * kBlock;
+
+__device__ __forceinline__ int grain_first(int lo, int mis) { return ((lo + mis) & ~3) - mis; }
+__device__ __forceinline__ int grain_count(int lo, int hi, int mis) {
+    return hi > lo ? (hi - grain_first(lo, mis) + 3) >> 2 : 0;
+}
+
+// Where a tile's coordinates land in LDS: granule q at s[4q .. 4q + 3], A's granules first;
+// A's entry a0 at index offA, B's entry b0 at offB.
+struct GrainLayout {
+    int firstA, nga, firstB, ngb, offA, offB;
+};
+
+__device__ __forceinline__ GrainLayout grain_layout(const TileSplit &sp, int misA, int misB) {
+    GrainLayout g;
+    g.firstA = grain_first(sp.a0, misA);
+    g.nga = grain_count(sp.a0, sp.a1, misA);
+    g.firstB = grain_first(sp.b0, misB);
+    g.ngb = grain_count(sp.b0, sp.b1, misB);
+    g.offA = sp.a0 - g.firstA;
+    g.offB = 4 * g.nga + (sp.b0 - g.firstB);
+    return g;
+}
+
+struct TileGrains {
+    grain_t v[kGrains];
+};
+
+// Loads are issued unconditionally (lanes past the end re-read the last granule) so that a
+// whole tile's loads are in flight at once.
+__device__ __forceinline__ void fetch_grains(TileGrains &tg, const GrainLayout &g,
+                                             const int *__restrict__ xa,
+                                             const int *__restrict__ xb, int tid) {
+    const int n = g.nga + g.ngb;
+    if (n == 0) return;  // uniform
+#pragma unroll
+    for (int j = 0; j < kGrains; ++j) {
+        const int q = min(tid + j * kBlock, n - 1);
+        const int *src = q < g.nga ? xa + g.firstA + 4 * q : xb + g.firstB + 4 * (q - g.nga);
+        tg.v[j] = *reinterpret_cast<const grain_t *>(src);
+    }
+}
+
+__device__ __forceinline__ void store_grains(const TileGrains &tg, const GrainLayout &g,
+                                             int *s, int tid) {
+    const int n = g.nga + g.ngb;
+#pragma unroll
+    for (int j = 0; j < kGrains; ++j) {
+        const int q = tid + j * kBlock;
+        if (q < n) *reinterpret_cast<grain_t *>(s + 4 * q) = tg.v[j];
+    }
+}
+
+// Row offsets of rows [lo, hi) of both operands (at most kRowBlock + 1 rows).
+struct RowGrains {
+    grain_t a[kRowGrains], b[kRowGrains];
+};
+
+__device__ __forceinline__ void fetch_row_grains(RowGrains &rg, const int *__restrict__ pa,
+                                                 const int *__restrict__ pb, int lo, int hi,
+                                                 const Misalign &mis, int tid) {
+    const int fa = grain_first(lo, mis.pa), na = grain_count(lo, hi, mis.pa);
+    const int fb = grain_first(lo, mis.pb), nb = grain_count(lo, hi, mis.pb);
+#pragma unroll
+    for (int j = 0; j < kRowGrains; ++j) {
+        const int qa = min(tid + j * kBlock, na - 1), qb = min(tid + j * kBlock, nb - 1);
+        rg.a[j] = *reinterpret_cast<const grain_t *>(pa + fa + 4 * qa);
+        rg.b[j] = *reinterpret_cast<const grain_t *>(pb + fb + 4 * qb);
+    }
+}
+
+// Tile-local starts of rows [lo, hi): s_ra[k] = max(pa[lo + k] - a0, 0), likewise s_rb.
+__device__ __forceinline__ void store_row_grains(const RowGrains &rg, int lo, int hi,
+                                                 const Misalign &mis, int a0, int b0,
+                                                 unsigned short *s_ra, unsigned short *s_rb,
+                                                 int tid) {
+    const int fa = grain_first(lo, mis.pa), fb = grain_first(lo, mis.pb);
+    const int n = hi - lo;
+#pragma unroll
+    for (int j = 0; j < kRowGrains; ++j) {
+        const int q = tid + j * kBlock;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int ka = fa + 4 * q + e - lo, kb = fb + 4 * q + e - lo;
+            if (ka >= 0 && ka < n) s_ra[ka] = static_cast<unsigned short>(max(rg.a[j][e] - a0, 0));
+            if (kb >= 0 && kb < n) s_rb[kb] = static_cast<unsigned short>(max(rg.b[j][e] - b0, 0));
+        }
+    }
+}
+
+// LDS of the pair count.
+struct PairShared {
+    int crd[kGrainCap];
+    unsigned short ra[kRowBlock + 4], rb[kRowBlock + 4];
+    int mpre[kRowBlock + 1];
+    int wave[kBlock / dev::kWave];
+    unsigned wsum[kBlock / dev::kWave];
+};
+
+// Running totals of a pair-count workgroup.
+struct PairTotals {
+    unsigned found;    // this lane's pairs since the last flush
+    unsigned entries;  // entries of both operands since the last flush (uniform)
+    unsigned total;    // the workgroup's output count (thread 0)
+};
+
+// One tile of the pair count: stage it from registers (tg, rg), refill the registers with
+// tile `t_next`'s loads (split `nsp`, if `has_next`), then count its pairs and, when STARTS,
+// store its lanes' write-kernel starts.
+template <bool STARTS>
+__device__ __forceinline__ void pair_tile(
+    PairShared &sh, int t, int t_last, const TileSplit &sp, const GrainLayout &g,
+    TileGrains &tg, RowGrains &rg, bool has_next, const TileSplit &nsp,
+    const int *__restrict__ pa, const int *__restrict__ ca, const int *__restrict__ pb,
+    const int *__restrict__ cb, const Misalign &mis, int write_chunk,
+    unsigned *__restrict__ chunk_count, uint2 *__restrict__ starts, PairTotals &acc, int tid) {
+    const int na = sp.a1 - sp.a0, nb = sp.b1 - sp.b0, nr = sp.r1 - sp.r0 + 1;
+    const int offA = g.offA, offB = g.offB;
+    store_grains(tg, g, sh.crd, tid);
+    store_row_grains(rg, sp.r0, min(sp.r0 + kRowBlock + 1, sp.r1 + 1), mis, sp.a0, sp.b0, sh.ra,
+                     sh.rb, tid);
+    if (has_next) {  // uniform: tile t_next's loads, in flight during the next two tiles
+        const GrainLayout ng = grain_layout(nsp, mis.ca, mis.cb);
+        fetch_grains(tg, ng, ca, cb, tid);
+        fetch_row_grains(rg, pa, pb, nsp.r0, min(nsp.r0 + kRowBlock + 1, nsp.r1 + 1), mis, tid);
+    }
+    // this lane's first item in the write kernel, relative to the tile's first item
+    const int tile_start = sp.a0 + sp.b0 + sp.r0, tile_end = sp.a1 + sp.b1 + sp.r1;
+    const int g_lo = tid == 0 ? tile_start : t * kTile + tid * kItemsPerLane;
+    const int rel = g_lo - tile_start;
+    bool have_start = g_lo >= tile_end;  // lanes without items keep the tile's start
+    LaneStart start{0u, static_cast<unsigned>(na)};
+    __syncthreads();
+    for (int kb = 0; kb < nr; kb += kRowBlock) {  // one pass unless nr > kRowBlock
+        const int nrb = min(kRowBlock, nr - kb);
+        if (kb > 0) {
+            // Further rows of a tile with more than kRowBlock rows: staged here, with plain
+            // loads (rare: such a tile holds few entries).
+            __syncthreads();
+            const int cnt = min(nrb + 1, nr - kb);
+            for (int k = tid; k < cnt; k += kBlock) {
+                sh.ra[k] = static_cast<unsigned short>(max(pa[sp.r0 + kb + k] - sp.a0, 0));
+                sh.rb[k] = static_cast<unsigned short>(max(pb[sp.r0 + kb + k] - sp.b0, 0));
+            }
+            __syncthreads();
+        }
+        // Per row: searches to do = the smaller side's entries when both sides have some.
+        constexpr int kR = (kRowBlock + kBlock - 1) / kBlock;
+        const int per = (nrb + kBlock - 1) / kBlock;  // rows per lane, contiguous
+        int m[kR];
+        int mine = 0;
+#pragma unroll
+        for (int i = 0; i < kR; ++i) {
+            m[i] = 0;
+            const int k = tid * per + i;
+            if (i < per && k < nrb) {
+                const bool last = kb + k + 1 == nr;
+                const int la = (last ? na : sh.ra[k + 1]) - sh.ra[k];
+                const int lb = (last ? nb : sh.rb[k + 1]) - sh.rb[k];
+                m[i] = (la > 0 && lb > 0) ? min(la, lb) : 0;
+                mine += m[i];
+            }
+        }
+        int work = 0;
+        int run = dev::block_exclusive_sum<kBlock, int, false>(mine, sh.wave, work);
+#pragma unroll
+        for (int i = 0; i < kR; ++i) {
+            const int k = tid * per + i;
+            if (i < per && k < nrb) sh.mpre[k] = run;
+            run += m[i];
+        }
+        __syncthreads();
+        for (int j = tid; j < work; j += kBlock) {
+            int lo = 0, hi = nrb - 1;  // the row: last k with mpre[k] <= j
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (sh.mpre[mid] <= j) {
+                    lo = mid;
+                } else {
+                    hi = mid - 1;
+                }
+            }
+            const int k = lo;
+            const bool last = kb + k + 1 == nr;
+            const int sa = sh.ra[k], ea = last ? na : sh.ra[k + 1];
+            const int sb = sh.rb[k], eb = last ? nb : sh.rb[k + 1];
+            const int nth = j - sh.mpre[k];
+            int x, base, l, h;
+            if (ea - sa <= eb - sb) {
+                x = sh.crd[offA + sa + nth];
+                base = offB;
+                l = sb;
+                h = eb;
+            } else {
+                x = sh.crd[offB + sb + nth];
+                base = offA;
+                l = sa;
+                h = ea;
+            }
+            const int end = h;
+            while (l < h) {  // first position >= x
+                const int mid = (l + h) >> 1;
+                if (sh.crd[base + mid] < x) {
+                    l = mid + 1;
+                } else {
+                    h = mid;
+                }
+            }
+            acc.found += (l < end && sh.crd[base + l] == x) ? 1u : 0u;
+        }
+        // The write kernel's start of this lane, if its first item lies in this pass's rows:
+        // the row (last k whose first item is at or before it), then the merge-path split of
+        // the row's A and B entries before it (ties: A first).
+        const bool last_pass = kb + nrb >= nr;
+        if (STARTS && !have_start && (last_pass || rel < sh.ra[nrb] + sh.rb[nrb] + kb + nrb)) {
+            int lo = 0, hi = nrb - 1;
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (sh.ra[mid] + sh.rb[mid] + kb + mid <= rel) {
+                    lo = mid;
+                } else {
+                    hi = mid - 1;
+                }
+            }
+            const int k = lo;
+            const bool last = kb + k + 1 == nr;
+            const int aS = sh.ra[k], aE = last ? na : sh.ra[k + 1];
+            const int bS = sh.rb[k], bE = last ? nb : sh.rb[k + 1];
+            const int D = rel - (kb + k);  // entries of the tile before the item
+            int slo = max(aS, D - bE), shi = min(aE, D - bS);
+            while (slo < shi) {
+                const int mid = (slo + shi) >> 1;
+                if (sh.crd[offA + mid] <= sh.crd[offB + D - 1 - mid]) {
+                    slo = mid + 1;
+                } else {
+                    shi = mid;
+                }
+            }
+            start = LaneStart{static_cast<unsigned>(kb + k) | (static_cast<unsigned>(slo) << 16),
+                              static_cast<unsigned>(na + D - slo)};
+            have_start = true;
+        }
+    }
+    if (STARTS) starts[static_cast<size_t>(t) * kBlock + tid] = make_uint2(start.k_ia, start.ib);
+    acc.entries += static_cast<unsigned>(na + nb);
+    if (t == t_last || (t + 1) % write_chunk == 0) {  // uniform: end of a write chunk
+        const unsigned pairs = block_sum<kBlock / dev::kWave>(acc.found, sh.wsum);
+        if (tid == 0) {
+            const unsigned c = acc.entries - pairs;
+            atomicAdd(&chunk_count[t / write_chunk], c);
+            acc.total += c;
+        }
+        acc.found = 0;
+        acc.entries = 0;
+    }
+    __syncthreads();  // every lane is done with this tile's LDS
+}
+
+// Output counts of a union level (na + nb - pairs per tile), added into
+// chunk_count[tile / write_chunk] (zeroed by the partition kernel): the counts of the write
+// kernel's chunks, whose grid is chosen independently of this kernel's (`chunk` tiles per
+// workgroup here, two tiles in flight).  Their sum, the result length, goes to `length_out`
+// from the last workgroup.  When STARTS, every lane's walk start in the write kernel (row,
+// A and B heads) is stored to starts[tile * kBlock + lane], found here by a search over the
+// staged rows and a merge-path split inside the row.
+template <bool STARTS>
+__global__ __launch_bounds__(kBlock) void csr_pair_count_kernel(
+    const int *__restrict__ pa, const int *__restrict__ ca, const int *__restrict__ pb,
+    const int *__restrict__ cb, Misalign mis, int num_tiles, int chunk, int write_chunk,
+    const int *__restrict__ split_r, const int *__restrict__ split_a,
+    const int *__restrict__ split_b, unsigned *__restrict__ chunk_count,
+    unsigned long long *__restrict__ done, int64_t *__restrict__ length_out,
+    uint2 *__restrict__ starts) {
+    __shared__ PairShared sh;
+    __shared__ int s_split[3 * (kMaxChunk + 1)];
+
+    const int tid = threadIdx.x;
+    int t0, t1;
+    chunk_range(num_tiles, chunk, t0, t1);
+    if (t0 >= t1) {
+        if (tid == 0) dev::add_to_total(0u, done, length_out);
+        return;
+    }
+    stage_splits(s_split, split_r, split_a, split_b, t0, t1);
+    __syncthreads();
+    // Two tiles in flight: tiles t0 + 2i go through (tg0, rg0), t0 + 2i + 1 through (tg1, rg1).
+    TileGrains tg0, tg1;
+    RowGrains rg0, rg1;
+    TileSplit sp0 = lds_split(s_split, 0);
+    TileSplit sp1 = lds_split(s_split, t0 + 1 < t1 ? 1 : 0);
+    GrainLayout g0 = grain_layout(sp0, mis.ca, mis.cb);
+    GrainLayout g1 = grain_layout(sp1, mis.ca, mis.cb);
+    fetch_grains(tg0, g0, ca, cb, tid);
+    fetch_row_grains(rg0, pa, pb, sp0.r0, min(sp0.r0 + kRowBlock + 1, sp0.r1 + 1), mis, tid);
+    if (t0 + 1 < t1) {
+        fetch_grains(tg1, g1, ca, cb, tid);
+        fetch_row_grains(rg1, pa, pb, sp1.r0, min(sp1.r0 + kRowBlock + 1, sp1.r1 + 1), mis, tid);
+    }
+    PairTotals acc{0u, 0u, 0u};
+    for (int t = t0; t < t1; t += 2) {
+        const bool n0 = t + 2 < t1, n1 = t + 3 < t1;
+        const TileSplit nsp0 = lds_split(s_split, n0 ? t + 2 - t0 : 0);
+        pair_tile<STARTS>(sh, t, t1 - 1, sp0, g0, tg0, rg0, n0, nsp0, pa, ca, pb, cb, mis,
+                          write_chunk, chunk_count, starts, acc, tid);
+        sp0 = nsp0;
+        g0 = grain_layout(sp0, mis.ca, mis.cb);
+        if (t + 1 < t1) {
+            const TileSplit nsp1 = lds_split(s_split, n1 ? t + 3 - t0 : 0);
+            pair_tile<STARTS>(sh, t + 1, t1 - 1, sp1, g1, tg1, rg1, n1, nsp1, pa, ca, pb, cb,
+                              mis, write_chunk, chunk_count, starts, acc, tid);
+            sp1 = nsp1;
+            g1 = grain_layout(sp1, mis.ca, mis.cb);
+        }
+    }
+    if (tid == 0) dev::add_to_total(acc.total, done, length_out);
+}
+
 // Writes the result: crd/val (VALUES) or crd plus child pointers (CHILD: for output o,
 // child_a[o] = next_a[a] and child_b[o] = next_b[b] at the A/B positions a, b reached before
 // o, so [child[o], child[o+1]) is the operand's child range under o, empty when absent; a
@@ -686,6 +1033,15 @@ __global__ __launch_bounds__(kBlock) void csr_compact_kernel(
 
 // ---- host ------------------------------------------------------------------------------
 
+// Offset of an int32 array's base from a 16-byte boundary, in elements; int32 arrays must
+// be 4-byte aligned.  A null (empty) array counts as aligned.
+int misalign(const void *p, int *out) {
+    const uintptr_t v = reinterpret_cast<uintptr_t>(p);
+    if (v & 3u) return NACHO_ERR_INVALID_ARGUMENT;
+    *out = static_cast<int>((v & 15u) >> 2);
+    return NACHO_OK;
+}
+
 int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
                 const LevelOperand &A, const LevelOperand &B, const LevelResult &Z,
                 long long *out_len, const char *kernel_name, bool keep_starts) {
@@ -700,10 +1056,11 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
 
     // Grid: as many workgroups as stay resident, each owning a contiguous chunk of tiles.
     int resident = 0;
-    const void *probe = values ? reinterpret_cast<const void *>(
-                                     csr_write_kernel<Op::Union, kItemsPerLane, true, false, false>)
-                               : reinterpret_cast<const void *>(
-                                     csr_write_kernel<Op::Union, kItemsPerLane, false, true, false>);
+    const void *probe =
+        values ? reinterpret_cast<const void *>(
+                     csr_write_kernel<Op::Union, kItemsPerLane, true, false, false>)
+               : reinterpret_cast<const void *>(
+                     csr_write_kernel<Op::Union, kItemsPerLane, false, true, false>);
     NACHO_TRY(resident_grid(probe, kBlock, &resident));
     int chunk = (num_tiles + resident - 1) / resident;
     if (chunk > kMaxChunk) chunk = kMaxChunk;  // more workgroups than resident: still correct
@@ -736,7 +1093,7 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
         NACHO_TRY(call.timer_start(kernel_name));  // the whole device pipeline of this level
         csr_partition_kernel<<<ceil_div(static_cast<size_t>(num_tiles) + 1, kPartBlock), kPartBlock, 0, s>>>(
             A.pos, A.crd, B.pos, B.crd, rows, static_cast<int>(total), num_tiles, split_r,
-            split_a, split_b, done);
+            split_a, split_b, done, nullptr, 0);
         NACHO_TRY_HIP(hipGetLastError());
         csr_write_kernel<Op::Intersect, kItemsPerLane, true, false, true>
             <<<grid, kBlock, 0, s>>>(A.pos, A.crd, A.val, B.pos, B.crd, B.val, A.len, B.len,
@@ -756,39 +1113,59 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
         *out_len = len;
         return NACHO_OK;
     }
-    uint2 *starts = nullptr;  // every lane's walk start, from the count kernel to the write
+    // Union: the pair count gives the write chunks' output counts (and the length) and, when
+    // keep_starts, every lane's walk start; without it the write pass searches for them.
+    Misalign mis{};
+    NACHO_TRY(misalign(A.crd, &mis.ca));
+    NACHO_TRY(misalign(B.crd, &mis.cb));
+    NACHO_TRY(misalign(A.pos, &mis.pa));
+    NACHO_TRY(misalign(B.pos, &mis.pb));
+    uint2 *starts = nullptr;
     if (keep_starts) NACHO_TRY(call.scratch_n(static_cast<size_t>(num_tiles) * kBlock, &starts));
+    // The count kernel's own grid: as many workgroups as it keeps resident (it holds less
+    // state than the write kernel, and needs the extra loads in flight).
+    int count_resident = 0;
+    const void *count_kernel =
+        keep_starts ? reinterpret_cast<const void *>(csr_pair_count_kernel<true>)
+                    : reinterpret_cast<const void *>(csr_pair_count_kernel<false>);
+    NACHO_TRY(resident_grid(count_kernel, kBlock, &count_resident));
+    int count_chunk = (num_tiles + count_resident - 1) / count_resident;
+    if (count_chunk > kMaxChunk) count_chunk = kMaxChunk;
+    const int count_grid = (num_tiles + count_chunk - 1) / count_chunk;
     NACHO_TRY(call.timer_start(kernel_name));  // the whole device pipeline of this level
     csr_partition_kernel<<<ceil_div(static_cast<size_t>(num_tiles) + 1, kPartBlock), kPartBlock, 0, s>>>(
         A.pos, A.crd, B.pos, B.crd, rows, static_cast<int>(total), num_tiles, split_r, split_a,
-        split_b, done);
+        split_b, done, counts, grid);
     NACHO_TRY_HIP(hipGetLastError());
-    csr_count_kernel<Op::Union, kItemsPerLane><<<grid, kBlock, 0, s>>>(
-        A.pos, A.crd, B.pos, B.crd, num_tiles, chunk, split_r, split_a, split_b, counts, done,
-        length_out, starts);
+    if (keep_starts) {
+        csr_pair_count_kernel<true><<<count_grid, kBlock, 0, s>>>(
+            A.pos, A.crd, B.pos, B.crd, mis, num_tiles, count_chunk, chunk, split_r, split_a,
+            split_b, counts, done, length_out, starts);
+    } else {
+        csr_pair_count_kernel<false><<<count_grid, kBlock, 0, s>>>(
+            A.pos, A.crd, B.pos, B.crd, mis, num_tiles, count_chunk, chunk, split_r, split_a,
+            split_b, counts, done, length_out, nullptr);
+    }
     NACHO_TRY_HIP(hipGetLastError());
     NACHO_TRY(call.mark_length());
-#define NACHO_WRITE_LAUNCH(OPV, VAL, CHD)                                                        \
-    csr_write_kernel<OPV, kItemsPerLane, VAL, CHD, false><<<grid, kBlock, 0, s>>>(               \
+#define NACHO_WRITE_LAUNCH(OPV, VAL, CHD, SRCH)                                                  \
+    csr_write_kernel<OPV, kItemsPerLane, VAL, CHD, false, SRCH><<<grid, kBlock, 0, s>>>(         \
         A.pos, A.crd, A.val, B.pos, B.crd, B.val, A.len, B.len, num_tiles, chunk, split_r,      \
         split_a, split_b, counts, rows, Z.pos, Z.crd, Z.val, A.next, B.next, Z.child_a,         \
         Z.child_b, length, 0, nullptr, nullptr, nullptr, nullptr, starts)
-    if (values && !keep_starts) {
+    if (values) {
         if (child) return NACHO_ERR_INVALID_ARGUMENT;
-        csr_write_kernel<Op::Union, kItemsPerLane, true, false, false, true>
-            <<<grid, kBlock, 0, s>>>(A.pos, A.crd, A.val, B.pos, B.crd, B.val, A.len, B.len,
-                                     num_tiles, chunk, split_r, split_a, split_b, counts, rows,
-                                     Z.pos, Z.crd, Z.val, nullptr, nullptr, nullptr, nullptr,
-                                     length, 0, nullptr, nullptr, nullptr, nullptr, nullptr);
+        if (keep_starts) {
+            NACHO_WRITE_LAUNCH(Op::Union, true, false, false);
+        } else {
+            NACHO_WRITE_LAUNCH(Op::Union, true, false, true);
+        }
     } else if (!keep_starts) {
-        return NACHO_ERR_INVALID_ARGUMENT;  // only the value level runs without stored starts
-    } else if (values) {
-        if (child) return NACHO_ERR_INVALID_ARGUMENT;
-        NACHO_WRITE_LAUNCH(Op::Union, true, false);
+        return NACHO_ERR_INVALID_ARGUMENT;  // only value levels run without stored starts
     } else if (child) {
-        NACHO_WRITE_LAUNCH(Op::Union, false, true);
+        NACHO_WRITE_LAUNCH(Op::Union, false, true, false);
     } else {
-        NACHO_WRITE_LAUNCH(Op::Union, false, false);
+        NACHO_WRITE_LAUNCH(Op::Union, false, false, false);
     }
 #undef NACHO_WRITE_LAUNCH
     NACHO_TRY_HIP(hipGetLastError());
@@ -868,7 +1245,7 @@ int csr_binary(bool intersect, const nacho_csr *a, const nacho_csr *b, nacho_csr
 // held for the life of the process.  Host code never passes `scratch` itself to a kernel
 // (in host code the name is a stand-in, not a device address): it looks up each device's
 // address once with hipGetSymbolAddress and uses that.
-constexpr size_t kNoAllocScratchBytes = size_t{1} << 20;
+constexpr size_t kNoAllocScratchBytes = size_t{8} << 20;
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
 constexpr int kMaxDevices = 64;

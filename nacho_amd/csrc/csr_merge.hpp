@@ -32,15 +32,16 @@ struct LevelResult {
 // Merge A and B row by row: union (or intersection) of each row's coordinates, with values
 // (a+b / a*b / copies) when `values`, or with child pointers when `child`.  Writes Z.pos for
 // every row and returns the result length in *out_len.  The call's kernel timer (if enabled)
-// brackets all of the level's kernels under `kernel_name`.  Without `keep_starts` (value
-// unions only) the count pass stores no lane starts and the write pass searches for them,
-// which keeps the scratch at a few bytes per tile.
+// brackets all of the level's kernels under `kernel_name`.  A union level stores every
+// lane's walk start for its write pass (8 bytes per lane and tile) unless `keep_starts` is
+// false (value levels only): the write pass then searches for them, and scratch stays at a
+// few bytes per tile.
 int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
                 const LevelOperand &A, const LevelOperand &B, const LevelResult &Z,
                 long long *out_len, const char *kernel_name, bool keep_starts = true);
 
-// Bytes of scratch merge_level takes from an arena Call without lane starts, for a level of
-// `items` merge items (entries of both operands plus rows).
+// Bytes of scratch merge_level takes from an arena Call for a union level of `items` merge
+// items (entries of both operands plus rows) without lane starts.
 size_t merge_level_arena_bytes(long long items);
 
 }  // namespace csr

@@ -17,16 +17,47 @@ constexpr int kWave = 64;
 
 __device__ __forceinline__ int lane() { return static_cast<int>(__lane_id()); }
 
-// Inclusive prefix sum over the 64 lanes of a wavefront.
+// Inclusive prefix sum of a 32-bit integer over the 64 lanes, on DPP: four row shifts
+// (1, 2, 4, 8) scan each row of 16 lanes, then row broadcasts of lane 15 into rows 1 and 3
+// and of lane 31 into rows 2 and 3 carry the row totals.  Lanes whose DPP source lies
+// outside their row keep `old` = 0 (bound_ctrl off, so such lanes are not written).  Every
+// lane must be active.
+__device__ __forceinline__ int wave_inclusive_sum_dpp(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31
+    return v;
+}
+
+// The same for a running maximum of values >= 0 (0 is the identity).
+__device__ __forceinline__ int wave_inclusive_max_dpp(int v) {
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false));
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false));
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false));
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false));
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false));
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false));
+    return v;
+}
+
+// Inclusive prefix sum over the 64 lanes of a wavefront (DPP for 32-bit integers, lane
+// shuffles otherwise).
 template <typename T>
 __device__ __forceinline__ T wave_inclusive_sum(T v) {
-    const int l = lane();
+    if constexpr (sizeof(T) == 4 && !__is_same(T, float)) {
+        return static_cast<T>(wave_inclusive_sum_dpp(static_cast<int>(v)));
+    } else {
+        const int l = lane();
 #pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-        T n = __shfl_up(v, off, kWave);
-        if (l >= off) v += n;
+        for (int off = 1; off < kWave; off <<= 1) {
+            T n = __shfl_up(v, off, kWave);
+            if (l >= off) v += n;
+        }
+        return v;
     }
-    return v;
 }
 
 // Sum over the 64 lanes, result in every lane.
@@ -83,12 +114,7 @@ template <bool SYNC_END = true>
 __device__ __forceinline__ int block_exclusive_max(int v, int *s_wave) {
     const int l = lane();
     const int w = threadIdx.x / kWave;
-    int incl = v;
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-        const int n = __shfl_up(incl, o, kWave);
-        if (l >= o) incl = max(incl, n);
-    }
+    const int incl = wave_inclusive_max_dpp(v);
     if (l == kWave - 1) s_wave[w] = incl;
     int excl = __shfl_up(incl, 1, kWave);
     if (l == 0) excl = 0;

@@ -20,15 +20,16 @@ namespace {
 // stream-ordered pool) costs tens of microseconds each.  Blocks are binned by size class
 // (powers of two split into 4 sub-classes, minimum 512 B).
 //
-// Ordering.  A block freed on stream S is reused at once by a later allocation on S (stream
-// order makes that safe).  A release records one event on S (shared by every block released
-// in the same batch), and an event on each other stream that nacho_record_stream named for
-// the block; an allocation that takes the block makes its own stream wait for those events
-// (hipStreamWaitEvent, outside the cache lock) unless they all sit on its own stream.  The
-// host never blocks on a stream for reuse.  When the driver runs out of memory the cache is
+// Ordering.  A block freed on stream S is reused only by later allocations on S, which
+// stream order puts after every use of the block on S; an allocation on another stream
+// takes a fresh block.  Work on other streams that used the block is announced with
+// nacho_record_stream: the release then records an event on each such stream, and the
+// allocation that takes the block makes S wait for those events (hipStreamWaitEvent,
+// outside the cache lock).  The host never blocks on a stream for reuse, and the common case
+// (one stream) records no event at all.  When the driver runs out of memory the cache is
 // emptied (after a device synchronise) and the allocation retried.
 
-// A pooled event shared by the blocks of one release batch.
+// A pooled event, possibly shared by several blocks.
 struct SharedEvent {
     hipEvent_t event;
     hipStream_t stream;  // where it was recorded
@@ -39,9 +40,9 @@ struct Block {
     void *ptr;
     size_t size;  // rounded size class
     int device;
-    hipStream_t stream;                  // stream of the last allocation or release
+    hipStream_t stream;                  // the stream that allocated / released it
     std::vector<hipStream_t> used_on;    // other streams named by nacho_record_stream
-    std::vector<SharedEvent *> pending;  // events to wait for before reuse (free blocks)
+    std::vector<SharedEvent *> pending;  // their events, waited for at reuse (free blocks)
 };
 
 std::mutex g_cache_mutex;
@@ -108,8 +109,8 @@ void release_cached_blocks_locked() {
 }
 
 // Make `stream` wait for the events a reused block carries (outside the cache lock), then
-// return the events.  An event recorded on `stream` itself needs no wait.  If the runtime
-// refuses a device-side wait, the host waits for the event instead.
+// return the events.  If the runtime refuses a device-side wait, the host waits for the
+// event instead.
 void wait_pending(std::vector<SharedEvent *> &pending, hipStream_t stream) {
     for (SharedEvent *e : pending) {
         if (e->stream == stream) continue;
@@ -136,22 +137,18 @@ void *default_allocate(size_t bytes, hipStream_t stream) {
     {
         std::lock_guard<std::mutex> lock(g_cache_mutex);
         auto it = g_free.find({device, size});
-        if (it != g_free.end() && !it->second.empty()) {
+        if (it != g_free.end()) {
             std::vector<Block> &bin = it->second;
-            size_t pick = bin.size() - 1;
-            for (size_t i = bin.size(); i-- > 0;) {
-                if (bin[i].stream == stream) {
-                    pick = i;
-                    break;
-                }
+            for (size_t i = bin.size(); i-- > 0;) {  // most recently freed first
+                if (bin[i].stream != stream) continue;
+                Block b = std::move(bin[i]);
+                bin.erase(bin.begin() + static_cast<std::ptrdiff_t>(i));
+                pending.swap(b.pending);
+                b.used_on.clear();
+                reused = b.ptr;
+                g_live[b.ptr] = std::move(b);
+                break;
             }
-            Block b = std::move(bin[pick]);
-            bin.erase(bin.begin() + static_cast<std::ptrdiff_t>(pick));
-            pending.swap(b.pending);
-            b.stream = stream;
-            b.used_on.clear();
-            reused = b.ptr;
-            g_live[b.ptr] = std::move(b);
         }
     }
     if (reused) {
@@ -174,25 +171,21 @@ void *default_allocate(size_t bytes, hipStream_t stream) {
     return ptr;
 }
 
-// Return blocks to the cache, stream-ordered on `stream`: one event recorded on `stream` is
-// shared by the whole batch, plus one per other stream named by nacho_record_stream.  If an
-// event cannot be recorded, the host synchronises that stream instead (rare fallback).
+// Return blocks to the cache of `stream` (the stream their last use is ordered on; a
+// block released on another stream than the one that allocated it moves to that stream's
+// cache).  For every other stream named by nacho_record_stream an event is recorded now; if
+// one cannot be recorded, the host synchronises that stream instead (rare fallback).
 // Pointers the cache does not own are ignored.
 void release_batch(void *const *ptrs, size_t n, hipStream_t stream) {
     std::lock_guard<std::mutex> lock(g_cache_mutex);
-    int owned = 0;
-    for (size_t i = 0; i < n; ++i) owned += (ptrs[i] && g_live.count(ptrs[i])) ? 1 : 0;
-    if (owned == 0) return;
-    SharedEvent *freed = record_shared_locked(stream, owned);
-    if (!freed) (void)hipStreamSynchronize(stream);
     for (size_t i = 0; i < n; ++i) {
         if (!ptrs[i]) continue;
         auto it = g_live.find(ptrs[i]);
         if (it == g_live.end()) continue;
         Block b = std::move(it->second);
         g_live.erase(it);
+        if (b.stream != stream) b.used_on.push_back(b.stream);
         b.stream = stream;
-        if (freed) b.pending.push_back(freed);
         for (hipStream_t u : b.used_on) {
             if (u == stream) continue;
             SharedEvent *e = record_shared_locked(u, 1);
@@ -261,7 +254,7 @@ Call::~Call() {
     if (alloc_) {
         for (void *p : scratch_) release(p);
     } else if (!scratch_.empty()) {
-        release_batch(scratch_.data(), scratch_.size(), stream_);  // one event for the batch
+        release_batch(scratch_.data(), scratch_.size(), stream_);
     }
 }
 

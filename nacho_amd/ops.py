@@ -35,7 +35,7 @@ def _same_device(*tensors):
 # ---- descriptor conversion -----------------------------------------------------------
 
 def _csr_desc(t: CSR_gpu) -> _lib.CsrDesc:
-    rows, cols = (int(x) for x in t.shape)
+    rows, cols = t._dims
     if t.dim_j_offsets.numel() != rows + 1:
         raise ValueError(f"CSR_gpu: dim_j_offsets has {t.dim_j_offsets.numel()} entries, "
                          f"expected rows + 1 = {rows + 1}")
@@ -46,7 +46,7 @@ def _csr_desc(t: CSR_gpu) -> _lib.CsrDesc:
 
 
 def _coo_desc(t: COO_gpu) -> _lib.CooDesc:
-    rows, cols = (int(x) for x in t.shape)
+    rows, cols = t._dims
     n = t.values.numel()
     if t.dim_i_indices.numel() != n or t.dim_j_indices.numel() != n:
         raise ValueError("COO_gpu: coordinate and value arrays differ in length")
@@ -55,7 +55,7 @@ def _coo_desc(t: COO_gpu) -> _lib.CooDesc:
 
 
 def _coo3_desc(t: COO3_gpu) -> _lib.Coo3Desc:
-    si, sj, sk = (int(x) for x in t.shape)
+    si, sj, sk = t._dims
     n = t.values.numel()
     if any(x.numel() != n for x in (t.dim_i_indices, t.dim_j_indices, t.dim_k_indices)):
         raise ValueError("COO3_gpu: coordinate and value arrays differ in length")
@@ -64,7 +64,7 @@ def _coo3_desc(t: COO3_gpu) -> _lib.Coo3Desc:
 
 
 def _dcsr_desc(t: DCSR_gpu) -> _lib.DcsrDesc:
-    rows, cols = (int(x) for x in t.shape)
+    rows, cols = t._dims
     ni, nj = t.dim_i_indices.numel(), t.dim_j_indices.numel()
     if t.dim_j_offsets.numel() != ni + 1:
         raise ValueError(f"DCSR_gpu: dim_j_offsets has {t.dim_j_offsets.numel()} entries, "
@@ -76,7 +76,7 @@ def _dcsr_desc(t: DCSR_gpu) -> _lib.DcsrDesc:
 
 
 def _csf3_desc(t: CSF3_gpu) -> _lib.Csf3Desc:
-    si, sj, sk = (int(x) for x in t.shape)
+    si, sj, sk = t._dims
     ni, nj, nk = t.dim_i_indices.numel(), t.dim_j_indices.numel(), t.dim_k_indices.numel()
     if t.dim_j_offsets.numel() != ni + 1 or t.dim_k_offsets.numel() != nj + 1:
         raise ValueError("CSF3_gpu: offsets arrays must have parent length + 1 entries")
@@ -162,7 +162,7 @@ def validate_csr(t: CSR_gpu) -> None:
     if not isinstance(t, CSR_gpu):
         raise TypeError(f"validate_csr: expected CSR_gpu, got {type(t).__name__}")
     desc = _csr_desc(t)
-    with torch.cuda.device(t.device):
+    with _device.on_device(t.device):
         rc = _lib.load().nacho_validate_csr(ctypes.byref(desc),
                                             ctypes.c_void_p(_device.current_stream(t.device)))
     if rc == -4:  # NACHO_ERR_MALFORMED_INPUT
@@ -193,7 +193,7 @@ def _call(entry, a, b, cls, desc_fn, result_desc, adopt_fn, num_blocks, threads_
         raise RuntimeError(f"{entry} is not exported by {_lib.LIBRARY_PATH.name}")
     da, db = desc_fn(a), desc_fn(b)
     z = result_desc()
-    with torch.cuda.device(device):
+    with _device.on_device(device):
         stream = _device.current_stream(device)
         rc = fn(ctypes.byref(da), ctypes.byref(db), ctypes.byref(z), int(num_blocks),
                 int(threads_per_block), ctypes.c_void_p(stream), None)
@@ -220,7 +220,7 @@ def _call3(entry, a, b, c, num_blocks, threads_per_block) -> CSR_gpu:
         raise RuntimeError(f"{entry} is not exported by {_lib.LIBRARY_PATH.name}")
     da, db, dc = _csr_desc(a), _csr_desc(b), _csr_desc(c)
     z = _lib.CsrDesc()
-    with torch.cuda.device(device):
+    with _device.on_device(device):
         stream = _device.current_stream(device)
         rc = fn(ctypes.byref(da), ctypes.byref(db), ctypes.byref(dc), ctypes.byref(z),
                 int(num_blocks), int(threads_per_block), ctypes.c_void_p(stream), None)

@@ -55,6 +55,7 @@ class _GpuTensor:
                 raise ValueError(f"{cls}: buffers on different devices ({device}, {buf.device})")
             object.__setattr__(self, "_" + name, buf)
         object.__setattr__(self, "_shape", _shape(shape, self._rank, cls))
+        object.__setattr__(self, "_dims", tuple(int(x) for x in self._shape.tolist()))
         object.__setattr__(self, "_device", device)
 
     @classmethod
@@ -63,12 +64,15 @@ class _GpuTensor:
         obj = object.__new__(cls)
         for (name, _), buf in zip(cls._fields, buffers):
             object.__setattr__(obj, "_" + name, buf)
-        object.__setattr__(obj, "_shape", torch.tensor(shape_list, dtype=_I32))
+        object.__setattr__(obj, "_shape", None)  # built on first access
+        object.__setattr__(obj, "_dims", tuple(int(x) for x in shape_list))
         object.__setattr__(obj, "_device", device)
         return obj
 
     @property
     def shape(self) -> torch.Tensor:
+        if self._shape is None:
+            object.__setattr__(self, "_shape", torch.tensor(self._dims, dtype=_I32))
         return self._shape
 
     @property
@@ -94,7 +98,7 @@ class _GpuTensor:
 
     def __repr__(self):
         parts = ", ".join(f"{n}[{getattr(self, n).numel()}]" for n, _ in self._fields)
-        return f"{type(self).__name__}({parts}, shape={self._shape.tolist()})"
+        return f"{type(self).__name__}({parts}, shape={list(self._dims)})"
 
 
 def _field(name):
