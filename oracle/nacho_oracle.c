@@ -803,11 +803,15 @@ typedef struct {
     int32_t *cz;
     float *vz;
     int phase;
-    int next_row; /* dynamic schedule: rows are claimed in chunks of SP_CHUNK */
-    int failed;
+    /* dynamic schedule: rows are claimed SP_CHUNK at a time; on a cache line of its own */
+    _Alignas(64) int next_row;
+    _Alignas(64) int failed;
 } sp_job;
 
-#define SP_CHUNK 16
+/* One row per claim: on power-law inputs the heaviest rows sit next to each other (R-MAT
+ * puts them at the lowest indices), and a chunk of several would hand them all to one
+ * thread. */
+#define SP_CHUNK 1
 
 /* Per-thread dense accumulator over k (an SPA): the row's distinct columns are the keys of
  * the expanded products; emitting them in ascending k order is the sort + compress. */
@@ -852,21 +856,28 @@ static void sort_keys(int32_t *keys, int32_t *tmp, int n, int cols) {
  * float64), then emit the distinct columns in ascending order (phase 1) or count them
  * (phase 0). */
 static void sp_row(sp_job *J, spa *s, int32_t *tmp, int r) {
+    /* the job's fields are read once: the shared row counter sits near them, and other
+     * threads' claims would otherwise invalidate the line under this loop */
+    const int32_t *const pb = J->pb, *const cb = J->cb;
+    const float *const vb = J->vb;
+    const int phase = J->phase;
+    int32_t *const mark = s->mark, *const keys = s->keys;
+    double *const acc = s->acc;
     int nkeys = 0;
     for (int p = J->pa[r]; p < J->pa[r + 1]; ++p) {
         const int j = J->ca[p];
         const float a = J->va[p];
-        for (int q = J->pb[j]; q < J->pb[j + 1]; ++q) {
-            const int k = J->cb[q];
-            if (s->mark[k] != r + 1) {
-                s->mark[k] = r + 1;
-                s->acc[k] = 0.0;
-                s->keys[nkeys++] = k;
+        for (int q = pb[j]; q < pb[j + 1]; ++q) {
+            const int k = cb[q];
+            if (mark[k] != r + 1) {
+                mark[k] = r + 1;
+                acc[k] = 0.0;
+                keys[nkeys++] = k;
             }
-            if (J->phase == 1) s->acc[k] += (double)(a * J->vb[q]); /* f32 product */
+            if (phase == 1) acc[k] += (double)(a * vb[q]); /* f32 product */
         }
     }
-    if (J->phase == 0) {
+    if (phase == 0) {
         J->row_nnz[r] = nkeys;
         return;
     }
@@ -990,8 +1001,8 @@ typedef struct {
     int64_t *pz;
     int32_t *cz;
     float *vz;
-    int next;
-    int failed;
+    _Alignas(64) int next; /* row claim counter, on a cache line of its own */
+    _Alignas(64) int failed;
 } ms_job;
 
 static void ms_row(ms_job *J, int32_t *mark, double *acc, char *hit, int r) {
@@ -1001,14 +1012,16 @@ static void ms_row(ms_job *J, int32_t *mark, double *acc, char *hit, int r) {
         acc[q - c0] = 0.0;
         hit[q - c0] = 0;
     }
+    const int32_t *const pb = J->pb, *const cb = J->cb;
+    const float *const vb = J->vb, *const vc = J->vc;
     for (int p = J->pa[r]; p < J->pa[r + 1]; ++p) {
         const int j = J->ca[p];
         const float a = J->va[p];
-        for (int q = J->pb[j]; q < J->pb[j + 1]; ++q) {
-            const int m = mark[J->cb[q]];
+        for (int q = pb[j]; q < pb[j + 1]; ++q) {
+            const int m = mark[cb[q]];
             if (m) {
-                const float ab = a * J->vb[q];
-                acc[m - 1] += (double)(ab * J->vc[c0 + m - 1]);
+                const float ab = a * vb[q];
+                acc[m - 1] += (double)(ab * vc[c0 + m - 1]);
                 hit[m - 1] = 1;
             }
         }

@@ -5,8 +5,11 @@ oracle (the GPU sums float32 products in float64 and rounds once, so it sits far
 Cases cover the reference smoke shapes (tests/smoke.py:213-218), the tile geometry (rows
 sharing tiles, rows of exactly one tile, rows needing several merge levels, runs of equal
 columns crossing tiles), wide column ranges (64-bit sort keys), empty operands and the full
-R-MAT scale-20 square, checked by a row sample and a size-independent checksum.
+R-MAT scale-20 square, checked row by row against the oracle and by a size-independent
+checksum.
 """
+
+import os
 
 import numpy as np
 import pytest
@@ -226,21 +229,40 @@ def test_dense_windows_and_wide_keys(gpu):
     run_and_check(gpu, 3, inner, cols, a, b, "dense windows")
 
 
-def _row_sample(pos, crd, val, rows):
-    """Rows `rows` of a CSR as a new CSR (same column space)."""
-    lens = (pos[rows + 1] - pos[rows]).astype(np.int64)
-    sp = np.zeros(len(rows) + 1, np.int64)
-    sp[1:] = np.cumsum(lens)
-    idx = np.concatenate([np.arange(pos[r], pos[r + 1]) for r in rows]) if sp[-1] else \
-        np.zeros(0, np.int64)
-    return sp.astype(np.int32), crd[idx], val[idx]
+def _oracle_threads():
+    return max(1, min(len(os.sched_getaffinity(0)), 16))
+
+
+def _row_blocks(zpos, max_rows, max_entries):
+    """Cut [0, rows) into consecutive row ranges of at most `max_rows` rows and, where a
+    single row allows it, at most `max_entries` result entries (by the offsets `zpos`)."""
+    rows = len(zpos) - 1
+    r0 = 0
+    while r0 < rows:
+        limit = min(rows, r0 + max_rows)
+        r1 = int(np.searchsorted(zpos, zpos[r0] + max_entries, side="right")) - 1
+        r1 = max(r0 + 1, min(r1, limit))
+        yield r0, r1
+        r0 = r1
+
+
+def _first_bad(got_c, want_c, got_v, want_v):
+    """Index of the first entry whose column differs or whose value is out of tolerance
+    (rel 1e-5 / abs 1e-6), or -1.  Device tensors of equal length."""
+    bad = got_c != want_c
+    bad |= (got_v - want_v).abs() > ATOL + RTOL * want_v.abs()
+    bad |= got_v.isnan() != want_v.isnan()
+    if not bool(bad.any().item()):
+        return -1
+    return int(torch.argmax(bad.to(torch.uint8)).item())
 
 
 def test_c4_full_size(gpu):
-    """R-MAT scale 20 squared: 6.0e9 products, 3.6e9 results (int64 offsets).  Checked by the
-    row-sum identity sum_ik C_ik = sum_j colsum(A)_j rowsum(A)_j, exact rows against the
-    oracle on a row sample (including the row with the most products), and the int32 entry
-    point refusing the result."""
+    """R-MAT scale 20 squared: 6.0e9 products, 3.6e9 results (int64 offsets).  Every row is
+    compared with the oracle: in row blocks (at most 2^16 rows or 2^28 entries each) the
+    oracle runs on the same rows of A, its offsets are compared on the host and its columns
+    and values, uploaded, on the device; nnz(C) must equal the oracle's total.  The row-sum identity sum_ik C_ik = sum_j colsum(A)_j rowsum(A)_j checks
+    the values once more as a whole, and the int32 entry point must refuse the result."""
     import nacho_amd
     from nacho_amd import synth
 
@@ -254,7 +276,8 @@ def test_c4_full_size(gpu):
     nnz = int(zpos[-1].item())
     assert nnz == z.values.numel() == z.dim_j_indices.numel()
     assert nnz > 2**31  # the reason for 64-bit offsets
-    assert bool((zpos[1:] >= zpos[:-1]).all().item()) and int(zpos[0].item()) == 0
+    zpos_h = zpos.cpu().numpy()
+    assert zpos_h[0] == 0 and bool(np.all(zpos_h[1:] >= zpos_h[:-1]))
     # checksum over every value
     total = float(z.values.to(torch.float64).sum().item())
     v64 = val.astype(np.float64)
@@ -265,19 +288,29 @@ def test_c4_full_size(gpu):
     want = float(np.dot(colsum, rowsum))
     # every entry is rounded once to float32 (relative error <= 2^-24)
     assert total == pytest.approx(want, rel=1e-7)
-    # exact rows on a sample
-    prods = np.bincount(row_of, weights=lens[crd].astype(np.float64), minlength=n)
-    rng = np.random.default_rng(12)
-    sample = np.unique(np.concatenate([[int(np.argmax(prods))], rng.integers(0, n, 300)]))
-    sa = _row_sample(pos, crd, val, sample)
-    wp, wc, wv = oracle.port_spgemm(len(sample), n, n, *sa, pos, crd, val)
-    zpos_h = zpos.cpu().numpy()
-    for i, r in enumerate(sample):
-        s, e = int(zpos_h[r]), int(zpos_h[r + 1])
-        np.testing.assert_array_equal(z.dim_j_indices[s:e].cpu().numpy(), wc[wp[i]:wp[i + 1]],
-                                      err_msg=f"row {r}")
-        np.testing.assert_allclose(z.values[s:e].cpu().numpy(), wv[wp[i]:wp[i + 1]],
-                                   rtol=RTOL, atol=ATOL, err_msg=f"row {r}")
+    # every row against the oracle, block by block (the comparison runs on the device)
+    threads = _oracle_threads()
+    oracle_total = 0
+    for r0, r1 in _row_blocks(zpos_h, 1 << 16, 1 << 28):
+        s, e = int(zpos_h[r0]), int(zpos_h[r1])
+        a0, a1 = int(pos[r0]), int(pos[r1])
+        wp, wc, wv = oracle.port_spgemm(r1 - r0, n, n, pos[r0:r1 + 1] - pos[r0],
+                                        crd[a0:a1], val[a0:a1], pos, crd, val,
+                                        nthreads=threads)
+        oracle_total += int(wp[-1])
+        np.testing.assert_array_equal(zpos_h[r0:r1 + 1] - s, wp,
+                                      err_msg=f"offsets of rows [{r0}, {r1})")
+        wc_d = torch.from_numpy(wc).to(gpu)
+        wv_d = torch.from_numpy(wv).to(gpu)
+        gc, gv = z.dim_j_indices[s:e], z.values[s:e]
+        bad = _first_bad(gc, wc_d, gv, wv_d)
+        if bad >= 0:
+            r = r0 + int(np.searchsorted(wp, bad, side="right")) - 1
+            pytest.fail(f"row {r}, entry {bad - int(wp[r - r0])}: got column "
+                        f"{int(gc[bad].item())} value {float(gv[bad].item())!r}, oracle "
+                        f"column {int(wc[bad])} value {float(wv[bad])!r}")
+        del wp, wc, wv, wc_d, wv_d
+    assert oracle_total == nnz
     del z
     try:
         with pytest.raises(RuntimeError, match="exceeds int32"):
