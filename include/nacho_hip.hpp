@@ -35,27 +35,11 @@
 #define NACHO_HIP_HPP
 
 #include <cstdint>
-#include <cstring>
-#include <stdexcept>
-#include <string>
-#include <type_traits>
 
 #include "nacho_hip.h"
+#include "nacho_hip_runtime.hpp"  // stream(), set_stream(), detail::to_c / from_c / check
 
 namespace nacho_hip {
-
-// ---- stream -----------------------------------------------------------------------------
-
-namespace detail {
-inline void *&stream_slot() {
-    thread_local void *s = nullptr;
-    return s;
-}
-}  // namespace detail
-
-// The hipStream_t the entry points below run on, per calling thread (default: null stream).
-inline void *stream() { return detail::stream_slot(); }
-inline void set_stream(void *s) { detail::stream_slot() = s; }
 
 // ---- tensor formats ---------------------------------------------------------------------
 // One template per (format, index variables) the declared kernels use
@@ -136,32 +120,6 @@ struct coo3_ijk {  // COO3 over (i, j, k): one merged level
 };
 
 namespace detail {
-
-// A format instantiated at <int32_t, float> and its C descriptor are the same sequence of
-// fields, so values convert by copying bytes.
-template <typename C, typename F>
-inline C to_c(const F &f) {
-    static_assert(sizeof(C) == sizeof(F) && std::is_trivially_copyable<F>::value,
-                  "format and C descriptor differ");
-    C c;
-    std::memcpy(&c, &f, sizeof(C));
-    return c;
-}
-
-template <typename F, typename C>
-inline F from_c(const C &c) {
-    static_assert(sizeof(C) == sizeof(F) && std::is_trivially_copyable<F>::value,
-                  "format and C descriptor differ");
-    F f;
-    std::memcpy(&f, &c, sizeof(F));
-    return f;
-}
-
-inline void check(int rc, const char *kernel) {
-    if (rc != NACHO_OK) {
-        throw std::runtime_error(std::string(kernel) + ": " + nacho_error_string(rc));
-    }
-}
 
 template <typename Z, typename CZ, typename CA, typename A, typename B, typename Fn>
 inline Z call2(Fn fn, const char *kernel, const A &a, const B &b, int32_t num_blocks,

@@ -6,6 +6,9 @@ shared library exporting the C ABI declared in `include/nacho_hip.h`.  The libra
 in-tree so that it travels with the repository to the GPU machine.
 
     python -m nacho_amd.build          # rebuild
+
+The HIP code generator for the GPU target (`nacho_amd/codegen`, host C++) is built beside it
+as `nacho_amd/codegen/nacho_hipgen` by `build_codegen()`.
 """
 
 from __future__ import annotations
@@ -22,6 +25,8 @@ REPO_DIR = PACKAGE_DIR.parent
 CSRC_DIR = PACKAGE_DIR / "csrc"
 BUILD_DIR = PACKAGE_DIR / "_build"
 LIBRARY = PACKAGE_DIR / "libnacho_hip.so"
+CODEGEN_DIR = PACKAGE_DIR / "codegen"
+CODEGEN_EXE = CODEGEN_DIR / "nacho_hipgen"
 
 ARCH = "gfx950"
 
@@ -95,5 +100,23 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     return LIBRARY
 
 
+def build_codegen(verbose: bool = False) -> Path:
+    """Compile the code generator's command line, nacho_hipgen (host C++17, g++)."""
+    cxx = shutil.which("g++") or shutil.which("c++")
+    if cxx is None:
+        raise RuntimeError("no host C++ compiler (g++) for the code generator")
+    tmp = CODEGEN_EXE.with_name(CODEGEN_EXE.name + ".tmp")
+    cmd = [cxx, "-O2", "-std=c++17", "-Wall", "-Wextra", *map(str, sorted(CODEGEN_DIR.glob("*.cpp"))),
+           "-o", str(tmp)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"code generator build failed:\n{proc.stdout}\n{proc.stderr}")
+    os.replace(tmp, CODEGEN_EXE)
+    if verbose:
+        print(f"built {CODEGEN_EXE}", file=sys.stderr)
+    return CODEGEN_EXE
+
+
 if __name__ == "__main__":
     build(verbose=True)
+    build_codegen(verbose=True)
