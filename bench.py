@@ -2,6 +2,8 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--only]
                     [--workload c2|c3|c4|c5|c5coo|c2coo|c3coo|c2dcsr|c3dcsr|c2add3|c4sssmm]
+    python bench.py --workload mtx --files A.mtx B.mtx [...]      (real data, local files)
+    python bench.py --workload tns --files T.tns [...] [--dims I,J,K]
 
 The default run prints the C2 csr_add line (the headline `value`) with a `workloads` list
 holding the other north-star configurations measured in the same run: C3 csr_mul, C5
@@ -33,6 +35,11 @@ Workload c4 (ESC SpGEMM, C = A*A on the R-MAT 2^20 operand) reports GFLOP/s = 2*
 time, P = number of intermediate products; its roofline bytes are
 4*(n+1) + 8*nnzA + 8*P (B's gathered entries) + 8*(n+1) + 8*nnzC, and its CPU baseline is
 the row-parallel C SpGEMM of oracle/ on a random row sample.
+
+Workloads mtx and tns run the same measurements on local files, paired as the reference's
+sweeps pair them (benchmarks/csr_add.py:45-124, benchmarks/frostt_tensors_add.py:52-149):
+consecutive .mtx files clipped to a common shape, through csr_add and csr_mul; each .tns
+file with its copy shifted by one along every mode, through csf_add and coo3d_add.
 
 Workloads c5 (csf_add), c5coo (coo3d_add), c2coo (coo_add), c3coo (coo_mul), c2dcsr
 (dcsr_add) and c3dcsr (dcsr_mul) report GB/s of algorithmic bytes: CSF3 and DCSR count every level array of A, B
@@ -146,6 +153,30 @@ def compact(workload, line):
         if key in line["config"]:
             rec[key] = line["config"][key]
     return rec
+
+
+def timed_steps(step, steps):
+    """Wall seconds of `steps` calls step(0) .. step(steps - 1), synchronized with the device
+    on both sides.  Python's garbage collector runs beforehand and is paused inside (as
+    timeit does), so a collection cannot land in the timed region; results are still
+    released as soon as they are dropped (reference counting)."""
+    import gc
+
+    import torch
+
+    gc.collect()
+    torch.cuda.synchronize()
+    enabled = gc.isenabled()
+    gc.disable()
+    try:
+        start = time.perf_counter()
+        for i in range(steps):
+            step(i)
+        torch.cuda.synchronize()
+        return time.perf_counter() - start
+    finally:
+        if enabled:
+            gc.enable()
 
 
 def make_operands(workload):
@@ -290,11 +321,7 @@ def bench_spgemm(args, device):
     nacho_amd.set_kernel_timing(False)
     torch.cuda.synchronize()
 
-    start = time.perf_counter()
-    for i in range(args.steps):
-        fn(copies[i % 2], copies[i % 2])
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - start
+    elapsed = timed_steps(lambda i: fn(copies[i % 2], copies[i % 2]), args.steps)
     ms_per_step = elapsed * 1e3 / args.steps
     value = flops / (ms_per_step * 1e-3) / 1e9
     kernel_avg_ms = sum(kernel_ms) / len(kernel_ms)
@@ -433,11 +460,7 @@ def bench_sssmm(args, device):
         kernel_ms.append(nacho_amd.last_kernel_ms())
     nacho_amd.set_kernel_timing(False)
     torch.cuda.synchronize()
-    start = time.perf_counter()
-    for i in range(args.steps):
-        fn(*(copies[i % 2],) * 3)
-    torch.cuda.synchronize()
-    ms_per_step = (time.perf_counter() - start) * 1e3 / args.steps
+    ms_per_step = timed_steps(lambda i: fn(*(copies[i % 2],) * 3), args.steps) * 1e3 / args.steps
     value = flops / (ms_per_step * 1e-3) / 1e9
     kernel_avg_ms = sum(kernel_ms) / len(kernel_ms)
     achieved = alg_bytes / (kernel_avg_ms * 1e-3) / 1e9
@@ -508,10 +531,11 @@ def dcsr_levels(pos, crd):
     return present.astype(np.int32), pj.astype(np.int32), np.asarray(crd, np.int32)
 
 
-def bench_tuple_workload(args, device, workload):
+def bench_tuple_workload(args, device, workload, prepared=None):
     """c5 (csf_add), c5coo (coo3d_add), c2coo (coo_add), c2dcsr / c3dcsr (dcsr_add /
     dcsr_mul): element-wise merges of coordinate trees or tuples; one step = one call with
-    operands resident in HBM."""
+    operands resident in HBM.  `prepared` = (spec, operands, shape, data) measures csf_add
+    (workload c5) or coo3d_add (c5coo) on given (i, j, k) operands (the file workloads)."""
     import numpy as np
     import torch
 
@@ -520,8 +544,13 @@ def bench_tuple_workload(args, device, workload):
     from nacho_amd.convert import csf3_levels
 
     spec = WORKLOADS[workload]
+    data = "synthetic (seeded generators in nacho_amd/synth.py)"
+    traffic_key = workload
     t0 = time.perf_counter()
-    if workload in ("c2dcsr", "c3dcsr"):
+    if prepared is not None:
+        spec, ops_np, shape, data = prepared
+        traffic_key = None
+    elif workload in ("c2dcsr", "c3dcsr"):
         ops = synth.c2_operands() if workload == "c2dcsr" else synth.c3_operands()
         ops_np = [(dcsr_levels(p, c), v) for p, c, v in ops]
         shape = (len(ops[0][0]) - 1, len(ops[0][0]) - 1)
@@ -537,8 +566,9 @@ def bench_tuple_workload(args, device, workload):
         (ac, av), (bc, bv) = synth.c5_operands()
         ops_np = [(tuple(ac[:, d] for d in range(3)), av), (tuple(bc[:, d] for d in range(3)), bv)]
         shape = synth.C5_SHAPE
-    log(f"generated {workload}: nnzA={len(ops_np[0][1])} nnzB={len(ops_np[1][1])} "
-        f"in {time.perf_counter() - t0:.1f}s")
+    if prepared is None:
+        log(f"generated {workload}: nnzA={len(ops_np[0][1])} nnzB={len(ops_np[1][1])} "
+            f"in {time.perf_counter() - t0:.1f}s")
 
     def upload(crd, val):
         t = [torch.from_numpy(np.ascontiguousarray(c, dtype=np.int32)).to(device) for c in crd]
@@ -587,11 +617,7 @@ def bench_tuple_workload(args, device, workload):
         kernel_ms.append(nacho_amd.last_kernel_ms())
     nacho_amd.set_kernel_timing(False)
     torch.cuda.synchronize()
-    start = time.perf_counter()
-    for i in range(args.steps):
-        fn(*copies[i % ROTATE])
-    torch.cuda.synchronize()
-    ms_per_step = (time.perf_counter() - start) * 1e3 / args.steps
+    ms_per_step = timed_steps(lambda i: fn(*copies[i % ROTATE]), args.steps) * 1e3 / args.steps
     value = alg_bytes / (ms_per_step * 1e-3) / 1e9
     kernel_avg_ms = sum(kernel_ms) / len(kernel_ms)
     achieved = alg_bytes / (kernel_avg_ms * 1e-3) / 1e9
@@ -646,7 +672,7 @@ def bench_tuple_workload(args, device, workload):
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (seeded generators in nacho_amd/synth.py)",
+        "data": data,
         "config": {
             "workload": spec["desc"],
             "nnz_a": nnz[0],
@@ -663,32 +689,39 @@ def bench_tuple_workload(args, device, workload):
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": traffic_from_profiles(workload, "tuple_merge"),
+            "traffic": traffic_from_profiles(traffic_key, "tuple_merge") if traffic_key
+                       else None,
             "kernel_avg_us": round(kernel_avg_ms * 1e3, 2),
         },
         "cpu_baseline": cpu,
     }
 
 
-def bench_csr(args, device, workload):
+def bench_csr(args, device, workload, prepared=None):
     """c2 (csr_add), c3 (csr_mul), c2add3 (csr_add_3): one step = one call with operands
-    resident in HBM, rotating over ROTATE copies."""
+    resident in HBM, rotating over ROTATE copies.  `prepared` = (spec, operands, (rows,
+    cols), data) runs the same measurement on given operands (the file workloads)."""
+    import numpy as np
     import torch
 
     import nacho_amd
     from nacho_amd import synth
 
-    spec = WORKLOADS[workload]
     t0 = time.perf_counter()
-    operands_np = make_operands(workload)
+    if prepared is None:
+        spec = WORKLOADS[workload]
+        operands_np = make_operands(workload)
+        rows = cols = len(operands_np[0][0]) - 1
+        data = "synthetic (seeded generators in nacho_amd/synth.py)"
+        log(f"generated {workload}: rows={rows} "
+            f"nnz={[len(o[1]) for o in operands_np]} in {time.perf_counter() - t0:.1f}s")
+    else:
+        spec, operands_np, (rows, cols), data = prepared
     a_np, b_np = operands_np[0], operands_np[1]
-    rows = len(a_np[0]) - 1
-    log(f"generated {workload}: rows={rows} "
-        f"nnz={[len(o[1]) for o in operands_np]} in {time.perf_counter() - t0:.1f}s")
 
     def upload(t):
-        pos, crd, val = (torch.from_numpy(x).to(device) for x in t)
-        return nacho_amd.CSR_gpu(pos, crd, val, torch.tensor([rows, rows], dtype=torch.int32))
+        pos, crd, val = (torch.from_numpy(np.ascontiguousarray(x)).to(device) for x in t)
+        return nacho_amd.CSR_gpu(pos, crd, val, torch.tensor([rows, cols], dtype=torch.int32))
 
     copies = [tuple(upload(o) for o in operands_np) for _ in range(ROTATE)]
     fn = {"add": nacho_amd.gpu_csr_add_f32, "mul": nacho_amd.gpu_csr_mul_f32,
@@ -716,12 +749,7 @@ def bench_csr(args, device, workload):
     torch.cuda.synchronize()
 
     # timed region: exactly K steps, synchronized on both sides
-    torch.cuda.synchronize()
-    start = time.perf_counter()
-    for i in range(args.steps):
-        fn(*copies[i % ROTATE])
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - start
+    elapsed = timed_steps(lambda i: fn(*copies[i % ROTATE]), args.steps)
     ms_per_step = elapsed * 1e3 / args.steps
     value = alg_bytes / (ms_per_step * 1e-3) / 1e9
 
@@ -748,10 +776,11 @@ def bench_csr(args, device, workload):
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (seeded generators in nacho_amd/synth.py)",
+        "data": data,
         "config": {
             "workload": spec["desc"],
             "rows": rows,
+            "cols": cols,
             "nnz_operands": [len(o[1]) for o in operands_np],
             "nnz_a": len(a_np[1]),
             "nnz_b": len(b_np[1]),
@@ -775,12 +804,84 @@ def bench_csr(args, device, workload):
     return line
 
 
+def bench_files(args, device):
+    """The real-data workloads on local files (one line; the first measurement is its
+    value, the others are listed under `workloads`).
+
+    mtx: consecutive pairs of the given Matrix Market files (a single file is paired with
+    itself), each clipped to a common shape as the reference's matrix sweep does
+    (benchmarks/csr_add.py:57-65), then csr_add and csr_mul.
+    tns: each FROSTT file as A (sorted, repeats summed) and its shifted copy as B
+    (benchmarks/frostt_tensors_add.py:62-64), then csf_add (CSF3) and coo3d_add (COO3)."""
+    import numpy as np
+
+    from nacho_amd import io
+
+    paths = [Path(p) for p in args.files]
+    if not paths:
+        raise SystemExit(f"--workload {args.workload} needs --files")
+    for p in paths:
+        if not p.is_file():
+            raise SystemExit(f"no such file: {p}")
+    lines = []
+    if args.workload == "mtx":
+        mats = []
+        for p in paths:
+            t0 = time.perf_counter()
+            mats.append(io.parse_matrix(p, device="cpu"))
+            log(f"parsed {p.name}: {tuple(mats[-1].shape)} nnz={mats[-1].values().numel()} "
+                f"in {time.perf_counter() - t0:.1f}s")
+        pairs = list(zip(range(len(paths) - 1), range(1, len(paths)))) or [(0, 0)]
+        for i, j in pairs:
+            rows, cols, a, b = io.clip_to_common_shape(mats[i], mats[j])
+            names = f"{paths[i].name} and {paths[j].name}"
+            for op, kernel in (("add", "csr_add"), ("mul", "csr_mul")):
+                spec = dict(WORKLOADS["c2" if op == "add" else "c3"])
+                spec["op"] = op
+                spec["desc"] = (f"{kernel} f32 of {names} clipped to {rows}x{cols} "
+                                f"(nnz {len(a[1])} + {len(b[1])})")
+                data = f"local Matrix Market files: {names}"
+                lines.append(bench_csr(args, device, "mtx",
+                                       prepared=(spec, (a, b), (rows, cols), data)))
+    else:
+        for p in paths:
+            t0 = time.perf_counter()
+            if args.dims:
+                dims = tuple(int(x) for x in args.dims.split(","))
+                coords, vals = io.load_frostt(p, dims)
+            else:
+                big = (2**31 - 1,) * 3
+                coords, vals = io.load_frostt(p, big)
+                dims = io.frostt_shape(coords)
+            a = io.coalesce_coordinates(coords, vals, dims)
+            b = io.shift_coordinates(a[0], a[1], dims)
+            log(f"parsed {p.name}: shape {dims} nnzA={len(a[1])} nnzB={len(b[1])} "
+                f"in {time.perf_counter() - t0:.1f}s")
+            ops = [(tuple(np.ascontiguousarray(c[0][:, d]) for d in range(3)), c[1])
+                   for c in (a, b)]
+            for w, kernel in (("c5", "csf_add"), ("c5coo", "coo3d_add")):
+                spec = dict(WORKLOADS[w])
+                spec["desc"] = (f"{kernel} f32 of {p.name} (shape {dims}, nnz {len(a[1])}) "
+                                f"and its copy shifted by one along every mode")
+                data = f"local FROSTT file: {p.name}"
+                lines.append(bench_tuple_workload(args, device, w,
+                                                  prepared=(spec, ops, dims, data)))
+    line = lines[0]
+    if len(lines) > 1:
+        line["workloads"] = [compact(args.workload, x) for x in lines[1:]]
+    return line
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c2")
+    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["mtx", "tns"], default="c2")
+    ap.add_argument("--files", nargs="*", default=[],
+                    help="mtx / tns workloads: local Matrix Market or FROSTT files")
+    ap.add_argument("--dims", default="",
+                    help="tns workload: I,J,K (default: one past the largest coordinates)")
     ap.add_argument("--only", action="store_true",
                     help="measure --workload alone (no `workloads` list)")
     ap.add_argument("--cpu-budget", type=float, default=12.0,
@@ -816,6 +917,9 @@ def main():
                           "launches": 5}))
         return
 
+    if args.workload in ("mtx", "tns"):
+        print(json.dumps(bench_files(args, device)), flush=True)
+        return
     line = run_workload(args, device, args.workload)
     if args.workload == "c2" and not args.only:
         # The other north-star configurations, measured in the same run: C3 csr_mul, C5 as

@@ -7,9 +7,11 @@ nacho.parse3D_i32_f32 at runtime/register_runtime.cpp:20-40): coordinates in fil
 (nacho_parse2d / nacho_parse3d in libnacho_hip.so) and raise RuntimeError where the
 reference would terminate the process.
 
-`parse_matrix`, `load_frostt` and `shift_coordinates` restate the benchmark helpers that
-turn those files into operands (benchmarks/common/parser.py:87-99,
-benchmarks/common/frostt.py:11-44), for local files: this package downloads nothing.
+`parse_matrix`, `load_frostt`, `shift_coordinates` and `clip_to_common_shape` restate the
+benchmark helpers that turn those files into operands (benchmarks/common/parser.py:87-99,
+benchmarks/common/frostt.py:11-44, benchmarks/csr_add.py:33-42), for local files: this
+package downloads nothing.  `coalesce_coordinates` and `frostt_shape` prepare a .tns file
+whose entries are unsorted or whose dims are not given.
 """
 
 from __future__ import annotations
@@ -118,29 +120,69 @@ def load_frostt(path, dims):
     return np.column_stack((t.row.numpy(), t.col.numpy(), t.dep.numpy())), t.data.numpy()
 
 
-def shift_coordinates(coordinates, values, shape):
-    """The second operand of the reference's tensor benchmarks
-    (benchmarks/common/frostt.py:27-44): every coordinate moved one step along each mode,
-    stopping at the last index, then entries that land on the same coordinate summed (in
-    their sorted order), lexicographically sorted.
+def _sorted_distinct(coords64, values, shape, dtype):
+    """Rows of `coords64` (int64, shape (n, 3)) lexicographically sorted, with the values of
+    equal rows summed in their sorted order.
 
     Coordinates become one int64 key (mode 0 most significant) when the shape allows it,
     else a three-column lexicographic sort gives the same order."""
-    c = np.asarray(coordinates)
     ext = np.asarray(shape, dtype=np.int64)
-    moved = np.minimum(c.astype(np.int64) + 1, ext - 1)
     if int(ext[0]) * int(ext[1]) * int(ext[2]) < (1 << 62):
-        key = (moved[:, 0] * ext[1] + moved[:, 1]) * ext[2] + moved[:, 2]
+        key = (coords64[:, 0] * ext[1] + coords64[:, 1]) * ext[2] + coords64[:, 2]
         order = np.argsort(key, kind="stable")
         key = key[order]
         head = np.ones(len(key), dtype=bool)
         head[1:] = key[1:] != key[:-1]
     else:
-        order = np.lexsort((moved[:, 2], moved[:, 1], moved[:, 0]))
-        m = moved[order]
+        order = np.lexsort((coords64[:, 2], coords64[:, 1], coords64[:, 0]))
+        m = coords64[order]
         head = np.ones(len(m), dtype=bool)
         head[1:] = (m[1:] != m[:-1]).any(axis=1)
     first = np.flatnonzero(head)
     ordered = np.asarray(values)[order]
     summed = np.add.reduceat(ordered, first) if len(first) else ordered
-    return moved[order][first].astype(c.dtype), summed
+    return coords64[order][first].astype(dtype), summed
+
+
+def shift_coordinates(coordinates, values, shape):
+    """The second operand of the reference's tensor benchmarks
+    (benchmarks/common/frostt.py:27-44): every coordinate moved one step along each mode,
+    stopping at the last index, then entries that land on the same coordinate summed (in
+    their sorted order), lexicographically sorted."""
+    c = np.asarray(coordinates)
+    ext = np.asarray(shape, dtype=np.int64)
+    moved = np.minimum(c.astype(np.int64) + 1, ext - 1)
+    return _sorted_distinct(moved, values, shape, c.dtype)
+
+
+def coalesce_coordinates(coordinates, values, shape):
+    """(i, j, k) rows in the form to_csf3 / to_coo3 take: sorted, distinct, the values of
+    repeated coordinates summed.  A FROSTT file need not be sorted or free of repeats."""
+    c = np.asarray(coordinates)
+    return _sorted_distinct(c.astype(np.int64), values, shape, c.dtype)
+
+
+def frostt_shape(coordinates):
+    """Shape of a tensor given without its dims: one past the largest coordinate per mode."""
+    c = np.asarray(coordinates)
+    if len(c) == 0:
+        return (1, 1, 1)
+    return tuple(int(x) + 1 for x in c.max(axis=0))
+
+
+def clip_to_common_shape(a: torch.Tensor, b: torch.Tensor):
+    """Two CSR matrices restricted to their common number of rows and declared as wide as
+    the wider one, as the reference's matrix benchmarks pair them
+    (benchmarks/csr_add.py:33-42, 59-65).  Returns (rows, cols, a, b) with each operand a
+    (pos, crd, val) triple of int32 / int32 / float32 numpy arrays."""
+    rows = min(int(a.shape[0]), int(b.shape[0]))
+    cols = max(int(a.shape[1]), int(b.shape[1]))
+
+    def clip(m):
+        crow = m.crow_indices().cpu()
+        nnz = int(crow[rows])
+        return (crow[:rows + 1].numpy().astype(np.int32),
+                m.col_indices().cpu()[:nnz].numpy().astype(np.int32),
+                m.values().cpu()[:nnz].numpy().astype(np.float32))
+
+    return rows, cols, clip(a), clip(b)

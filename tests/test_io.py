@@ -167,3 +167,36 @@ def test_parse_matrix_builds_csr_and_coo(tmp_path):
     coo = io.parse_matrix(f, return_coo=True, device="cpu")
     assert coo.is_coalesced()
     np.testing.assert_array_equal(coo.to_dense().numpy(), csr.to_dense().numpy())
+
+
+def test_clip_to_common_shape_keeps_leading_rows_and_widens():
+    """benchmarks/csr_add.py:33-42, 59-65: rows = min, cols = max, entries of the dropped
+    rows removed."""
+    from nacho_amd import io
+
+    a = torch.tensor([[1.0, 0, 2], [0, 3, 0], [4, 0, 0]]).to_sparse_csr()
+    b = torch.tensor([[0, 5.0, 0, 0], [6, 0, 0, 7]]).to_sparse_csr()
+    rows, cols, ta, tb = io.clip_to_common_shape(a, b)
+    assert (rows, cols) == (2, 4)
+    np.testing.assert_array_equal(ta[0], [0, 2, 3])
+    np.testing.assert_array_equal(ta[1], [0, 2, 1])
+    np.testing.assert_array_equal(ta[2], np.float32([1, 2, 3]))
+    np.testing.assert_array_equal(tb[0], [0, 1, 3])
+    assert ta[0].dtype == np.int32 and ta[1].dtype == np.int32 and ta[2].dtype == np.float32
+
+
+def test_coalesce_and_shape_of_an_unsorted_tensor():
+    from nacho_amd import io
+
+    c = np.array([[2, 1, 1], [0, 0, 0], [2, 1, 1], [1, 5, 2]], np.int32)
+    v = np.float32([1, 2, 3, 4])
+    assert io.frostt_shape(c) == (3, 6, 3)
+    got_c, got_v = io.coalesce_coordinates(c, v, (3, 6, 3))
+    np.testing.assert_array_equal(got_c, [[0, 0, 0], [1, 5, 2], [2, 1, 1]])
+    np.testing.assert_array_equal(got_v, np.float32([2, 4, 4]))
+    # the wide-shape branch (lexicographic sort) gives the same result
+    wide = (2**31 - 1,) * 3
+    wc, wv = io.coalesce_coordinates(c, v, wide)
+    np.testing.assert_array_equal(wc, got_c)
+    np.testing.assert_array_equal(wv, got_v)
+    assert io.frostt_shape(np.zeros((0, 3), np.int32)) == (1, 1, 1)
