@@ -36,6 +36,7 @@
 // reference's.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <climits>
 #include <cstdint>
 #include <mutex>
@@ -76,16 +77,103 @@ __device__ __forceinline__ void merge_split(ReadA A, ReadB B, int aS, int aE, in
     if (a > aS && b < bE && A(a - 1) == B(b)) ++b;
 }
 
+// ---- sparse-overlap union count: row pass + pair search --------------------------------
+// A union's output count is na + nb - pairs, and pairs only occur in rows where both
+// operands have entries.  When those rows hold few entries (C2: 244K of 33M), searching each
+// entry of a row's smaller side in its larger side counts the pairs without streaming every
+// coordinate through the count kernel.
+//
+// The row pass (extra workgroups of the partition kernel's launch) finds those rows and
+// writes one record per row; the count kernel totals the entries to search (M) and picks the
+// mode it and the write kernel follow:
+//   search: M * kSearchRatio <= nnzA + nnzB.  The count kernel searches every such entry
+//           (pair_search), adds the pairs into pair_count[write chunk] and publishes the
+//           length nnzA + nnzB - pairs; the write kernel's chunk w starts at output
+//           split_a[t0] + split_b[t0] - (pairs of chunks before w).
+//   count:  the count kernel runs its tile walk (chunk output counts, no lane starts).
+// In both modes the write kernel finds its lanes' starts itself (SEARCH).
+constexpr int kModeCount = 0;
+constexpr int kModeSearch = 1;
+constexpr int kSearchRatio = 16;
+constexpr int kRowPassMaxBlocks = 1024;  // workgroups of the row pass (a multiple of kBlock)
+
+struct RowPairs {
+    // records of row-pass workgroup b at rec[blk_base[b] + k], k < blk_recs[b]:
+    // {first entry (within b's entries), smaller side's begin, larger side's begin,
+    //  larger side's length | bit 31 set when the smaller side is B}
+    // Workgroup b's region starts at its first row, or, when `px` is set, at px[first row]
+    // (px: the offsets of the operand with fewer entries, whose entries in b's rows bound
+    // b's records), whichever needs less scratch.
+    int4 *rec;
+    const int *px;
+    int *blk_base;   // region start per workgroup
+    int *blk_elems;  // entries to search per workgroup
+    int *blk_recs;   // records per workgroup
+    int *mode;       // kModeSearch or kModeCount (stored by the count kernel)
+    int rows_per_thread;
+    int nb;  // workgroups of the row pass
+};
+
+// Workgroup `block` of the row pass (one wave): one thread per rows_per_thread consecutive
+// rows.  It runs as extra workgroups of the partition kernel's launch, and nothing in it
+// waits for other workgroups: the count kernel, launched next, totals blk_elems and chooses
+// the mode.
+__device__ __forceinline__ void row_pass_block(const int *__restrict__ pa,
+                                               const int *__restrict__ pb, int rows,
+                                               const RowPairs &rp, int block) {
+    static_assert(kPartBlock == dev::kWave, "the row pass scans within one wave");
+    const int tid = threadIdx.x;
+    const int rpt = rp.rows_per_thread;
+    const long long per_block = static_cast<long long>(kPartBlock) * rpt;
+    const long long row0 = block * per_block;  // < rows (or 0)
+    const long long first = row0 + static_cast<long long>(tid) * rpt;
+    int elems = 0, recs = 0;
+    for (int j = 0; j < rpt; ++j) {
+        const long long r = first + j;
+        if (r >= rows) break;
+        const int la = pa[r + 1] - pa[r], lb = pb[r + 1] - pb[r];
+        if (la > 0 && lb > 0) {
+            elems += min(la, lb);
+            ++recs;
+        }
+    }
+    const int e_incl = dev::wave_inclusive_sum(elems);
+    const int r_incl = dev::wave_inclusive_sum(recs);
+    int e_off = e_incl - elems;
+    const int region = rp.px ? rp.px[row0] : static_cast<int>(row0);
+    int4 *out = rp.rec + region + (r_incl - recs);
+    for (int j = 0; j < rpt; ++j) {
+        const long long r = first + j;
+        if (r >= rows) break;
+        const int a0 = pa[r], la = pa[r + 1] - a0, b0 = pb[r], lb = pb[r + 1] - b0;
+        if (la > 0 && lb > 0) {
+            const bool a_small = la <= lb;
+            *out++ = make_int4(e_off, a_small ? a0 : b0, a_small ? b0 : a0,
+                               a_small ? lb : (la | INT_MIN));
+            e_off += min(la, lb);
+        }
+    }
+    if (tid == dev::kWave - 1) {
+        rp.blk_base[block] = region;
+        rp.blk_elems[block] = e_incl;
+        rp.blk_recs[block] = r_incl;
+    }
+}
+
 // One thread per tile boundary t in [0, num_tiles]: split of diagonal min(t*TILE, total).
 // Thread 0 also zeroes the ticket counter that the next kernel's length total uses, and the
 // first n_counts threads zero the chunk counts (n_counts <= num_tiles + 1).
 // (Launched in kPartBlock-thread workgroups: the few thousand boundaries then spread over
-// every CU instead of a few dozen.)
+// every CU instead of a few dozen.)  Workgroups from part_blocks on run the row pass.
 __global__ __launch_bounds__(kPartBlock) void csr_partition_kernel(
     const int *__restrict__ pa, const int *__restrict__ ca, const int *__restrict__ pb,
     const int *__restrict__ cb, int rows, int total, int num_tiles, int *__restrict__ split_r,
     int *__restrict__ split_a, int *__restrict__ split_b, unsigned long long *__restrict__ done,
-    unsigned *__restrict__ zero_counts, int n_counts) {
+    unsigned *__restrict__ zero_counts, int n_counts, int part_blocks, RowPairs rp) {
+    if (static_cast<int>(blockIdx.x) >= part_blocks) {  // the row pass's workgroups
+        row_pass_block(pa, pb, rows, rp, static_cast<int>(blockIdx.x) - part_blocks);
+        return;
+    }
     const int t = blockIdx.x * blockDim.x + threadIdx.x;
     if (t > num_tiles) return;
     if (t == 0) *done = 0ull;  // accumulator of the kernel that totals the length
@@ -759,13 +847,148 @@ __device__ __forceinline__ void pair_tile(
     __syncthreads();  // every lane is done with this tile's LDS
 }
 
+// The row pass's totals staged in LDS by every count workgroup: s_start[b] = entries to
+// search before workgroup b, s_start[nb] = M.  Returns the mode (the same in every
+// workgroup); workgroup 0 stores it for the write kernel.  Ends synchronised.
+__device__ __forceinline__ int stage_row_pass(PairShared &sh, const RowPairs &rp,
+                                              long long items) {
+    static_assert(3 * kRowPassMaxBlocks + 1 <= kGrainCap, "row-pass totals fit the LDS");
+    constexpr int kPer = kRowPassMaxBlocks / kBlock;
+    const int tid = threadIdx.x;
+    const int nb = rp.nb;
+    int *s_start = sh.crd;                            // nb + 1 entries
+    int *s_recs = sh.crd + kRowPassMaxBlocks + 1;      // nb entries
+    int *s_base = sh.crd + 2 * kRowPassMaxBlocks + 1;  // nb entries
+    int v[kPer], sum = 0;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int i = tid * kPer + k;
+        v[k] = i < nb ? rp.blk_elems[i] : 0;
+        sum += v[k];
+        if (i < nb) {
+            s_recs[i] = rp.blk_recs[i];
+            s_base[i] = rp.blk_base[i];
+        }
+    }
+    int total = 0;
+    int off = dev::block_exclusive_sum<kBlock>(sum, sh.wave, total);
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int i = tid * kPer + k;
+        if (i < nb) s_start[i] = off;
+        off += v[k];
+    }
+    if (tid == 0) s_start[nb] = total;
+    const int mode =
+        static_cast<long long>(total) * kSearchRatio <= items ? kModeSearch : kModeCount;
+    if (blockIdx.x == 0 && tid == 0) *rp.mode = mode;
+    __syncthreads();
+    return mode;
+}
+
+// Search mode of the count kernel: a grid-stride loop over the M entries to search.  Entry e
+// lies in row-pass workgroup b (staged offsets), record k of b (binary search of the
+// records' first entries), and is the smaller side's entry rec.y + (e - first); a lower
+// bound in the larger side tells whether its column is there.  A pair's write chunk is the
+// chunk whose A range holds its A entry (the partition keeps pairs inside one tile).
+__device__ __forceinline__ void pair_search(PairShared &sh, const int *__restrict__ ca,
+                                            const int *__restrict__ cb, const RowPairs &rp,
+                                            const int *__restrict__ split_a, int num_tiles,
+                                            int write_chunk, int write_grid,
+                                            unsigned *__restrict__ pair_count,
+                                            unsigned long long *__restrict__ done,
+                                            int64_t *__restrict__ length_out, long long items) {
+    const int tid = threadIdx.x;
+    const int nb = rp.nb;
+    const int *s_start = sh.crd;  // staged by stage_row_pass
+    const int *s_recs = sh.crd + kRowPassMaxBlocks + 1;
+    const int *s_base = sh.crd + 2 * kRowPassMaxBlocks + 1;
+    const int m_total = s_start[nb];
+    unsigned found = 0;  // pairs seen by this wave (uniform in the wave)
+    for (long long base = static_cast<long long>(blockIdx.x) * kBlock; base < m_total;
+         base += static_cast<long long>(gridDim.x) * kBlock) {
+        const long long e = base + tid;
+        int chunk_id = -1;
+        if (e < m_total) {
+            int lo = 0, hi = nb - 1;
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (s_start[mid] <= e) {
+                    lo = mid;
+                } else {
+                    hi = mid - 1;
+                }
+            }
+            const int local = static_cast<int>(e - s_start[lo]);
+            const int4 *recs = rp.rec + s_base[lo];
+            int klo = 0, khi = s_recs[lo] - 1;
+            while (klo < khi) {
+                const int mid = (klo + khi + 1) >> 1;
+                if (recs[mid].x <= local) {
+                    klo = mid;
+                } else {
+                    khi = mid - 1;
+                }
+            }
+            const int4 rc = recs[klo];
+            const bool b_small = rc.w < 0;
+            const int l_len = rc.w & INT_MAX;
+            const int s_idx = rc.y + (local - rc.x);
+            const int x = b_small ? cb[s_idx] : ca[s_idx];
+            const int *large = b_small ? ca : cb;
+            int p = rc.z, q = rc.z + l_len;
+            while (p < q) {
+                const int mid = (p + q) >> 1;
+                if (large[mid] < x) {
+                    p = mid + 1;
+                } else {
+                    q = mid;
+                }
+            }
+            if (p < rc.z + l_len && large[p] == x) {
+                const int a_idx = b_small ? p : s_idx;
+                int wlo = 0, whi = write_grid - 1;
+                while (wlo < whi) {
+                    const int mid = (wlo + whi + 1) >> 1;
+                    if (split_a[min(mid * write_chunk, num_tiles)] <= a_idx) {
+                        wlo = mid;
+                    } else {
+                        whi = mid - 1;
+                    }
+                }
+                chunk_id = wlo;
+            }
+        }
+        // one atomic per distinct write chunk among the wave's pairs
+        unsigned long long pending = __ballot(chunk_id >= 0);
+        found += static_cast<unsigned>(__popcll(pending));
+        while (pending) {
+            const int leader = __ffsll(static_cast<long long>(pending)) - 1;
+            const int c = __shfl(chunk_id, leader, dev::kWave);
+            const unsigned long long same = __ballot(chunk_id == c);
+            if (dev::lane() == leader) atomicAdd(&pair_count[c], static_cast<unsigned>(__popcll(same)));
+            pending &= ~same;
+        }
+    }
+    if (dev::lane() == 0) sh.wsum[tid / dev::kWave] = found;
+    __syncthreads();
+    if (tid == 0) {
+        unsigned pairs = 0;
+#pragma unroll
+        for (int w = 0; w < kBlock / dev::kWave; ++w) pairs += sh.wsum[w];
+        dev::subtract_total(pairs, done, items, length_out);
+    }
+}
+
 // Output counts of a union level (na + nb - pairs per tile), added into
 // chunk_count[tile / write_chunk] (zeroed by the partition kernel): the counts of the write
 // kernel's chunks, whose grid is chosen independently of this kernel's (`chunk` tiles per
 // workgroup here, two tiles in flight).  Their sum, the result length, goes to `length_out`
 // from the last workgroup.  When STARTS, every lane's walk start in the write kernel (row,
 // A and B heads) is stored to starts[tile * kBlock + lane], found here by a search over the
-// staged rows and a merge-path split inside the row.
+// staged rows and a merge-path split inside the row.  Without STARTS and after a row pass
+// (rp.blk_elems set), the launch first totals the row pass and, in search mode, runs
+// pair_search instead (chunk_count then receives the pairs of each write chunk).
 template <bool STARTS>
 __global__ __launch_bounds__(kBlock) void csr_pair_count_kernel(
     const int *__restrict__ pa, const int *__restrict__ ca, const int *__restrict__ pb,
@@ -773,11 +996,18 @@ __global__ __launch_bounds__(kBlock) void csr_pair_count_kernel(
     const int *__restrict__ split_r, const int *__restrict__ split_a,
     const int *__restrict__ split_b, unsigned *__restrict__ chunk_count,
     unsigned long long *__restrict__ done, int64_t *__restrict__ length_out,
-    uint2 *__restrict__ starts) {
+    uint2 *__restrict__ starts, RowPairs rp, int write_grid, long long items) {
     __shared__ PairShared sh;
     __shared__ int s_split[3 * (kMaxChunk + 1)];
 
     const int tid = threadIdx.x;
+    if (!STARTS && rp.blk_elems != nullptr) {  // after a row pass
+        if (stage_row_pass(sh, rp, items) == kModeSearch) {  // uniform
+            pair_search(sh, ca, cb, rp, split_a, num_tiles, write_chunk, write_grid,
+                        chunk_count, done, length_out, items);
+            return;
+        }
+    }
     int t0, t1;
     chunk_range(num_tiles, chunk, t0, t1);
     if (t0 >= t1) {
@@ -832,7 +1062,8 @@ __global__ __launch_bounds__(kBlock) void csr_pair_count_kernel(
 //
 // SEARCH (union without stored lane starts): every lane finds its start from the tile's
 // row-start bins and a search inside its row, as the spread intersection does, instead of
-// loading it from `starts`.
+// loading it from `starts`.  When `mode` is non-null and holds kModeSearch, chunk_count
+// holds each chunk's pairs instead of its output count.
 template <Op OP, int IPT, bool VALUES, bool CHILD, bool SPREAD, bool SEARCH = false>
 __global__ __launch_bounds__(kBlock) void csr_write_kernel(
     const int *__restrict__ pa, const int *__restrict__ ca, const float *__restrict__ va,
@@ -844,7 +1075,8 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
     const int *__restrict__ next_b, int *__restrict__ child_a, int *__restrict__ child_b,
     unsigned *__restrict__ length, int spread_by_a, int64_t *__restrict__ tile_count,
     int64_t *__restrict__ chunk_total, unsigned long long *__restrict__ done,
-    int64_t *__restrict__ length_out, const uint2 *__restrict__ starts) {
+    int64_t *__restrict__ length_out, const uint2 *__restrict__ starts,
+    const int *__restrict__ mode) {
     static_assert(!(VALUES && CHILD), "a level carries values or child pointers, not both");
     static_assert(!SPREAD || (OP == Op::Intersect && !CHILD), "spread output: intersection");
     constexpr int kCap = kBlock * IPT + 2;
@@ -882,6 +1114,11 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
         int total = 0;
         (void)dev::block_exclusive_sum<kBlock>(before, s_wave, total);
         base = total;
+        if (SEARCH && mode != nullptr && *mode == kModeSearch) {
+            // chunk_count holds pairs: outputs before this chunk are its A and B entries
+            // before it (the staged splits of tile t0) less the pairs merged among them
+            base = s_split[1] + s_split[2] - total;
+        }
     } else {
         __syncthreads();  // the staged splits
     }
@@ -1044,7 +1281,7 @@ int misalign(const void *p, int *out) {
 
 int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
                 const LevelOperand &A, const LevelOperand &B, const LevelResult &Z,
-                long long *out_len, const char *kernel_name, bool keep_starts) {
+                long long *out_len, const char *kernel_name, UnionCount count_plan) {
     const long long total = static_cast<long long>(A.len) + B.len + rows;
     if (total > static_cast<long long>(INT_MAX) - 2 * kTile) return NACHO_ERR_INDEX_OVERFLOW;
     const int num_tiles = total > 0 ? static_cast<int>((total + kTile - 1) / kTile) : 1;
@@ -1091,16 +1328,17 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
         NACHO_TRY(call.scratch_n(static_cast<size_t>(grid) + 1, &chunk_total));
         int64_t *len_dev = chunk_total + grid;
         NACHO_TRY(call.timer_start(kernel_name));  // the whole device pipeline of this level
-        csr_partition_kernel<<<ceil_div(static_cast<size_t>(num_tiles) + 1, kPartBlock), kPartBlock, 0, s>>>(
+        const int part_blocks = static_cast<int>(ceil_div(static_cast<size_t>(num_tiles) + 1, kPartBlock));
+        csr_partition_kernel<<<part_blocks, kPartBlock, 0, s>>>(
             A.pos, A.crd, B.pos, B.crd, rows, static_cast<int>(total), num_tiles, split_r,
-            split_a, split_b, done, nullptr, 0);
+            split_a, split_b, done, nullptr, 0, part_blocks, RowPairs{});
         NACHO_TRY_HIP(hipGetLastError());
         csr_write_kernel<Op::Intersect, kItemsPerLane, true, false, true>
             <<<grid, kBlock, 0, s>>>(A.pos, A.crd, A.val, B.pos, B.crd, B.val, A.len, B.len,
                                      num_tiles, chunk, split_r, split_a, split_b, nullptr, rows,
                                      Z.pos, tmp_crd, tmp_val, nullptr, nullptr, nullptr,
                                      nullptr, nullptr, by_a, tile_count, chunk_total, done,
-                                     length_out, nullptr);
+                                     length_out, nullptr, nullptr);
         NACHO_TRY_HIP(hipGetLastError());
         NACHO_TRY(call.mark_length());
         csr_compact_kernel<<<num_tiles, kBlock, 0, s>>>(
@@ -1120,8 +1358,37 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
     NACHO_TRY(misalign(B.crd, &mis.cb));
     NACHO_TRY(misalign(A.pos, &mis.pa));
     NACHO_TRY(misalign(B.pos, &mis.pb));
+    if (!values && count_plan != UnionCount::kAuto) return NACHO_ERR_INVALID_ARGUMENT;
+    const bool keep_starts = !values;  // levels without values: stored lane starts
+    const bool row_pass = values && count_plan == UnionCount::kAuto;
+    const long long items = static_cast<long long>(A.len) + B.len;
     uint2 *starts = nullptr;
     if (keep_starts) NACHO_TRY(call.scratch_n(static_cast<size_t>(num_tiles) * kBlock, &starts));
+    RowPairs rp{};
+    int row_grid = 0;
+    if (row_pass) {
+        // at most kRowPassMaxBlocks workgroups of kPartBlock threads, at least 16 rows each
+        const long long per_thread = std::max<long long>(
+            16, (static_cast<long long>(rows) + kPartBlock * kRowPassMaxBlocks - 1) /
+                    (kPartBlock * kRowPassMaxBlocks));
+        const long long per_block = per_thread * kPartBlock;
+        row_grid = static_cast<int>(std::max<long long>(1, (rows + per_block - 1) / per_block));
+        rp.rows_per_thread = static_cast<int>(per_thread);
+        rp.nb = row_grid;
+        // record regions by row, or by the entries of the operand with fewer of them
+        const long long by_rows = static_cast<long long>(row_grid) * per_block;
+        const long long by_entries = std::min<long long>(A.len, B.len);
+        rp.px = by_entries < by_rows ? (A.len <= B.len ? A.pos : B.pos) : nullptr;
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(std::max<long long>(
+                                     1, std::min(by_rows, by_entries))),
+                                 &rp.rec));
+        int *words = nullptr;
+        NACHO_TRY(call.scratch_n(3 * static_cast<size_t>(row_grid) + 1, &words));
+        rp.blk_base = words;
+        rp.blk_elems = words + row_grid;
+        rp.blk_recs = words + 2 * row_grid;
+        rp.mode = words + 3 * row_grid;
+    }
     // The count kernel's own grid: as many workgroups as it keeps resident (it holds less
     // state than the write kernel, and needs the extra loads in flight).
     int count_resident = 0;
@@ -1133,18 +1400,19 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
     if (count_chunk > kMaxChunk) count_chunk = kMaxChunk;
     const int count_grid = (num_tiles + count_chunk - 1) / count_chunk;
     NACHO_TRY(call.timer_start(kernel_name));  // the whole device pipeline of this level
-    csr_partition_kernel<<<ceil_div(static_cast<size_t>(num_tiles) + 1, kPartBlock), kPartBlock, 0, s>>>(
+    const int part_blocks = static_cast<int>(ceil_div(static_cast<size_t>(num_tiles) + 1, kPartBlock));
+    csr_partition_kernel<<<part_blocks + row_grid, kPartBlock, 0, s>>>(
         A.pos, A.crd, B.pos, B.crd, rows, static_cast<int>(total), num_tiles, split_r, split_a,
-        split_b, done, counts, grid);
+        split_b, done, counts, grid, part_blocks, rp);
     NACHO_TRY_HIP(hipGetLastError());
     if (keep_starts) {
         csr_pair_count_kernel<true><<<count_grid, kBlock, 0, s>>>(
             A.pos, A.crd, B.pos, B.crd, mis, num_tiles, count_chunk, chunk, split_r, split_a,
-            split_b, counts, done, length_out, starts);
+            split_b, counts, done, length_out, starts, RowPairs{}, grid, items);
     } else {
         csr_pair_count_kernel<false><<<count_grid, kBlock, 0, s>>>(
             A.pos, A.crd, B.pos, B.crd, mis, num_tiles, count_chunk, chunk, split_r, split_a,
-            split_b, counts, done, length_out, nullptr);
+            split_b, counts, done, length_out, nullptr, rp, grid, items);
     }
     NACHO_TRY_HIP(hipGetLastError());
     NACHO_TRY(call.mark_length());
@@ -1152,16 +1420,10 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
     csr_write_kernel<OPV, kItemsPerLane, VAL, CHD, false, SRCH><<<grid, kBlock, 0, s>>>(         \
         A.pos, A.crd, A.val, B.pos, B.crd, B.val, A.len, B.len, num_tiles, chunk, split_r,      \
         split_a, split_b, counts, rows, Z.pos, Z.crd, Z.val, A.next, B.next, Z.child_a,         \
-        Z.child_b, length, 0, nullptr, nullptr, nullptr, nullptr, starts)
+        Z.child_b, length, 0, nullptr, nullptr, nullptr, nullptr, starts, rp.mode)
     if (values) {
         if (child) return NACHO_ERR_INVALID_ARGUMENT;
-        if (keep_starts) {
-            NACHO_WRITE_LAUNCH(Op::Union, true, false, false);
-        } else {
-            NACHO_WRITE_LAUNCH(Op::Union, true, false, true);
-        }
-    } else if (!keep_starts) {
-        return NACHO_ERR_INVALID_ARGUMENT;  // only value levels run without stored starts
+        NACHO_WRITE_LAUNCH(Op::Union, true, false, true);
     } else if (child) {
         NACHO_WRITE_LAUNCH(Op::Union, false, true, false);
     } else {
@@ -1298,7 +1560,7 @@ int csr_add_noalloc(const nacho_csr *a, const nacho_csr *b, nacho_csr *z, int32_
     const LevelResult Z{pc, cc, vc, nullptr, nullptr};
     long long nnz = 0;
     NACHO_TRY(merge_level(call, false, true, false, rows, A, B, Z, &nnz,
-                          "csr_add (no-alloc): partition+count+write", false));
+                          "csr_add (no-alloc): partition+count+write", UnionCount::kTileWalk));
     if (nnz > nnz_a + nnz_b) return NACHO_ERR_MALFORMED_INPUT;
     z->dim_i_size = rows;
     z->dim_j_size = a->dim_j_size;

@@ -29,16 +29,27 @@ struct LevelResult {
     int *child_b;
 };
 
+// How a union level counts its output before writing it.
+enum class UnionCount {
+    // Levels without values: a tile walk that also stores every lane's walk start for the
+    // write pass (8 bytes per lane and tile).  Value levels: a row pass finds the rows where
+    // both operands have entries and chooses, on the device, between searching those rows'
+    // smaller sides for pairs (few such entries) and the tile walk; the write pass searches
+    // for its lanes' starts.
+    kAuto,
+    // Value levels only: the tile walk without lane starts and no row pass, so that scratch
+    // stays at a few bytes per tile (an arena Call).
+    kTileWalk,
+};
+
 // Merge A and B row by row: union (or intersection) of each row's coordinates, with values
 // (a+b / a*b / copies) when `values`, or with child pointers when `child`.  Writes Z.pos for
 // every row and returns the result length in *out_len.  The call's kernel timer (if enabled)
-// brackets all of the level's kernels under `kernel_name`.  A union level stores every
-// lane's walk start for its write pass (8 bytes per lane and tile) unless `keep_starts` is
-// false (value levels only): the write pass then searches for them, and scratch stays at a
-// few bytes per tile.
+// brackets all of the level's kernels under `kernel_name`.
 int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
                 const LevelOperand &A, const LevelOperand &B, const LevelResult &Z,
-                long long *out_len, const char *kernel_name, bool keep_starts = true);
+                long long *out_len, const char *kernel_name,
+                UnionCount count = UnionCount::kAuto);
 
 // Bytes of scratch merge_level takes from an arena Call for a union level of `items` merge
 // items (entries of both operands plus rows) without lane starts.

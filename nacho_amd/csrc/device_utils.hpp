@@ -139,5 +139,15 @@ __device__ __forceinline__ void add_to_total(uint32_t part, unsigned long long *
     }
 }
 
+// The same, storing `from` minus the total (a result length counted as the operands'
+// entries less the pairs that merge).
+__device__ __forceinline__ void subtract_total(uint32_t part, unsigned long long *acc,
+                                               int64_t from, int64_t *out) {
+    const unsigned long long prev = atomicAdd(acc, (1ull << 32) | part);
+    if ((prev >> 32) == gridDim.x - 1) {
+        *out = from - static_cast<int64_t>((prev + part) & 0xffffffffull);
+    }
+}
+
 }  // namespace dev
 }  // namespace nacho
