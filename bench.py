@@ -64,16 +64,17 @@ PEAK_HBM_GBS = 8000.0
 ROTATE = 4  # independent operand copies cycled through by the timed steps
 
 WORKLOADS = {
-    "c2": dict(op="add", kernel="csr_partition_kernel + csr_count_kernel<Union> + "
-                              "csr_write_kernel<Union> (one call's device pipeline)",
+    "c2": dict(op="add", kernel="csr_partition_kernel (with the row pass) + "
+                              "csr_pair_count_kernel (pair search) + csr_write_kernel<Union> "
+                              "(one call's device pipeline)",
                desc="C2 csr_add f32 2^20x2^20, Zipf(1.6) rows rescaled to mean 16 "
                     "(16.7M nnz each), seeds 1/2"),
-    "c3": dict(op="mul", kernel="csr_partition_kernel + csr_count_kernel<Intersect> + "
-                              "csr_write_kernel<Intersect> (one call's device pipeline)",
+    "c3": dict(op="mul", kernel="csr_partition_kernel + csr_write_kernel<Intersect> (spread) "
+                              "+ csr_compact_kernel (one call's device pipeline)",
                desc="C3 csr_mul f32 2^20x2^20, A as C2, B = 50% of A + fresh columns "
                     "(seed 3)"),
     "c5": dict(op="csf_add", kernel="three chained level merges (csr_partition_kernel + "
-                                   "csr_count_kernel + csr_write_kernel per level)",
+                                   "csr_pair_count_kernel + csr_write_kernel per level)",
                desc="C5 csf_add f32, two CSF3 tensors of shape (200000, 100000, 1000), 20M "
                     "draws each (mode 0 Zipf(1.3), modes 1-2 uniform), deduplicated, seeds 1/2"),
     "c5coo": dict(op="coo3d_add", kernel="coo_partition_kernel + coo_count_kernel + "
@@ -90,7 +91,7 @@ WORKLOADS = {
                    desc="csr_add_3 f32: three C2 operands (Zipf(1.6) rows, 16.7M nnz each, "
                         "seeds 1, 2, 4)"),
     "c2dcsr": dict(op="dcsr_add", kernel="two chained level merges (csr_partition_kernel + "
-                                        "csr_count_kernel + csr_write_kernel per level)",
+                                        "csr_pair_count_kernel + csr_write_kernel per level)",
                    desc="C2 as DCSR: dcsr_add f32 of the C2 operands with empty rows "
                         "dropped"),
     "c3dcsr": dict(op="dcsr_mul", kernel="two chained level merges + row compaction",

@@ -16,11 +16,16 @@
 //    tile*kTile by a binary search over rows on S(r) = posA[r] + posB[r] + r, then a
 //    merge-path search inside the row.  An A/B pair with equal coordinates is never split
 //    across tiles (the reference's balancing step, partition.cpp:964-983).
-//  * csr_count_kernel and csr_write_kernel: each workgroup owns a fixed, contiguous chunk of
-//    tiles.  The count kernel reads only coordinates and row offsets and stores the chunk's
-//    output count; the write kernel starts from the sum of the preceding chunks' counts and
-//    carries a running offset through its tiles.  No workgroup ever waits on another (an
-//    earlier single-pass design with decoupled look-back spent most of its time waiting).
+//  * csr_pair_count_kernel and csr_write_kernel: each workgroup owns a fixed, contiguous
+//    chunk of tiles.  The count kernel reads only coordinates and row offsets and adds each
+//    write chunk's output count (a union tile emits na + nb - pairs); the write kernel starts
+//    from the sum of the preceding chunks' counts and carries a running offset through its
+//    tiles.  No workgroup ever waits on another (an earlier single-pass design with
+//    decoupled look-back spent most of its time waiting).
+//  * A union value level first runs a row pass (extra workgroups of the partition launch)
+//    over the rows where both operands have entries; when those hold few entries, the count
+//    kernel searches each of them in the other operand's row instead of walking the tiles
+//    (pair_search), and the write kernel derives its chunk offsets from the splits.
 //  * Inside a tile (both kernels): the tile's crd/val ranges of A and B and a packed word per
 //    row are staged in LDS from registers that were loaded one tile ahead; lane t owns items
 //    [t*IPT, (t+1)*IPT) of the tile, found by a merge-path search in LDS, and walks them in a
@@ -318,13 +323,18 @@ __device__ __forceinline__ void stage_tile(const Staged<LOADS> &st, const TileSp
 
 // This lane's first row (tile-local) from the row-start bins of the tile staged with `tag`
 // (see stage_tile): the largest row recorded at or before this lane.  Call after the barrier
-// that ends the staging.  One barrier inside; `s_wave` must not be written again before the
-// caller's next barrier.
-__device__ __forceinline__ int lane_first_row(const unsigned *s_bin, unsigned tag, int *s_wave,
-                                              int tid) {
-    const unsigned v = s_bin[tid];
-    const int mine = (v >> 16) == tag ? static_cast<int>(v & 0xffffu) : 0;
-    return max(mine, dev::block_exclusive_max<false>(mine, s_wave));
+// that ends the staging.  No barrier: each wave reads the earlier waves' bins itself (at most
+// three per lane) and takes their maximum along with its own running maximum.
+__device__ __forceinline__ int lane_first_row(const unsigned *s_bin, unsigned tag, int tid) {
+    auto row_at = [&](int i) {
+        const unsigned v = s_bin[i];
+        return (v >> 16) == tag ? static_cast<int>(v & 0xffffu) : 0;
+    };
+    const int w = tid / dev::kWave, l = tid % dev::kWave;
+    int before = 0;
+    for (int j = 0; j < w; ++j) before = max(before, row_at(j * dev::kWave + l));  // uniform
+    before = __builtin_amdgcn_readlane(dev::wave_inclusive_max_dpp(before), dev::kWave - 1);
+    return max(before, dev::wave_inclusive_max_dpp(row_at(tid)));
 }
 
 // ---- one lane's walk -------------------------------------------------------------------
@@ -491,75 +501,6 @@ __device__ __forceinline__ T block_sum(T v, T *s_wave) {
     for (int i = 0; i < WAVES; ++i) all += s_wave[i];
     __syncthreads();
     return all;
-}
-
-// Output count of each chunk (coordinates and row offsets only), and their sum, the result
-// length, stored to `length_out` by the last workgroup.  Every lane's walk start (found by
-// its search) goes to starts[tile * kBlock + lane] for the write kernel.
-template <Op OP, int IPT>
-// (At most 128 VGPRs: four waves per SIMD, which its LDS use also allows.)
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) void csr_count_kernel(
-    const int *__restrict__ pa, const int *__restrict__ ca, const int *__restrict__ pb,
-    const int *__restrict__ cb, int num_tiles, int chunk, const int *__restrict__ split_r,
-    const int *__restrict__ split_a, const int *__restrict__ split_b,
-    unsigned *__restrict__ chunk_count, unsigned long long *__restrict__ done,
-    int64_t *__restrict__ length_out, uint2 *__restrict__ starts) {
-    constexpr int kCap = kBlock * IPT + 2;
-    constexpr int kLoads = (kCap + kBlock - 1) / kBlock;
-    static_assert(kCap < 65536, "row offsets are packed in 16 bits");
-    __shared__ int s_crd[kCap];
-    __shared__ unsigned s_row[kCap];
-    __shared__ unsigned s_wave[kBlock / dev::kWave];
-    __shared__ int s_wmax[kBlock / dev::kWave];
-    __shared__ unsigned s_bin[kBlock];  // row-start bins (see stage_tile)
-    __shared__ int s_split[3 * (kMaxChunk + 1)];
-
-    const int tid = threadIdx.x;
-    int t0, t1;
-    chunk_range(num_tiles, chunk, t0, t1);
-    if (t0 >= t1) {
-        if (tid == 0) {
-            chunk_count[blockIdx.x] = 0u;
-            dev::add_to_total(0u, done, length_out);
-        }
-        return;
-    }
-    s_bin[tid] = 0u;
-    stage_splits(s_split, split_r, split_a, split_b, t0, t1);
-    __syncthreads();
-    TileSplit sp = lds_split(s_split, 0);
-    Staged<kLoads> st;
-    fetch_tile<false, kLoads>(st, sp, pa, ca, nullptr, pb, cb, nullptr, tid);
-    stage_tile<false, kLoads, IPT>(st, sp, s_crd, nullptr, s_row, tid, s_bin, 1u, t0 * kBlock * IPT);
-    __syncthreads();
-    LaneStart start{static_cast<unsigned>(lane_first_row(s_bin, 1u, s_wmax, tid)), 0u};
-    TileSplit nsp = lds_split(s_split, t0 + 1 < t1 ? 1 : 0);
-    unsigned mine = 0;  // this lane's outputs over the chunk
-    for (int t = t0; t < t1; ++t) {
-        fetch_tile<false, kLoads>(st, nsp, pa, ca, nullptr, pb, cb, nullptr, tid);
-        const TileSplit nsp2 = lds_split(s_split, t + 2 < t1 ? t + 2 - t0 : t + 1 < t1 ? t + 1 - t0 : t - t0);
-        LaneOut<IPT + 1> lo;
-        walk_lane<OP, false, false, IPT, Start::RowGiven>(lo, sp, t, s_crd, nullptr, s_row, tid,
-                                                          start);
-        if (starts) starts[static_cast<size_t>(t) * kBlock + tid] = make_uint2(start.k_ia, start.ib);
-        mine += static_cast<unsigned>(__popc(lo.valid));  // summed over the chunk at the end
-        if (t + 1 < t1) {
-            __syncthreads();  // every lane is done reading this tile's LDS
-            const unsigned tag = static_cast<unsigned>(t + 2 - t0);
-            stage_tile<false, kLoads, IPT>(st, nsp, s_crd, nullptr, s_row, tid, s_bin, tag,
-                                           (t + 1) * kBlock * IPT);
-            __syncthreads();
-            start = LaneStart{static_cast<unsigned>(lane_first_row(s_bin, tag, s_wmax, tid)), 0u};
-        }
-        sp = nsp;
-        nsp = nsp2;
-    }
-    const unsigned total = block_sum<kBlock / dev::kWave>(mine, s_wave);
-    if (tid == 0) {
-        chunk_count[blockIdx.x] = total;
-        // The last workgroup to finish stores the result length (the sum of every chunk).
-        dev::add_to_total(total, done, length_out);
-    }
 }
 
 // ---- pair count: the union's count pass ----------------------------------------------
@@ -1089,7 +1030,6 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
     __shared__ int s_split[3 * (kMaxChunk + 1)];
     constexpr bool kOwn = SPREAD || SEARCH;  // lanes find their own starts
     __shared__ unsigned s_bin[kOwn ? kBlock : 1];  // row-start bins (see stage_tile)
-    __shared__ int s_wmax[kBlock / dev::kWave];
 
     const int tid = threadIdx.x;
     int t0, t1;
@@ -1143,7 +1083,7 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
         const uint2 v = starts[static_cast<size_t>(t0) * kBlock + tid];
         cur = LaneStart{v.x, v.y};
     } else {
-        cur = LaneStart{static_cast<unsigned>(lane_first_row(s_bin, 1u, s_wmax, tid)), 0u};
+        cur = LaneStart{static_cast<unsigned>(lane_first_row(s_bin, 1u, tid)), 0u};
     }
     for (int t = t0; t < t1; ++t) {
         fetch_tile<VALUES, kLoads>(st, nsp, pa, ca, va, pb, cb, vb, tid);
@@ -1224,7 +1164,7 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
                                                 (t + 1) * kBlock * IPT);
             __syncthreads();
             if (!kGiven) {
-                cur = LaneStart{static_cast<unsigned>(lane_first_row(s_bin, tag, s_wmax, tid)),
+                cur = LaneStart{static_cast<unsigned>(lane_first_row(s_bin, tag, tid)),
                                 0u};
             }
         }
