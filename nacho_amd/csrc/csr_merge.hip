@@ -101,6 +101,10 @@ constexpr int kModeCount = 0;
 constexpr int kModeSearch = 1;
 constexpr int kSearchRatio = 16;
 constexpr int kRowPassMaxBlocks = 1024;  // workgroups of the row pass (a multiple of kBlock)
+// The row pass reads two offsets per row, so it runs only where rows hold this many entries
+// on average: with about one entry per row (a CSF3 k level) its reads cost as much as the
+// tile walk it may save, and the few entries per row make the walk's lane starts cheap.
+constexpr int kRowPassMinEntriesPerRow = 8;
 
 struct RowPairs {
     // records of row-pass workgroup b at rec[blk_base[b] + k], k < blk_recs[b]:
@@ -1299,9 +1303,11 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
     NACHO_TRY(misalign(A.pos, &mis.pa));
     NACHO_TRY(misalign(B.pos, &mis.pb));
     if (!values && count_plan != UnionCount::kAuto) return NACHO_ERR_INVALID_ARGUMENT;
-    const bool keep_starts = !values;  // levels without values: stored lane starts
-    const bool row_pass = values && count_plan == UnionCount::kAuto;
     const long long items = static_cast<long long>(A.len) + B.len;
+    const bool row_pass = values && count_plan == UnionCount::kAuto &&
+                          static_cast<long long>(rows) * kRowPassMinEntriesPerRow <= items;
+    // stored lane starts: levels without values, and value levels that skip the row pass
+    const bool keep_starts = !values || (count_plan == UnionCount::kAuto && !row_pass);
     uint2 *starts = nullptr;
     if (keep_starts) NACHO_TRY(call.scratch_n(static_cast<size_t>(num_tiles) * kBlock, &starts));
     RowPairs rp{};
@@ -1363,7 +1369,11 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
         Z.child_b, length, 0, nullptr, nullptr, nullptr, nullptr, starts, rp.mode)
     if (values) {
         if (child) return NACHO_ERR_INVALID_ARGUMENT;
-        NACHO_WRITE_LAUNCH(Op::Union, true, false, true);
+        if (keep_starts) {
+            NACHO_WRITE_LAUNCH(Op::Union, true, false, false);
+        } else {
+            NACHO_WRITE_LAUNCH(Op::Union, true, false, true);
+        }
     } else if (child) {
         NACHO_WRITE_LAUNCH(Op::Union, false, true, false);
     } else {

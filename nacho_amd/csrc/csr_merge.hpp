@@ -32,10 +32,11 @@ struct LevelResult {
 // How a union level counts its output before writing it.
 enum class UnionCount {
     // Levels without values: a tile walk that also stores every lane's walk start for the
-    // write pass (8 bytes per lane and tile).  Value levels: a row pass finds the rows where
-    // both operands have entries and chooses, on the device, between searching those rows'
-    // smaller sides for pairs (few such entries) and the tile walk; the write pass searches
-    // for its lanes' starts.
+    // write pass (8 bytes per lane and tile).  Value levels whose rows hold at least 8
+    // entries on average: a row pass finds the rows where both operands have entries and
+    // chooses, on the device, between searching those rows' smaller sides for pairs (few
+    // such entries) and the tile walk; the write pass searches for its lanes' starts.
+    // Value levels with shorter rows: the tile walk with stored lane starts.
     kAuto,
     // Value levels only: the tile walk without lane starts and no row pass, so that scratch
     // stays at a few bytes per tile (an arena Call).
