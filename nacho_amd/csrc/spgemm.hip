@@ -15,26 +15,31 @@
 //      column into nb buckets of 2^shift columns (one device-wide radix digit, k >> shift);
 //      each bucket is a segment.  Segments are numbered row-major, bucket-minor, so their
 //      concatenation in order is every row's products grouped by column range.
-//   3. histogram: a long row's products per column bucket, summed over its A entries from
-//      the runs of equal bucket in B's rows (no product is visited); scan of segment lengths.
-//      Scatter: chunks of kChunk consecutive products decode their (A entry, row) with a
-//      load-balanced search in LDS, gather (k, a_ij * b_jk) from B with coalesced loads and
-//      write them into their segment (ranges reserved per chunk with one atomic per
-//      segment; short rows keep natural order).
+//   3. expand to runs: a product (k, a_ij * b_jk) is never written to memory.  B's rows are
+//      cut into runs of equal column bucket; a segment's products are the concatenation of
+//      its runs, each run one A entry times a contiguous range of one B row, described by
+//      {first B entry, length, a_ij} (a short row's runs are its A entries' whole B rows, in
+//      natural order; a long row's runs of bucket b come from B's run table).  A histogram
+//      over B's runs gives each long-row segment's products and runs without visiting a
+//      product; scans give segment product offsets and run offsets; the run descriptors are
+//      then written per segment (4.4e8 of 16 bytes at C4, against 6.0e9 products of 8).
 //   4. units: a segment with more than kShort products is a dense unit; smaller segments
 //      whose first product falls in the same kShort-aligned window share one sort unit
-//      (fewer than 2*kShort products).  Each kind gets a compacted work list.
-//   5. reduce: a sort unit sorts (segment ordinal, k) in LDS and sums each run in float64;
-//      a dense unit accumulates its 2^shift-column range in an LDS float64 array (windows of
-//      kDenseCols columns) and compacts the touched columns in order.  Both write the
-//      distinct (k, sum rounded once to float32) at the unit's product offset in a second
-//      buffer and record the unit's count and the local offset of every row starting in it.
+//      (fewer than 2*kShort products), or one bitmap unit when they are at most
+//      kMaxBitmapBuckets narrow column buckets of long rows.  Each kind gets a compacted list.
+//   5. reduce: a unit expands its runs, gathering (k, a_ij * b_jk) from B.  A sort unit sorts
+//      (segment ordinal, k) in LDS and sums each run of equal keys in float64; a bitmap unit
+//      ranks each bucket's columns in an LDS bitmap and sums by rank; a dense unit accumulates
+//      its 2^shift-column range in an LDS float64 array (windows of kDenseCols columns) and
+//      compacts the touched columns in order.  All write the distinct (k, sum rounded once to
+//      float32) at the unit's product offset in an output staging buffer and record the
+//      unit's count and the local offset of every row starting in it.
 //   6. output: scan of unit counts -> result offsets; copy each unit's entries; row offsets
 //      from the unit offsets.  Every distinct column is kept (structural result, as the
 //      reference).
-// Summation order inside a segment follows the scatter's arrival order and LDS atomics, so
-// values are reproducible to within one float32 rounding of the float64 sum (the reference's
-// own order is not deterministic either).
+// Summation order inside a segment follows the runs' order and LDS atomics, so values are
+// reproducible to within one float32 rounding of the float64 sum (the reference's own order
+// is not deterministic either).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -49,7 +54,6 @@ namespace nacho {
 namespace spgemm {
 
 constexpr int kBlock = 256;
-constexpr int kChunk = 4096;            // products per histogram / scatter workgroup
 constexpr int kTile = 4096;             // LDS capacity of a sort unit
 constexpr int kPer = kTile / kBlock;    // 16 positions per lane
 constexpr int kShort = kTile / 2;       // segments with at most this many products are sorted
@@ -58,15 +62,15 @@ constexpr int kDenseBits = 13;          // dense accumulation window: 8192 colum
 constexpr int kDenseCols = 1 << kDenseBits;
 constexpr int kMaxBucketBits = 10;      // at most 1024 column buckets per long row
 constexpr int kMaxBuckets = 1 << kMaxBucketBits;
-constexpr int kMaxLongPerChunk = 3;     // rows longer than kShort meeting one chunk
 constexpr int kDenseMin = kShort;       // a long row's bucket above this is accumulated densely
 constexpr int kMaxBitmapSegs = 256;     // segments (empty ones included) of a bitmap unit
 constexpr int kMaxBitmapBuckets = 16;   // nonempty buckets of a bitmap unit (larger buckets)
 constexpr int kBitmapWords = 8192 / 32; // one bit per column of an 8192-column bucket
+constexpr int kBitmapBlock = 512;       // threads of a bitmap unit's workgroup
 constexpr int kHistGrid = 8192;         // workgroups of the long-row histogram
 
 static_assert(kTile == 1 << kOrdBits, "segment ordinals must fit kOrdBits");
-static_assert(kChunk == kBlock * kPer, "chunk decode assumes kPer products per lane");
+static_assert(kTile == kBlock * kPer, "a unit's products are kPer per lane");
 
 // ---- small device helpers --------------------------------------------------------------
 
@@ -103,18 +107,25 @@ __global__ void rows_kernel(const int *__restrict__ pos_a, int rows,
     }
 }
 
-// Segment table: row of each segment, lengths (short rows known now, long rows counted by the
-// histogram pass) and the scatter's fill counters.
+// Segment table: row of each segment, product and run counts (short rows known now: one run
+// per A entry whose B row is not empty; long rows counted by the histogram pass) and the
+// zeroed fill counters of the long rows' run emission.
 __global__ void segments_kernel(const int64_t *__restrict__ row_off,
                                 const int64_t *__restrict__ seg_prefix, int rows,
+                                const int *__restrict__ pos_a, const int64_t *__restrict__ len,
                                 int *__restrict__ seg_row, int64_t *__restrict__ seg_len,
-                                int64_t *__restrict__ seg_fill) {
+                                int64_t *__restrict__ seg_runs, int64_t *__restrict__ seg_fill) {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < rows; i += gridDim.x * blockDim.x) {
         const int64_t s0 = seg_prefix[i], s1 = seg_prefix[i + 1];
         const int64_t prod = row_off[i + 1] - row_off[i];
+        int64_t runs = 0;
+        if (prod > 0 && prod <= kShort) {
+            for (int p = pos_a[i]; p < pos_a[i + 1]; ++p) runs += len[p] > 0 ? 1 : 0;
+        }
         for (int64_t s = s0; s < s1; ++s) {
             seg_row[s] = i;
             seg_len[s] = prod > kShort ? 0 : prod;
+            seg_runs[s] = runs;
             seg_fill[s] = 0;
         }
     }
@@ -191,241 +202,253 @@ __global__ void hist_rows_kernel(const int64_t *__restrict__ blk_off, int rows,
     }
 }
 
+// B row k's runs, packed (bucket, length) in run[] and first entries in run_start[].
+struct BRuns {
+    const int64_t *run_idx;  // B row k's runs are [run_idx[pos_b[k]], run_idx[pos_b[k + 1]])
+    const int2 *run;
+    const int *run_start;
+};
+
 // Work blocks strided over the grid (a heavy row's blocks land on different workgroups):
-// every thread takes one A entry of the block and adds the lengths of its B row's runs to
-// an LDS histogram of the row's buckets; nonzero bins are then added to the row's seg_len
-// (zeroed by segments_kernel), stored directly when the row has a single block.
+// every thread takes one A entry of the block and adds, per run of its B row, the run's
+// length and one run to LDS histograms of the row's buckets; nonzero bins are then added to
+// the row's seg_len and seg_runs (zeroed by segments_kernel), stored directly when the row
+// has a single block.
 __global__ __launch_bounds__(kBlock) void long_hist_kernel(
     const int *__restrict__ pos_a, const int *__restrict__ crd_a,
     const int64_t *__restrict__ blk_off, const int *__restrict__ blk_row, int rows,
-    const int *__restrict__ pos_b, const int64_t *__restrict__ run_idx,
-    const int2 *__restrict__ run, int nb, const int64_t *__restrict__ seg_prefix,
-    int64_t *__restrict__ seg_len) {
+    const int *__restrict__ pos_b, BRuns br, int nb, const int64_t *__restrict__ seg_prefix,
+    int64_t *__restrict__ seg_len, int64_t *__restrict__ seg_runs) {
     __shared__ int s_hist[kMaxBuckets];
+    __shared__ int s_runs[kMaxBuckets];
     const int64_t n_blk = blk_off[rows];
     for (int64_t blk = blockIdx.x; blk < n_blk; blk += gridDim.x) {
         const int i = blk_row[blk];
         const int64_t first = blk_off[i];
-        for (int b = threadIdx.x; b < nb; b += kBlock) s_hist[b] = 0;
+        for (int b = threadIdx.x; b < nb; b += kBlock) {
+            s_hist[b] = 0;
+            s_runs[b] = 0;
+        }
         __syncthreads();
         const int p = pos_a[i] + static_cast<int>(blk - first) * kBlock + threadIdx.x;
         if (p < pos_a[i + 1]) {
             const int k = crd_a[p];
-            const int64_t q0 = run_idx[pos_b[k]];
-            const int n_runs = static_cast<int>(run_idx[pos_b[k + 1]] - q0);
-            const int2 *r = run + q0;
+            const int64_t q0 = br.run_idx[pos_b[k]];
+            const int n_runs = static_cast<int>(br.run_idx[pos_b[k + 1]] - q0);
+            const int2 *r = br.run + q0;
             // four runs per iteration, so that four loads are in flight
             int j = 0;
             for (; j + 4 <= n_runs; j += 4) {
                 const int2 x0 = r[j], x1 = r[j + 1], x2 = r[j + 2], x3 = r[j + 3];
-                if (x0.x < nb) atomicAdd(&s_hist[x0.x], x0.y);
-                if (x1.x < nb) atomicAdd(&s_hist[x1.x], x1.y);
-                if (x2.x < nb) atomicAdd(&s_hist[x2.x], x2.y);
-                if (x3.x < nb) atomicAdd(&s_hist[x3.x], x3.y);
+                if (x0.x < nb) { atomicAdd(&s_hist[x0.x], x0.y); atomicAdd(&s_runs[x0.x], 1); }
+                if (x1.x < nb) { atomicAdd(&s_hist[x1.x], x1.y); atomicAdd(&s_runs[x1.x], 1); }
+                if (x2.x < nb) { atomicAdd(&s_hist[x2.x], x2.y); atomicAdd(&s_runs[x2.x], 1); }
+                if (x3.x < nb) { atomicAdd(&s_hist[x3.x], x3.y); atomicAdd(&s_runs[x3.x], 1); }
             }
             for (; j < n_runs; ++j) {
                 const int2 x = r[j];
-                if (x.x < nb) atomicAdd(&s_hist[x.x], x.y);
+                if (x.x < nb) {
+                    atomicAdd(&s_hist[x.x], x.y);
+                    atomicAdd(&s_runs[x.x], 1);
+                }
             }
         }
         __syncthreads();
         const int64_t s0 = seg_prefix[i];
         const bool alone = blk_off[i + 1] - first == 1;
         for (int b = threadIdx.x; b < nb; b += kBlock) {
-            const int c = s_hist[b];
+            const int c = s_hist[b], n = s_runs[b];
             if (alone) {
                 seg_len[s0 + b] = c;
+                seg_runs[s0 + b] = n;
             } else if (c > 0) {
                 atomicAdd(reinterpret_cast<unsigned long long *>(&seg_len[s0 + b]),
                           static_cast<unsigned long long>(c));
+                atomicAdd(reinterpret_cast<unsigned long long *>(&seg_runs[s0 + b]),
+                          static_cast<unsigned long long>(n));
             }
         }
-        __syncthreads();  // the histogram is read before the next block clears it
+        __syncthreads();  // the histograms are read before the next block clears them
     }
 }
 
-// ---- 3b: scatter over product chunks ----------------------------------------------------
+// ---- 3b: run descriptors -----------------------------------------------------------------
 
-struct ChunkHeader {
-    int64_t p_lo;  // A entry of the chunk's first product
-    int r_lo;      // row of the chunk's first product
-    int n_long;    // long rows meeting the chunk
-    int long_row[kMaxLongPerChunk];
-};
+// A run of products: B entries [x, x + y) times the A value with bits z (w unused).
+__device__ __forceinline__ int4 make_run(int first, int length, float a) {
+    return make_int4(first, length, __float_as_int(a), 0);
+}
 
-// Per chunk of kChunk products: the A entries and rows of its first and last products
-// (searched here for all chunks at once rather than serially at each chunk's start).
-__global__ void chunk_bounds_kernel(const int64_t *__restrict__ off, int64_t nnz_a,
-                                    const int64_t *__restrict__ row_off, int rows, int64_t P,
-                                    int64_t chunks, int *__restrict__ bounds) {
-    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
-         i < 2 * chunks; i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        const int64_t c = i >> 1;
-        const int64_t q = (i & 1) ? min((c + 1) * kChunk, P) - 1 : c * kChunk;
-        bounds[4 * c + (i & 1)] = static_cast<int>(last_le(off, 0, nnz_a - 1, q));
-        bounds[4 * c + 2 + (i & 1)] = static_cast<int>(last_le(row_off, 0, rows - 1, q));
+// Long rows: the same work blocks as the histogram.  Each bucket's runs from the block are
+// counted in LDS, a range of the segment's run slots is reserved with one atomic per
+// nonempty bucket (none when the row has a single block), and every run is written at the
+// next slot of its bucket's range.  The order of runs inside a segment is free: the reduce
+// is order-independent (up to float64 rounding).  (Staging a block's runs in LDS to store
+// each bucket's range coalesced cost more in occupancy than it saved: 8.4 -> 12.6 ms at C4.)
+__global__ __launch_bounds__(kBlock) void long_runs_kernel(
+    const int *__restrict__ pos_a, const int *__restrict__ crd_a, const float *__restrict__ val_a,
+    const int64_t *__restrict__ blk_off, const int *__restrict__ blk_row, int rows,
+    const int *__restrict__ pos_b, BRuns br, int nb, const int64_t *__restrict__ seg_prefix,
+    const int64_t *__restrict__ seg_roff, int64_t *__restrict__ seg_fill,
+    int4 *__restrict__ desc) {
+    __shared__ int s_cnt[kMaxBuckets];
+    __shared__ int64_t s_base[kMaxBuckets];
+    const int64_t n_blk = blk_off[rows];
+    for (int64_t blk = blockIdx.x; blk < n_blk; blk += gridDim.x) {
+        const int i = blk_row[blk];
+        const int64_t first = blk_off[i];
+        for (int b = threadIdx.x; b < nb; b += kBlock) s_cnt[b] = 0;
+        __syncthreads();
+        const int p = pos_a[i] + static_cast<int>(blk - first) * kBlock + threadIdx.x;
+        const bool mine = p < pos_a[i + 1];
+        int64_t q0 = 0;
+        int n_runs = 0;
+        float a = 0.0f;
+        if (mine) {
+            const int k = crd_a[p];
+            a = val_a[p];
+            q0 = br.run_idx[pos_b[k]];
+            n_runs = static_cast<int>(br.run_idx[pos_b[k + 1]] - q0);
+            const int2 *rr = br.run + q0;
+            int j = 0;
+            for (; j + 4 <= n_runs; j += 4) {  // four loads in flight
+                const int b0 = rr[j].x, b1 = rr[j + 1].x, b2 = rr[j + 2].x, b3 = rr[j + 3].x;
+                if (b0 < nb) atomicAdd(&s_cnt[b0], 1);
+                if (b1 < nb) atomicAdd(&s_cnt[b1], 1);
+                if (b2 < nb) atomicAdd(&s_cnt[b2], 1);
+                if (b3 < nb) atomicAdd(&s_cnt[b3], 1);
+            }
+            for (; j < n_runs; ++j) {
+                const int bk = rr[j].x;
+                if (bk < nb) atomicAdd(&s_cnt[bk], 1);
+            }
+        }
+        __syncthreads();
+        const int64_t s0 = seg_prefix[i];
+        const bool alone = blk_off[i + 1] - first == 1;
+        for (int b = threadIdx.x; b < nb; b += kBlock) {
+            const int c = s_cnt[b];
+            int64_t at = 0;
+            if (c > 0 && !alone) {
+                at = static_cast<int64_t>(atomicAdd(
+                    reinterpret_cast<unsigned long long *>(&seg_fill[s0 + b]),
+                    static_cast<unsigned long long>(c)));
+            }
+            s_base[b] = seg_roff[s0 + b] + at;
+            s_cnt[b] = 0;
+        }
+        __syncthreads();
+        for (int j0 = 0; j0 < n_runs; j0 += 4) {  // four runs' loads in flight
+            int2 x[4];
+            int first_b[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int64_t q = q0 + min(j0 + u, n_runs - 1);
+                x[u] = br.run[q];
+                first_b[u] = br.run_start[q];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                if (j0 + u < n_runs && x[u].x < nb) {
+                    const int64_t slot = s_base[x[u].x] + atomicAdd(&s_cnt[x[u].x], 1);
+                    desc[slot] = make_run(first_b[u], x[u].y, a);
+                }
+            }
+        }
+        __syncthreads();  // s_cnt and s_base are read before the next block resets them
     }
 }
 
-// Load-balanced search for the chunk [c0, c0 + n): s_e[x] = entry of product c0+x minus
-// p_lo, s_r[x] = its row minus r_lo (an inclusive max-scan of the entries' and rows' start
-// marks), and the long rows meeting the chunk.
-__device__ __forceinline__ void decode_chunk(const int64_t *__restrict__ off,
-                                             const int64_t *__restrict__ row_off,
-                                             const int *__restrict__ bounds, int64_t c0, int n,
-                                             int *s_e, int *s_r, ChunkHeader *hdr,
-                                             int *s_wave) {
-    // bounds (chunk_bounds_kernel): entries and rows of the chunk's first and last products
-    const int64_t p_lo = bounds[4 * blockIdx.x], p_hi = bounds[4 * blockIdx.x + 1];
-    const int r_lo = bounds[4 * blockIdx.x + 2], r_hi = bounds[4 * blockIdx.x + 3];
-    for (int x = threadIdx.x; x < kChunk; x += kBlock) {
-        s_e[pad(x)] = 0;
-        s_r[pad(x)] = 0;
-    }
-    if (threadIdx.x == 0) {
-        hdr->p_lo = p_lo;
-        hdr->r_lo = r_lo;
-        const bool first_long = row_off[r_lo + 1] - row_off[r_lo] > kShort;
-        hdr->n_long = first_long ? 1 : 0;
-        hdr->long_row[0] = r_lo;
-    }
-    __syncthreads();
-    for (int64_t p = p_lo + 1 + threadIdx.x; p <= p_hi; p += kBlock) {
-        const int64_t x = off[p] - c0;
-        if (x >= 0 && x < n) atomicMax(&s_e[pad(static_cast<int>(x))], static_cast<int>(p - p_lo));
-    }
-    for (int r = r_lo + 1 + threadIdx.x; r <= r_hi; r += kBlock) {
-        const int64_t x = row_off[r] - c0;
-        if (x >= 0 && x < n) {
-            atomicMax(&s_r[pad(static_cast<int>(x))], r - r_lo);
-            if (row_off[r + 1] - row_off[r] > kShort) {
-                const int slot = atomicAdd(&hdr->n_long, 1);
-                hdr->long_row[slot] = r;
-            }
+// Short rows: one run per A entry whose B row is not empty, in natural order (the row's
+// products in their natural order).  One thread per row.
+__global__ void short_runs_kernel(const int *__restrict__ pos_a, const int *__restrict__ crd_a,
+                                  const float *__restrict__ val_a, int rows,
+                                  const int64_t *__restrict__ row_off,
+                                  const int64_t *__restrict__ seg_prefix,
+                                  const int64_t *__restrict__ seg_roff,
+                                  const int *__restrict__ pos_b, int4 *__restrict__ desc) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < rows; i += gridDim.x * blockDim.x) {
+        const int64_t prod = row_off[i + 1] - row_off[i];
+        if (prod == 0 || prod > kShort) continue;
+        int64_t slot = seg_roff[seg_prefix[i]];
+        for (int p = pos_a[i]; p < pos_a[i + 1]; ++p) {
+            const int k = crd_a[p];
+            const int b0 = pos_b[k], b1 = pos_b[k + 1];
+            if (b1 > b0) desc[slot++] = make_run(b0, b1 - b0, val_a[p]);
         }
     }
-    __syncthreads();
-    // inclusive max-scan of both arrays, blocked kPer per lane
+}
+
+// A unit's products, expanded from its runs desc[r0, r0 + R) (in segment order): run r
+// contributes (crd_b[q], a_r * val_b[q]) for q in [first_r, first_r + length_r), and the unit's
+// products [0, n) are the runs' products concatenated.  Lane t of the BLOCK-thread workgroup
+// receives positions [t * PER, (t + 1) * PER) in kk / vv (positions >= n repeat position
+// n - 1), BLOCK * PER == kTile.  Every run has at least one product, so R <= n <= kTile.
+// s_bs and s_a (R entries) and s_mark (kPadded entries) are scratch; ends synchronised, with
+// the scratch free.  The product is one float32 multiply a * b, as the reference's
+// a_ij * b_jk.
+template <int BLOCK, int PER>
+__device__ __forceinline__ void expand_runs(const int4 *__restrict__ desc, int64_t r0, int R,
+                                            int n, const int *__restrict__ crd_b,
+                                            const float *__restrict__ val_b, int *s_bs,
+                                            float *s_a, int *s_mark, int *s_wave,
+                                            int (&kk)[PER], float (&vv)[PER]) {
+    static_assert(BLOCK * PER == kTile, "a unit's products are PER per lane");
+    constexpr int kPer = PER;
     const int base = threadIdx.x * kPer;
-    int me = 0, mr = 0;
 #pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-        me = max(me, s_e[pad(base + u)]);
-        mr = max(mr, s_r[pad(base + u)]);
-    }
-    int ce = block_exclusive_max(me, s_wave);
-    int cr = block_exclusive_max(mr, s_wave);
+    for (int j = 0; j < kPer; ++j) s_mark[pad(base + j)] = 0;
+    int4 d[kPer];
+    int mine = 0;
 #pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-        ce = max(ce, s_e[pad(base + u)]);
-        cr = max(cr, s_r[pad(base + u)]);
-        s_e[pad(base + u)] = ce;
-        s_r[pad(base + u)] = cr;
+    for (int j = 0; j < kPer; ++j) {
+        const int r = base + j;
+        d[j] = r < R ? desc[r0 + r] : make_int4(0, 0, 0, 0);
+        mine += d[j].y;
     }
-    __syncthreads();
-}
-
-__device__ __forceinline__ int long_slot(const ChunkHeader &h, int row) {
-    int slot = -1;
+    int total = 0;
+    // (its barriers also order the clears above before the marks below)
+    int off = dev::block_exclusive_sum<BLOCK>(mine, s_wave, total);
 #pragma unroll
-    for (int i = 0; i < kMaxLongPerChunk; ++i) {
-        if (i < h.n_long && h.long_row[i] == row) slot = i;
-    }
-    return slot;
-}
-
-// Writes every product of the chunk to its segment (key/val at seg_off + reserved rank;
-// short rows at their natural position, which is their segment's offset).
-__global__ __launch_bounds__(kBlock) void chunk_kernel(
-    const int *__restrict__ crd_a, const float *__restrict__ val_a, int64_t nnz_a,
-    const int64_t *__restrict__ off, const int64_t *__restrict__ row_off, int rows, int64_t P,
-    const int *__restrict__ pos_b, const int *__restrict__ crd_b, const float *__restrict__ val_b,
-    int shift, int nb, const int64_t *__restrict__ seg_prefix,
-    const int64_t *__restrict__ seg_off, int64_t *__restrict__ seg_fill,
-    const int *__restrict__ bounds, int *__restrict__ key, float *__restrict__ val) {
-    // entry and row maps of the decode; reused for the reserved bases of the scatter
-    __shared__ int64_t s_dec[kPadded];
-    int *s_e = reinterpret_cast<int *>(s_dec);
-    int *s_r = s_e + kPadded;
-    __shared__ int s_hist[kMaxLongPerChunk * kMaxBuckets];
-    __shared__ int s_wave[kBlock / dev::kWave];
-    __shared__ ChunkHeader hdr;
-    const int64_t c0 = blockIdx.x * static_cast<int64_t>(kChunk);
-    const int n = static_cast<int>(min(static_cast<int64_t>(kChunk), P - c0));
-    decode_chunk(off, row_off, bounds, c0, n, s_e, s_r, &hdr, s_wave);
-    const ChunkHeader h = hdr;
-    for (int i = threadIdx.x; i < h.n_long * nb; i += kBlock) s_hist[i] = 0;
-    __syncthreads();
-
-    // Striped positions (neighbouring lanes read neighbouring B entries).  The gathers are
-    // issued in dependent batches over all kPer products so that their latencies overlap.
-    int kk[kPer];
-    float vv[kPer];
-    int where[kPer];  // slot*nb + bucket, or -1 for a short row's product
-    int rank[kPer];
-    int64_t bpos[kPer];
-#pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-        const int x = min(static_cast<int>(threadIdx.x) + u * kBlock, n - 1);
-        const int64_t p = h.p_lo + s_e[pad(x)];
-        where[u] = long_slot(h, h.r_lo + s_r[pad(x)]);
-        bpos[u] = p;
-        kk[u] = crd_a[p];
-        vv[u] = val_a[p];
-    }
-#pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-        const int x = min(static_cast<int>(threadIdx.x) + u * kBlock, n - 1);
-        bpos[u] = pos_b[kk[u]] + (c0 + x - off[bpos[u]]);
-    }
-#pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-        kk[u] = crd_b[bpos[u]];
-        vv[u] *= val_b[bpos[u]];
-    }
-    // Neighbouring lanes hold neighbouring products, mostly of one B row with ascending
-    // columns, so equal bins come in runs: one LDS atomic per run reserves its ranks.
-    const int l = dev::lane();
-    const unsigned long long upto = l == dev::kWave - 1 ? ~0ull : (2ull << l) - 1ull;
-#pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-        const int x = static_cast<int>(threadIdx.x) + u * kBlock;
-        if (x >= n) where[u] = -2;  // past the chunk: nothing to count or write
-        if (where[u] >= 0) where[u] = where[u] * nb + (kk[u] >> shift);
-        const int bin = where[u];
-        const int prev = __shfl_up(bin, 1, dev::kWave);
-        const unsigned long long bounds = __ballot(l == 0 || prev != bin);
-        const int leader = 63 - __clzll(bounds & upto);
-        const unsigned long long above = bounds & ~upto;
-        const int next = above ? __ffsll(above) - 1 : dev::kWave;
-        int got = 0;
-        if (bin >= 0 && l == leader) got = atomicAdd(&s_hist[bin], next - l);
-        rank[u] = __shfl(got, leader, dev::kWave) + (l - leader);
-    }
-    __syncthreads();
-    // reserve each bin's range in its segment; the bases reuse the decode arrays
-    int64_t *s_base = s_dec;
-    static_assert(kMaxLongPerChunk * kMaxBuckets <= kChunk, "bases must fit the decode arrays");
-    for (int i = threadIdx.x; i < h.n_long * nb; i += kBlock) {
-        const int c = s_hist[i];
-        if (c > 0) {
-            const int64_t s = seg_prefix[h.long_row[i / nb]] + (i % nb);
-            const unsigned long long got = atomicAdd(
-                reinterpret_cast<unsigned long long *>(&seg_fill[s]),
-                static_cast<unsigned long long>(c));
-            s_base[i] = seg_off[s] + static_cast<int64_t>(got);
+    for (int j = 0; j < kPer; ++j) {
+        const int r = base + j;
+        if (r < R) {
+            s_bs[r] = d[j].x - off;  // product x of run r is B entry s_bs[r] + x
+            s_a[r] = __int_as_float(d[j].z);
+            if (d[j].y > 0) s_mark[pad(off)] = r + 1;
+            off += d[j].y;
         }
     }
     __syncthreads();
+    int m = 0;
 #pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-        const int x = threadIdx.x + u * kBlock;
-        if (where[u] != -2) {
-            const int64_t dst = where[u] < 0 ? c0 + x : s_base[where[u]] + rank[u];
-            key[dst] = kk[u];
-            val[dst] = vv[u];
+    for (int j = 0; j < kPer; ++j) m = max(m, s_mark[pad(base + j)]);
+    int cur = block_exclusive_max(m, s_wave);
+    int qv[kPer];
+    float av[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        cur = max(cur, s_mark[pad(base + j)]);
+        const int r = max(cur - 1, 0);
+        qv[j] = s_bs[r] + min(base + j, n - 1);  // past n: the last run's last product
+        av[j] = s_a[r];
+    }
+    if (n > 0) {
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            kk[j] = crd_b[qv[j]];
+            vv[j] = val_b[qv[j]];
+        }
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) vv[j] = av[j] * vv[j];
+    } else {
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            kk[j] = 0;
+            vv[j] = 0.0f;
         }
     }
+    __syncthreads();  // every lane is done with the scratch
 }
 
 // ---- 4: units --------------------------------------------------------------------------
@@ -697,9 +720,11 @@ __global__ __launch_bounds__(kBlock) void sort_unit_kernel(
     const int64_t *__restrict__ unit_start, int64_t n_units,
     int64_t n_seg, const int64_t *__restrict__ seg_len, const int64_t *__restrict__ seg_off,
     const int *__restrict__ seg_row, const int64_t *__restrict__ row_off, int col_shift,
-    const int *__restrict__ key, const float *__restrict__ val, int *__restrict__ ukey,
+    const int4 *__restrict__ desc, const int64_t *__restrict__ seg_roff,
+    const int *__restrict__ crd_b, const float *__restrict__ val_b, int *__restrict__ ukey,
     float *__restrict__ uval, int64_t *__restrict__ unit_nnz, int *__restrict__ row_unit,
     int *__restrict__ row_local) {
+    static_assert(sizeof(K) >= sizeof(int), "run starts are staged in s_key");
     __shared__ K s_key[kPadded];
     __shared__ float s_val[kPadded];
     __shared__ int s_mark[kPadded];
@@ -712,19 +737,17 @@ __global__ __launch_bounds__(kBlock) void sort_unit_kernel(
     const int n = static_cast<int>(unit_start[u + 1] - start);
     const int64_t s_end = u + 1 < n_units ? unit_seg[u + 1] : n_seg;
     {
-        // coalesced staging of the raw columns and values: every load issued first (clamped
-        // to the unit), then the LDS stores
+        // the unit's products from its runs, then staged in LDS (blocked positions)
         int kk[kPer];
         float vv[kPer];
+        const int64_t r0 = seg_roff[s0];
+        const int R = static_cast<int>(seg_roff[s_end] - r0);
+        expand_runs<kBlock, kPer>(desc, r0, R, n, crd_b, val_b, reinterpret_cast<int *>(s_key),
+                                  s_val, s_mark, s_wave, kk, vv);
+        const int lo = threadIdx.x * kPer;
 #pragma unroll
         for (int j = 0; j < kPer; ++j) {
-            const int64_t q = start + max(0, min(static_cast<int>(threadIdx.x) + j * kBlock, n - 1));
-            kk[j] = n > 0 ? key[q] : 0;
-            vv[j] = n > 0 ? val[q] : 0.0f;
-        }
-#pragma unroll
-        for (int j = 0; j < kPer; ++j) {
-            const int q = threadIdx.x + j * kBlock;
+            const int q = lo + j;
             s_mark[pad(q)] = 0;
             if (q < n) {
                 s_key[pad(q)] = static_cast<K>(static_cast<uint32_t>(kk[j]));
@@ -861,17 +884,20 @@ __device__ __forceinline__ void mark_bucket(unsigned *bm, const unsigned short *
 // product range of the unit; once every bucket is done, a scan of their counts gives the
 // output offsets and the workgroup stores the unit's entries with consecutive lanes on
 // consecutive outputs.
-__global__ __launch_bounds__(kBlock) void bitmap_unit_kernel(
+__global__ __launch_bounds__(kBitmapBlock) void bitmap_unit_kernel(
     const int *__restrict__ bitmap_list, const int *__restrict__ unit_seg,
     const int64_t *__restrict__ unit_start, int64_t n_units, int64_t n_seg,
     const int64_t *__restrict__ seg_len, const int64_t *__restrict__ seg_off,
     const int64_t *__restrict__ seg_prefix, const int *__restrict__ seg_row,
-    const int64_t *__restrict__ row_off, int shift, const int *__restrict__ key,
-    const float *__restrict__ val, int *__restrict__ ukey, float *__restrict__ uval,
+    const int64_t *__restrict__ row_off, int shift, const int4 *__restrict__ desc,
+    const int64_t *__restrict__ seg_roff, const int *__restrict__ crd_b,
+    const float *__restrict__ val_b, int *__restrict__ ukey, float *__restrict__ uval,
     int64_t *__restrict__ unit_nnz, int *__restrict__ row_unit, int *__restrict__ row_local) {
-    constexpr int kWaves = kBlock / dev::kWave;
+    constexpr int kWaves = kBitmapBlock / dev::kWave;
+    constexpr int kPerB = kTile / kBitmapBlock;
     __shared__ double s_acc[kTile];
     __shared__ unsigned short s_col[kTile];  // column offset inside its bucket's window
+    __shared__ float s_pv[kPadded];          // product values (padded positions)
     __shared__ unsigned s_bits[kWaves][kBitmapWords];
     __shared__ int s_pre[kWaves][kBitmapWords];
     __shared__ int s_x0[kMaxBitmapSegs + 1];
@@ -888,23 +914,32 @@ __global__ __launch_bounds__(kBlock) void bitmap_unit_kernel(
     const int64_t s = s0 + threadIdx.x;
     const bool here = s < s1 && seg_len[s] > 0;
     int n_buckets = 0;
-    const int ord = dev::block_exclusive_sum<kBlock>(here ? 1 : 0, s_wave, n_buckets);
+    const int ord = dev::block_exclusive_sum<kBitmapBlock>(here ? 1 : 0, s_wave, n_buckets);
     if (here) {
         s_x0[ord] = static_cast<int>(seg_off[s] - start);
         s_base[ord] = static_cast<int>((s - seg_prefix[seg_row[s]]) << shift);
         s_sid[ord] = static_cast<int>(s);
     }
     if (threadIdx.x == 0) s_x0[n_buckets] = n;
-    // the unit's columns, staged once (bucket = column >> shift, so the window offset is
-    // the column's low bits); values are read from the product buffer when accumulated
+    // the unit's products from its runs: window offsets (bucket = column >> shift, so the
+    // offset is the column's low bits) and values, staged once
     const int low = (1 << shift) - 1;
-    for (int q0 = threadIdx.x; q0 < n; q0 += 4 * kBlock) {
-        int kv[4];  // four loads in flight (clamped to the unit)
+    {
+        int kk[kPerB];
+        float vv[kPerB];
+        const int64_t r0 = seg_roff[s0];
+        const int R = static_cast<int>(seg_roff[s1] - r0);
+        expand_runs<kBitmapBlock, kPerB>(desc, r0, R, n, crd_b, val_b, reinterpret_cast<int *>(s_acc),
+                    reinterpret_cast<float *>(s_acc) + kTile, reinterpret_cast<int *>(s_pv),
+                    s_wave, kk, vv);
+        const int lo = threadIdx.x * kPerB;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) kv[j] = key[start + min(q0 + j * kBlock, n - 1)];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            if (q0 + j * kBlock < n) s_col[q0 + j * kBlock] = static_cast<unsigned short>(kv[j] & low);
+        for (int j = 0; j < kPerB; ++j) {
+            const int q = lo + j;
+            if (q < n) {
+                s_col[q] = static_cast<unsigned short>(kk[j] & low);
+                s_pv[pad(q)] = vv[j];
+            }
         }
     }
     __syncthreads();
@@ -935,9 +970,9 @@ __global__ __launch_bounds__(kBlock) void bitmap_unit_kernel(
         }
         wave_sync();
         for (int xb = x0 + l; xb < x1; xb += 4 * dev::kWave) {
-            float vv[4];  // four value loads in flight (clamped to the bucket)
+            float vv[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) vv[j] = val[start + min(xb + j * dev::kWave, x1 - 1)];
+            for (int j = 0; j < 4; ++j) vv[j] = s_pv[pad(min(xb + j * dev::kWave, x1 - 1))];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int x = xb + j * dev::kWave;
@@ -969,12 +1004,12 @@ __global__ __launch_bounds__(kBlock) void bitmap_unit_kernel(
     // output offset of each bucket inside the unit
     int total = 0;
     const int cnt = static_cast<int>(threadIdx.x) < n_buckets ? s_out[threadIdx.x] : 0;
-    const int off = dev::block_exclusive_sum<kBlock>(cnt, s_wave, total);
+    const int off = dev::block_exclusive_sum<kBitmapBlock>(cnt, s_wave, total);
     if (static_cast<int>(threadIdx.x) < n_buckets) s_out[threadIdx.x] = off;
     __syncthreads();
     // the unit's entries, consecutive lanes on consecutive outputs: output i belongs to the
     // last bucket whose offset is at most i
-    for (int i = threadIdx.x; i < total; i += kBlock) {
+    for (int i = threadIdx.x; i < total; i += kBitmapBlock) {
         int o = 0;
         for (int b = 1; b < n_buckets; ++b) o += s_out[b] <= i ? 1 : 0;
         const int x = s_x0[o] + (i - s_out[o]);
@@ -1001,22 +1036,27 @@ __global__ __launch_bounds__(kBlock) void bitmap_unit_kernel(
 // columns at a time in an LDS float64 array (plus a bitmap of touched columns), then
 // compacted in column order, 16 columns per lane.
 constexpr int kDenseBlock = 512;
+constexpr int kDensePer = 4;  // products per lane per round
 
 __global__ __launch_bounds__(kDenseBlock) void dense_unit_kernel(
     const int *__restrict__ dense_list, const int *__restrict__ unit_seg,
     const int64_t *__restrict__ unit_start,
     const int64_t *__restrict__ seg_len, const int64_t *__restrict__ seg_prefix,
     const int *__restrict__ seg_row, const int64_t *__restrict__ row_off, int shift, int cols,
-    const int *__restrict__ key, const float *__restrict__ val, int *__restrict__ ukey,
+    const int4 *__restrict__ desc, const int64_t *__restrict__ seg_roff,
+    const int *__restrict__ crd_b, const float *__restrict__ val_b, int *__restrict__ ukey,
     float *__restrict__ uval, int64_t *__restrict__ unit_nnz, int *__restrict__ row_unit,
     int *__restrict__ row_local) {
     __shared__ double s_acc[kDenseCols];
     __shared__ unsigned s_bits[kDenseCols / 32];
     __shared__ int s_wave[kDenseBlock / dev::kWave];
+    // a batch of up to kDenseBlock runs: first product offset, B entry of product 0, A value
+    __shared__ int s_off[kDenseBlock];
+    __shared__ int s_bs[kDenseBlock];
+    __shared__ float s_a[kDenseBlock];
     static_assert(kDenseCols / 16 == kDenseBlock, "16 bitmap bits per lane");
     const int64_t u = dense_list[blockIdx.x];
     const int s = unit_seg[u];
-    const int64_t len = seg_len[s];
     const int64_t start = unit_start[u];
     const int row = seg_row[s];
     const int64_t bucket = s - seg_prefix[row];
@@ -1031,26 +1071,57 @@ __global__ __launch_bounds__(kDenseBlock) void dense_unit_kernel(
         for (int i = threadIdx.x; i < kDenseCols; i += kDenseBlock) s_acc[i] = 0.0;
         if (threadIdx.x < kDenseCols / 32) s_bits[threadIdx.x] = 0u;
         __syncthreads();
-        // four products per iteration, their loads issued first (clamped to the segment)
-        for (int64_t x0 = threadIdx.x; x0 < len; x0 += 4 * kDenseBlock) {
-            int kk[4];
-            float vv[4];
+        // runs in batches of kDenseBlock (one per lane); the batch's products are spread over
+        // the lanes, kDensePer consecutive ones per lane per round, each lane finding the run
+        // of its first product by a search of the batch's offsets and advancing from there
+        for (int64_t rb = seg_roff[s]; rb < seg_roff[s + 1]; rb += kDenseBlock) {
+            const int nr = static_cast<int>(min(static_cast<int64_t>(kDenseBlock), seg_roff[s + 1] - rb));
+            const int4 d = static_cast<int>(threadIdx.x) < nr ? desc[rb + threadIdx.x]
+                                                              : make_int4(0, 0, 0, 0);
+            int total = 0;
+            const int off = dev::block_exclusive_sum<kDenseBlock>(d.y, s_wave, total);
+            s_off[threadIdx.x] = off;
+            s_bs[threadIdx.x] = d.x - off;
+            s_a[threadIdx.x] = __int_as_float(d.z);
+            __syncthreads();
+            for (int x0 = threadIdx.x * kDensePer; x0 < total; x0 += kDensePer * kDenseBlock) {
+                int lo = 0, hi = nr - 1;  // last run starting at or before x0
+                while (lo < hi) {
+                    const int mid = (lo + hi + 1) >> 1;
+                    if (s_off[mid] <= x0) {
+                        lo = mid;
+                    } else {
+                        hi = mid - 1;
+                    }
+                }
+                int r = lo;
+                int qv[kDensePer];
+                float av[kDensePer];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int64_t x = min(x0 + q * kDenseBlock, len - 1);
-                kk[q] = key[start + x];
-                vv[q] = val[start + x];
-            }
+                for (int q = 0; q < kDensePer; ++q) {
+                    const int x = min(x0 + q, total - 1);
+                    while (r + 1 < nr && s_off[r + 1] <= x) ++r;
+                    qv[q] = s_bs[r] + x;
+                    av[q] = s_a[r];
+                }
+                int kk[kDensePer];
+                float vv[kDensePer];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int64_t c = kk[q] - w0;
-                if (x0 + q * kDenseBlock < len && c >= 0 && c < kDenseCols) {
-                    atomicAdd(&s_acc[c], static_cast<double>(vv[q]));
-                    atomicOr(&s_bits[c >> 5], 1u << (c & 31));
+                for (int q = 0; q < kDensePer; ++q) {
+                    kk[q] = crd_b[qv[q]];
+                    vv[q] = val_b[qv[q]];
+                }
+#pragma unroll
+                for (int q = 0; q < kDensePer; ++q) {
+                    const int64_t c = kk[q] - w0;
+                    if (x0 + q < total && c >= 0 && c < kDenseCols) {
+                        atomicAdd(&s_acc[c], static_cast<double>(av[q] * vv[q]));
+                        atomicOr(&s_bits[c >> 5], 1u << (c & 31));
+                    }
                 }
             }
+            __syncthreads();  // the batch's tables are read before the next batch
         }
-        __syncthreads();
         const unsigned half = (s_bits[threadIdx.x >> 1] >> ((threadIdx.x & 1) * 16)) & 0xffffu;
         int total = 0;
         int rank = dev::block_exclusive_sum<kDenseBlock>(static_cast<int>(__popc(half)), s_wave,
@@ -1145,7 +1216,7 @@ int multiply(Call &call, const nacho_csr *a, const nacho_csr *b, Product *z) {
     const int shift = std::max(std::min(kDenseBits, cb), cb - kMaxBucketBits);
     const int nb = cols > 0 ? ((cols - 1) >> shift) + 1 : 1;
     const int dense_min = shift <= kDenseBits ? kDenseMin : kShort;
-    const char *name = "spgemm: expand+scatter+reduce+copy";
+    const char *name = "spgemm: runs+reduce+copy";
     NACHO_TRY(call.timer_start(name));
 
     // 1-2. products per A entry, per row; segments per row
@@ -1182,27 +1253,23 @@ int multiply(Call &call, const nacho_csr *a, const nacho_csr *b, Product *z) {
         // segment table
         int *seg_row = nullptr;
         int64_t *seg_len = nullptr, *seg_off = nullptr, *seg_fill = nullptr;
+        int64_t *seg_runs = nullptr, *seg_roff = nullptr;
         NACHO_TRY(call.scratch_n(static_cast<size_t>(n_seg), &seg_row));
         NACHO_TRY(call.scratch_n(static_cast<size_t>(n_seg) + 1, &seg_len));
         NACHO_TRY(call.scratch_n(static_cast<size_t>(n_seg) + 1, &seg_off));
         NACHO_TRY(call.scratch_n(static_cast<size_t>(n_seg), &seg_fill));
-        segments_kernel<<<grid_for(rows, 256), 256, 0, st>>>(row_off, seg_prefix, rows, seg_row,
-                                                            seg_len, seg_fill);
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(n_seg) + 1, &seg_runs));
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(n_seg) + 1, &seg_roff));
+        segments_kernel<<<grid_for(rows, 256), 256, 0, st>>>(row_off, seg_prefix, rows,
+                                                            a->dim_j_offsets, len, seg_row,
+                                                            seg_len, seg_runs, seg_fill);
         NACHO_TRY_HIP(hipGetLastError());
 
-        // 3. histogram, segment offsets, scatter
-        int *key = nullptr, *ukey = nullptr;
-        float *val = nullptr, *uval = nullptr;
-        NACHO_TRY(call.scratch_n(static_cast<size_t>(P), &key));
-        NACHO_TRY(call.scratch_n(static_cast<size_t>(P), &val));
+        // 3. histogram, segment offsets, runs
+        int *ukey = nullptr;
+        float *uval = nullptr;
         NACHO_TRY(call.scratch_n(static_cast<size_t>(P), &ukey));
         NACHO_TRY(call.scratch_n(static_cast<size_t>(P), &uval));
-        const unsigned chunks = static_cast<unsigned>((P + kChunk - 1) / kChunk);
-        int *bounds = nullptr;
-        NACHO_TRY(call.scratch_n(4 * static_cast<size_t>(chunks), &bounds));
-        chunk_bounds_kernel<<<grid_for(2 * static_cast<int64_t>(chunks), 256), 256, 0, st>>>(
-            off, nnz_a, row_off, rows, P, chunks, bounds);
-        NACHO_TRY_HIP(hipGetLastError());
         // long rows' bucket counts from B's runs (P > 0, so B has entries)
         const int64_t nnz_b = b->dim_j_length;
         const int rows_b = b->dim_i_size;
@@ -1239,19 +1306,30 @@ int multiply(Call &call, const nacho_csr *a, const nacho_csr *b, Product *z) {
         NACHO_TRY(scan::exclusive_scan_i64(call, nblk, rows, blk_off));
         hist_rows_kernel<<<grid_for(rows, 256), 256, 0, st>>>(blk_off, rows, blk_row);
         NACHO_TRY_HIP(hipGetLastError());
+        const BRuns br{run_idx, run, run_start};
         long_hist_kernel<<<kHistGrid, kBlock, 0, st>>>(
-            a->dim_j_offsets, a->dim_j_indices, blk_off, blk_row, rows, b->dim_j_offsets,
-            run_idx, run, nb, seg_prefix, seg_len);
+            a->dim_j_offsets, a->dim_j_indices, blk_off, blk_row, rows, b->dim_j_offsets, br,
+            nb, seg_prefix, seg_len, seg_runs);
         NACHO_TRY_HIP(hipGetLastError());
         NACHO_TRY(scan::exclusive_scan_i64(call, seg_len, n_seg, seg_off));
-        chunk_kernel<<<chunks, kBlock, 0, st>>>(
-            a->dim_j_indices, a->values, nnz_a, off, row_off, rows, P, b->dim_j_offsets,
-            b->dim_j_indices, b->values, shift, nb, seg_prefix, seg_off, seg_fill, bounds, key,
-            val);
+        NACHO_TRY(scan::exclusive_scan_i64(call, seg_runs, n_seg, seg_roff));
+        int64_t n_runs = 0;
+        NACHO_TRY(call.timer_stop());
+        NACHO_TRY(call.read_back(&n_runs, seg_roff + n_seg, sizeof(n_runs)));
+        NACHO_TRY(call.timer_start(name));
+        int4 *desc = nullptr;
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(std::max<int64_t>(n_runs, 1)), &desc));
+        long_runs_kernel<<<kHistGrid, kBlock, 0, st>>>(
+            a->dim_j_offsets, a->dim_j_indices, a->values, blk_off, blk_row, rows,
+            b->dim_j_offsets, br, nb, seg_prefix, seg_roff, seg_fill, desc);
+        NACHO_TRY_HIP(hipGetLastError());
+        short_runs_kernel<<<grid_for(rows, 256), 256, 0, st>>>(
+            a->dim_j_offsets, a->dim_j_indices, a->values, rows, row_off, seg_prefix, seg_roff,
+            b->dim_j_offsets, desc);
         NACHO_TRY_HIP(hipGetLastError());
 
         // 4. units
-        int64_t *seg_units = seg_fill;  // the fill counters are spent
+        int64_t *seg_units = seg_fill;  // the run fill counters are spent
         int64_t *unit_prefix = nullptr;
         NACHO_TRY(call.scratch_n(static_cast<size_t>(n_seg) + 1, &unit_prefix));
         unit_count_kernel<<<grid_for(n_seg, 256), 256, 0, st>>>(
@@ -1302,23 +1380,27 @@ int multiply(Call &call, const nacho_csr *a, const nacho_csr *b, Product *z) {
         if (n_kind[1] > 0 && cb + kOrdBits <= 32) {
             sort_unit_kernel<uint32_t><<<static_cast<unsigned>(n_kind[1]), kBlock, 0, st>>>(
                 sort_list, unit_seg, unit_start, n_units, n_seg, seg_len, seg_off, seg_row,
-                row_off, cb, key, val, ukey, uval, unit_nnz, row_unit, row_local);
+                row_off, cb, desc, seg_roff, b->dim_j_indices, b->values, ukey, uval, unit_nnz,
+                row_unit, row_local);
         } else if (n_kind[1] > 0) {
             sort_unit_kernel<uint64_t><<<static_cast<unsigned>(n_kind[1]), kBlock, 0, st>>>(
                 sort_list, unit_seg, unit_start, n_units, n_seg, seg_len, seg_off, seg_row,
-                row_off, 32, key, val, ukey, uval, unit_nnz, row_unit, row_local);
+                row_off, 32, desc, seg_roff, b->dim_j_indices, b->values, ukey, uval, unit_nnz,
+                row_unit, row_local);
         }
         NACHO_TRY_HIP(hipGetLastError());
         if (n_kind[2] > 0) {
-            bitmap_unit_kernel<<<static_cast<unsigned>(n_kind[2]), kBlock, 0, st>>>(
+            bitmap_unit_kernel<<<static_cast<unsigned>(n_kind[2]), kBitmapBlock, 0, st>>>(
                 bitmap_list, unit_seg, unit_start, n_units, n_seg, seg_len, seg_off, seg_prefix,
-                seg_row, row_off, shift, key, val, ukey, uval, unit_nnz, row_unit, row_local);
+                seg_row, row_off, shift, desc, seg_roff, b->dim_j_indices, b->values, ukey,
+                uval, unit_nnz, row_unit, row_local);
             NACHO_TRY_HIP(hipGetLastError());
         }
         if (n_kind[0] > 0) {
             dense_unit_kernel<<<static_cast<unsigned>(n_kind[0]), kDenseBlock, 0, st>>>(
                 dense_list, unit_seg, unit_start, seg_len, seg_prefix, seg_row, row_off, shift,
-                cols, key, val, ukey, uval, unit_nnz, row_unit, row_local);
+                cols, desc, seg_roff, b->dim_j_indices, b->values, ukey, uval, unit_nnz,
+                row_unit, row_local);
             NACHO_TRY_HIP(hipGetLastError());
         }
         NACHO_TRY(scan::exclusive_scan_i64(call, unit_nnz, n_units, unit_out));
