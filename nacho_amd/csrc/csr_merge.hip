@@ -449,13 +449,18 @@ __device__ __forceinline__ void walk_lane(LaneOut<IPT + 1> &out, const TileSplit
         out.pos[s] = 0;
         if (s < steps) {
             if (xa == kMax && xb == kMax) {  // row end
+                // (reads at indices always inside the staged arrays, then selects: no nested
+                // branches, each waiting for its own read)
                 row_ends |= 1u << s;
                 ++k;
-                iae = end_a(k);
-                ibe = end_b(k);
+                const unsigned rn = s_row[min(k + 1, nr - 1)];
+                const int ha = s_crd[ia], hb = s_crd[ib];
+                const bool last_row = k >= nr - 1;
+                iae = last_row ? na : static_cast<int>(rn & 0xffffu);
+                ibe = na + (last_row ? nb : static_cast<int>(rn >> 16));
                 last_a = -1;
-                xa = ia < iae ? s_crd[ia] : kMax;
-                xb = ib < ibe ? s_crd[ib] : kMax;
+                xa = ia < iae ? ha : kMax;
+                xb = ib < ibe ? hb : kMax;
             } else {
                 const bool take_a = xa <= xb;
                 const bool pair = take_a && xa == xb;
@@ -463,10 +468,11 @@ __device__ __forceinline__ void walk_lane(LaneOut<IPT + 1> &out, const TileSplit
                 out.crd[s] = min(xa, xb);
                 if (VALUES) {
                     const float own = s_val[take_a ? ia : ib];
+                    const float vb = s_val[ib];  // read even when unpaired: no branch
                     if (OP == Op::Union) {
-                        out.val[s] = pair ? own + s_val[ib] : own;
+                        out.val[s] = pair ? own + vb : own;
                     } else {
-                        out.val[s] = own * s_val[ib];
+                        out.val[s] = own * vb;
                     }
                 }
                 const bool emit = (OP == Op::Union) ? (take_a || last_a != xb) : pair;
