@@ -870,9 +870,14 @@ __device__ __forceinline__ void mark_bucket(unsigned *bm, const unsigned short *
 #pragma unroll
     for (int i = 0; i < kBitmapWords / dev::kWave; ++i) bm[l + i * dev::kWave] = 0u;
     wave_sync();
-    for (int x = x0 + l; x < x1; x += dev::kWave) {
-        const int c = s_col[x];
-        atomicOr(&bm[c >> 5], 1u << (c & 31));
+    for (int xb = x0 + l; xb < x1; xb += 4 * dev::kWave) {  // four reads in flight
+        int c[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) c[j] = s_col[min(xb + j * dev::kWave, x1 - 1)];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (xb + j * dev::kWave < x1) atomicOr(&bm[c[j] >> 5], 1u << (c[j] & 31));
+        }
     }
     wave_sync();
 }
@@ -970,18 +975,20 @@ __global__ __launch_bounds__(kBitmapBlock) void bitmap_unit_kernel(
         }
         wave_sync();
         for (int xb = x0 + l; xb < x1; xb += 4 * dev::kWave) {
+            // every read of four products first (clamped to the bucket), then the adds
             float vv[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) vv[j] = s_pv[pad(min(xb + j * dev::kWave, x1 - 1))];
+            int r[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int x = xb + j * dev::kWave;
-                if (x < x1) {
-                    const int c = s_col[x];
-                    const int wd = c >> 5;
-                    const int r = pre[wd] + __popc(bm[wd] & ((1u << (c & 31)) - 1u));
-                    atomicAdd(&s_acc[x0 + r], static_cast<double>(vv[j]));
-                }
+                const int x = min(xb + j * dev::kWave, x1 - 1);
+                vv[j] = s_pv[pad(x)];
+                const int c = s_col[x];
+                const int wd = c >> 5;
+                r[j] = pre[wd] + __popc(bm[wd] & ((1u << (c & 31)) - 1u));
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (xb + j * dev::kWave < x1) atomicAdd(&s_acc[x0 + r[j]], static_cast<double>(vv[j]));
             }
         }
         wave_sync();  // every column of the bucket is read: its slots take the output columns
@@ -1008,10 +1015,10 @@ __global__ __launch_bounds__(kBitmapBlock) void bitmap_unit_kernel(
     if (static_cast<int>(threadIdx.x) < n_buckets) s_out[threadIdx.x] = off;
     __syncthreads();
     // the unit's entries, consecutive lanes on consecutive outputs: output i belongs to the
-    // last bucket whose offset is at most i
+    // last bucket whose offset is at most i (a lane's outputs only move forward)
+    int o = 0;
     for (int i = threadIdx.x; i < total; i += kBitmapBlock) {
-        int o = 0;
-        for (int b = 1; b < n_buckets; ++b) o += s_out[b] <= i ? 1 : 0;
+        while (o + 1 < n_buckets && s_out[o + 1] <= i) ++o;
         const int x = s_x0[o] + (i - s_out[o]);
         ukey[start + i] = s_base[o] + s_col[x];
         uval[start + i] = static_cast<float>(s_acc[x]);
