@@ -80,11 +80,12 @@ WORKLOADS = {
     "c5coo": dict(op="coo3d_add", kernel="coo_partition_kernel + coo_count_kernel + "
                                          "coo_write_kernel (packed 64-bit keys)",
                   desc="C5 as COO3: coo3d_add f32 of the same (i, j, k) tuples"),
-    "c3coo": dict(op="coo_mul", kernel="coo_partition_kernel + coo_write_kernel (spread) + "
-                                      "coo_compact_kernel (packed 64-bit keys)",
+    "c3coo": dict(op="coo_mul", kernel="coo_row_offsets_kernel + csr_partition_kernel + "
+                                      "csr_write_kernel<Intersect> (spread, rows out) + "
+                                      "csr_compact_kernel",
                   desc="C3 as COO: coo_mul f32 of the C3 operands' (i, j) tuples"),
-    "c2coo": dict(op="coo_add", kernel="coo_partition_kernel + coo_count_kernel + "
-                                      "coo_write_kernel (packed 64-bit keys)",
+    "c2coo": dict(op="coo_add", kernel="coo_row_offsets_kernel + csr_partition_kernel + "
+                                      "csr_pair_count_kernel + csr_write_kernel<Union> (rows out)",
                   desc="C2 as COO: coo_add f32 of the C2 operands' (i, j) tuples"),
     "c2add3": dict(op="add3", kernel="fused three-way merge (csr3_partition_kernel + "
                                     "csr3_count_kernel + csr3_write_kernel)",

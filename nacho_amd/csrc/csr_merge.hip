@@ -58,6 +58,7 @@ enum class Op { Union, Intersect };
 constexpr int kBlock = 256;
 constexpr int kItemsPerLane = 15;  // odd: lanes' LDS walks spread over banks
 constexpr int kTile = kBlock * kItemsPerLane;
+static_assert(kLevelTileSlack >= kTile, "callers' item-count headroom covers merge_level's");
 constexpr int kPartBlock = 64;  // threads per workgroup of the partition kernel
 
 
@@ -1027,8 +1028,9 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
     unsigned *__restrict__ length, int spread_by_a, int64_t *__restrict__ tile_count,
     int64_t *__restrict__ chunk_total, unsigned long long *__restrict__ done,
     int64_t *__restrict__ length_out, const uint2 *__restrict__ starts,
-    const int *__restrict__ mode) {
+    const int *__restrict__ mode, int *__restrict__ rc) {
     static_assert(!(VALUES && CHILD), "a level carries values or child pointers, not both");
+    // rc (value levels, optional): each output's row, staged in s_row once the walk is done
     static_assert(!SPREAD || (OP == Op::Intersect && !CHILD), "spread output: intersection");
     constexpr int kCap = kBlock * IPT + 2;
     constexpr int kLoads = (kCap + kBlock - 1) / kBlock;
@@ -1134,6 +1136,7 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
             if (lo.valid & (1u << s)) {
                 s_crd[o] = lo.crd[s];
                 if (VALUES) s_val[o] = lo.val[s];
+                if (VALUES && rc) s_row[o] = static_cast<unsigned>(r);
                 if (CHILD) {
                     reinterpret_cast<int *>(s_val)[o] = ca_v[s];
                     reinterpret_cast<int *>(s_row)[o] = cb_v[s];
@@ -1148,6 +1151,7 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
             if (q < tile_total) {
                 cc[base + q] = s_crd[q];
                 if (VALUES) vc[base + q] = s_val[q];
+                if (VALUES && rc) rc[base + q] = static_cast<int>(s_row[q]);
                 if (CHILD) {
                     child_a[base + q] = reinterpret_cast<const int *>(s_val)[q];
                     child_b[base + q] = reinterpret_cast<const int *>(s_row)[q];
@@ -1195,7 +1199,8 @@ __global__ __launch_bounds__(kBlock) void csr_compact_kernel(
     const int *__restrict__ split_b, int num_tiles, int chunk, int rows, int spread_by_a,
     const int64_t *__restrict__ tile_count, const int64_t *__restrict__ chunk_total,
     const int *__restrict__ tmp_crd, const float *__restrict__ tmp_val, int *__restrict__ pc,
-    int *__restrict__ cc, float *__restrict__ vc, int64_t *__restrict__ length) {
+    int *__restrict__ cc, float *__restrict__ vc, int64_t *__restrict__ length,
+    const int *__restrict__ tmp_row, int *__restrict__ rc) {
     __shared__ int64_t s_wave[kBlock / dev::kWave];
     const int t = blockIdx.x;
     const int c = t / chunk;
@@ -1211,6 +1216,7 @@ __global__ __launch_bounds__(kBlock) void csr_compact_kernel(
     for (int q = threadIdx.x; q < n; q += kBlock) {
         cc[to + q] = tmp_crd[from + q];
         vc[to + q] = tmp_val[from + q];
+        if (rc) rc[to + q] = tmp_row[from + q];
     }
     const int r_end = t + 1 < num_tiles ? split_r[t + 1] : rows;
     for (int r = split_r[t] + static_cast<int>(threadIdx.x); r < r_end; r += kBlock) {
@@ -1269,11 +1275,12 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
         if (!values || child) return NACHO_ERR_INVALID_ARGUMENT;
         const int by_a = A.len <= B.len ? 1 : 0;
         const size_t cap = static_cast<size_t>(by_a ? A.len : B.len);
-        int *tmp_crd = nullptr;
+        int *tmp_crd = nullptr, *tmp_row = nullptr;
         float *tmp_val = nullptr;
         int64_t *tile_count = nullptr, *chunk_total = nullptr;
         NACHO_TRY(call.scratch_n(cap, &tmp_crd));
         NACHO_TRY(call.scratch_n(cap, &tmp_val));
+        if (Z.row) NACHO_TRY(call.scratch_n(cap, &tmp_row));
         NACHO_TRY(call.scratch_n(static_cast<size_t>(num_tiles), &tile_count));
         NACHO_TRY(call.scratch_n(static_cast<size_t>(grid) + 1, &chunk_total));
         int64_t *len_dev = chunk_total + grid;
@@ -1288,12 +1295,12 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
                                      num_tiles, chunk, split_r, split_a, split_b, nullptr, rows,
                                      Z.pos, tmp_crd, tmp_val, nullptr, nullptr, nullptr,
                                      nullptr, nullptr, by_a, tile_count, chunk_total, done,
-                                     length_out, nullptr, nullptr);
+                                     length_out, nullptr, nullptr, tmp_row);
         NACHO_TRY_HIP(hipGetLastError());
         NACHO_TRY(call.mark_length());
         csr_compact_kernel<<<num_tiles, kBlock, 0, s>>>(
             split_r, split_a, split_b, num_tiles, chunk, rows, by_a, tile_count, chunk_total,
-            tmp_crd, tmp_val, Z.pos, Z.crd, Z.val, len_dev);
+            tmp_crd, tmp_val, Z.pos, Z.crd, Z.val, len_dev, tmp_row, Z.row);
         NACHO_TRY_HIP(hipGetLastError());
         NACHO_TRY(call.timer_stop());
         int64_t len = 0;
@@ -1372,7 +1379,8 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
     csr_write_kernel<OPV, kItemsPerLane, VAL, CHD, false, SRCH><<<grid, kBlock, 0, s>>>(         \
         A.pos, A.crd, A.val, B.pos, B.crd, B.val, A.len, B.len, num_tiles, chunk, split_r,      \
         split_a, split_b, counts, rows, Z.pos, Z.crd, Z.val, A.next, B.next, Z.child_a,         \
-        Z.child_b, length, 0, nullptr, nullptr, nullptr, nullptr, starts, rp.mode)
+        Z.child_b, length, 0, nullptr, nullptr, nullptr, nullptr, starts, rp.mode,             \
+        VAL ? Z.row : nullptr)
     if (values) {
         if (child) return NACHO_ERR_INVALID_ARGUMENT;
         if (keep_starts) {

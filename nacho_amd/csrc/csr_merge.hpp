@@ -19,14 +19,16 @@ struct LevelOperand {
     const int *next;
 };
 
-// Result buffers, sized by the caller for the worst case: pos rows + 1, crd/val the union
-// (or intersection) bound, child_a/child_b that bound + 1.
+// Result buffers, sized by the caller for the worst case: pos rows + 1, crd/val (and row)
+// the union (or intersection) bound, child_a/child_b that bound + 1.
 struct LevelResult {
     int *pos;
     int *crd;
     float *val;
     int *child_a;
     int *child_b;
+    // Value levels only, optional: the row of every output (a COO result's i coordinate).
+    int *row = nullptr;
 };
 
 // How a union level counts its output before writing it.
@@ -42,6 +44,10 @@ enum class UnionCount {
     // stays at a few bytes per tile (an arena Call).
     kTileWalk,
 };
+
+// Headroom merge_level keeps below INT_MAX for its item count (entries of both operands plus
+// rows): it refuses larger levels with NACHO_ERR_INDEX_OVERFLOW.
+constexpr long long kLevelTileSlack = 4096;
 
 // Merge A and B row by row: union (or intersection) of each row's coordinates, with values
 // (a+b / a*b / copies) when `values`, or with child pointers when `child`.  Writes Z.pos for
