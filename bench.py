@@ -890,7 +890,7 @@ def main():
                     help="seconds of CPU baseline timing (0 disables)")
     ap.add_argument("--extra-cpu-budget", type=float, default=8.0,
                     help="seconds of CPU baseline timing per listed workload")
-    ap.add_argument("--extra-steps", type=int, default=10,
+    ap.add_argument("--extra-steps", type=int, default=20,
                     help="timed steps per listed workload (at most --steps)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 1 GiB device copy (rocprof counter calibration)")
