@@ -28,6 +28,7 @@
 // Every value is the reference's float32 sum in operand order, so results are bit-exact.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <climits>
 #include <cstdint>
 
@@ -97,15 +98,110 @@ __device__ __forceinline__ void split3(RA A, RB B, RC C, int aS, int aE, int bS,
 
 // ---- partition ----------------------------------------------------------------------------
 
+// ---- sparse-overlap count: row pass + duplicate search ------------------------------------
+// The union's output count is nnzA + nnzB + nnzC less its duplicates: the B entries whose
+// column is in A's row (|A ∩ B|) and the C entries whose column is in A's or B's row
+// (|C ∩ (A ∪ B)|).  Duplicates only occur in rows where at least two operands have entries;
+// when those rows hold few entries (three C2 operands: 0.8M searches for 50M entries), a
+// search per entry of the smaller side counts them without streaming every coordinate
+// through a walk.  Per row the searched entries are
+//   |A ∩ B|: the smaller of A's and B's entries (A on a tie), each searched in the other;
+//   |C ∩ (A ∪ B)|: C's entries, each searched in A and in B, when C has at most as many as A
+//            and B together; otherwise A's entries searched in C, and B's entries searched
+//            in C and counted only when absent from A.
+// Each duplicate is charged to the write chunk holding the searched entry (a key group never
+// spans tiles, so that is the chunk that merges it).
+// The row pass (extra workgroups of the partition launch) writes one record per row with
+// searches; the count kernel totals them (M) and picks the mode it and the write kernel follow:
+//   search: M * kSearchRatio <= nnzA + nnzB + nnzC: the count kernel searches every entry,
+//           chunk_count receives each write chunk's duplicates, and the write chunk starting
+//           at tile t0 starts at output a0 + b0 + c0 of t0's split less the duplicates
+//           before it; write lanes search their own starts.
+//   count:  the tile walk of csr3_count_kernel (chunk output counts, stored lane starts).
+constexpr int kModeCount = 0;
+constexpr int kModeSearch = 1;
+constexpr int kSearchRatio = 16;
+constexpr int kRowPassMaxBlocks = 1024;  // workgroups of the row pass (a multiple of kBlock)
+constexpr int kRowPassMinEntriesPerRow = 8;
+
+struct Rows3 {
+    // record k of row-pass workgroup b: rec[2 * (blk_base[b] + k)] = {first search (within
+    // b's), posA[r], posB[r], posC[r]} and rec[2 * (blk_base[b] + k) + 1] = {la, lb, lc, 0}
+    int4 *rec;
+    int *blk_base;   // record region of each workgroup (its first row)
+    int *blk_elems;  // searches per workgroup
+    int *blk_recs;   // records per workgroup
+    int *mode;       // kModeSearch or kModeCount (stored by the count kernel)
+    int rows_per_thread;
+    int nb;  // workgroups of the row pass
+};
+
+// Searches of one row with la, lb, lc entries in A, B and C.
+__device__ __forceinline__ int dup_searches(int la, int lb, int lc) {
+    const int wb = (la > 0 && lb > 0) ? min(la, lb) : 0;
+    const int lab = la + lb;
+    return wb + ((lc > 0 && lab > 0) ? min(lc, lab) : 0);
+}
+
+// Workgroup `block` of the row pass (one wave): one thread per rows_per_thread consecutive
+// rows; nothing waits on other workgroups.
+__device__ __forceinline__ void row_pass3(const int *__restrict__ pa, const int *__restrict__ pb,
+                                          const int *__restrict__ pc, int rows, const Rows3 &rp,
+                                          int block) {
+    static_assert(kPartBlock == dev::kWave, "the row pass scans within one wave");
+    const int tid = threadIdx.x;
+    const int rpt = rp.rows_per_thread;
+    const long long row0 = static_cast<long long>(block) * kPartBlock * rpt;  // < rows (or 0)
+    const long long first = row0 + static_cast<long long>(tid) * rpt;
+    int elems = 0, recs = 0;
+    for (int j = 0; j < rpt; ++j) {
+        const long long r = first + j;
+        if (r >= rows) break;
+        const int w = dup_searches(pa[r + 1] - pa[r], pb[r + 1] - pb[r], pc[r + 1] - pc[r]);
+        elems += w;
+        recs += w > 0;
+    }
+    const int e_incl = dev::wave_inclusive_sum(elems);
+    const int r_incl = dev::wave_inclusive_sum(recs);
+    int e_off = e_incl - elems;
+    int4 *out = rp.rec + 2 * (row0 + (r_incl - recs));
+    for (int j = 0; j < rpt; ++j) {
+        const long long r = first + j;
+        if (r >= rows) break;
+        const int a0 = pa[r], b0 = pb[r], c0 = pc[r];
+        const int la = pa[r + 1] - a0, lb = pb[r + 1] - b0, lc = pc[r + 1] - c0;
+        const int w = dup_searches(la, lb, lc);
+        if (w > 0) {
+            out[0] = make_int4(e_off, a0, b0, c0);
+            out[1] = make_int4(la, lb, lc, 0);
+            out += 2;
+            e_off += w;
+        }
+    }
+    if (tid == dev::kWave - 1) {
+        rp.blk_base[block] = static_cast<int>(row0);
+        rp.blk_elems[block] = e_incl;
+        rp.blk_recs[block] = r_incl;
+    }
+}
+
 // One thread per tile boundary t in [0, num_tiles]: the split (row, a, b, c) of diagonal
 // min(t * kTile, total), moved past the rest of a key group it would cut.  Thread 0 also
-// zeroes the accumulator of the count kernel's length total.
+// zeroes the accumulator of the count kernel's length total, and the first n_counts threads
+// the chunk counts (n_counts <= num_tiles + 1).  Workgroups from part_blocks on run the row
+// pass.
 __global__ __launch_bounds__(kPartBlock) void csr3_partition_kernel(
     const int *__restrict__ pa, const int *__restrict__ ca, const int *__restrict__ pb,
     const int *__restrict__ cb, const int *__restrict__ pc, const int *__restrict__ cc,
     int rows, int total, int num_tiles, int *__restrict__ split,
-    unsigned long long *__restrict__ done) {
+    unsigned long long *__restrict__ done, unsigned *__restrict__ zero_counts, int n_counts,
+    int part_blocks, Rows3 rp) {
+    if (static_cast<int>(blockIdx.x) >= part_blocks) {  // the row pass's workgroups
+        row_pass3(pa, pb, pc, rows, rp, static_cast<int>(blockIdx.x) - part_blocks);
+        return;
+    }
     const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t < n_counts) zero_counts[t] = 0u;
     if (t > num_tiles) return;
     if (t == 0) *done = 0ull;
     const long long d64 = static_cast<long long>(t) * kTile;
@@ -242,11 +338,11 @@ struct Lane3Out {
 };
 
 // A lane's start: (row k | A position << 16, B position | C position << 16), tile-local.
-// GIVEN: taken from `start` (the count kernel's); otherwise searched and stored to `start`.
-template <bool VALUES, bool COUNT_ONLY, bool GIVEN>
+// `given`: taken from `start` (the count kernel's); otherwise searched and stored to `start`.
+template <bool VALUES, bool COUNT_ONLY>
 __device__ __forceinline__ void walk3(Lane3Out &out, const Split3 &sp, int tile, const int *s_crd,
                                       const float *s_val, const unsigned *s_row,
-                                      const int *s_rowc, int tid, uint2 &start) {
+                                      const int *s_rowc, int tid, uint2 &start, bool given) {
     const int na = sp.a1 - sp.a0, nb = sp.b1 - sp.b0, nc = sp.c1 - sp.c0;
     const int nab = na + nb, n = nab + nc, nr = sp.r1 - sp.r0 + 1;
     // tile-local row starts in the staged arrays (A at [0, na), B at [na, nab), C at
@@ -266,7 +362,7 @@ __device__ __forceinline__ void walk3(Lane3Out &out, const Split3 &sp, int tile,
     const int steps = tid == kBlock - 1 ? tile_end - g_lo
                                         : min(tile_lo + (tid + 1) * kIpt, tile_end) - g_lo;
     int k = 0, ia = 0, ib = na, ic = nab;
-    if (GIVEN) {
+    if (given) {
         k = min(static_cast<int>(start.x & 0xffffu), nr - 1);
         ia = static_cast<int>(start.x >> 16);
         ib = static_cast<int>(start.y & 0xffffu);
@@ -287,7 +383,7 @@ __device__ __forceinline__ void walk3(Lane3Out &out, const Split3 &sp, int tile,
         const int d = local - (ra(k) + (rb(k) - na) + (rc(k) - nab) + k);
         split3(at, at, at, ra(k), ea(k), rb(k), eb(k), rc(k), ec(k), d, ia, ib, ic);
     }
-    if (!GIVEN) {
+    if (!given) {
         start = make_uint2(static_cast<unsigned>(k) | (static_cast<unsigned>(ia) << 16),
                            static_cast<unsigned>(ib) | (static_cast<unsigned>(ic) << 16));
     }
@@ -364,26 +460,213 @@ __device__ __forceinline__ void stage_splits3(int *s_split, const int *__restric
     for (int i = threadIdx.x; i < n; i += kBlock) s_split[i] = split[4 * t0 + i];
 }
 
+// The row pass's totals staged in LDS by every count workgroup: s_start[b] = searches before
+// row-pass workgroup b (s_start[nb] = M), and each workgroup's record count and region.
+// Returns the mode (the same in every workgroup); workgroup 0 stores it for the write
+// kernel.  Ends synchronised.
+__device__ __forceinline__ int stage_rows3(int *s_start, int *s_recs, int *s_base, int *s_wave,
+                                           const Rows3 &rp, long long entries) {
+    constexpr int kPer = kRowPassMaxBlocks / kBlock;
+    const int tid = threadIdx.x;
+    const int nb = rp.nb;
+    int v[kPer], sum = 0;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int i = tid * kPer + k;
+        v[k] = i < nb ? rp.blk_elems[i] : 0;
+        sum += v[k];
+        if (i < nb) {
+            s_recs[i] = rp.blk_recs[i];
+            s_base[i] = rp.blk_base[i];
+        }
+    }
+    int total = 0;
+    int off = dev::block_exclusive_sum<kBlock>(sum, s_wave, total);
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int i = tid * kPer + k;
+        if (i < nb) s_start[i] = off;
+        off += v[k];
+    }
+    if (tid == 0) s_start[nb] = total;
+    const int mode =
+        static_cast<long long>(total) * kSearchRatio <= entries ? kModeSearch : kModeCount;
+    if (blockIdx.x == 0 && tid == 0) *rp.mode = mode;
+    __syncthreads();
+    return mode;
+}
+
+// Whether x is among c[lo, lo + n) (ascending).
+__device__ __forceinline__ bool holds(const int *__restrict__ c, int lo, int n, int x) {
+    int p = lo, q = lo + n;
+    while (p < q) {
+        const int mid = (p + q) >> 1;
+        if (c[mid] < x) {
+            p = mid + 1;
+        } else {
+            q = mid;
+        }
+    }
+    return p < lo + n && c[p] == x;
+}
+
+// Search mode of the count kernel: a grid-stride loop over the M searches.  Search e lies in
+// row-pass workgroup b (staged offsets) and record k of b (binary search of the records'
+// first searches); its place in the row's searches picks the entry and the rows searched
+// (see the row pass).  Duplicates are added into chunk_count[write chunk], and the last
+// workgroup stores nnzA + nnzB + nnzC less all of them to `length_out`.
+__device__ __forceinline__ void dup_search(const int *s_start, const int *s_recs,
+                                           const int *s_base, unsigned *s_wsum, int *s_cs,
+                                           const Rows3 &rp, const int *__restrict__ ca,
+                                           const int *__restrict__ cb, const int *__restrict__ cc,
+                                           const int *__restrict__ split, int num_tiles, int chunk,
+                                           unsigned *__restrict__ chunk_count,
+                                           unsigned long long *__restrict__ done,
+                                           int64_t *__restrict__ length_out, long long entries) {
+    const int tid = threadIdx.x;
+    const int nb = rp.nb;
+    const int m_total = s_start[nb];
+    const int n_chunks = (num_tiles + chunk - 1) / chunk;
+    // the write chunks' first A, B and C positions, staged when they fit (s_cs[(op - 1) *
+    // n_chunks + w] for op 1..3)
+    const bool staged = 3 * n_chunks <= kCap;
+    if (staged) {
+        for (int i = tid; i < 3 * n_chunks; i += kBlock) {
+            const int op = i / n_chunks, w = i - op * n_chunks;
+            s_cs[i] = split[4 * min(w * chunk, num_tiles) + op + 1];
+        }
+        __syncthreads();
+    }
+    unsigned found = 0;  // duplicates seen by this wave (uniform in the wave)
+    for (long long base = static_cast<long long>(blockIdx.x) * kBlock; base < m_total;
+         base += static_cast<long long>(gridDim.x) * kBlock) {
+        const long long e = base + tid;
+        int chunk_id = -1;
+        if (e < m_total) {
+            int lo = 0, hi = nb - 1;
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (s_start[mid] <= e) {
+                    lo = mid;
+                } else {
+                    hi = mid - 1;
+                }
+            }
+            const int local = static_cast<int>(e - s_start[lo]);
+            const int4 *recs = rp.rec + 2 * static_cast<long long>(s_base[lo]);
+            int klo = 0, khi = s_recs[lo] - 1;
+            while (klo < khi) {
+                const int mid = (klo + khi + 1) >> 1;
+                if (recs[2 * mid].x <= local) {
+                    klo = mid;
+                } else {
+                    khi = mid - 1;
+                }
+            }
+            const int4 r0 = recs[2 * klo], r1 = recs[2 * klo + 1];
+            const int a0 = r0.y, b0 = r0.z, c0 = r0.w, la = r1.x, lb = r1.y, lc = r1.z;
+            const int j = local - r0.x;
+            const int wb = (la > 0 && lb > 0) ? min(la, lb) : 0;
+            const int jc = j - wb;  // index among the row's |C ∩ (A ∪ B)| searches
+            int op, pos;  // the searched entry: operand (1 A, 2 B, 3 C) and position
+            bool dup;
+            if (j < wb) {  // |A ∩ B|
+                if (la <= lb) {
+                    op = 1;
+                    pos = a0 + j;
+                    dup = holds(cb, b0, lb, ca[pos]);
+                } else {
+                    op = 2;
+                    pos = b0 + j;
+                    dup = holds(ca, a0, la, cb[pos]);
+                }
+            } else if (lc <= la + lb) {  // |C ∩ (A ∪ B)| by C's entries
+                op = 3;
+                pos = c0 + jc;
+                const int x = cc[pos];
+                dup = holds(ca, a0, la, x) || holds(cb, b0, lb, x);
+            } else if (jc < la) {  // ... by A's entries
+                op = 1;
+                pos = a0 + jc;
+                dup = holds(cc, c0, lc, ca[pos]);
+            } else {  // ... by B's entries absent from A
+                op = 2;
+                pos = b0 + (jc - la);
+                const int x = cb[pos];
+                dup = holds(cc, c0, lc, x) && !holds(ca, a0, la, x);
+            }
+            if (dup) {
+                // the write chunk holding it: last w whose first split is at or before pos
+                int wlo = 0, whi = n_chunks - 1;
+                const int *cs = s_cs + (op - 1) * n_chunks;
+                while (wlo < whi) {
+                    const int mid = (wlo + whi + 1) >> 1;
+                    if ((staged ? cs[mid] : split[4 * min(mid * chunk, num_tiles) + op]) <= pos) {
+                        wlo = mid;
+                    } else {
+                        whi = mid - 1;
+                    }
+                }
+                chunk_id = wlo;
+            }
+        }
+        // one atomic per distinct write chunk among the wave's duplicates
+        unsigned long long pending = __ballot(chunk_id >= 0);
+        found += static_cast<unsigned>(__popcll(pending));
+        while (pending) {
+            const int leader = __ffsll(static_cast<long long>(pending)) - 1;
+            const int c = __shfl(chunk_id, leader, dev::kWave);
+            const unsigned long long same = __ballot(chunk_id == c);
+            if (dev::lane() == leader) {
+                atomicAdd(&chunk_count[c], static_cast<unsigned>(__popcll(same)));
+            }
+            pending &= ~same;
+        }
+    }
+    if (dev::lane() == 0) s_wsum[tid / dev::kWave] = found;
+    __syncthreads();
+    if (tid == 0) {
+        unsigned dups = 0;
+#pragma unroll
+        for (int w = 0; w < kBlock / dev::kWave; ++w) dups += s_wsum[w];
+        dev::subtract_total(dups, done, entries, length_out);
+    }
+}
+
 // Output count of each chunk, and their sum (the result length) stored to `length_out` by
-// the last workgroup.
+// the last workgroup.  After a row pass (rp.blk_elems set) the launch first totals it and,
+// in search mode, runs dup_search instead (chunk_count then receives each chunk's
+// duplicates, and no lane starts are stored).
 __global__ __launch_bounds__(kBlock) void csr3_count_kernel(
     const int *__restrict__ pa, const int *__restrict__ ca, const int *__restrict__ pb,
     const int *__restrict__ cb, const int *__restrict__ pc, const int *__restrict__ cc,
     int num_tiles, int chunk, const int *__restrict__ split, unsigned *__restrict__ chunk_count,
     unsigned long long *__restrict__ done, int64_t *__restrict__ length_out,
-    uint2 *__restrict__ starts) {
+    uint2 *__restrict__ starts, Rows3 rp, long long entries) {
     __shared__ int s_crd[kCap];
     __shared__ unsigned s_row[kCap];
     __shared__ int s_rowc[kCap];
     __shared__ unsigned s_wave[kBlock / dev::kWave];
+    __shared__ int s_iwave[kBlock / dev::kWave];
     __shared__ int s_split[4 * (kMaxChunk + 1)];
+    static_assert(kRowPassMaxBlocks + 1 <= kCap && 2 * kRowPassMaxBlocks <= kCap,
+                  "the row pass's totals fit the tile arrays");
     const int tid = threadIdx.x;
+    if (rp.blk_elems != nullptr) {  // after a row pass
+        int *s_start = s_crd;
+        int *s_recs = reinterpret_cast<int *>(s_row);
+        int *s_base = s_recs + kRowPassMaxBlocks;
+        if (stage_rows3(s_start, s_recs, s_base, s_iwave, rp, entries) == kModeSearch) {
+            dup_search(s_start, s_recs, s_base, s_wave, s_rowc, rp, ca, cb, cc, split,
+                       num_tiles, chunk, chunk_count, done, length_out, entries);
+            return;
+        }
+    }
+    // Workgroup w counts write chunk w; the launch may hold more workgroups than write chunks
+    // (for the search mode), and those have no chunk.
     const int t0 = blockIdx.x * chunk, t1 = min(t0 + chunk, num_tiles);
     if (t0 >= t1) {
-        if (tid == 0) {
-            chunk_count[blockIdx.x] = 0u;
-            dev::add_to_total(0u, done, length_out);
-        }
+        if (tid == 0) dev::add_to_total(0u, done, length_out);
         return;
     }
     stage_splits3(s_split, split, t0, t1);
@@ -399,7 +682,7 @@ __global__ __launch_bounds__(kBlock) void csr3_count_kernel(
         if (t + 1 < t1) fetch3<false>(st, nsp, pa, ca, nullptr, pb, cb, nullptr, pc, cc, nullptr, tid);
         Lane3Out lo;
         uint2 start;
-        walk3<false, true, false>(lo, sp, t, s_crd, nullptr, s_row, s_rowc, tid, start);
+        walk3<false, true>(lo, sp, t, s_crd, nullptr, s_row, s_rowc, tid, start, false);
         starts[static_cast<size_t>(t) * kBlock + tid] = start;
         mine += static_cast<unsigned>(lo.count);
         if (t + 1 < t1) {
@@ -430,7 +713,8 @@ __global__ __launch_bounds__(kBlock) void csr3_write_kernel(
     const int *__restrict__ pc, const int *__restrict__ cc, const float *__restrict__ vc,
     int num_tiles, int chunk, const int *__restrict__ split,
     const unsigned *__restrict__ chunk_count, const uint2 *__restrict__ starts, int rows,
-    long long cap, int *__restrict__ pz, int *__restrict__ cz, float *__restrict__ vz) {
+    long long cap, int *__restrict__ pz, int *__restrict__ cz, float *__restrict__ vz,
+    const int *__restrict__ mode) {
     __shared__ int s_crd[kCap];
     __shared__ float s_val[kCap];
     __shared__ unsigned s_row[kCap];
@@ -440,15 +724,19 @@ __global__ __launch_bounds__(kBlock) void csr3_write_kernel(
     const int tid = threadIdx.x;
     const int t0 = blockIdx.x * chunk, t1 = min(t0 + chunk, num_tiles);
     if (t0 >= t1) return;
+    // search mode (see dup_search): chunk_count holds duplicates, and lanes search their starts
+    const bool search = mode != nullptr && *mode == kModeSearch;
     stage_splits3(s_split, split, t0, t1);
     int before = 0;
     for (int i = tid; i < static_cast<int>(blockIdx.x); i += kBlock) before += chunk_count[i];
     int base = 0;
     (void)dev::block_exclusive_sum<kBlock>(before, s_wave, base);  // (ends synchronised)
+    // outputs before the chunk: its first split's entries less the duplicates before it
+    if (search) base = s_split[1] + s_split[2] + s_split[3] - base;
     if (blockIdx.x == 0 && tid == 0) pz[0] = 0;
     Split3 sp = lds_split3(s_split, 0);
     Staged3 st;
-    uint2 start = starts[static_cast<size_t>(t0) * kBlock + tid];
+    uint2 start = search ? make_uint2(0u, 0u) : starts[static_cast<size_t>(t0) * kBlock + tid];
     fetch3<true>(st, sp, pa, ca, va, pb, cb, vb, pc, cc, vc, tid);
     stage3<true>(st, sp, s_crd, s_val, s_row, s_rowc, tid);
     __syncthreads();
@@ -457,10 +745,10 @@ __global__ __launch_bounds__(kBlock) void csr3_write_kernel(
         uint2 next_start = start;
         if (t + 1 < t1) {
             fetch3<true>(st, nsp, pa, ca, va, pb, cb, vb, pc, cc, vc, tid);
-            next_start = starts[static_cast<size_t>(t + 1) * kBlock + tid];
+            if (!search) next_start = starts[static_cast<size_t>(t + 1) * kBlock + tid];
         }
         Lane3Out lo;
-        walk3<true, false, true>(lo, sp, t, s_crd, s_val, s_row, s_rowc, tid, start);
+        walk3<true, false>(lo, sp, t, s_crd, s_val, s_row, s_rowc, tid, start, !search);
         int tile_total = 0;
         const int offset = dev::block_exclusive_sum<kBlock>(lo.count, s_wave, tile_total);
         // (the scan's barriers also mean every lane is done reading this tile's inputs)
@@ -482,7 +770,7 @@ __global__ __launch_bounds__(kBlock) void csr3_write_kernel(
         __syncthreads();
         for (int q = tid; q < min(tile_total, kCap); q += kBlock) {
             const long long dst = static_cast<long long>(base) + q;
-            if (dst < cap) {
+            if (dst >= 0 && dst < cap) {
                 cz[dst] = s_crd[q];
                 vz[dst] = s_val[q];
             }
@@ -545,29 +833,63 @@ int csr_add3_fused(const nacho_csr *a, const nacho_csr *b, const nacho_csr *c, n
     NACHO_TRY(call.scratch_n(static_cast<size_t>(grid) + 6, &counts));
     unsigned long long *done =
         reinterpret_cast<unsigned long long *>(counts + ((grid + 2) & ~1));
-    uint2 *starts = nullptr;  // every lane's start in every tile, from the count kernel
+    // every lane's start in every tile, from the count kernel's tile walk (count mode)
+    uint2 *starts = nullptr;
     NACHO_TRY(call.scratch_n(static_cast<size_t>(num_tiles) * kBlock, &starts));
     int64_t *length_out = nullptr;
     NACHO_TRY(call.length_word(&length_out));
 
+    // Row pass (rows holding at least kRowPassMinEntriesPerRow entries on average): at most
+    // kRowPassMaxBlocks workgroups of kPartBlock threads, at least 16 rows per thread, one
+    // two-int4 record per row with searches, each workgroup's records at its first row.
+    Rows3 rp{};
+    int row_grid = 0;
+    if (static_cast<long long>(rows) * kRowPassMinEntriesPerRow <= cap) {
+        const long long per_thread = std::max<long long>(
+            16, (static_cast<long long>(rows) + kPartBlock * kRowPassMaxBlocks - 1) /
+                    (kPartBlock * kRowPassMaxBlocks));
+        const long long per_block = per_thread * kPartBlock;
+        row_grid = static_cast<int>(std::max<long long>(1, (rows + per_block - 1) / per_block));
+        rp.rows_per_thread = static_cast<int>(per_thread);
+        rp.nb = row_grid;
+        NACHO_TRY(call.scratch_n(2 * static_cast<size_t>(std::max(rows, 1)), &rp.rec));
+        int *words = nullptr;
+        NACHO_TRY(call.scratch_n(3 * static_cast<size_t>(row_grid) + 1, &words));
+        rp.blk_base = words;
+        rp.blk_elems = words + row_grid;
+        rp.blk_recs = words + 2 * row_grid;
+        rp.mode = words + 3 * row_grid;
+    }
+
+    // The count launch: the write chunks, or as many workgroups as it keeps resident when
+    // that is more (they only take part in the search mode).
+    int count_grid = grid;
+    if (row_grid > 0) {
+        int count_resident = 0;
+        NACHO_TRY(resident_grid(reinterpret_cast<const void *>(csr3_count_kernel), kBlock,
+                                &count_resident));
+        count_grid = std::max(grid, count_resident);
+    }
     const hipStream_t s = call.stream();
     NACHO_TRY(call.timer_start("csr_add_3: fused three-way merge"));
-    csr3_partition_kernel<<<ceil_div(static_cast<size_t>(num_tiles) + 1, kPartBlock), kPartBlock,
-                            0, s>>>(
+    const int part_blocks =
+        static_cast<int>(ceil_div(static_cast<size_t>(num_tiles) + 1, kPartBlock));
+    csr3_partition_kernel<<<part_blocks + row_grid, kPartBlock, 0, s>>>(
         a->dim_j_offsets, a->dim_j_indices, b->dim_j_offsets, b->dim_j_indices,
         c->dim_j_offsets, c->dim_j_indices, rows, static_cast<int>(total), num_tiles, split,
-        done);
+        done, counts, grid, part_blocks, rp);
     NACHO_TRY_HIP(hipGetLastError());
-    csr3_count_kernel<<<grid, kBlock, 0, s>>>(a->dim_j_offsets, a->dim_j_indices,
+    csr3_count_kernel<<<count_grid, kBlock, 0, s>>>(a->dim_j_offsets, a->dim_j_indices,
                                              b->dim_j_offsets, b->dim_j_indices,
                                              c->dim_j_offsets, c->dim_j_indices, num_tiles,
-                                             chunk, split, counts, done, length_out, starts);
+                                             chunk, split, counts, done, length_out, starts, rp,
+                                             cap);
     NACHO_TRY_HIP(hipGetLastError());
     NACHO_TRY(call.mark_length());
     csr3_write_kernel<<<grid, kBlock, 0, s>>>(
         a->dim_j_offsets, a->dim_j_indices, a->values, b->dim_j_offsets, b->dim_j_indices,
         b->values, c->dim_j_offsets, c->dim_j_indices, c->values, num_tiles, chunk, split,
-        counts, starts, rows, cap, pz, cz, vz);
+        counts, starts, rows, cap, pz, cz, vz, rp.mode);
     NACHO_TRY_HIP(hipGetLastError());
     NACHO_TRY(call.timer_stop());
     int64_t nz = 0;

@@ -75,3 +75,25 @@ def test_key_groups_across_tiles(gpu, pattern):
         ops = [csr_from_rows(rows, cols, l, rng.standard_normal(sum(map(len, l))).tolist())
                for l in lists]
     assert_csr_equal(run(rows, cols, ops, gpu), oracle.port_csr_add3(rows, *ops), pattern)
+
+
+def test_duplicate_search_branches(gpu):
+    """Many rows that hold one operand only (so the count searches for duplicates instead of
+    walking every tile), and rows that take each search branch: A smaller or larger than B,
+    C at most A + B (C's entries searched) or more (A's and B's searched in C, B's counted
+    only when absent from A), empty A or B, keys in two and in all three operands."""
+    rng = np.random.default_rng(11)
+    rows, cols = 2000, 5000
+    shapes = [(3, 10, 2), (10, 3, 50), (0, 5, 20), (5, 0, 3), (12, 12, 40), (7, 2, 0)]
+    lists = [[], [], []]
+    for r in range(rows):
+        if r < 1880:  # one operand, 100 entries
+            for o in range(3):
+                lists[o].append(sorted(rng.choice(cols, 100, replace=False).tolist())
+                                if r % 3 == o else [])
+        else:  # overlapping rows, keys from a small pool
+            for o, n in enumerate(shapes[r % len(shapes)]):
+                lists[o].append(sorted(rng.choice(64, n, replace=False).tolist()))
+    ops = [csr_from_rows(rows, cols, l, rng.standard_normal(sum(map(len, l))).tolist())
+           for l in lists]
+    assert_csr_equal(run(rows, cols, ops, gpu), oracle.port_csr_add3(rows, *ops), "branches")
