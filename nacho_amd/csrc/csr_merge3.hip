@@ -21,10 +21,13 @@
 //    the smallest head (ties A, B, C), or consumes a row end.  The first item of a key group
 //    emits (its value is the sum of the group's present values, in the order (a + b) + c,
 //    the others are peeked at their heads); later items of the group are skipped by
-//    comparing with the previous item's key, so groups may straddle lanes.  The count
-//    kernel totals the result length for the early readback and stores every lane's start;
-//    the write kernel walks from those starts, stages its outputs in LDS and stores them
-//    coalesced.
+//    comparing with the previous item's key, so groups may straddle lanes.  The write
+//    kernel stages its outputs in LDS and stores them coalesced.
+//  * The count: where few entries can be duplicates (the rows where two or three operands
+//    have entries hold few of them), a row pass and a search per such entry count the
+//    duplicates of each write chunk (search mode, below); otherwise the count kernel walks
+//    every tile as above and stores every lane's start for the write kernel (tile mode).
+//    Either way it totals the result length for the early readback.
 // Every value is the reference's float32 sum in operand order, so results are bit-exact.
 #include <hip/hip_runtime.h>
 
