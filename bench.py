@@ -77,8 +77,9 @@ WORKLOADS = {
                                    "csr_pair_count_kernel + csr_write_kernel per level)",
                desc="C5 csf_add f32, two CSF3 tensors of shape (200000, 100000, 1000), 20M "
                     "draws each (mode 0 Zipf(1.3), modes 1-2 uniform), deduplicated, seeds 1/2"),
-    "c5coo": dict(op="coo3d_add", kernel="coo_partition_kernel + coo_count_kernel + "
-                                         "coo_write_kernel (packed 64-bit keys)",
+    "c5coo": dict(op="coo3d_add", kernel="coo3_keys_kernel (row offsets, (j, k) keys) + "
+                                         "csr_partition_kernel + csr_pair_count_kernel + "
+                                         "csr_write_kernel<Union> (rows out, keys split)",
                   desc="C5 as COO3: coo3d_add f32 of the same (i, j, k) tuples"),
     "c3coo": dict(op="coo_mul", kernel="coo_row_offsets_kernel + csr_partition_kernel + "
                                       "csr_write_kernel<Intersect> (spread, rows out) + "

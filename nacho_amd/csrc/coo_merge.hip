@@ -21,6 +21,7 @@
 // (compute.cpp:476-491), so results are bit-exact.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <climits>
 #include <cstdint>
 
@@ -688,6 +689,138 @@ int coo2_rows(const nacho_coo *a, const nacho_coo *b, nacho_coo *z, void *stream
     return NACHO_OK;
 }
 
+// ---- COO3 through row offsets ------------------------------------------------------------
+//
+// A COO3 operand sorted by (i, j, k) is a matrix with rows i and columns (j, k) in
+// lexicographic order.  When the j and k extents fit 31 bits together and the largest key
+// stays below INT_MAX, the column key j << kbits | k (kbits = bits of the k extent) orders
+// entries as (j, k) does, so coo3d_add
+// builds both operands' row offsets and keys in one pass, runs the CSR level union on them,
+// and the write kernel stores each output key split back into j and k, with its row as i.
+
+struct KeysJob {
+    const int *ci, *cj, *ck;
+    int nnz;
+    int *pos;  // rows + 1 row offsets
+    int *key;  // nnz column keys cj << kbits | ck
+};
+
+// Row offsets (as coo_row_offsets_kernel) and column keys of both COO3 operands in one
+// launch: workgroups [0, blocks_a) take A, the rest B; each thread kRowOffsetsPer consecutive
+// entries, whose i, j and k loads are all issued before anything is stored (16-byte loads
+// and stores when every array is 16-byte aligned).
+__global__ void coo3_keys_kernel(KeysJob ja, KeysJob jb, int blocks_a, int rows, int kbits) {
+    const bool first = static_cast<int>(blockIdx.x) < blocks_a;
+    const KeysJob &job = first ? ja : jb;
+    const int *__restrict__ ci = job.ci;
+    const int *__restrict__ cj = job.cj;
+    const int *__restrict__ ck = job.ck;
+    int *__restrict__ pos = job.pos;
+    int *__restrict__ key = job.key;
+    const int nnz = job.nnz;
+    const int64_t block = first ? blockIdx.x : blockIdx.x - blocks_a;
+    const int64_t blocks = first ? blocks_a : gridDim.x - blocks_a;
+    const int64_t n_groups = (static_cast<int64_t>(nnz) + kRowOffsetsPer) / kRowOffsetsPer;
+    const bool aligned = ((reinterpret_cast<uintptr_t>(ci) | reinterpret_cast<uintptr_t>(cj) |
+                           reinterpret_cast<uintptr_t>(ck) | reinterpret_cast<uintptr_t>(key)) &
+                          15u) == 0;
+    static_assert(kRowOffsetsPer == 8, "two 16-byte groups per thread");
+    for (int64_t g = block * blockDim.x + threadIdx.x; g < n_groups; g += blocks * blockDim.x) {
+        const int64_t p0 = g * kRowOffsetsPer;
+        int v[kRowOffsetsPer], kv[kRowOffsetsPer];
+        const int before = p0 == 0 ? -1 : ci[p0 - 1];
+        if (aligned && p0 + kRowOffsetsPer <= nnz) {
+            const int4 i0 = *reinterpret_cast<const int4 *>(ci + p0);
+            const int4 i1 = *reinterpret_cast<const int4 *>(ci + p0 + 4);
+            const int4 j0 = *reinterpret_cast<const int4 *>(cj + p0);
+            const int4 j1 = *reinterpret_cast<const int4 *>(cj + p0 + 4);
+            const int4 k0 = *reinterpret_cast<const int4 *>(ck + p0);
+            const int4 k1 = *reinterpret_cast<const int4 *>(ck + p0 + 4);
+            v[0] = i0.x; v[1] = i0.y; v[2] = i0.z; v[3] = i0.w;
+            v[4] = i1.x; v[5] = i1.y; v[6] = i1.z; v[7] = i1.w;
+            kv[0] = j0.x << kbits | k0.x; kv[1] = j0.y << kbits | k0.y;
+            kv[2] = j0.z << kbits | k0.z; kv[3] = j0.w << kbits | k0.w;
+            kv[4] = j1.x << kbits | k1.x; kv[5] = j1.y << kbits | k1.y;
+            kv[6] = j1.z << kbits | k1.z; kv[7] = j1.w << kbits | k1.w;
+            *reinterpret_cast<int4 *>(key + p0) = make_int4(kv[0], kv[1], kv[2], kv[3]);
+            *reinterpret_cast<int4 *>(key + p0 + 4) = make_int4(kv[4], kv[5], kv[6], kv[7]);
+        } else {
+#pragma unroll
+            for (int u = 0; u < kRowOffsetsPer; ++u) {
+                const bool in = p0 + u < nnz;
+                v[u] = in ? ci[p0 + u] : rows;  // past the end: closes the last rows
+                if (in) key[p0 + u] = cj[p0 + u] << kbits | ck[p0 + u];
+            }
+        }
+        int prev = min(max(before, -1), rows);
+#pragma unroll
+        for (int u = 0; u < kRowOffsetsPer; ++u) {
+            const int64_t p = p0 + u;
+            if (p > nnz) break;
+            const int cur = min(max(v[u], -1), rows);
+            for (int r = prev + 1; r <= cur; ++r) pos[r] = static_cast<int>(p);
+            prev = max(prev, cur);
+        }
+    }
+}
+
+int coo3_rows(const nacho_coo3 *a, const nacho_coo3 *b, nacho_coo3 *z, void *stream,
+              const nacho_allocator *alloc, int kbits, const char *name) {
+    const int rows = a->dim_i_size;
+    const int nnz_a = a->nnz, nnz_b = b->nnz;
+    const long long cap = static_cast<long long>(nnz_a) + nnz_b;
+    Call call(stream, alloc);
+    int *pa = nullptr, *pb = nullptr, *pz = nullptr, *ka = nullptr, *kb = nullptr;
+    int *zi = nullptr, *zj = nullptr, *zk = nullptr;
+    float *zv = nullptr;
+    NACHO_TRY(call.scratch_n(static_cast<size_t>(rows) + 1, &pa));
+    NACHO_TRY(call.scratch_n(static_cast<size_t>(rows) + 1, &pb));
+    NACHO_TRY(call.scratch_n(static_cast<size_t>(rows) + 1, &pz));
+    NACHO_TRY(call.scratch_n(static_cast<size_t>(std::max(nnz_a, 1)), &ka));
+    NACHO_TRY(call.scratch_n(static_cast<size_t>(std::max(nnz_b, 1)), &kb));
+    NACHO_TRY(call.result_n(static_cast<size_t>(cap), &zi));
+    NACHO_TRY(call.result_n(static_cast<size_t>(cap), &zj));
+    NACHO_TRY(call.result_n(static_cast<size_t>(cap), &zk));
+    NACHO_TRY(call.result_n(static_cast<size_t>(cap), &zv));
+    const hipStream_t s = call.stream();
+    NACHO_TRY(call.timer_start(name));
+    const unsigned ga = ceil_div(static_cast<size_t>(nnz_a) / kRowOffsetsPer + 1, 256);
+    const unsigned gb = ceil_div(static_cast<size_t>(nnz_b) / kRowOffsetsPer + 1, 256);
+    const KeysJob ja{a->dim_i_indices, a->dim_j_indices, a->dim_k_indices, nnz_a, pa, ka};
+    const KeysJob jb{b->dim_i_indices, b->dim_j_indices, b->dim_k_indices, nnz_b, pb, kb};
+    coo3_keys_kernel<<<ga + gb, 256, 0, s>>>(ja, jb, static_cast<int>(ga), rows, kbits);
+    NACHO_TRY_HIP(hipGetLastError());
+    NACHO_TRY(call.timer_stop());
+    NACHO_TRY(call.collect_timer());  // (kernel timing only) before the merge's own interval
+    const csr::LevelOperand A{pa, ka, a->values, nnz_a, nullptr};
+    const csr::LevelOperand B{pb, kb, b->values, nnz_b, nullptr};
+    const csr::LevelResult Z{pz, zj, zv, nullptr, nullptr, zi, zk, kbits};
+    long long nnz = 0;
+    NACHO_TRY(csr::merge_level(call, false, true, false, rows, A, B, Z, &nnz, name));
+    if (nnz > cap) return NACHO_ERR_MALFORMED_INPUT;
+    if (nnz == 0) {
+        call.drop_result(zi);
+        call.drop_result(zj);
+        call.drop_result(zk);
+        call.drop_result(zv);
+        zi = zj = zk = nullptr;
+        zv = nullptr;
+    }
+    z->dim_i_size = a->dim_i_size;
+    z->dim_j_size = a->dim_j_size;
+    z->dim_k_size = a->dim_k_size;
+    z->dim_i_length = static_cast<int32_t>(nnz);
+    z->dim_i_indices = zi;
+    z->dim_j_length = static_cast<int32_t>(nnz);
+    z->dim_j_indices = zj;
+    z->dim_k_length = static_cast<int32_t>(nnz);
+    z->dim_k_indices = zk;
+    z->values = zv;
+    z->nnz = static_cast<int32_t>(nnz);
+    call.commit();
+    return NACHO_OK;
+}
+
 bool bad_coo(const nacho_coo *t) {
     if (!t || t->dim_i_size < 0 || t->dim_j_size < 0 || t->nnz < 0) return true;
     if (t->dim_i_length != t->nnz || t->dim_j_length != t->nnz) return true;
@@ -771,6 +904,19 @@ int nacho_gpu_coo3d_add_f32(const nacho_coo3 *a, const nacho_coo3 *b, nacho_coo3
     if (a->dim_i_size != b->dim_i_size || a->dim_j_size != b->dim_j_size ||
         a->dim_k_size != b->dim_k_size) {
         return NACHO_ERR_INVALID_ARGUMENT;
+    }
+    NACHO_TRY(nacho::check_launch_hints(num_blocks, threads_per_block));
+    const long long entries = static_cast<long long>(a->nnz) + b->nnz;
+    // the row path's column keys stay below INT_MAX, the merge's exhausted-row sentinel
+    const int kbits = bits_for_extent(a->dim_k_size);
+    const bool keys_fit = a->dim_j_size >= 1 && a->dim_k_size >= 1 &&
+                          bits_for_extent(a->dim_j_size) + kbits <= 31 &&
+                          ((static_cast<long long>(a->dim_j_size - 1) << kbits) |
+                           (a->dim_k_size - 1)) < INT_MAX;
+    if (keys_fit &&
+        entries + a->dim_i_size <= static_cast<long long>(INT_MAX) - 2 * nacho::csr::kLevelTileSlack &&
+        a->dim_i_size <= kRowPathRowsPerEntry * entries + (1 << 20)) {
+        return coo3_rows(a, b, z, stream, alloc, kbits, "coo3d_add (row offsets + CSR merge)");
     }
     const int32_t extents[3] = {a->dim_i_size, a->dim_j_size, a->dim_k_size};
     int32_t *out[3];

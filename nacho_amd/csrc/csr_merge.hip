@@ -1028,9 +1028,11 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
     unsigned *__restrict__ length, int spread_by_a, int64_t *__restrict__ tile_count,
     int64_t *__restrict__ chunk_total, unsigned long long *__restrict__ done,
     int64_t *__restrict__ length_out, const uint2 *__restrict__ starts,
-    const int *__restrict__ mode, int *__restrict__ rc) {
+    const int *__restrict__ mode, int *__restrict__ rc, int *__restrict__ ck, int kbits) {
     static_assert(!(VALUES && CHILD), "a level carries values or child pointers, not both");
-    // rc (value levels, optional): each output's row, staged in s_row once the walk is done
+    // rc (value levels, optional): each output's row, staged in s_row once the walk is done;
+    // ck (value levels, optional): outputs stored split, c >> kbits to cc and the low kbits
+    // to ck
     static_assert(!SPREAD || (OP == Op::Intersect && !CHILD), "spread output: intersection");
     constexpr int kCap = kBlock * IPT + 2;
     constexpr int kLoads = (kCap + kBlock - 1) / kBlock;
@@ -1149,7 +1151,13 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
         for (int j = 0; j < kLoads; ++j) {
             const int q = tid + j * kBlock;
             if (q < tile_total) {
-                cc[base + q] = s_crd[q];
+                if (VALUES && ck) {
+                    const int c = s_crd[q];
+                    cc[base + q] = c >> kbits;
+                    ck[base + q] = c & ((1 << kbits) - 1);
+                } else {
+                    cc[base + q] = s_crd[q];
+                }
                 if (VALUES) vc[base + q] = s_val[q];
                 if (VALUES && rc) rc[base + q] = static_cast<int>(s_row[q]);
                 if (CHILD) {
@@ -1272,7 +1280,7 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
     if (intersect) {
         // One walk: each tile writes its pairs at its own position in the smaller operand's
         // range of a scratch buffer, then one compaction moves them into place.
-        if (!values || child) return NACHO_ERR_INVALID_ARGUMENT;
+        if (!values || child || Z.crd_low) return NACHO_ERR_INVALID_ARGUMENT;
         const int by_a = A.len <= B.len ? 1 : 0;
         const size_t cap = static_cast<size_t>(by_a ? A.len : B.len);
         int *tmp_crd = nullptr, *tmp_row = nullptr;
@@ -1295,7 +1303,7 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
                                      num_tiles, chunk, split_r, split_a, split_b, nullptr, rows,
                                      Z.pos, tmp_crd, tmp_val, nullptr, nullptr, nullptr,
                                      nullptr, nullptr, by_a, tile_count, chunk_total, done,
-                                     length_out, nullptr, nullptr, tmp_row);
+                                     length_out, nullptr, nullptr, tmp_row, nullptr, 0);
         NACHO_TRY_HIP(hipGetLastError());
         NACHO_TRY(call.mark_length());
         csr_compact_kernel<<<num_tiles, kBlock, 0, s>>>(
@@ -1380,7 +1388,7 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
         A.pos, A.crd, A.val, B.pos, B.crd, B.val, A.len, B.len, num_tiles, chunk, split_r,      \
         split_a, split_b, counts, rows, Z.pos, Z.crd, Z.val, A.next, B.next, Z.child_a,         \
         Z.child_b, length, 0, nullptr, nullptr, nullptr, nullptr, starts, rp.mode,             \
-        VAL ? Z.row : nullptr)
+        VAL ? Z.row : nullptr, VAL ? Z.crd_low : nullptr, Z.low_bits)
     if (values) {
         if (child) return NACHO_ERR_INVALID_ARGUMENT;
         if (keep_starts) {

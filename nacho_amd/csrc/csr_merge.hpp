@@ -29,6 +29,10 @@ struct LevelResult {
     int *child_b;
     // Value levels only, optional: the row of every output (a COO result's i coordinate).
     int *row = nullptr;
+    // Union value levels only, optional: each output coordinate c is stored split, as
+    // c >> low_bits to crd and c & (2^low_bits - 1) to crd_low (a COO3 result's j and k).
+    int *crd_low = nullptr;
+    int low_bits = 0;
 };
 
 // How a union level counts its output before writing it.

@@ -63,6 +63,28 @@ def test_coo3_random(gpu, seed):
     assert_coo_equal(got, oracle.port_coo_binary("add", a, va, b, vb), f"seed={seed}")
 
 
+@pytest.mark.parametrize("shape", [(7, 2**16, 2**15), (7, 2**16, 2**15 - 1),
+                                   (7, 2**16 + 1, 2**15), (3, 1000, 1), (2**23, 50, 50)])
+def test_coo3_column_key_bounds(gpu, shape):
+    """(j, k) keys of 31 bits whose largest is INT_MAX (the merge's sentinel: packed path)
+    and of 32 bits (packed path), a k extent of one (no k bits: row-offset path), and far
+    more rows than entries (packed path)."""
+    rng = np.random.default_rng(sum(shape))
+    n = 30000
+    coords = np.unique(np.stack([rng.integers(0, e, size=n) for e in shape], axis=1), axis=0)
+    coords[-1] = [e - 1 for e in shape]  # the largest key
+    coords = np.unique(coords, axis=0)
+    split = rng.random(len(coords)) < 0.6
+    both = rng.random(len(coords)) < 0.3
+    a, b = coords[split | both], coords[~split | both]
+    va = rng.uniform(-1, 1, len(a)).astype(np.float32)
+    vb = rng.uniform(-1, 1, len(b)).astype(np.float32)
+    ta = tuple(a[:, d].astype(np.int32) for d in range(3))
+    tb = tuple(b[:, d].astype(np.int32) for d in range(3))
+    got = run("add", shape, ta, va, tb, vb, gpu)
+    assert_coo_equal(got, oracle.port_coo_binary("add", ta, va, tb, vb), f"shape={shape}")
+
+
 def test_coo3_wide_keys(gpu):
     """Extents whose bit widths sum past 64 take the wide-key path."""
     rng = np.random.default_rng(9)
