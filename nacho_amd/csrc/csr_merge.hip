@@ -101,6 +101,11 @@ __device__ __forceinline__ void merge_split(ReadA A, ReadB B, int aS, int aE, in
 constexpr int kModeCount = 0;
 constexpr int kModeSearch = 1;
 constexpr int kSearchRatio = 16;
+// Tile mode of the pair count: a tile whose rows need at least this many searches counts its
+// pairs by walking each lane's items instead (about 16 dependent LDS steps per lane against
+// about 14 per search); lower when the lane's start is searched anyway (STARTS).
+constexpr int kWalkMin = 2 * kBlock;
+constexpr int kWalkMinStarts = kBlock;
 constexpr int kRowPassMaxBlocks = 1024;  // workgroups of the row pass (a multiple of kBlock)
 // The row pass reads two offsets per row, so it runs only where rows hold this many entries
 // on average: with about one entry per row (a CSF3 k level) its reads cost as much as the
@@ -673,6 +678,10 @@ __device__ __forceinline__ void pair_tile(
     const int rel = g_lo - tile_start;
     bool have_start = g_lo >= tile_end;  // lanes without items keep the tile's start
     LaneStart start{0u, static_cast<unsigned>(na)};
+    // this lane's items in the write kernel (for the walk count)
+    const int steps = tid == kBlock - 1
+                          ? tile_end - g_lo
+                          : min(t * kTile + (tid + 1) * kItemsPerLane, tile_end) - g_lo;
     __syncthreads();
     for (int kb = 0; kb < nr; kb += kRowBlock) {  // one pass unless nr > kRowBlock
         const int nrb = min(kRowBlock, nr - kb);
@@ -713,7 +722,10 @@ __device__ __forceinline__ void pair_tile(
             run += m[i];
         }
         __syncthreads();
-        for (int j = tid; j < work; j += kBlock) {
+        // Tiles with many searches (both operands dense in the same rows) count their pairs
+        // with a merge walk of each lane's write-kernel items instead (single-pass tiles).
+        const bool walk = nr <= kRowBlock && work >= (STARTS ? kWalkMinStarts : kWalkMin);
+        for (int j = walk ? work : tid; j < work; j += kBlock) {
             int lo = 0, hi = nrb - 1;  // the row: last k with mpre[k] <= j
             while (lo < hi) {
                 const int mid = (lo + hi + 1) >> 1;
@@ -755,7 +767,8 @@ __device__ __forceinline__ void pair_tile(
         // the row (last k whose first item is at or before it), then the merge-path split of
         // the row's A and B entries before it (ties: A first).
         const bool last_pass = kb + nrb >= nr;
-        if (STARTS && !have_start && (last_pass || rel < sh.ra[nrb] + sh.rb[nrb] + kb + nrb)) {
+        if ((STARTS || walk) && !have_start &&
+            (last_pass || rel < sh.ra[nrb] + sh.rb[nrb] + kb + nrb)) {
             int lo = 0, hi = nrb - 1;
             while (lo < hi) {
                 const int mid = (lo + hi + 1) >> 1;
@@ -782,6 +795,39 @@ __device__ __forceinline__ void pair_tile(
             start = LaneStart{static_cast<unsigned>(kb + k) | (static_cast<unsigned>(slo) << 16),
                               static_cast<unsigned>(na + D - slo)};
             have_start = true;
+            if (walk) {  // (kb == 0) count the pairs among this lane's items: a pair at its A
+                constexpr int kEnd = INT_MAX;  // head of an exhausted row side
+                auto end_a = [&](int r) { return r + 1 < nr ? static_cast<int>(sh.ra[r + 1]) : na; };
+                auto end_b = [&](int r) { return r + 1 < nr ? static_cast<int>(sh.rb[r + 1]) : nb; };
+                int r = k, ia = slo, ib = D - slo;
+                int iae = end_a(r), ibe = end_b(r);
+                int xa = ia < iae ? sh.crd[offA + ia] : kEnd;
+                int xb = ib < ibe ? sh.crd[offB + ib] : kEnd;
+                unsigned pairs = 0;
+#pragma unroll
+                for (int st = 0; st < kItemsPerLane + 1; ++st) {
+                    if (st < steps) {
+                        if (xa == kEnd && xb == kEnd) {  // row end
+                            ++r;
+                            iae = end_a(r);
+                            ibe = end_b(r);
+                            xa = ia < iae ? sh.crd[offA + ia] : kEnd;
+                            xb = ib < ibe ? sh.crd[offB + ib] : kEnd;
+                        } else {
+                            const bool take_a = xa <= xb;
+                            pairs += (take_a && xa == xb) ? 1u : 0u;
+                            if (take_a) {
+                                ++ia;
+                                xa = ia < iae ? sh.crd[offA + ia] : kEnd;
+                            } else {
+                                ++ib;
+                                xb = ib < ibe ? sh.crd[offB + ib] : kEnd;
+                            }
+                        }
+                    }
+                }
+                acc.found += pairs;
+            }
         }
     }
     if (STARTS) starts[static_cast<size_t>(t) * kBlock + tid] = make_uint2(start.k_ia, start.ib);
