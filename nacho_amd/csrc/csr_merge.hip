@@ -1163,17 +1163,6 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
         const int offset = dev::block_exclusive_sum<kBlock, int, false>(
             static_cast<int>(__popc(lo.valid)), s_wave, tile_total);
 
-        int ca_v[kSteps], cb_v[kSteps];
-        if (CHILD) {
-#pragma unroll
-            for (int s = 0; s < kSteps; ++s) {
-                // pos is 0 for steps that emitted nothing: (a0, b0), inside both operands
-                const int pa_s = sp.a0 + static_cast<int>(lo.pos[s] & 0xffffu);
-                const int pb_s = sp.b0 + static_cast<int>(lo.pos[s] >> 16);
-                ca_v[s] = next_a ? next_a[pa_s] : pa_s;
-                cb_v[s] = next_b ? next_b[pb_s] : pb_s;
-            }
-        }
         int o = offset, r = lo.first_row;
 #pragma unroll
         for (int s = 0; s < kSteps; ++s) {
@@ -1185,14 +1174,28 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
                 s_crd[o] = lo.crd[s];
                 if (VALUES) s_val[o] = lo.val[s];
                 if (VALUES && rc) s_row[o] = static_cast<unsigned>(r);
-                if (CHILD) {
-                    reinterpret_cast<int *>(s_val)[o] = ca_v[s];
-                    reinterpret_cast<int *>(s_row)[o] = cb_v[s];
-                }
+                // child pointers: the A / B positions before the output, tile-local, packed;
+                // the pointers themselves are gathered by the coalesced store below
+                if (CHILD) s_row[o] = lo.pos[s];
                 ++o;
             }
         }
         __syncthreads();
+        // child pointers of this lane's outputs, all gathered before any is stored (lanes past
+        // the tile's end repeat its last output; a tile of only empty rows gathers nothing,
+        // since s_row then holds no positions of this tile)
+        int ga[CHILD ? kLoads : 1], gb[CHILD ? kLoads : 1];
+        if (CHILD && tile_total > 0) {
+#pragma unroll
+            for (int j = 0; j < kLoads; ++j) {
+                const int q = min(tid + j * kBlock, tile_total - 1);
+                const unsigned pq = s_row[q];
+                const int pa_q = sp.a0 + static_cast<int>(pq & 0xffffu);
+                const int pb_q = sp.b0 + static_cast<int>(pq >> 16);
+                ga[j] = next_a ? next_a[pa_q] : pa_q;
+                gb[j] = next_b ? next_b[pb_q] : pb_q;
+            }
+        }
 #pragma unroll
         for (int j = 0; j < kLoads; ++j) {
             const int q = tid + j * kBlock;
@@ -1207,8 +1210,8 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
                 if (VALUES) vc[base + q] = s_val[q];
                 if (VALUES && rc) rc[base + q] = static_cast<int>(s_row[q]);
                 if (CHILD) {
-                    child_a[base + q] = reinterpret_cast<const int *>(s_val)[q];
-                    child_b[base + q] = reinterpret_cast<const int *>(s_row)[q];
+                    child_a[base + q] = ga[j];
+                    child_b[base + q] = gb[j];
                 }
             }
         }
