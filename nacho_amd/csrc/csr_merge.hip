@@ -12,10 +12,11 @@
 //    so empty rows and Zipf-heavy rows cost the same per item (the reference counts only
 //    nonzeros, tensor.cpp:308-413).  Item count T = nnzA + nnzB + rows, cut into tiles of
 //    kTile items.
-//  * csr_partition_kernel: one thread per tile boundary finds (row, a, b) for diagonal
-//    tile*kTile by a binary search over rows on S(r) = posA[r] + posB[r] + r, then a
-//    merge-path search inside the row.  An A/B pair with equal coordinates is never split
-//    across tiles (the reference's balancing step, partition.cpp:964-983).
+//  * csr_partition_kernel: a group of lanes per tile boundary finds (row, a, b) for diagonal
+//    tile*kTile by a many-way search over rows on S(r) = posA[r] + posB[r] + r, then a
+//    merge-path search inside the row (each round: one probe per lane and a ballot).  An A/B
+//    pair with equal coordinates is never split across tiles (the reference's balancing step,
+//    partition.cpp:964-983).
 //  * csr_pair_count_kernel and csr_write_kernel: each workgroup owns a fixed, contiguous
 //    chunk of tiles.  The count kernel reads only coordinates and row offsets and adds each
 //    write chunk's output count (a union tile emits na + nb - pairs); the write kernel starts
@@ -60,28 +61,11 @@ constexpr int kItemsPerLane = 15;  // odd: lanes' LDS walks spread over banks
 constexpr int kTile = kBlock * kItemsPerLane;
 static_assert(kLevelTileSlack >= kTile, "callers' item-count headroom covers merge_level's");
 constexpr int kPartBlock = 64;  // threads per workgroup of the partition kernel
+// Lanes that search one tile boundary together: each round of the searches costs one
+// dependent load and narrows the range (kPartLanes + 1)-fold; wider groups spend more
+// divergent loads per round.
+constexpr int kPartLanes = 8;
 
-
-// Merge-path split of the merged order of A[aS, aE) and B[bS, bE) (ties: A first) at the
-// point where `a + b == D`, followed by the pair rule: if the last A taken equals the next B,
-// that B joins this side.  `A(x)` and `B(y)` read coordinates by absolute position.
-template <typename ReadA, typename ReadB>
-__device__ __forceinline__ void merge_split(ReadA A, ReadB B, int aS, int aE, int bS, int bE,
-                                            int D, int &a, int &b) {
-    int lo = max(aS, D - bE);
-    int hi = min(aE, D - bS);
-    while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
-        if (A(mid) <= B(D - 1 - mid)) {
-            lo = mid + 1;
-        } else {
-            hi = mid;
-        }
-    }
-    a = lo;
-    b = D - lo;
-    if (a > aS && b < bE && A(a - 1) == B(b)) ++b;
-}
 
 // ---- sparse-overlap union count: row pass + pair search --------------------------------
 // A union's output count is na + nb - pairs, and pairs only occur in rows where both
@@ -107,6 +91,7 @@ constexpr int kSearchRatio = 16;
 constexpr int kWalkMin = 2 * kBlock;
 constexpr int kWalkMinStarts = kBlock;
 constexpr int kRowPassMaxBlocks = 1024;  // workgroups of the row pass (a multiple of kBlock)
+constexpr int kRowUnroll = 8;  // row steps of the row pass whose loads are issued together
 // The row pass reads two offsets per row, so it runs only where rows hold this many entries
 // on average: with about one entry per row (a CSF3 k level) its reads cost as much as the
 // tile walk it may save, and the few entries per row make the walk's lane starts cheap.
@@ -129,57 +114,63 @@ struct RowPairs {
     int nb;  // workgroups of the row pass
 };
 
-// Workgroup `block` of the row pass (one wave): one thread per rows_per_thread consecutive
-// rows.  It runs as extra workgroups of the partition kernel's launch, and nothing in it
+// Workgroup `block` of the row pass (one wave): rows_per_thread * 64 consecutive rows.  It
+// runs as extra workgroups of the partition kernel's launch, and nothing in it
 // waits for other workgroups: the count kernel, launched next, totals blk_elems and chooses
 // the mode.
 __device__ __forceinline__ void row_pass_block(const int *__restrict__ pa,
                                                const int *__restrict__ pb, int rows,
                                                const RowPairs &rp, int block) {
     static_assert(kPartBlock == dev::kWave, "the row pass scans within one wave");
-    const int tid = threadIdx.x;
+    const int l = threadIdx.x;
     const int rpt = rp.rows_per_thread;
     const long long per_block = static_cast<long long>(kPartBlock) * rpt;
     const long long row0 = block * per_block;  // < rows (or 0)
-    const long long first = row0 + static_cast<long long>(tid) * rpt;
-    int elems = 0, recs = 0;
-    for (int j = 0; j < rpt; ++j) {
-        const long long r = first + j;
-        if (r >= rows) break;
-        const int la = pa[r + 1] - pa[r], lb = pb[r + 1] - pb[r];
-        if (la > 0 && lb > 0) {
-            elems += min(la, lb);
-            ++recs;
-        }
-    }
-    const int e_incl = dev::wave_inclusive_sum(elems);
-    const int r_incl = dev::wave_inclusive_sum(recs);
-    int e_off = e_incl - elems;
     const int region = rp.px ? rp.px[row0] : static_cast<int>(row0);
-    int4 *out = rp.rec + region + (r_incl - recs);
-    for (int j = 0; j < rpt; ++j) {
-        const long long r = first + j;
-        if (r >= rows) break;
-        const int a0 = pa[r], la = pa[r + 1] - a0, b0 = pb[r], lb = pb[r + 1] - b0;
-        if (la > 0 && lb > 0) {
-            const bool a_small = la <= lb;
-            *out++ = make_int4(e_off, a_small ? a0 : b0, a_small ? b0 : a0,
-                               a_small ? lb : (la | INT_MIN));
-            e_off += min(la, lb);
+    int4 *out = rp.rec + region;
+    int e_base = 0, r_base = 0;  // entries to search and records of the rows before
+    // Step j covers rows row0 + j*64 .. +63, one per lane (coalesced), so the records come out
+    // in row order from one wave scan per step; kRowUnroll steps' loads are issued together.
+    for (int j0 = 0; j0 < rpt && rows > 0; j0 += kRowUnroll) {
+        int a0[kRowUnroll], a1[kRowUnroll], b0[kRowUnroll], b1[kRowUnroll];
+#pragma unroll
+        for (int u = 0; u < kRowUnroll; ++u) {
+            const long long r = row0 + static_cast<long long>(j0 + u) * dev::kWave + l;
+            const long long rc = r < rows ? r : rows - 1;
+            a0[u] = pa[rc];
+            a1[u] = pa[rc + 1];
+            b0[u] = pb[rc];
+            b1[u] = pb[rc + 1];
+        }
+#pragma unroll
+        for (int u = 0; u < kRowUnroll; ++u) {
+            const long long r = row0 + static_cast<long long>(j0 + u) * dev::kWave + l;
+            const int la = a1[u] - a0[u], lb = b1[u] - b0[u];
+            const bool rec = j0 + u < rpt && r < rows && la > 0 && lb > 0;
+            const int e = rec ? min(la, lb) : 0;
+            const int e_incl = dev::wave_inclusive_sum(e);
+            const int r_incl = dev::wave_inclusive_sum(static_cast<int>(rec));
+            if (rec) {
+                const bool a_small = la <= lb;
+                out[r_base + r_incl - 1] =
+                    make_int4(e_base + e_incl - e, a_small ? a0[u] : b0[u],
+                              a_small ? b0[u] : a0[u], a_small ? lb : (la | INT_MIN));
+            }
+            e_base += __builtin_amdgcn_readlane(e_incl, dev::kWave - 1);
+            r_base += __builtin_amdgcn_readlane(r_incl, dev::kWave - 1);
         }
     }
-    if (tid == dev::kWave - 1) {
+    if (l == 0) {
         rp.blk_base[block] = region;
-        rp.blk_elems[block] = e_incl;
-        rp.blk_recs[block] = r_incl;
+        rp.blk_elems[block] = e_base;
+        rp.blk_recs[block] = r_base;
     }
 }
 
-// One thread per tile boundary t in [0, num_tiles]: split of diagonal min(t*TILE, total).
-// Thread 0 also zeroes the ticket counter that the next kernel's length total uses, and the
-// first n_counts threads zero the chunk counts (n_counts <= num_tiles + 1).
-// (Launched in kPartBlock-thread workgroups: the few thousand boundaries then spread over
-// every CU instead of a few dozen.)  Workgroups from part_blocks on run the row pass.
+// kPartLanes lanes per tile boundary t in [0, num_tiles]: split of diagonal
+// min(t*TILE, total).  Boundary 0 also zeroes the ticket counter that the next kernel's length
+// total uses, and the first n_counts boundaries zero the chunk counts (n_counts <=
+// num_tiles + 1).  Workgroups from part_blocks on run the row pass.
 __global__ __launch_bounds__(kPartBlock) void csr_partition_kernel(
     const int *__restrict__ pa, const int *__restrict__ ca, const int *__restrict__ pb,
     const int *__restrict__ cb, int rows, int total, int num_tiles, int *__restrict__ split_r,
@@ -189,36 +180,38 @@ __global__ __launch_bounds__(kPartBlock) void csr_partition_kernel(
         row_pass_block(pa, pb, rows, rp, static_cast<int>(blockIdx.x) - part_blocks);
         return;
     }
-    const int t = blockIdx.x * blockDim.x + threadIdx.x;
-    if (t > num_tiles) return;
-    if (t == 0) *done = 0ull;  // accumulator of the kernel that totals the length
-    if (t < n_counts) zero_counts[t] = 0u;  // chunk counts the count kernel adds into
+    const int t = (static_cast<int>(blockIdx.x) * kPartBlock + static_cast<int>(threadIdx.x)) /
+                  kPartLanes;
+    if (t > num_tiles) return;  // whole lane groups
+    const bool lead = threadIdx.x % kPartLanes == 0;
+    if (lead && t == 0) *done = 0ull;  // accumulator of the kernel that totals the length
+    if (lead && t < n_counts) zero_counts[t] = 0u;  // chunk counts the count kernel adds into
     const long long d64 = static_cast<long long>(t) * kTile;
     const int diag = d64 > total ? total : static_cast<int>(d64);
 
-    // Largest row r in [0, rows] with S(r) <= diag.
-    int lo = 0, hi = rows;
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (pa[mid] + pb[mid] + mid <= diag) {
-            lo = mid;
-        } else {
-            hi = mid - 1;
-        }
-    }
-    const int r = lo;
+    // Largest row r in [0, rows] with S(r) <= diag (S(0) = 0).
+    const int r = dev::group_last_true<kPartLanes>(
+        0, rows, [&](int x) { return pa[x] + pb[x] + x <= diag; });
     int a, b;
     if (r == rows) {
         a = pa[rows];
         b = pb[rows];
     } else {
-        const int D = diag - r;  // a + b at the split, in absolute positions
-        merge_split([&](int x) { return ca[x]; }, [&](int y) { return cb[y]; }, pa[r], pa[r + 1],
-                    pb[r], pb[r + 1], D, a, b);
+        // Merge-path split of the row at a + b == D (ties: A first): a is one past the last
+        // x in [lo, hi) with A[x] <= B[D - 1 - x], then the pair rule.
+        const int D = diag - r;
+        const int aS = pa[r], aE = pa[r + 1], bS = pb[r], bE = pb[r + 1];
+        const int lo = max(aS, D - bE), hi = min(aE, D - bS);
+        a = dev::group_last_true<kPartLanes>(
+                lo - 1, hi - 1, [&](int x) { return ca[x] <= cb[D - 1 - x]; }) + 1;
+        b = D - a;
+        if (a > aS && b < bE && ca[a - 1] == cb[b]) ++b;
     }
-    split_r[t] = r;
-    split_a[t] = a;
-    split_b[t] = b;
+    if (lead) {
+        split_r[t] = r;
+        split_a[t] = a;
+        split_b[t] = b;
+    }
 }
 
 
@@ -1342,7 +1335,7 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
         NACHO_TRY(call.scratch_n(static_cast<size_t>(grid) + 1, &chunk_total));
         int64_t *len_dev = chunk_total + grid;
         NACHO_TRY(call.timer_start(kernel_name));  // the whole device pipeline of this level
-        const int part_blocks = static_cast<int>(ceil_div(static_cast<size_t>(num_tiles) + 1, kPartBlock));
+        const int part_blocks = static_cast<int>(ceil_div((static_cast<size_t>(num_tiles) + 1) * kPartLanes, kPartBlock));
         csr_partition_kernel<<<part_blocks, kPartBlock, 0, s>>>(
             A.pos, A.crd, B.pos, B.crd, rows, static_cast<int>(total), num_tiles, split_r,
             split_a, split_b, done, nullptr, 0, part_blocks, RowPairs{});
@@ -1416,7 +1409,7 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
     if (count_chunk > kMaxChunk) count_chunk = kMaxChunk;
     const int count_grid = (num_tiles + count_chunk - 1) / count_chunk;
     NACHO_TRY(call.timer_start(kernel_name));  // the whole device pipeline of this level
-    const int part_blocks = static_cast<int>(ceil_div(static_cast<size_t>(num_tiles) + 1, kPartBlock));
+    const int part_blocks = static_cast<int>(ceil_div((static_cast<size_t>(num_tiles) + 1) * kPartLanes, kPartBlock));
     csr_partition_kernel<<<part_blocks + row_grid, kPartBlock, 0, s>>>(
         A.pos, A.crd, B.pos, B.crd, rows, static_cast<int>(total), num_tiles, split_r, split_a,
         split_b, done, counts, grid, part_blocks, rp);

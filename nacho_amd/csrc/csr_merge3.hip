@@ -51,6 +51,7 @@ constexpr int kLoads = (kCap + kBlock - 1) / kBlock;
 constexpr int kSteps = kIpt + 2;         // a lane's range plus the group rule's two items
 constexpr int kMaxChunk = 64;
 constexpr int kPartBlock = 64;           // partition workgroups: boundaries over every CU
+constexpr int kPartLanes = 8;            // lanes that search one tile boundary together
 constexpr int kMax = INT_MAX;            // head sentinel: that operand's row is exhausted
 static_assert(kCap < 65536, "tile-local offsets are packed in 16 bits");
 
@@ -61,7 +62,10 @@ static_assert(kCap < 65536, "tile-local offsets are packed in 16 bits");
 // before the d-th item of the row's merged order (ties: A, then B, then C).  Nested search:
 // X = the (A, B) merge, Y = C; x = number of X items taken is the largest with
 // X[x - 1] <= Y[d - x] (X first on ties); X[q] is found by a two-way split at rank q + 1.
-template <typename RA, typename RB, typename RC>
+// G lanes call it together (dev::group_last_true; G = 1: one lane alone): the outer search
+// and the final two-way split are shared by the group, and each lane finds its own X[q] with
+// a binary search.
+template <int G, typename RA, typename RB, typename RC>
 __device__ __forceinline__ void split3(RA A, RB B, RC C, int aS, int aE, int bS, int bE, int cS,
                                        int cE, int d, int &a, int &b, int &c) {
     const int la = aE - aS, lb = bE - bS, lc = cE - cS;
@@ -84,19 +88,17 @@ __device__ __forceinline__ void split3(RA A, RB B, RC C, int aS, int aE, int bS,
         const int kb = tb > 0 ? B(bS + tb - 1) : INT_MIN;
         return max(ka, kb);
     };
-    int lo = max(0, d - lc), hi = min(la + lb, d);
-    while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
-        if (x_at(mid) <= C(cS + d - 1 - mid)) {
-            lo = mid + 1;
-        } else {
-            hi = mid;
-        }
-    }
-    const int ta = split2(lo);
+    // x: one past the last m in [lo, hi) with X[m] <= Y[d - 1 - m]
+    const int lo = max(0, d - lc), hi = min(la + lb, d);
+    const int x = dev::group_last_true<G>(
+                      lo - 1, hi - 1, [&](int m) { return x_at(m) <= C(cS + d - 1 - m); }) + 1;
+    // the two-way split of the (A, B) merge at x
+    const int lo2 = max(0, x - lb), hi2 = min(la, x);
+    const int ta = dev::group_last_true<G>(
+                       lo2 - 1, hi2 - 1, [&](int m) { return A(aS + m) <= B(bS + x - 1 - m); }) + 1;
     a = aS + ta;
-    b = bS + lo - ta;
-    c = cS + d - lo;
+    b = bS + x - ta;
+    c = cS + d - x;
 }
 
 // ---- partition ----------------------------------------------------------------------------
@@ -125,6 +127,7 @@ constexpr int kModeCount = 0;
 constexpr int kModeSearch = 1;
 constexpr int kSearchRatio = 16;
 constexpr int kRowPassMaxBlocks = 1024;  // workgroups of the row pass (a multiple of kBlock)
+constexpr int kRowUnroll = 8;  // row steps of the row pass whose loads are issued together
 constexpr int kRowPassMinEntriesPerRow = 8;
 
 struct Rows3 {
@@ -146,53 +149,62 @@ __device__ __forceinline__ int dup_searches(int la, int lb, int lc) {
     return wb + ((lc > 0 && lab > 0) ? min(lc, lab) : 0);
 }
 
-// Workgroup `block` of the row pass (one wave): one thread per rows_per_thread consecutive
-// rows; nothing waits on other workgroups.
+// Workgroup `block` of the row pass (one wave): rows_per_thread * 64 consecutive rows;
+// nothing waits on other workgroups.  Step j covers rows row0 + j*64 .. +63, one per lane
+// (coalesced), so the records come out in row order from one wave scan per step; kRowUnroll
+// steps' loads are issued together.
 __device__ __forceinline__ void row_pass3(const int *__restrict__ pa, const int *__restrict__ pb,
                                           const int *__restrict__ pc, int rows, const Rows3 &rp,
                                           int block) {
     static_assert(kPartBlock == dev::kWave, "the row pass scans within one wave");
-    const int tid = threadIdx.x;
+    const int l = threadIdx.x;
     const int rpt = rp.rows_per_thread;
     const long long row0 = static_cast<long long>(block) * kPartBlock * rpt;  // < rows (or 0)
-    const long long first = row0 + static_cast<long long>(tid) * rpt;
-    int elems = 0, recs = 0;
-    for (int j = 0; j < rpt; ++j) {
-        const long long r = first + j;
-        if (r >= rows) break;
-        const int w = dup_searches(pa[r + 1] - pa[r], pb[r + 1] - pb[r], pc[r + 1] - pc[r]);
-        elems += w;
-        recs += w > 0;
-    }
-    const int e_incl = dev::wave_inclusive_sum(elems);
-    const int r_incl = dev::wave_inclusive_sum(recs);
-    int e_off = e_incl - elems;
-    int4 *out = rp.rec + 2 * (row0 + (r_incl - recs));
-    for (int j = 0; j < rpt; ++j) {
-        const long long r = first + j;
-        if (r >= rows) break;
-        const int a0 = pa[r], b0 = pb[r], c0 = pc[r];
-        const int la = pa[r + 1] - a0, lb = pb[r + 1] - b0, lc = pc[r + 1] - c0;
-        const int w = dup_searches(la, lb, lc);
-        if (w > 0) {
-            out[0] = make_int4(e_off, a0, b0, c0);
-            out[1] = make_int4(la, lb, lc, 0);
-            out += 2;
-            e_off += w;
+    int4 *out = rp.rec + 2 * row0;
+    int e_base = 0, r_base = 0;  // searches and records of the rows before
+    for (int j0 = 0; j0 < rpt && rows > 0; j0 += kRowUnroll) {
+        int a0[kRowUnroll], a1[kRowUnroll], b0[kRowUnroll], b1[kRowUnroll], c0[kRowUnroll],
+            c1[kRowUnroll];
+#pragma unroll
+        for (int u = 0; u < kRowUnroll; ++u) {
+            const long long r = row0 + static_cast<long long>(j0 + u) * dev::kWave + l;
+            const long long rc = r < rows ? r : rows - 1;
+            a0[u] = pa[rc];
+            a1[u] = pa[rc + 1];
+            b0[u] = pb[rc];
+            b1[u] = pb[rc + 1];
+            c0[u] = pc[rc];
+            c1[u] = pc[rc + 1];
+        }
+#pragma unroll
+        for (int u = 0; u < kRowUnroll; ++u) {
+            const long long r = row0 + static_cast<long long>(j0 + u) * dev::kWave + l;
+            const int la = a1[u] - a0[u], lb = b1[u] - b0[u], lc = c1[u] - c0[u];
+            const bool in = j0 + u < rpt && r < rows;
+            const int w = in ? dup_searches(la, lb, lc) : 0;
+            const int e_incl = dev::wave_inclusive_sum(w);
+            const int r_incl = dev::wave_inclusive_sum(static_cast<int>(w > 0));
+            if (w > 0) {
+                int4 *o = out + 2 * (r_base + r_incl - 1);
+                o[0] = make_int4(e_base + e_incl - w, a0[u], b0[u], c0[u]);
+                o[1] = make_int4(la, lb, lc, 0);
+            }
+            e_base += __builtin_amdgcn_readlane(e_incl, dev::kWave - 1);
+            r_base += __builtin_amdgcn_readlane(r_incl, dev::kWave - 1);
         }
     }
-    if (tid == dev::kWave - 1) {
+    if (l == 0) {
         rp.blk_base[block] = static_cast<int>(row0);
-        rp.blk_elems[block] = e_incl;
-        rp.blk_recs[block] = r_incl;
+        rp.blk_elems[block] = e_base;
+        rp.blk_recs[block] = r_base;
     }
 }
 
-// One thread per tile boundary t in [0, num_tiles]: the split (row, a, b, c) of diagonal
-// min(t * kTile, total), moved past the rest of a key group it would cut.  Thread 0 also
-// zeroes the accumulator of the count kernel's length total, and the first n_counts threads
-// the chunk counts (n_counts <= num_tiles + 1).  Workgroups from part_blocks on run the row
-// pass.
+// kPartLanes lanes per tile boundary t in [0, num_tiles]: the split (row, a, b, c) of
+// diagonal min(t * kTile, total), moved past the rest of a key group it would cut.  Boundary 0
+// also zeroes the accumulator of the count kernel's length total, and the first n_counts
+// boundaries the chunk counts (n_counts <= num_tiles + 1).  Workgroups from part_blocks on
+// run the row pass.
 __global__ __launch_bounds__(kPartBlock) void csr3_partition_kernel(
     const int *__restrict__ pa, const int *__restrict__ ca, const int *__restrict__ pb,
     const int *__restrict__ cb, const int *__restrict__ pc, const int *__restrict__ cc,
@@ -203,29 +215,24 @@ __global__ __launch_bounds__(kPartBlock) void csr3_partition_kernel(
         row_pass3(pa, pb, pc, rows, rp, static_cast<int>(blockIdx.x) - part_blocks);
         return;
     }
-    const int t = blockIdx.x * blockDim.x + threadIdx.x;
-    if (t < n_counts) zero_counts[t] = 0u;
-    if (t > num_tiles) return;
-    if (t == 0) *done = 0ull;
+    const int t = (static_cast<int>(blockIdx.x) * kPartBlock + static_cast<int>(threadIdx.x)) /
+                  kPartLanes;
+    if (t > num_tiles) return;  // whole lane groups
+    const bool lead = threadIdx.x % kPartLanes == 0;
+    if (lead && t < n_counts) zero_counts[t] = 0u;
+    if (lead && t == 0) *done = 0ull;
     const long long d64 = static_cast<long long>(t) * kTile;
     const int diag = d64 > total ? total : static_cast<int>(d64);
-    int lo = 0, hi = rows;  // largest row r with S(r) <= diag
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (pa[mid] + pb[mid] + pc[mid] + mid <= diag) {
-            lo = mid;
-        } else {
-            hi = mid - 1;
-        }
-    }
-    const int r = lo;
+    // largest row r with S(r) <= diag (S(0) = 0)
+    const int r = dev::group_last_true<kPartLanes>(
+        0, rows, [&](int x) { return pa[x] + pb[x] + pc[x] + x <= diag; });
     int a = pa[r], b = pb[r], c = pc[r];
     if (r < rows) {
         const int aE = pa[r + 1], bE = pb[r + 1], cE = pc[r + 1];
         const int aS = a, bS = b, cS = c;
         const int d = diag - (aS + bS + cS + r);  // 0 <= d <= row length
-        split3([&](int x) { return ca[x]; }, [&](int y) { return cb[y]; },
-               [&](int z) { return cc[z]; }, aS, aE, bS, bE, cS, cE, d, a, b, c);
+        split3<kPartLanes>([&](int x) { return ca[x]; }, [&](int y) { return cb[y]; },
+                           [&](int z) { return cc[z]; }, aS, aE, bS, bE, cS, cE, d, a, b, c);
         // key group rule: B or C entries equal to the last key taken join this side
         int last = INT_MIN;
         if (a > aS) last = max(last, ca[a - 1]);
@@ -236,10 +243,12 @@ __global__ __launch_bounds__(kPartBlock) void csr3_partition_kernel(
             if (c < cE && cc[c] == last) ++c;
         }
     }
-    split[4 * t] = r;
-    split[4 * t + 1] = a;
-    split[4 * t + 2] = b;
-    split[4 * t + 3] = c;
+    if (lead) {
+        split[4 * t] = r;
+        split[4 * t + 1] = a;
+        split[4 * t + 2] = b;
+        split[4 * t + 3] = c;
+    }
 }
 
 // ---- tile staging -------------------------------------------------------------------------
@@ -384,7 +393,7 @@ __device__ __forceinline__ void walk3(Lane3Out &out, const Split3 &sp, int tile,
         }
         k = lo;
         const int d = local - (ra(k) + (rb(k) - na) + (rc(k) - nab) + k);
-        split3(at, at, at, ra(k), ea(k), rb(k), eb(k), rc(k), ec(k), d, ia, ib, ic);
+        split3<1>(at, at, at, ra(k), ea(k), rb(k), eb(k), rc(k), ec(k), d, ia, ib, ic);
     }
     if (!given) {
         start = make_uint2(static_cast<unsigned>(k) | (static_cast<unsigned>(ia) << 16),
@@ -875,8 +884,8 @@ int csr_add3_fused(const nacho_csr *a, const nacho_csr *b, const nacho_csr *c, n
     }
     const hipStream_t s = call.stream();
     NACHO_TRY(call.timer_start("csr_add_3: fused three-way merge"));
-    const int part_blocks =
-        static_cast<int>(ceil_div(static_cast<size_t>(num_tiles) + 1, kPartBlock));
+    const int part_blocks = static_cast<int>(
+        ceil_div((static_cast<size_t>(num_tiles) + 1) * kPartLanes, kPartBlock));
     csr3_partition_kernel<<<part_blocks + row_grid, kPartBlock, 0, s>>>(
         a->dim_j_offsets, a->dim_j_indices, b->dim_j_offsets, b->dim_j_indices,
         c->dim_j_offsets, c->dim_j_indices, rows, static_cast<int>(total), num_tiles, split,

@@ -107,6 +107,43 @@ __device__ __forceinline__ int64_t last_le(const T *__restrict__ a, int64_t lo, 
     return lo;
 }
 
+// Largest x in [lo, hi] with pred(x) true, for a predicate that holds up to some point and
+// fails after it; pred(lo) is taken to hold and is not evaluated.  G consecutive lanes (an
+// aligned group of a wave, G a power of two up to 64; G = 1 is a binary search) call it together with the same lo,
+// hi and pred, and all receive the result; other groups of the wave may search at the same
+// time.  Each round splits the interval into G + 1 parts of at most `step` points and every
+// lane of the group evaluates pred at the start of one of the last G parts, so n points take ceil(log_{G+1} n) rounds (one dependent
+// load each) instead of log2 n.  Points evaluated lie in (lo, hi].  On a predicate that is
+// not monotone the rounds still end, with some x in [lo, hi].
+template <int G, typename Pred>
+__device__ __forceinline__ int group_last_true(int lo, int hi, Pred pred) {
+    static_assert(G >= 1 && G <= kWave && (G & (G - 1)) == 0, "G: a power of two in [1, 64]");
+    if constexpr (G == 1) {  // one lane: a plain binary search
+        while (lo < hi) {
+            const int mid = static_cast<int>((static_cast<long long>(lo) + hi + 1) >> 1);
+            if (pred(mid)) {
+                lo = mid;
+            } else {
+                hi = mid - 1;
+            }
+        }
+        return lo;
+    }
+    const int l = lane() % G;
+    const int first = lane() - l;  // the group's first lane
+    while (lo < hi) {  // uniform within the group
+        const int step = static_cast<int>((static_cast<long long>(hi) - lo + 1 + G) / (G + 1));
+        const long long x = lo + static_cast<long long>(l + 1) * step;
+        const bool t = x <= hi && pred(static_cast<int>(x));
+        const unsigned long long bits = __ballot(t) >> first;
+        // the points that hold: lanes 0 .. c-1 of the group
+        const int c = __popcll(G == kWave ? bits : bits & ((1ull << (G % kWave)) - 1));
+        lo += c * step;
+        hi = static_cast<int>(min(static_cast<long long>(hi), static_cast<long long>(lo) + step - 1));
+    }
+    return lo;
+}
+
 // Exclusive max over the workgroup (values >= 0, identity 0).  Ends synchronised, unless
 // SYNC_END is false: then `s_wave` must not be written again before the caller's next
 // barrier.
