@@ -3,9 +3,8 @@
  *
  * Each GPU kernel that the reference declares for the operations this backend covers
  * (csr_add, csr_add_3, csr_mul, coo_add, coo_mul, coo3d_add, csf_add, dcsr_add, dcsr_mul,
- * dcsr_mul_without_recursive_partitioning, spgemm, sssmm: compiler.cpp:112-153) gets one
- * extern "C" entry point here.  The reference's coo_csr_add, inner_prod and inner_prod_coo
- * declarations (compiler.cpp:122, 141, 143) have none.  The reference binds
+ * dcsr_mul_without_recursive_partitioning, spgemm, sssmm, coo_csr_add, inner_prod,
+ * inner_prod_coo: compiler.cpp:112-153) gets one extern "C" entry point here.  The reference binds
  * `namespace <k> { Z_tensor_format <k>_gpu_i32_f32(a, b, num_blocks, threads_per_block); }`
  * (entry point printed at src/backend/stitch_and_generate.cpp:299-301,
  * called from the wrapper written by src/backend/generate_bindings.cpp:288-314).  These
@@ -155,6 +154,14 @@ typedef struct nacho_csf3 {
     int32_t nnz;
 } nacho_csf3;
 
+/* Scalar, format {} named "Scalar" (compiler.cpp:75): the single value of a full
+ * reduction.  Reference struct: {values, nnz} (tensor.cpp:13-61 with no levels; the values
+ * buffer holds one element). */
+typedef struct nacho_scalar {
+    float *values; /* 1 entry */
+    int32_t nnz;   /* 1       */
+} nacho_scalar;
+
 /* ---- allocation ------------------------------------------------------------------- */
 
 /* Caller-supplied device allocator, used for results and scratch.  `allocate` returns NULL
@@ -252,6 +259,30 @@ int nacho_gpu_coo_mul_f32(const nacho_coo *a, const nacho_coo *b, nacho_coo *z,
 int nacho_gpu_coo3d_add_f32(const nacho_coo3 *a, const nacho_coo3 *b, nacho_coo3 *z,
                             int32_t num_blocks, int32_t threads_per_block, void *stream,
                             const nacho_allocator *alloc);
+
+/* Z = a + b with a CSR left operand and a COO right operand, giving CSR (union; a + b where
+ * both hold a coordinate, explicit zeros kept).  The COO operand must be sorted by (i, j)
+ * without duplicates, as nacho.to_coo builds it.  Replaces coo_csr_add::coo_csr_add_gpu_i32_f32
+ * (kernel declared at compiler.cpp:122). */
+int nacho_gpu_coo_csr_add_f32(const nacho_csr *a, const nacho_coo *b, nacho_csr *z,
+                              int32_t num_blocks, int32_t threads_per_block, void *stream,
+                              const nacho_allocator *alloc);
+
+/* z = sum_ijk a_ijk * b_ijk over CSF3 operands: the inner product, a Scalar.  Each product
+ * is one float32 multiply (as the reference's a * b); the products are summed in float64
+ * in a fixed order (deterministic run to run) and rounded once, where the reference adds
+ * float32 partial sums with atomics (compute.cpp:498-520, nacho_kernel_utils.h:40-58).
+ * Replaces inner_prod::inner_prod_gpu_i32_f32 (compiler.cpp:141).  Asynchronous: the value
+ * is ready when `stream` reaches the end of the call's work. */
+int nacho_gpu_inner_prod_f32(const nacho_csf3 *a, const nacho_csf3 *b, nacho_scalar *z,
+                             int32_t num_blocks, int32_t threads_per_block, void *stream,
+                             const nacho_allocator *alloc);
+
+/* The same inner product over COO3 operands (sorted by (i, j, k), no duplicates).
+ * Replaces inner_prod_coo::inner_prod_coo_gpu_i32_f32 (compiler.cpp:143). */
+int nacho_gpu_inner_prod_coo_f32(const nacho_coo3 *a, const nacho_coo3 *b, nacho_scalar *z,
+                                 int32_t num_blocks, int32_t threads_per_block, void *stream,
+                                 const nacho_allocator *alloc);
 
 /* Z = a + b over CSF3 (union at every level; every coordinate of each level's union is
  * emitted).  Replaces csf_add::csf_add_gpu_i32_f32 (compiler.cpp:135). */

@@ -119,12 +119,21 @@ struct coo3_ijk {  // COO3 over (i, j, k): one merged level
     index_t nnz;
 };
 
+template <typename index_t, typename value_t>
+struct scalar {  // Scalar (format {}): a full reduction's single value, no levels
+    value_t *values;  // 1 entry
+    index_t nnz;
+};
+
 namespace detail {
 
-template <typename Z, typename CZ, typename CA, typename A, typename B, typename Fn>
+// a converts to CA, b to CB (default CA), the result from CZ
+template <typename Z, typename CZ, typename CA, typename CB = CA, typename A, typename B,
+          typename Fn>
 inline Z call2(Fn fn, const char *kernel, const A &a, const B &b, int32_t num_blocks,
                int32_t threads_per_block) {
-    const CA ca = to_c<CA>(a), cb = to_c<CA>(b);
+    const CA ca = to_c<CA>(a);
+    const CB cb = to_c<CB>(b);
     CZ cz{};
     check(fn(&ca, &cb, &cz, num_blocks, threads_per_block, stream(), nullptr), kernel);
     return from_c<Z>(cz);
@@ -144,8 +153,9 @@ inline Z call3(Fn fn, const char *kernel, const A &a, const B &b, const C &c,
 
 // ---- the generated namespaces ------------------------------------------------------------
 
-// Two operands a, b of one format and a result Z of another (compiler.cpp:112-138).
-#define NACHO_HIP_BINARY(K, FA, FB, FZ, CDESC)                                                   \
+// Two operands a, b and a result Z; CA, CB and CZ are their C descriptors
+// (compiler.cpp:112-148).
+#define NACHO_HIP_BINARY(K, FA, FB, FZ, CA, CB, CZ)                                              \
     namespace K {                                                                               \
     using index_t = int32_t;                                                                    \
     using value_t = float;                                                                      \
@@ -158,22 +168,29 @@ inline Z call3(Fn fn, const char *kernel, const A &a, const B &b, const C &c,
     inline Z_tensor_format<index_t, value_t> K##_gpu_i32_f32(                                   \
         const a_tensor_format<index_t, value_t> a, const b_tensor_format<index_t, value_t> b,   \
         const int32_t num_blocks, const int32_t threads_per_block) {                            \
-        return nacho_hip::detail::call2<Z_tensor_format<index_t, value_t>, CDESC, CDESC>(       \
+        return nacho_hip::detail::call2<Z_tensor_format<index_t, value_t>, CZ, CA, CB>(         \
             nacho_gpu_##K##_f32, #K, a, b, num_blocks, threads_per_block);                      \
     }                                                                                           \
     }
 
-NACHO_HIP_BINARY(csr_add, csr_ij, csr_ij, csr_ij, nacho_csr)                  // compiler.cpp:112
-NACHO_HIP_BINARY(csr_mul, csr_ij, csr_ij, csr_ij, nacho_csr)                  // compiler.cpp:116
-NACHO_HIP_BINARY(coo_add, coo_ij, coo_ij, coo_ij, nacho_coo)                  // compiler.cpp:118
-NACHO_HIP_BINARY(coo_mul, coo_ij, coo_ij, coo_ij, nacho_coo)                  // compiler.cpp:120
-NACHO_HIP_BINARY(dcsr_add, dcsr_ij, dcsr_ij, dcsr_ij, nacho_dcsr)             // compiler.cpp:124
-NACHO_HIP_BINARY(dcsr_mul, dcsr_ij, dcsr_ij, dcsr_ij, nacho_dcsr)             // compiler.cpp:126
-NACHO_HIP_BINARY(dcsr_mul_without_recursive_partitioning, dcsr_ij, dcsr_ij, dcsr_ij,
-                 nacho_dcsr)                                                  // compiler.cpp:128-133
-NACHO_HIP_BINARY(csf_add, csf3_ijk, csf3_ijk, csf3_ijk, nacho_csf3)           // compiler.cpp:135
-NACHO_HIP_BINARY(coo3d_add, coo3_ijk, coo3_ijk, coo3_ijk, nacho_coo3)         // compiler.cpp:138
-NACHO_HIP_BINARY(spgemm, csr_ij, csr_jk, csr_ik, nacho_csr)                   // compiler.cpp:145-148
+#define NACHO_HIP_SAME(K, F, FZ, C, CZ) NACHO_HIP_BINARY(K, F, F, FZ, C, C, CZ)
+NACHO_HIP_SAME(csr_add, csr_ij, csr_ij, nacho_csr, nacho_csr)                 // compiler.cpp:112
+NACHO_HIP_SAME(csr_mul, csr_ij, csr_ij, nacho_csr, nacho_csr)                 // compiler.cpp:116
+NACHO_HIP_SAME(coo_add, coo_ij, coo_ij, nacho_coo, nacho_coo)                 // compiler.cpp:118
+NACHO_HIP_SAME(coo_mul, coo_ij, coo_ij, nacho_coo, nacho_coo)                 // compiler.cpp:120
+NACHO_HIP_BINARY(coo_csr_add, csr_ij, coo_ij, csr_ij, nacho_csr, nacho_coo,
+                 nacho_csr)                                                   // compiler.cpp:122
+NACHO_HIP_SAME(dcsr_add, dcsr_ij, dcsr_ij, nacho_dcsr, nacho_dcsr)            // compiler.cpp:124
+NACHO_HIP_SAME(dcsr_mul, dcsr_ij, dcsr_ij, nacho_dcsr, nacho_dcsr)            // compiler.cpp:126
+NACHO_HIP_SAME(dcsr_mul_without_recursive_partitioning, dcsr_ij, dcsr_ij, nacho_dcsr,
+               nacho_dcsr)                                                    // compiler.cpp:128-133
+NACHO_HIP_SAME(csf_add, csf3_ijk, csf3_ijk, nacho_csf3, nacho_csf3)           // compiler.cpp:135
+NACHO_HIP_SAME(coo3d_add, coo3_ijk, coo3_ijk, nacho_coo3, nacho_coo3)         // compiler.cpp:138
+NACHO_HIP_SAME(inner_prod, csf3_ijk, scalar, nacho_csf3, nacho_scalar)        // compiler.cpp:141
+NACHO_HIP_SAME(inner_prod_coo, coo3_ijk, scalar, nacho_coo3, nacho_scalar)    // compiler.cpp:143
+NACHO_HIP_BINARY(spgemm, csr_ij, csr_jk, csr_ik, nacho_csr, nacho_csr,
+                 nacho_csr)                                                   // compiler.cpp:145-148
+#undef NACHO_HIP_SAME
 #undef NACHO_HIP_BINARY
 
 // Three operands a, b, c (compiler.cpp:114, 150-153).

@@ -11,6 +11,7 @@ from .convert import to_coo, to_coo3, to_csf3, to_csr, to_dcsr  # noqa: F401
 from .ops import (  # noqa: F401
     gpu_coo3d_add_f32,
     gpu_coo_add_f32,
+    gpu_coo_csr_add_f32,
     gpu_coo_mul_f32,
     gpu_csf_add_f32,
     gpu_csr_add_3_f32,
@@ -19,6 +20,8 @@ from .ops import (  # noqa: F401
     gpu_dcsr_add_f32,
     gpu_dcsr_mul_f32,
     gpu_dcsr_mul_without_recursive_partitioning_f32,
+    gpu_inner_prod_coo_f32,
+    gpu_inner_prod_f32,
     gpu_spgemm64_f32,
     gpu_sssmm_f32,
     gpu_spgemm_f32,
@@ -30,6 +33,7 @@ from .ops import (  # noqa: F401
 )
 from ._device import record_stream  # noqa: F401
 from .io import COO2D, COO3D_parsed, parse2D, parse3D_i32_f32  # noqa: F401
-from .tensors import COO3_gpu, COO_gpu, CSF3_gpu, CSR64_gpu, CSR_gpu, DCSR_gpu  # noqa: F401
+from .tensors import (  # noqa: F401
+    COO3_gpu, COO_gpu, CSF3_gpu, CSR64_gpu, CSR_gpu, DCSR_gpu, Scalar_gpu)
 
 __version__ = "0.1.0"

@@ -101,6 +101,13 @@ class Csf3Desc(ctypes.Structure):
     ]
 
 
+class ScalarDesc(ctypes.Structure):
+    _fields_ = [
+        ("values", ctypes.c_void_p),
+        ("nnz", ctypes.c_int32),
+    ]
+
+
 class Coo2dHost(ctypes.Structure):
     _fields_ = [
         ("N", ctypes.c_int32),
@@ -145,8 +152,15 @@ ENTRY_POINTS = {
     "nacho_gpu_dcsr_mul_f32": (DcsrDesc, DcsrDesc),
     "nacho_gpu_dcsr_mul_without_recursive_partitioning_f32": (DcsrDesc, DcsrDesc),
     "nacho_gpu_csf_add_f32": (Csf3Desc, Csf3Desc),
+    "nacho_gpu_inner_prod_f32": (Csf3Desc, ScalarDesc),
+    "nacho_gpu_inner_prod_coo_f32": (Coo3Desc, ScalarDesc),
     "nacho_gpu_spgemm_f32": (CsrDesc, CsrDesc),
     "nacho_gpu_spgemm64_f32": (CsrDesc, Csr64Desc),
+}
+
+# entry points whose two operands differ in format: name -> (a, b, result)
+ENTRY_POINTS_MIXED = {
+    "nacho_gpu_coo_csr_add_f32": (CsrDesc, CooDesc, CsrDesc),
 }
 
 # three-operand entry points (a, b, c, z, ...)
@@ -180,6 +194,14 @@ def load() -> ctypes.CDLL:
             continue
         fn.restype = ctypes.c_int
         fn.argtypes = [ctypes.POINTER(operand), ctypes.POINTER(operand), ctypes.POINTER(result),
+                       ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p,
+                       ctypes.POINTER(Allocator)]
+    for name, (da, db, result) in ENTRY_POINTS_MIXED.items():
+        fn = getattr(lib, name, None)
+        if fn is None:
+            continue
+        fn.restype = ctypes.c_int
+        fn.argtypes = [ctypes.POINTER(da), ctypes.POINTER(db), ctypes.POINTER(result),
                        ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p,
                        ctypes.POINTER(Allocator)]
     for name, (operand, result) in ENTRY_POINTS_3.items():

@@ -841,6 +841,155 @@ bool bad_coo3(const nacho_coo3 *t) {
     return false;
 }
 
+// ---- CSR + COO, and the COO3 inner product ------------------------------------------------
+
+// Z = a + b for a CSR a and a COO b (compiler.cpp:122): b's row offsets are built from its i
+// coordinates (coo_row_offsets_kernel) and the CSR level union merges the two as csr_add
+// does, so the result is the CSR that csr_add gives for a and b converted to CSR.
+int coo_csr_add(const nacho_csr *a, const nacho_coo *b, nacho_csr *z, int32_t nb, int32_t tpb,
+                void *stream, const nacho_allocator *alloc) {
+    if (!z) return NACHO_ERR_INVALID_ARGUMENT;
+    *z = nacho_csr{};
+    NACHO_TRY(check_launch_hints(nb, tpb));
+    if (csr::bad_csr(a) || bad_coo(b)) return NACHO_ERR_INVALID_ARGUMENT;
+    if (a->dim_i_size != b->dim_i_size || a->dim_j_size != b->dim_j_size) {
+        return NACHO_ERR_INVALID_ARGUMENT;
+    }
+    const int rows = a->dim_i_size;
+    const long long nnz_a = a->dim_j_length, nnz_b = b->nnz;
+    if (nnz_a + nnz_b + rows > static_cast<long long>(INT_MAX) - 2 * csr::kLevelTileSlack) {
+        return NACHO_ERR_INDEX_OVERFLOW;
+    }
+    const long long cap = nnz_a + nnz_b;
+    Call call(stream, alloc);
+    int *pb = nullptr, *pc = nullptr, *cc = nullptr;
+    float *vc = nullptr;
+    NACHO_TRY(call.scratch_n(static_cast<size_t>(rows) + 1, &pb));
+    NACHO_TRY(call.result_n(static_cast<size_t>(rows) + 1, &pc));
+    NACHO_TRY(call.result_n(static_cast<size_t>(cap), &cc));
+    NACHO_TRY(call.result_n(static_cast<size_t>(cap), &vc));
+    const hipStream_t s = call.stream();
+    NACHO_TRY(call.timer_start("coo_csr_add"));
+    const unsigned gb = ceil_div(static_cast<size_t>(nnz_b) / kRowOffsetsPer + 1, 256);
+    const RowOffsetsJob jb{b->dim_i_indices, static_cast<int>(nnz_b), pb};
+    coo_row_offsets_kernel<<<gb, 256, 0, s>>>(jb, jb, 0, rows);
+    NACHO_TRY_HIP(hipGetLastError());
+    NACHO_TRY(call.timer_stop());
+    NACHO_TRY(call.collect_timer());  // (kernel timing only) before the merge's own interval
+    const csr::LevelOperand A{a->dim_j_offsets, a->dim_j_indices, a->values,
+                              a->dim_j_length, nullptr};
+    const csr::LevelOperand B{pb, b->dim_j_indices, b->values, b->nnz, nullptr};
+    const csr::LevelResult Z{pc, cc, vc, nullptr, nullptr};
+    long long nnz = 0;
+    NACHO_TRY(csr::merge_level(call, false, true, false, rows, A, B, Z, &nnz, "coo_csr_add"));
+    if (nnz > cap) return NACHO_ERR_MALFORMED_INPUT;
+    if (nnz == 0) {
+        call.drop_result(cc);
+        call.drop_result(vc);
+        cc = nullptr;
+        vc = nullptr;
+    }
+    z->dim_i_size = rows;
+    z->dim_j_size = a->dim_j_size;
+    z->dim_j_offsets = pc;
+    z->dim_j_length = static_cast<int32_t>(nnz);
+    z->dim_j_indices = cc;
+    z->values = vc;
+    z->nnz = static_cast<int32_t>(nnz);
+    call.commit();
+    return NACHO_OK;
+}
+
+// Releases a buffer that an entry point returned to the caller, on `stream`.
+static void release_result(void *ptr, void *stream, const nacho_allocator *alloc) {
+    if (!ptr) return;
+    if (alloc) {
+        alloc->release(alloc->ctx, ptr, stream);
+    } else {
+        (void)nacho_free(ptr, stream);
+    }
+}
+
+// z = sum of a * b over the (i, j, k) both COO3 operands hold (compiler.cpp:143).  When the
+// (j, k) keys fit (as for coo3d_add), both operands become rows i of column keys
+// (coo3_keys_kernel) and the CSR level intersection sums its products (LevelResult::dot).
+// Otherwise the packed-tuple intersection computes the products, which are then summed.
+int coo3_inner_prod(const nacho_coo3 *a, const nacho_coo3 *b, nacho_scalar *z, int32_t nb,
+                    int32_t tpb, void *stream, const nacho_allocator *alloc) {
+    if (!z) return NACHO_ERR_INVALID_ARGUMENT;
+    *z = nacho_scalar{};
+    if (bad_coo3(a) || bad_coo3(b)) return NACHO_ERR_INVALID_ARGUMENT;
+    if (a->dim_i_size != b->dim_i_size || a->dim_j_size != b->dim_j_size ||
+        a->dim_k_size != b->dim_k_size) {
+        return NACHO_ERR_INVALID_ARGUMENT;
+    }
+    NACHO_TRY(check_launch_hints(nb, tpb));
+    const long long entries = static_cast<long long>(a->nnz) + b->nnz;
+    const int kbits = bits_for_extent(a->dim_k_size);
+    const bool keys_fit = a->dim_j_size >= 1 && a->dim_k_size >= 1 &&
+                          bits_for_extent(a->dim_j_size) + kbits <= 31 &&
+                          ((static_cast<long long>(a->dim_j_size - 1) << kbits) |
+                           (a->dim_k_size - 1)) < INT_MAX;
+    if (keys_fit &&
+        entries + a->dim_i_size <= static_cast<long long>(INT_MAX) - 2 * csr::kLevelTileSlack &&
+        a->dim_i_size <= kRowPathRowsPerEntry * entries + (1 << 20)) {
+        const int rows = a->dim_i_size;
+        const int nnz_a = a->nnz, nnz_b = b->nnz;
+        Call call(stream, alloc);
+        float *value = nullptr;
+        int *pa = nullptr, *pb = nullptr, *ka = nullptr, *kb = nullptr;
+        NACHO_TRY(call.result_n(1, &value));
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(rows) + 1, &pa));
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(rows) + 1, &pb));
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(std::max(nnz_a, 1)), &ka));
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(std::max(nnz_b, 1)), &kb));
+        const hipStream_t s = call.stream();
+        NACHO_TRY(call.timer_start("inner_prod_coo"));
+        const unsigned ga = ceil_div(static_cast<size_t>(nnz_a) / kRowOffsetsPer + 1, 256);
+        const unsigned gb = ceil_div(static_cast<size_t>(nnz_b) / kRowOffsetsPer + 1, 256);
+        const KeysJob ja{a->dim_i_indices, a->dim_j_indices, a->dim_k_indices, nnz_a, pa, ka};
+        const KeysJob jb{b->dim_i_indices, b->dim_j_indices, b->dim_k_indices, nnz_b, pb, kb};
+        coo3_keys_kernel<<<ga + gb, 256, 0, s>>>(ja, jb, static_cast<int>(ga), rows, kbits);
+        NACHO_TRY_HIP(hipGetLastError());
+        NACHO_TRY(call.timer_stop());
+        NACHO_TRY(call.collect_timer());  // (kernel timing only) before the merge's interval
+        const csr::LevelOperand A{pa, ka, a->values, nnz_a, nullptr};
+        const csr::LevelOperand B{pb, kb, b->values, nnz_b, nullptr};
+        csr::LevelResult Z{nullptr, nullptr, nullptr, nullptr, nullptr};
+        Z.dot = value;
+        long long unused = 0;
+        NACHO_TRY(csr::merge_level(call, true, true, false, rows, A, B, Z, &unused,
+                                   "inner_prod_coo"));
+        z->values = value;
+        z->nnz = 1;
+        call.commit();
+        return NACHO_OK;
+    }
+    // packed-tuple intersection, then the sum of its values
+    const int32_t extents[3] = {a->dim_i_size, a->dim_j_size, a->dim_k_size};
+    int32_t *out[3] = {nullptr, nullptr, nullptr};
+    float *val = nullptr;
+    int32_t n = 0;
+    NACHO_TRY(coo_binary<Op::Intersect>(
+        3, extents, Coords{a->dim_i_indices, a->dim_j_indices, a->dim_k_indices}, a->values,
+        a->nnz, Coords{b->dim_i_indices, b->dim_j_indices, b->dim_k_indices}, b->values, b->nnz,
+        nb, tpb, stream, alloc, "inner_prod_coo (tuple intersection)", out, &val, &n));
+    int rc = NACHO_OK;
+    float *value = nullptr;
+    {
+        Call call(stream, alloc);
+        rc = call.result_n(1, &value);
+        if (rc == NACHO_OK) rc = csr::sum_values(call, val, n, value);
+        if (rc == NACHO_OK) call.commit();
+    }
+    for (int d = 0; d < 3; ++d) release_result(out[d], stream, alloc);
+    release_result(val, stream, alloc);
+    if (rc != NACHO_OK) return rc;
+    z->values = value;
+    z->nnz = 1;
+    return NACHO_OK;
+}
+
 template <Op OP>
 int coo2(const nacho_coo *a, const nacho_coo *b, nacho_coo *z, int32_t nb, int32_t tpb,
          void *stream, const nacho_allocator *alloc, const char *name) {
@@ -892,6 +1041,18 @@ int nacho_gpu_coo_mul_f32(const nacho_coo *a, const nacho_coo *b, nacho_coo *z,
     return nacho::coo::coo2<nacho::coo::Op::Intersect>(a, b, z, num_blocks, threads_per_block,
                                                        stream, alloc,
                                                        "coo_merge_tile_kernel<Intersect>");
+}
+
+int nacho_gpu_coo_csr_add_f32(const nacho_csr *a, const nacho_coo *b, nacho_csr *z,
+                              int32_t num_blocks, int32_t threads_per_block, void *stream,
+                              const nacho_allocator *alloc) {
+    return nacho::coo::coo_csr_add(a, b, z, num_blocks, threads_per_block, stream, alloc);
+}
+
+int nacho_gpu_inner_prod_coo_f32(const nacho_coo3 *a, const nacho_coo3 *b, nacho_scalar *z,
+                                 int32_t num_blocks, int32_t threads_per_block, void *stream,
+                                 const nacho_allocator *alloc) {
+    return nacho::coo::coo3_inner_prod(a, b, z, num_blocks, threads_per_block, stream, alloc);
 }
 
 int nacho_gpu_coo3d_add_f32(const nacho_coo3 *a, const nacho_coo3 *b, nacho_coo3 *z,

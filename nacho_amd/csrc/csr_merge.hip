@@ -1285,6 +1285,77 @@ int misalign(const void *p, int *out) {
     return NACHO_OK;
 }
 
+// ---- inner product of a spread intersection -------------------------------------------
+
+// Binary64 sum of the kBlock values of `sh` into sh[0], in a fixed order; ends synchronised.
+__device__ __forceinline__ void block_sum_fixed(double *sh) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int w = kBlock / 2; w > 0; w >>= 1) {
+        __syncthreads();
+        if (tid < w) sh[tid] += sh[tid + w];
+    }
+    __syncthreads();
+}
+
+// Workgroup t sums the products that tile t of the spread intersection wrote (tile_count[t]
+// of them, at its own start position in the smaller operand's range) in binary64, in a
+// fixed order: partial[t].
+__global__ __launch_bounds__(kBlock) void dot_tiles_kernel(
+    const int *__restrict__ split_a, const int *__restrict__ split_b, int by_a,
+    const int64_t *__restrict__ tile_count, const float *__restrict__ prod,
+    double *__restrict__ partial) {
+    __shared__ double sh[kBlock];
+    const int t = blockIdx.x;
+    const int base = by_a ? split_a[t] : split_b[t];
+    const int n = static_cast<int>(tile_count[t]);
+    double acc = 0.0;
+    for (int i = threadIdx.x; i < n; i += kBlock) acc += static_cast<double>(prod[base + i]);
+    sh[threadIdx.x] = acc;
+    block_sum_fixed(sh);
+    if (threadIdx.x == 0) partial[t] = sh[0];
+}
+
+// One workgroup: the sum of the n tile partials in a fixed order, rounded once to *dot.
+__global__ __launch_bounds__(kBlock) void dot_final_kernel(const double *__restrict__ partial,
+                                                           int n, float *__restrict__ dot) {
+    __shared__ double sh[kBlock];
+    double acc = 0.0;
+    for (int i = threadIdx.x; i < n; i += kBlock) acc += partial[i];
+    sh[threadIdx.x] = acc;
+    block_sum_fixed(sh);
+    if (threadIdx.x == 0) *dot = static_cast<float>(sh[0]);
+}
+
+// Workgroup b sums v[b * kSumTile, min(n, (b + 1) * kSumTile)) in binary64, in a fixed
+// order: partial[b].
+constexpr int kSumTile = 16 * kBlock;
+__global__ __launch_bounds__(kBlock) void sum_blocks_kernel(const float *__restrict__ v,
+                                                            long long n,
+                                                            double *__restrict__ partial) {
+    __shared__ double sh[kBlock];
+    const long long lo = static_cast<long long>(blockIdx.x) * kSumTile;
+    const long long hi = min(n, lo + kSumTile);
+    double acc = 0.0;
+    for (long long i = lo + threadIdx.x; i < hi; i += kBlock) acc += static_cast<double>(v[i]);
+    sh[threadIdx.x] = acc;
+    block_sum_fixed(sh);
+    if (threadIdx.x == 0) partial[blockIdx.x] = sh[0];
+}
+
+int sum_values(Call &call, const float *v, long long n, float *out) {
+    const long long blocks = std::max<long long>(1, (n + kSumTile - 1) / kSumTile);
+    if (blocks > INT_MAX) return NACHO_ERR_INDEX_OVERFLOW;
+    double *partial = nullptr;
+    NACHO_TRY(call.scratch_n(static_cast<size_t>(blocks), &partial));
+    const hipStream_t s = call.stream();
+    sum_blocks_kernel<<<static_cast<unsigned>(blocks), kBlock, 0, s>>>(v, n, partial);
+    NACHO_TRY_HIP(hipGetLastError());
+    dot_final_kernel<<<1, kBlock, 0, s>>>(partial, static_cast<int>(blocks), out);
+    NACHO_TRY_HIP(hipGetLastError());
+    return NACHO_OK;
+}
+
 int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
                 const LevelOperand &A, const LevelOperand &B, const LevelResult &Z,
                 long long *out_len, const char *kernel_name, UnionCount count_plan) {
@@ -1332,8 +1403,17 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
         NACHO_TRY(call.scratch_n(cap, &tmp_val));
         if (Z.row) NACHO_TRY(call.scratch_n(cap, &tmp_row));
         NACHO_TRY(call.scratch_n(static_cast<size_t>(num_tiles), &tile_count));
-        NACHO_TRY(call.scratch_n(static_cast<size_t>(grid) + 1, &chunk_total));
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(grid) + 2, &chunk_total));
         int64_t *len_dev = chunk_total + grid;
+        int *pos = Z.pos;
+        double *partial = nullptr;
+        if (Z.dot) {
+            // the inner product: the spread write's pos and length go to scratch, and the
+            // host does not wait for the length
+            NACHO_TRY(call.scratch_n(static_cast<size_t>(rows) + 1, &pos));
+            NACHO_TRY(call.scratch_n(static_cast<size_t>(num_tiles), &partial));
+            length_out = chunk_total + grid + 1;
+        }
         NACHO_TRY(call.timer_start(kernel_name));  // the whole device pipeline of this level
         const int part_blocks = static_cast<int>(ceil_div((static_cast<size_t>(num_tiles) + 1) * kPartLanes, kPartBlock));
         csr_partition_kernel<<<part_blocks, kPartBlock, 0, s>>>(
@@ -1343,10 +1423,21 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
         csr_write_kernel<Op::Intersect, kItemsPerLane, true, false, true>
             <<<grid, kBlock, 0, s>>>(A.pos, A.crd, A.val, B.pos, B.crd, B.val, A.len, B.len,
                                      num_tiles, chunk, split_r, split_a, split_b, nullptr, rows,
-                                     Z.pos, tmp_crd, tmp_val, nullptr, nullptr, nullptr,
+                                     pos, tmp_crd, tmp_val, nullptr, nullptr, nullptr,
                                      nullptr, nullptr, by_a, tile_count, chunk_total, done,
                                      length_out, nullptr, nullptr, tmp_row, nullptr, 0);
         NACHO_TRY_HIP(hipGetLastError());
+        if (Z.dot) {
+            dot_tiles_kernel<<<num_tiles, kBlock, 0, s>>>(split_a, split_b, by_a, tile_count,
+                                                          tmp_val, partial);
+            NACHO_TRY_HIP(hipGetLastError());
+            dot_final_kernel<<<1, kBlock, 0, s>>>(partial, num_tiles, Z.dot);
+            NACHO_TRY_HIP(hipGetLastError());
+            NACHO_TRY(call.timer_stop());
+            NACHO_TRY(call.collect_timer());  // (kernel timing only: waits for the stream)
+            *out_len = 0;
+            return NACHO_OK;
+        }
         NACHO_TRY(call.mark_length());
         csr_compact_kernel<<<num_tiles, kBlock, 0, s>>>(
             split_r, split_a, split_b, num_tiles, chunk, rows, by_a, tile_count, chunk_total,

@@ -33,6 +33,12 @@ struct LevelResult {
     // c >> low_bits to crd and c & (2^low_bits - 1) to crd_low (a COO3 result's j and k).
     int *crd_low = nullptr;
     int low_bits = 0;
+    // Intersection value levels only, optional: the level's inner product instead of its
+    // result.  Σ a·b over the pairs (each product one binary32 multiply, as the result's
+    // values) is summed in binary64 in a fixed order, rounded once and stored to this device
+    // float; pos, crd and val are then not written (they may be null), *out_len is 0, and
+    // the host does not wait for the device.
+    float *dot = nullptr;
 };
 
 // How a union level counts its output before writing it.
@@ -61,6 +67,13 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
                 const LevelOperand &A, const LevelOperand &B, const LevelResult &Z,
                 long long *out_len, const char *kernel_name,
                 UnionCount count = UnionCount::kAuto);
+
+// Σ v[0, n) summed in binary64 in a fixed order and rounded once to the device float *out
+// (kernels queued on the call's stream; v may be null when n is 0).
+int sum_values(Call &call, const float *v, long long n, float *out);
+
+// A CSR descriptor that no entry point can take (negative sizes, missing buffers).
+bool bad_csr(const nacho_csr *t);
 
 // Bytes of scratch merge_level takes from an arena Call for a union level of `items` merge
 // items (entries of both operands plus rows) without lane starts.

@@ -15,7 +15,7 @@ import ctypes
 import torch
 
 from . import _device, _lib
-from .tensors import COO3_gpu, COO_gpu, CSF3_gpu, CSR64_gpu, CSR_gpu, DCSR_gpu
+from .tensors import COO3_gpu, COO_gpu, CSF3_gpu, CSR64_gpu, CSR_gpu, DCSR_gpu, Scalar_gpu
 
 _I32, _I64, _F32 = torch.int32, torch.int64, torch.float32
 
@@ -142,6 +142,10 @@ def _adopt_csf3(z: _lib.Csf3Desc, device, stream) -> CSF3_gpu:
                              [z.dim_i_size, z.dim_j_size, z.dim_k_size], device)
 
 
+def _adopt_scalar(z: _lib.ScalarDesc, device, stream) -> Scalar_gpu:
+    return Scalar_gpu._trusted((_device.adopt(z.values, 1, _F32, device, stream),), [], device)
+
+
 # ---- input validation ----------------------------------------------------------------
 
 _VALIDATE = False
@@ -180,10 +184,14 @@ def _maybe_validate(*operands):
 
 # ---- generic call --------------------------------------------------------------------
 
-def _call(entry, a, b, cls, desc_fn, result_desc, adopt_fn, num_blocks, threads_per_block):
-    for name, t in (("a", a), ("b", b)):
-        if not isinstance(t, cls):
-            raise TypeError(f"{entry}: operand {name} must be {cls.__name__}, "
+def _call(entry, a, b, cls, desc_fn, result_desc, adopt_fn, num_blocks, threads_per_block,
+          cls_b=None, desc_fn_b=None):
+    """One two-operand entry point: a (class `cls`) and b (class `cls_b`, default `cls`)."""
+    cls_b = cls_b or cls
+    desc_fn_b = desc_fn_b or desc_fn
+    for name, t, c in (("a", a, cls), ("b", b, cls_b)):
+        if not isinstance(t, c):
+            raise TypeError(f"{entry}: operand {name} must be {c.__name__}, "
                             f"got {type(t).__name__}")
     _maybe_validate(a, b)
     device = _same_device(a, b)
@@ -191,7 +199,7 @@ def _call(entry, a, b, cls, desc_fn, result_desc, adopt_fn, num_blocks, threads_
     fn = getattr(lib, entry, None)
     if fn is None:
         raise RuntimeError(f"{entry} is not exported by {_lib.LIBRARY_PATH.name}")
-    da, db = desc_fn(a), desc_fn(b)
+    da, db = desc_fn(a), desc_fn_b(b)
     z = result_desc()
     with _device.on_device(device):
         stream = _device.current_stream(device)
@@ -300,6 +308,30 @@ def gpu_csf_add_f32(a: CSF3_gpu, b: CSF3_gpu, num_blocks: int = 256,
     """Z = a + b over CSF3 (union at every level).  compiler.cpp:135."""
     return _call("nacho_gpu_csf_add_f32", a, b, CSF3_gpu, _csf3_desc, _lib.Csf3Desc,
                  _adopt_csf3, num_blocks, threads_per_block)
+
+
+def gpu_coo_csr_add_f32(a: CSR_gpu, b: COO_gpu, num_blocks: int = 256,
+                        threads_per_block: int = 256) -> CSR_gpu:
+    """Z = a + b for a CSR a and a COO b (sorted, no duplicates), giving CSR.
+    compiler.cpp:122."""
+    return _call("nacho_gpu_coo_csr_add_f32", a, b, CSR_gpu, _csr_desc, _lib.CsrDesc,
+                 _adopt_csr, num_blocks, threads_per_block, cls_b=COO_gpu,
+                 desc_fn_b=_coo_desc)
+
+
+def gpu_inner_prod_f32(a: CSF3_gpu, b: CSF3_gpu, num_blocks: int = 256,
+                       threads_per_block: int = 256) -> Scalar_gpu:
+    """z = sum_ijk a_ijk * b_ijk over CSF3 operands (float32 products summed in float64,
+    rounded once).  compiler.cpp:141."""
+    return _call("nacho_gpu_inner_prod_f32", a, b, CSF3_gpu, _csf3_desc, _lib.ScalarDesc,
+                 _adopt_scalar, num_blocks, threads_per_block)
+
+
+def gpu_inner_prod_coo_f32(a: COO3_gpu, b: COO3_gpu, num_blocks: int = 256,
+                           threads_per_block: int = 256) -> Scalar_gpu:
+    """The same inner product over COO3 operands.  compiler.cpp:143."""
+    return _call("nacho_gpu_inner_prod_coo_f32", a, b, COO3_gpu, _coo3_desc, _lib.ScalarDesc,
+                 _adopt_scalar, num_blocks, threads_per_block)
 
 
 def gpu_spgemm_f32(a: CSR_gpu, b: CSR_gpu, num_blocks: int = 256,

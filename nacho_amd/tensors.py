@@ -13,7 +13,8 @@ those names, argument orders and field names for the GPU target:
              values, shape)
 
 plus CSR64_gpu, the same as CSR_gpu with int64 offsets, for SpGEMM results longer than 2^31
-(the reference is int32-only).  Buffers are torch tensors on a HIP device ("cuda" in torch).
+(the reference is int32-only), and Scalar_gpu(values), a full reduction's single value: no
+levels and no shape (generate_bindings.cpp:181-183).  Buffers are torch tensors on a HIP device ("cuda" in torch).
 """
 
 from __future__ import annotations
@@ -164,3 +165,26 @@ CSF3_gpu = _make(
     3,
     "CSF order-3 tensor, every level compressed (reference class CSF3_gpu).",
 )
+
+
+class Scalar_gpu(_GpuTensor):
+    """A full reduction's single value on the GPU (reference class Scalar_gpu, the format {}
+    named "Scalar", compiler.cpp:75): one `values` buffer of one element and, having no
+    dimensions left, no shape (generate_bindings.cpp:181-183)."""
+
+    _fields = (("values", _F32),)
+    _rank = 0
+    values = _field("values")
+
+    def __init__(self, values):
+        _GpuTensor.__init__(self, values, shape=torch.zeros(0, dtype=_I32))
+        if values.numel() != 1:
+            raise ValueError(f"Scalar_gpu.values holds one element, got {values.numel()}")
+
+    @property
+    def shape(self):
+        raise AttributeError("Scalar_gpu has no shape: a full reduction has no dimensions")
+
+    def item(self) -> float:
+        """The value, copied to the host (waits for the stream that produced it)."""
+        return float(self.values.item())

@@ -36,6 +36,9 @@
  *     fibre, even when a product fibre is empty.  Serial restatement of the lattice.
  *   - sssmm: masked SpGEMM (GPU-only in the reference, compiler.cpp:150-153), row by row
  *     with a dense mask marker; products in ascending j, summed in float64.
+ *   - csf3_inner / coo3_inner: the full reductions inner_prod and inner_prod_coo
+ *     (compiler.cpp:141, 143): the intersection lattice at every level, float32 products
+ *     summed in float64 (details at oracle_csf3_inner below).
  *   - spgemm: the reference has no CPU SpGEMM (compiler.cpp:145-148 is GPU-only).  This is
  *     the ESC semantics of its GPU path (stitch_and_generate_gpu.cpp:14-138, 257-366) run
  *     row-parallel on the CPU: per row, expand a_ij * b_jk, sort by k, and sum runs.
@@ -1595,5 +1598,184 @@ int oracle_csr_add3_mt(int rows, const int32_t *pa, const int32_t *ca, const flo
     *o_crd = J.crd;
     *o_val = J.val;
     *o_nnz = (int)tot[0];
+    return ORC_OK;
+}
+
+/* ---------------------------------------------------------------------------------- */
+/* inner products (inner_prod, inner_prod_coo)                                           */
+/*
+ * z = sum over the coordinates both operands hold of a * b (compiler.cpp:141, 143): the
+ * intersection lattice at every level (for i in A_i ∩ B_i, for j in A_ij ∩ B_ij, for k in
+ * A_ijk ∩ B_ijk), each product one float32 multiply (compute.cpp:476-491 evaluates a * b
+ * in value_t).  The reference accumulates float32 partial sums per thread and adds them
+ * with atomics (compute.cpp:498-520, runtime/nacho_kernel_utils.h:40-58), an order that
+ * depends on its partitioning; here the products are summed in float64 (the product path's
+ * arithmetic) over a range of the top level per thread, ranges in ascending order, and the
+ * thread totals added in thread order.  The float64 total is returned; callers round it.
+ */
+
+/* Sum of a[k] * b[k] over the k both sorted fibres hold. */
+static double k_intersect(const int32_t *ak, const float *av, int a0, int a1,
+                          const int32_t *bk, const float *bv, int b0, int b1) {
+    double s = 0.0;
+    while (a0 < a1 && b0 < b1) {
+        if (ak[a0] < bk[b0]) {
+            ++a0;
+        } else if (bk[b0] < ak[a0]) {
+            ++b0;
+        } else {
+            s += (double)(av[a0] * bv[b0]);
+            ++a0;
+            ++b0;
+        }
+    }
+    return s;
+}
+
+/* First index x in [lo, hi) with key[x] >= q (hi when none). */
+static int lower_bound_i32(const int32_t *key, int lo, int hi, int32_t q) {
+    while (lo < hi) {
+        const int mid = lo + (hi - lo) / 2;
+        if (key[mid] < q) {
+            lo = mid + 1;
+        } else {
+            hi = mid;
+        }
+    }
+    return lo;
+}
+
+typedef struct {
+    const int32_t *a_ci, *a_pj, *a_cj, *a_pk, *a_ck;
+    const float *a_v;
+    int a_ni;
+    const int32_t *b_ci, *b_pj, *b_cj, *b_pk, *b_ck;
+    const float *b_v;
+    int b_ni;
+    int nt;
+    double *part;
+} csf_inner_job;
+
+/* Thread t: A's i entries [t*a_ni/nt, (t+1)*a_ni/nt) against the B i entries of equal or
+ * larger coordinate, walked as the three-level intersection. */
+static void csf_inner_task(int t, void *arg) {
+    csf_inner_job *J = (csf_inner_job *)arg;
+    int ia = (int)((long)J->a_ni * t / J->nt), ia_end = (int)((long)J->a_ni * (t + 1) / J->nt);
+    double s = 0.0;
+    int ib = ia < ia_end ? lower_bound_i32(J->b_ci, 0, J->b_ni, J->a_ci[ia]) : J->b_ni;
+    while (ia < ia_end && ib < J->b_ni) {
+        if (J->a_ci[ia] < J->b_ci[ib]) {
+            ++ia;
+            continue;
+        }
+        if (J->b_ci[ib] < J->a_ci[ia]) {
+            ++ib;
+            continue;
+        }
+        int ja = J->a_pj[ia], jae = J->a_pj[ia + 1], jb = J->b_pj[ib], jbe = J->b_pj[ib + 1];
+        while (ja < jae && jb < jbe) {
+            if (J->a_cj[ja] < J->b_cj[jb]) {
+                ++ja;
+            } else if (J->b_cj[jb] < J->a_cj[ja]) {
+                ++jb;
+            } else {
+                s += k_intersect(J->a_ck, J->a_v, J->a_pk[ja], J->a_pk[ja + 1], J->b_ck,
+                                 J->b_v, J->b_pk[jb], J->b_pk[jb + 1]);
+                ++ja;
+                ++jb;
+            }
+        }
+        ++ia;
+        ++ib;
+    }
+    J->part[t] = s;
+}
+
+/* Inner product of two CSF3 tensors (arrays as oracle_csf3_union takes them), on nthreads
+ * threads (<= 0: one per online CPU). */
+int oracle_csf3_inner(const int32_t *a_ci, int a_ni, const int32_t *a_pj, const int32_t *a_cj,
+                      const int32_t *a_pk, const int32_t *a_ck, const float *a_v,
+                      const int32_t *b_ci, int b_ni, const int32_t *b_pj, const int32_t *b_cj,
+                      const int32_t *b_pk, const int32_t *b_ck, const float *b_v, int nthreads,
+                      double *out) {
+    const int nt = nthreads > 0 ? nthreads : oracle_default_threads();
+    double *part = (double *)calloc((size_t)nt, sizeof(double));
+    if (!part) return ORC_ENOMEM;
+    csf_inner_job J = {a_ci, a_pj, a_cj, a_pk, a_ck, a_v, a_ni,
+                       b_ci, b_pj, b_cj, b_pk, b_ck, b_v, b_ni, nt, part};
+    parallel_for(nt, csf_inner_task, &J);
+    double s = 0.0;
+    for (int t = 0; t < nt; ++t) s += part[t];
+    free(part);
+    *out = s;
+    return ORC_OK;
+}
+
+typedef struct {
+    const int32_t *ai, *aj, *ak;
+    const float *av;
+    int na;
+    const int32_t *bi, *bj, *bk;
+    const float *bv;
+    int nb;
+    int nt;
+    double *part;
+} coo3_inner_job;
+
+static int tuple_cmp(const int32_t *xi, const int32_t *xj, const int32_t *xk, int x,
+                     const int32_t *yi, const int32_t *yj, const int32_t *yk, int y) {
+    if (xi[x] != yi[y]) return xi[x] < yi[y] ? -1 : 1;
+    if (xj[x] != yj[y]) return xj[x] < yj[y] ? -1 : 1;
+    if (xk[x] != yk[y]) return xk[x] < yk[y] ? -1 : 1;
+    return 0;
+}
+
+/* Thread t: A's entries [t*na/nt, (t+1)*na/nt) merged against B from the first B tuple not
+ * below the range's first A tuple. */
+static void coo3_inner_task(int t, void *arg) {
+    coo3_inner_job *J = (coo3_inner_job *)arg;
+    int a = (int)((long)J->na * t / J->nt), a_end = (int)((long)J->na * (t + 1) / J->nt);
+    double s = 0.0;
+    int b = J->nb;
+    if (a < a_end) {
+        int lo = 0, hi = J->nb;
+        while (lo < hi) {
+            const int mid = lo + (hi - lo) / 2;
+            if (tuple_cmp(J->bi, J->bj, J->bk, mid, J->ai, J->aj, J->ak, a) < 0) {
+                lo = mid + 1;
+            } else {
+                hi = mid;
+            }
+        }
+        b = lo;
+    }
+    while (a < a_end && b < J->nb) {
+        const int c = tuple_cmp(J->ai, J->aj, J->ak, a, J->bi, J->bj, J->bk, b);
+        if (c < 0) {
+            ++a;
+        } else if (c > 0) {
+            ++b;
+        } else {
+            s += (double)(J->av[a] * J->bv[b]);
+            ++a;
+            ++b;
+        }
+    }
+    J->part[t] = s;
+}
+
+/* Inner product of two COO3 tensors sorted by (i, j, k) without duplicates. */
+int oracle_coo3_inner(const int32_t *ai, const int32_t *aj, const int32_t *ak, const float *av,
+                      int na, const int32_t *bi, const int32_t *bj, const int32_t *bk,
+                      const float *bv, int nb, int nthreads, double *out) {
+    const int nt = nthreads > 0 ? nthreads : oracle_default_threads();
+    double *part = (double *)calloc((size_t)nt, sizeof(double));
+    if (!part) return ORC_ENOMEM;
+    coo3_inner_job J = {ai, aj, ak, av, na, bi, bj, bk, bv, nb, nt, part};
+    parallel_for(nt, coo3_inner_task, &J);
+    double s = 0.0;
+    for (int t = 0; t < nt; ++t) s += part[t];
+    free(part);
+    *out = s;
     return ORC_OK;
 }

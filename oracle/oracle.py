@@ -15,7 +15,8 @@ the repository's design notes: csr/coo/coo3/csf union and intersection are pinne
 closed forms, by scipy, by brute force on tiny inputs and by the reference's own smoke
 cases (tests/smoke.py semantics); dcsr union / intersection by the DCSR closed form over the
 expanded CSR matrices; csr_add3 by the three-way closed form; spgemm and sssmm are
-pinned by float64 scipy products.
+pinned by float64 scipy products; the csf3 / coo3 inner products by the key-intersection
+closed form and by brute force over coordinate dictionaries.
 """
 
 from __future__ import annotations
@@ -96,6 +97,14 @@ def load() -> ctypes.CDLL:
             [ctypes.c_int] + [_i32p, ctypes.c_int, _i32p, _i32p, _f32p] * 2 + [ctypes.c_int]
             + [ctypes.POINTER(_i32p)] * 3 + [ctypes.POINTER(_f32p)]
             + [ctypes.POINTER(ctypes.c_int)] * 2)
+        lib.oracle_csf3_inner.restype = ctypes.c_int
+        lib.oracle_csf3_inner.argtypes = (
+            [_i32p, ctypes.c_int, _i32p, _i32p, _i32p, _i32p, _f32p] * 2
+            + [ctypes.c_int, ctypes.POINTER(ctypes.c_double)])
+        lib.oracle_coo3_inner.restype = ctypes.c_int
+        lib.oracle_coo3_inner.argtypes = (
+            [_i32p, _i32p, _i32p, _f32p, ctypes.c_int] * 2
+            + [ctypes.c_int, ctypes.POINTER(ctypes.c_double)])
         lib.oracle_spgemm.restype = ctypes.c_int
         lib.oracle_spgemm.argtypes = [
             ctypes.c_int, ctypes.c_int, ctypes.c_int, _i32p, _i32p, _f32p, _i32p, _i32p, _f32p,
@@ -390,6 +399,66 @@ def closed_csr_binary(op, rows, cols, pa, ca, va, pb, cb, vb):
     pos = np.zeros(int(rows) + 1, np.int64)
     np.add.at(pos, r + 1, 1)
     return np.cumsum(pos).astype(np.int32), crd, val
+
+
+def port_csf3_inner(a_levels, a_val, b_levels, b_val, nthreads=0, timing=None) -> float:
+    """Inner product of two CSF3 tensors (levels = (crd_i, pos_j, crd_j, pos_k, crd_k)) as
+    the float64 sum of the float32 products (oracle_csf3_inner); nthreads 0 = all cores."""
+    import time
+
+    lib = load()
+
+    def prep(levels, val):
+        ci, pj, cj, pk, ck = (_as(x, np.int32) for x in levels)
+        return ci, len(levels[0]), pj, cj, pk, ck, _as(val, np.float32)
+
+    def args(p):
+        ci, ni, pj, cj, pk, ck, v = p
+        return [_ptr(ci, ctypes.c_int32), ni, _ptr(pj, ctypes.c_int32),
+                _ptr(cj, ctypes.c_int32), _ptr(pk, ctypes.c_int32), _ptr(ck, ctypes.c_int32),
+                _ptr(v, ctypes.c_float)]
+
+    pa, pb = prep(a_levels, a_val), prep(b_levels, b_val)
+    out = ctypes.c_double()
+    t0 = time.perf_counter()
+    rc = lib.oracle_csf3_inner(*args(pa), *args(pb), int(nthreads), ctypes.byref(out))
+    if timing is not None:
+        timing["seconds"] = time.perf_counter() - t0
+    if rc != 0:
+        raise RuntimeError(f"oracle_csf3_inner failed ({rc})")
+    return out.value
+
+
+def port_coo3_inner(a_crd, va, b_crd, vb, nthreads=0, timing=None) -> float:
+    """Inner product of two COO3 tensors (crd = (i, j, k) arrays sorted lexicographically,
+    no duplicates) as the float64 sum of the float32 products (oracle_coo3_inner)."""
+    import time
+
+    lib = load()
+    a = [_as(x, np.int32) for x in a_crd] + [_as(va, np.float32), len(va)]
+    b = [_as(x, np.int32) for x in b_crd] + [_as(vb, np.float32), len(vb)]
+
+    def args(p):
+        return [_ptr(p[0], ctypes.c_int32), _ptr(p[1], ctypes.c_int32),
+                _ptr(p[2], ctypes.c_int32), _ptr(p[3], ctypes.c_float), p[4]]
+
+    out = ctypes.c_double()
+    t0 = time.perf_counter()
+    rc = lib.oracle_coo3_inner(*args(a), *args(b), int(nthreads), ctypes.byref(out))
+    if timing is not None:
+        timing["seconds"] = time.perf_counter() - t0
+    if rc != 0:
+        raise RuntimeError(f"oracle_coo3_inner failed ({rc})")
+    return out.value
+
+
+def closed_inner(shape, a_crd, va, b_crd, vb) -> float:
+    """Inner product from the mathematics: the coordinate tuples both hold (packed keys,
+    np.intersect1d), their float32 products summed in float64."""
+    ka, kb = _tuple_keys(a_crd, shape), _tuple_keys(b_crd, shape)
+    _, ia, ib = np.intersect1d(ka, kb, assume_unique=True, return_indices=True)
+    prod = np.asarray(va, np.float32)[ia] * np.asarray(vb, np.float32)[ib]
+    return float(np.sum(prod.astype(np.float64)))
 
 
 def _tuple_keys(crd, shape):

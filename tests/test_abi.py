@@ -50,7 +50,8 @@ def test_python_bindings_cover_every_gpu_entry_point():
     from nacho_amd import _lib
 
     gpu = [n for n in declared_functions() if n.startswith("nacho_gpu_")]
-    bound = set(_lib.ENTRY_POINTS) | set(_lib.ENTRY_POINTS_3) | set(_lib.ENTRY_POINTS_NOALLOC)
+    bound = (set(_lib.ENTRY_POINTS) | set(_lib.ENTRY_POINTS_3) | set(_lib.ENTRY_POINTS_NOALLOC)
+             | set(_lib.ENTRY_POINTS_MIXED))
     assert set(gpu) <= bound, set(gpu) - bound
 
 
@@ -137,6 +138,7 @@ def test_every_descriptor_layout_matches_the_c_compiler(tmp_path):
     pairs = {"nacho_csr": _lib.CsrDesc, "nacho_csr64": _lib.Csr64Desc,
              "nacho_coo": _lib.CooDesc, "nacho_coo3": _lib.Coo3Desc,
              "nacho_dcsr": _lib.DcsrDesc, "nacho_csf3": _lib.Csf3Desc,
+             "nacho_scalar": _lib.ScalarDesc,
              "nacho_coo2d_host": _lib.Coo2dHost, "nacho_coo3d_host": _lib.Coo3dHost}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "nacho_hip.h"',
              "int main(void) {"]
@@ -182,9 +184,11 @@ def test_cpp_shim_matches_the_generated_signatures(tmp_path):
         "nacho_hip::csf3_ijk<int32_t, float>": ("nacho_csf3", {}),
         "nacho_hip::coo_ij<int32_t, float>": ("nacho_coo", {}),
         "nacho_hip::coo3_ijk<int32_t, float>": ("nacho_coo3", {}),
+        "nacho_hip::scalar<int32_t, float>": ("nacho_scalar", {}),
     }
     descs = {"nacho_csr": _lib.CsrDesc, "nacho_dcsr": _lib.DcsrDesc,
-             "nacho_csf3": _lib.Csf3Desc, "nacho_coo": _lib.CooDesc, "nacho_coo3": _lib.Coo3Desc}
+             "nacho_csf3": _lib.Csf3Desc, "nacho_coo": _lib.CooDesc, "nacho_coo3": _lib.Coo3Desc,
+             "nacho_scalar": _lib.ScalarDesc}
     lines = ["#include <cstddef>", "#include <cstdio>", '#include "nacho_hip.hpp"',
              "int main() {", "int bad = 0;"]
     for shim, (cname, rename) in pairs.items():
@@ -204,7 +208,9 @@ def test_cpp_shim_matches_the_generated_signatures(tmp_path):
         "  (void *)&dcsr_mul_without_recursive_partitioning::"
         "dcsr_mul_without_recursive_partitioning_gpu_i32_f32,",
         "  (void *)&csf_add::csf_add_gpu_i32_f32, (void *)&spgemm::spgemm_gpu_i32_f32,",
-        "  (void *)&sssmm::sssmm_gpu_i32_f32};",
+        "  (void *)&sssmm::sssmm_gpu_i32_f32, (void *)&coo_csr_add::coo_csr_add_gpu_i32_f32,",
+        "  (void *)&inner_prod::inner_prod_gpu_i32_f32,",
+        "  (void *)&inner_prod_coo::inner_prod_coo_gpu_i32_f32};",
         "for (void *f : fns) bad += f == nullptr;",
         "csr_add::a_tensor_format<int32_t, float> a{4, 4, nullptr, 0, nullptr, nullptr, 0};",
         "csr_add::b_tensor_format<int32_t, float> b{5, 4, nullptr, 0, nullptr, nullptr, 0};",

@@ -1,0 +1,145 @@
+"""GPU parity of inner_prod (CSF3) and inner_prod_coo (COO3) against the oracle.
+
+The GPU sums the float32 products in float64 in a fixed order and rounds once; the oracle
+(oracle_csf3_inner / oracle_coo3_inner, pinned in test_oracle_inner.py) sums the same
+products in float64 in another order.  Tolerance: the float32 rounding of the result
+(1.2e-7 relative) plus 1e-12 of the sum of |a * b| for the two float64 orders.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from nacho_amd.convert import csf3_levels
+from oracle import oracle
+from tests.test_oracle_inner import random_coords
+
+pytestmark = pytest.mark.gpu
+
+
+def gpu_inner(kind, shape, ac, av, bc, bv, device):
+    import nacho_amd
+
+    print(f"[gpu] inner_prod {kind} shape={shape} nnz=({len(av)},{len(bv)})", flush=True)
+    if kind == "csf":
+        z = nacho_amd.gpu_inner_prod_f32(nacho_amd.to_csf3(ac, av, shape, device),
+                                         nacho_amd.to_csf3(bc, bv, shape, device))
+    else:
+        z = nacho_amd.gpu_inner_prod_coo_f32(nacho_amd.to_coo3(ac, av, shape, device),
+                                             nacho_amd.to_coo3(bc, bv, shape, device))
+    assert isinstance(z, nacho_amd.Scalar_gpu)
+    torch.cuda.synchronize()
+    vals = z.values.cpu().numpy()
+    assert vals.dtype == np.float32 and vals.shape == (1,)
+    return float(vals[0])
+
+
+def want_inner(kind, ac, av, bc, bv):
+    if kind == "csf":
+        return oracle.port_csf3_inner(csf3_levels(ac), av, csf3_levels(bc), bv, nthreads=16)
+    return oracle.port_coo3_inner(tuple(ac[:, d] for d in range(3)), av,
+                                  tuple(bc[:, d] for d in range(3)), bv, nthreads=16)
+
+
+def assert_close(got, want, ac, av, bc, bv, what):
+    scale = float(np.abs(av.astype(np.float64)).max(initial=0.0)
+                  * np.abs(bv.astype(np.float64)).max(initial=0.0)) * min(len(av), len(bv))
+    tol = 1.2e-7 * abs(want) + 1e-12 * scale
+    assert abs(got - want) <= tol, f"{what}: got {got!r}, want {want!r} (tol {tol:.3g})"
+    assert np.float32(got) == got
+
+
+KINDS = ["csf", "coo"]
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("seed", range(4))
+def test_random(gpu, kind, seed):
+    rng = np.random.default_rng(900 + seed)
+    shape = tuple(int(rng.choice([1, 7, 300, 20000])) for _ in range(3))
+    n = int(rng.choice([1, 50, 5000, 400000]))
+    ac, av = random_coords(rng, shape, n)
+    bc, bv = random_coords(rng, shape, n)
+    got = gpu_inner(kind, shape, ac, av, bc, bv, gpu)
+    assert_close(got, want_inner(kind, ac, av, bc, bv), ac, av, bc, bv, f"{kind} seed={seed}")
+
+
+@pytest.mark.parametrize("kind", KINDS)
+def test_reference_smoke_case(gpu, kind):
+    rng = np.random.default_rng(0)
+    shape = (40, 30, 25)
+
+    def random_coo_3d():
+        coords = np.unique(np.stack([rng.integers(0, e, 900) for e in shape], axis=1), axis=0)
+        return coords.astype(np.int32), rng.random(coords.shape[0]).astype(np.float32)
+
+    (ac, av), (bc, bv) = random_coo_3d(), random_coo_3d()
+    got = gpu_inner(kind, shape, ac, av, bc, bv, gpu)
+    a_entries = {tuple(int(x) for x in c): float(v) for c, v in zip(ac, av)}
+    expected = sum(a_entries[k] * float(v) for c, v in zip(bc, bv)
+                   if (k := tuple(int(x) for x in c)) in a_entries)
+    assert abs(got - expected) <= 1e-4 * max(1.0, abs(expected))  # the reference's TOLERANCE
+    assert_close(got, want_inner(kind, ac, av, bc, bv), ac, av, bc, bv, "smoke")
+
+
+@pytest.mark.parametrize("kind", KINDS)
+def test_empty_and_disjoint(gpu, kind):
+    rng = np.random.default_rng(12)
+    shape = (30, 30, 64)
+    ac, av = random_coords(rng, (30, 30, 30), 2000)
+    e, ev = np.zeros((0, 3), np.int32), np.zeros(0, np.float32)
+    assert gpu_inner(kind, shape, e, ev, ac, av, gpu) == 0.0
+    assert gpu_inner(kind, shape, ac, av, e, ev, gpu) == 0.0
+    assert gpu_inner(kind, shape, e, ev, e, ev, gpu) == 0.0
+    bc = ac.copy()
+    bc[:, 2] += 31  # same (i, j) fibres, every k beyond A's
+    assert gpu_inner(kind, shape, ac, av, bc, av, gpu) == 0.0
+
+
+@pytest.mark.parametrize("kind", KINDS)
+def test_self_product(gpu, kind):
+    """a . a = the sum of squares (every coordinate pairs with itself)."""
+    rng = np.random.default_rng(13)
+    shape = (200, 300, 100)
+    ac, av = random_coords(rng, shape, 300000)
+    got = gpu_inner(kind, shape, ac, av, ac, av, gpu)
+    want = float(np.sum((av * av).astype(np.float64)))
+    assert_close(got, want, ac, av, ac, av, "self")
+
+
+def test_coo_wide_keys(gpu):
+    """COO3 whose (j, k) keys do not fit 31 bits: the packed-tuple intersection path, then
+    the sum of its products."""
+    rng = np.random.default_rng(14)
+    shape = (50, 1 << 20, 1 << 20)
+    ac, av = random_coords(rng, shape, 100000)
+    keep = rng.random(len(ac)) < 0.5
+    bc = ac[keep]
+    bv = rng.uniform(-1, 1, len(bc)).astype(np.float32)
+    got = gpu_inner("coo", shape, ac, av, bc, bv, gpu)
+    assert_close(got, want_inner("coo", ac, av, bc, bv), ac, av, bc, bv, "wide keys")
+
+
+def test_c5_reduced(gpu):
+    """Both layouts on the C5 generator (Zipf(1.3) mode 0) at 2M draws per operand."""
+    from nacho_amd import synth
+
+    (ac, av), (bc, bv) = (synth.zipf3_coords(2_000_000, synth.C5_SHAPE, s) for s in (1, 2))
+    csf = gpu_inner("csf", synth.C5_SHAPE, ac, av, bc, bv, gpu)
+    coo = gpu_inner("coo", synth.C5_SHAPE, ac, av, bc, bv, gpu)
+    want = want_inner("csf", ac, av, bc, bv)
+    assert_close(csf, want, ac, av, bc, bv, "csf C5 2M")
+    assert_close(coo, want, ac, av, bc, bv, "coo C5 2M")
+
+
+@pytest.mark.parametrize("kind", KINDS)
+def test_c5_full_size(gpu, kind):
+    """The C5 operand pair at full size (20M draws each), and each operand with itself."""
+    from nacho_amd import synth
+
+    (ac, av), (bc, bv) = synth.c5_operands()
+    got = gpu_inner(kind, synth.C5_SHAPE, ac, av, bc, bv, gpu)
+    assert_close(got, want_inner(kind, ac, av, bc, bv), ac, av, bc, bv, f"{kind} C5")
+    got = gpu_inner(kind, synth.C5_SHAPE, ac, av, ac, av, gpu)
+    want = float(np.sum((av * av).astype(np.float64)))
+    assert_close(got, want, ac, av, ac, av, f"{kind} C5 self")
