@@ -161,13 +161,16 @@ Declaration analyse(const std::string &kernel, const Expr &expression) {
             flatten(root, ExprNode::Kind::Mul, kernel, leaves);
             break;
         case ExprNode::Kind::Sum: {
-            d.form = Form::SumOfProducts;
-            d.reduced_index = root->name;
-            const ExprNode *body = root->lhs.get();
-            if (body->kind == ExprNode::Kind::Sum) {
-                throw UnsupportedForm(kernel + ": a reduction over more than one index (" +
-                                      root->name + ", " + body->name +
-                                      ", ...) has no HIP kernel");
+            const ExprNode *body = root;
+            while (body->kind == ExprNode::Kind::Sum) {
+                d.reduced_indices.push_back(body->name);
+                body = body->lhs.get();
+            }
+            if (d.reduced_indices.size() == 1) {
+                d.form = Form::SumOfProducts;
+                d.reduced_index = root->name;
+            } else {
+                d.form = Form::FullReduction;  // plan() checks that nothing is left
             }
             if (body->kind != ExprNode::Kind::Mul) {
                 throw UnsupportedForm(kernel + ": only a reduction of a product has a HIP "
@@ -212,7 +215,63 @@ Plan plan(const Declaration &d) {
     }
     Plan p;
     const Storage s0 = storage_of(d.operands.at(0).type.format);
-    if (d.form == Form::Add || d.form == Form::Mul) {
+    if (d.form == Form::Add && d.operands.size() == 2 &&
+        storage_of(d.operands[1].type.format) != s0) {
+        // a CSR operand plus a COO operand (compiler.cpp:122): CSR result
+        const Operand *csr = nullptr, *coo = nullptr;
+        for (const Operand &o : d.operands) {
+            const Storage s = storage_of(o.type.format);
+            if (s == Storage::CSR) csr = &o;
+            if (s == Storage::COO) coo = &o;
+        }
+        if (!csr || !coo) {
+            throw UnsupportedForm(
+                k + ": operands of different formats (" + storage_word(s0) + " and " +
+                storage_word(storage_of(d.operands[1].type.format)) +
+                ") have a HIP kernel only as a CSR plus a COO");
+        }
+        if (index_list(csr->type.format) != index_list(coo->type.format)) {
+            throw UnsupportedForm(k + ": elementwise operands must share their index order");
+        }
+        if (index_list(csr->type.format)[0] == index_list(csr->type.format)[1]) {
+            throw UnsupportedForm(k + ": an index repeated within one operand (a diagonal) "
+                                      "has no HIP kernel");
+        }
+        p.entry_point = "nacho_gpu_coo_csr_add_f32";
+        p.descriptor = p.result_descriptor = "nacho_csr";
+        p.operand_descriptor[csr->name] = "nacho_csr";
+        p.operand_descriptor[coo->name] = "nacho_coo";
+        p.roles = {csr->name, coo->name};
+        p.result_format = csr->type.format;
+    } else if (d.form == Form::FullReduction) {
+        // Sum over every index of a * b, both CSF3 or both COO3 (compiler.cpp:141, 143)
+        if (d.operands.size() != 2) {
+            throw UnsupportedForm(k + ": a reduction over several indices has a HIP kernel "
+                                      "only for the product of two operands");
+        }
+        const auto idx = index_list(d.operands[0].type.format);
+        if (index_list(d.operands[1].type.format) != idx) {
+            throw UnsupportedForm(k + ": a reduction over several indices needs both "
+                                      "operands in one index order");
+        }
+        const std::set<std::string> summed(d.reduced_indices.begin(), d.reduced_indices.end());
+        if (summed != std::set<std::string>(idx.begin(), idx.end()) ||
+            summed.size() != d.reduced_indices.size()) {
+            throw UnsupportedForm(k + ": a reduction over more than one index that does not "
+                                      "sum every index of its operands once has no HIP kernel");
+        }
+        const Storage s1 = storage_of(d.operands[1].type.format);
+        if (s0 != s1 || (s0 != Storage::CSF3 && s0 != Storage::COO3)) {
+            throw UnsupportedForm(k + ": a full reduction has a HIP kernel only over two CSF3 "
+                                      "or two COO3 operands");
+        }
+        p.entry_point = s0 == Storage::CSF3 ? "nacho_gpu_inner_prod_f32"
+                                            : "nacho_gpu_inner_prod_coo_f32";
+        p.descriptor = descriptor_of(s0);
+        p.result_descriptor = "nacho_scalar";
+        for (const Operand &o : d.operands) p.roles.push_back(o.name);
+        p.result_format = Format::ordered({}).named("Scalar");
+    } else if (d.form == Form::Add || d.form == Form::Mul) {
         const auto idx0 = index_list(d.operands[0].type.format);
         for (const Operand &o : d.operands) {
             const Storage s = storage_of(o.type.format);
@@ -440,6 +499,10 @@ std::string text_of(const Declaration &d) {
         body += ")";
     }
     if (d.form == Form::SumOfProducts) return "Sum(" + d.reduced_index + ", " + body + ")";
+    if (d.form == Form::FullReduction) {
+        for (auto it = d.reduced_indices.rbegin(); it != d.reduced_indices.rend(); ++it)
+            body = "Sum(" + *it + ", " + body + ")";
+    }
     return body;
 }
 
@@ -464,6 +527,12 @@ const Operand &operand_named(const Declaration &d, const std::string &name) {
     for (const Operand &o : d.operands)
         if (o.name == name) return o;
     throw std::logic_error("no operand " + name);
+}
+
+// C descriptor of operand `name`.
+const std::string &descriptor_for(const Plan &p, const std::string &name) {
+    auto it = p.operand_descriptor.find(name);
+    return it == p.operand_descriptor.end() ? p.descriptor : it->second;
 }
 
 void write_header(const Declaration &d, const Plan &p, const std::string &path) {
@@ -498,7 +567,7 @@ void write_header(const Declaration &d, const Plan &p, const std::string &path) 
         out << "}  // namespace layout\n\n";
     };
     for (const std::string &name : d.ordering)
-        write_struct(name, operand_named(d, name).type.format, p.descriptor);
+        write_struct(name, operand_named(d, name).type.format, descriptor_for(p, name));
     write_struct(d.result_name, p.result_format, p.result_descriptor);
 
     const std::string zt = d.result_name + "_tensor_format<index_t, value_t>";
@@ -507,8 +576,9 @@ void write_header(const Declaration &d, const Plan &p, const std::string &path) 
         out << "const " << name << "_tensor_format<index_t, value_t> " << name << ", ";
     out << "const int32_t num_blocks, const int32_t threads_per_block) {\n";
     for (const std::string &name : d.ordering) {
-        out << "    const " << p.descriptor << " desc_" << name << " = nacho_hip::detail::to_c<"
-            << p.descriptor << ">(" << name << ");\n";
+        out << "    const " << descriptor_for(p, name) << " desc_" << name
+            << " = nacho_hip::detail::to_c<" << descriptor_for(p, name) << ">(" << name
+            << ");\n";
     }
     out << "    " << p.result_descriptor << " desc_result{};\n";
     out << "    nacho_hip::detail::check(" << p.entry_point << "(";
@@ -545,8 +615,8 @@ void write_wrapper(const Declaration &d, const Plan &p, const std::string &path)
         const PyClass &pc = record_class(cls, f);
         const Format canon = canonical(f);
         const auto bufs = class_buffers(canon);
-        out << p.descriptor << " unwrap_" << name << "(const " << cls << " &v) {\n"
-            << "    " << p.descriptor << " t = {};\n";
+        out << descriptor_for(p, name) << " unwrap_" << name << "(const " << cls << " &v) {\n"
+            << "    " << descriptor_for(p, name) << " t = {};\n";
         for (size_t x = 0; x < canon.levels().size(); ++x) {
             out << "    t.dim_" << kCanonical[x] << "_size = v.shape.data()[" << x << "];\n";
         }
@@ -572,10 +642,15 @@ void write_wrapper(const Declaration &d, const Plan &p, const std::string &path)
             out << "        nacho::adopt_gpu<" << (b.is_value ? "float" : "int32_t") << ">(t."
                 << b.c_field << ", (size_t)(" << b.extent << ")),\n";
         }
-        out << "        nacho::make_shape<" << canon.levels().size() << ">({";
-        for (size_t x = 0; x < canon.levels().size(); ++x)
-            out << (x ? ", " : "") << "t.dim_" << kCanonical[x] << "_size";
-        out << "}),\n    };\n}\n\n";
+        // a full reduction has no dimensions left and carries no shape
+        // (generate_bindings.cpp:181-183)
+        if (!canon.levels().empty()) {
+            out << "        nacho::make_shape<" << canon.levels().size() << ">({";
+            for (size_t x = 0; x < canon.levels().size(); ++x)
+                out << (x ? ", " : "") << "t.dim_" << kCanonical[x] << "_size";
+            out << "}),\n";
+        }
+        out << "    };\n}\n\n";
         (void)pc;
     }
 
@@ -586,8 +661,8 @@ void write_wrapper(const Declaration &d, const Plan &p, const std::string &path)
     }
     out << "int32_t num_blocks, int32_t threads_per_block) {\n";
     for (const std::string &name : d.ordering)
-        out << "    const " << p.descriptor << " desc_" << name << " = unwrap_" << name << "("
-            << name << ");\n";
+        out << "    const " << descriptor_for(p, name) << " desc_" << name << " = unwrap_"
+            << name << "(" << name << ");\n";
     out << "    " << p.result_descriptor << " desc_result = {};\n"
         << "    nacho_hip::detail::check(" << p.entry_point << "(";
     for (const std::string &role : p.roles) out << "&desc_" << role << ", ";

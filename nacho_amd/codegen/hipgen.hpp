@@ -115,6 +115,7 @@ enum class Form {
     Add,            // elementwise sum of the operands
     Mul,            // elementwise product of the operands
     SumOfProducts,  // Sum over one index of a product of the operands
+    FullReduction,  // nested Sums over several indices of a product of the operands
 };
 
 struct Declaration {
@@ -123,6 +124,7 @@ struct Declaration {
     std::vector<Operand> operands;       // in the expression's order
     std::vector<std::string> ordering;   // parameter order of the entry point
     std::string reduced_index;           // SumOfProducts only
+    std::vector<std::string> reduced_indices;  // FullReduction: the summed indices, outer first
     std::string result_name = "Z";
     std::string python_name;             // default gpu_<kernel>_f32
     bool recursive_partitioning = true;
@@ -141,7 +143,8 @@ Declaration analyse(const std::string &kernel, const Expr &expression);
 // The library entry point a declaration maps to and the formats it fixes.
 struct Plan {
     std::string entry_point;        // e.g. nacho_gpu_csr_add_f32
-    std::string descriptor;         // C descriptor type of every operand, e.g. nacho_csr
+    std::string descriptor;         // C descriptor type of the operands, e.g. nacho_csr
+    std::map<std::string, std::string> operand_descriptor;  // per operand, when they differ
     std::string result_descriptor;  // C descriptor type of the result
     std::vector<std::string> roles; // operand names in the entry point's argument order
     Format result_format;           // the result's levels (index names from the operands)

@@ -105,3 +105,8 @@ struct COO3_gpu {
     nacho::ArrayGPU<float> values;
     nacho::ShapeTuple<3> shape;
 };
+
+// A full reduction's result: values only, no shape (generate_bindings.cpp:181-183).
+struct Scalar_gpu {
+    nacho::ArrayGPU<float> values;
+};

@@ -35,12 +35,11 @@ EXPECTED = {  # kernel of compiler.cpp -> entry point
     "coo3d_add": "nacho_gpu_coo3d_add_f32",
     "spgemm": "nacho_gpu_spgemm_f32",
     "sssmm": "nacho_gpu_sssmm_f32",
+    "coo_csr_add": "nacho_gpu_coo_csr_add_f32",
+    "inner_prod": "nacho_gpu_inner_prod_f32",
+    "inner_prod_coo": "nacho_gpu_inner_prod_coo_f32",
 }
-REFUSED = {  # kernel -> part of the reason
-    "coo_csr_add": "operands of different formats",
-    "inner_prod": "more than one index",
-    "inner_prod_coo": "more than one index",
-}
+REFUSED = {}  # kernel of compiler.cpp -> part of the reason (every declaration has a kernel)
 # Python-facing signature of each generated wrapper, in the test double's classes
 SIGNATURES = {
     "csr_add": ("CSR_gpu", ["CSR_gpu"] * 2), "csr_add_3": ("CSR_gpu", ["CSR_gpu"] * 3),
@@ -50,6 +49,9 @@ SIGNATURES = {
     "dcsr_mul_without_recursive_partitioning": ("DCSR_gpu", ["DCSR_gpu"] * 2),
     "csf_add": ("CSF3_gpu", ["CSF3_gpu"] * 2), "coo3d_add": ("COO3_gpu", ["COO3_gpu"] * 2),
     "spgemm": ("CSR_gpu", ["CSR_gpu"] * 2), "sssmm": ("CSR_gpu", ["CSR_gpu"] * 3),
+    "coo_csr_add": ("CSR_gpu", ["CSR_gpu", "COO_gpu"]),
+    "inner_prod": ("Scalar_gpu", ["CSF3_gpu"] * 2),
+    "inner_prod_coo": ("Scalar_gpu", ["COO3_gpu"] * 2),
 }
 
 
@@ -137,12 +139,49 @@ def test_generated_namespace_matches_the_reference_signature(generated):
     assert "nacho_gpu_sssmm_f32(&desc_a, &desc_b, &desc_c, &desc_result" in s
 
 
-def test_naming_an_unsupported_kernel_fails(hipgen, tmp_path):
-    run = subprocess.run([str(hipgen), "--kernels", "inner_prod", "--output-dir",
+NAMED_UNSUPPORTED = r"""
+#include <iostream>
+#include "hipgen.hpp"
+using namespace nacho_hipgen;
+
+int main(int argc, char **argv) {
+    if (!parse_command_line(argc, argv)) return 1;
+    Format csf = Format::ordered({{"i", LevelFormat::Compressed_unique},
+                                  {"j", LevelFormat::Compressed_unique},
+                                  {"k", LevelFormat::Compressed_unique}}).named("CSF3");
+    Expr s = Tensor::make(TensorType(csf, dType::Float32), "s");
+    Expr t = Tensor::make(TensorType(csf, dType::Float32), "t");
+    try {
+        Kernel("csf_mul").expr(s * t).emit();
+        Kernel("csf_add").expr(s + t).emit();
+    } catch (const UnsupportedForm &e) {
+        std::cerr << "nacho_hipgen: " << e.what() << "\n";
+        return 1;
+    }
+    for (const auto &[name, reason] : refused()) std::cerr << "not generated: " << reason << "\n";
+    return 0;
+}
+"""
+
+
+def test_naming_an_unsupported_kernel_fails(gxx, tmp_path):
+    """A declaration without a HIP kernel is listed as not generated, and naming it with
+    --kernels is an error before anything is written."""
+    src = tmp_path / "named.cpp"
+    src.write_text(NAMED_UNSUPPORTED)
+    exe = tmp_path / "named"
+    subprocess.run([gxx, "-std=c++17", "-Wall", "-Werror", f"-I{CODEGEN}", str(src),
+                    str(CODEGEN / "hipgen.cpp"), "-o", str(exe)], check=True)
+    run = subprocess.run([str(exe), "--kernels", "csf_mul", "--output-dir",
                           str(tmp_path / "o")], capture_output=True, text=True)
     assert run.returncode == 1
-    assert "inner_prod: a reduction over more than one index" in run.stderr
+    assert "csf_mul: no HIP kernel for a product of 2 operands in CSF3" in run.stderr
     assert not (tmp_path / "o").exists() or not any((tmp_path / "o").iterdir())
+    run = subprocess.run([str(exe), "--output-dir", str(tmp_path / "p")], capture_output=True,
+                         text=True)
+    assert run.returncode == 0 and "not generated: csf_mul: no HIP kernel" in run.stderr
+    assert sorted(p.name for p in (tmp_path / "p").iterdir()) == [
+        "csf_add_gpu.h", "csf_add_gpu_nb.cpp"]
 
 
 def test_kernel_selection_and_usage(hipgen, tmp_path):
@@ -168,6 +207,10 @@ def test_generated_headers_compile_link_and_reach_the_c_abi(generated, gxx, libd
         "csr_mul": "csr_mul::csr_mul_gpu_i32_f32({4, 4}, {4, 5}, 256, 256)",
         "spgemm": "spgemm::spgemm_gpu_i32_f32({4, 3}, {5, 4}, 256, 256)",
         "sssmm": "sssmm::sssmm_gpu_i32_f32({4, 3}, {3, 4}, {4, 5}, 256, 256)",
+        "coo_csr_add": "coo_csr_add::coo_csr_add_gpu_i32_f32({4, 4}, {5, 4}, 256, 256)",
+        "inner_prod": "inner_prod::inner_prod_gpu_i32_f32({4, 4, 4}, {4, 5, 4}, 256, 256)",
+        "inner_prod_coo":
+            "inner_prod_coo::inner_prod_coo_gpu_i32_f32({4, 4, 4}, {4, 4, 5}, 256, 256)",
     }
     for k, call in calls.items():
         lines.append(f"try {{ (void){call}; ++bad; std::printf(\"{k} did not throw\\n\"); }}")
