@@ -1,7 +1,8 @@
 """Benchmark of the nacho GPU path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--only]
-                    [--workload c2|c3|c4|c5|c5coo|c2coo|c3coo|c2dcsr|c3dcsr|c2add3|c4sssmm]
+                    [--workload c2|c3|c4|c5|c5coo|c2coo|c3coo|c2dcsr|c3dcsr|c2add3|c4sssmm
+                                |c5inner|c5innercoo|c2coocsr]
     python bench.py --workload mtx --files A.mtx B.mtx [...]      (real data, local files)
     python bench.py --workload tns --files T.tns [...] [--dims I,J,K]
 
@@ -42,8 +43,11 @@ consecutive .mtx files clipped to a common shape, through csr_add and csr_mul; e
 file with its copy shifted by one along every mode, through csf_add and coo3d_add.
 
 Workloads c5 (csf_add), c5coo (coo3d_add), c2coo (coo_add), c3coo (coo_mul), c2dcsr
-(dcsr_add) and c3dcsr (dcsr_mul) report GB/s of algorithmic bytes: CSF3 and DCSR count every level array of A, B
-and C once; COO3 16 bytes and COO 12 bytes per entry of A, B and C.
+(dcsr_add) and c3dcsr (dcsr_mul) report GB/s of algorithmic bytes: CSF3 and DCSR count
+every level array of A, B and C once; COO3 16 bytes and COO 12 bytes per entry of A, B and
+C.  c5inner / c5innercoo (inner_prod / inner_prod_coo of the C5 operands) count every array
+of A and B once plus the 4-byte result; c2coocsr (coo_csr_add of the C2 operands, B as COO)
+counts A and C as CSR and B as COO.
 """
 
 from __future__ import annotations
@@ -96,6 +100,20 @@ WORKLOADS = {
                                         "csr_pair_count_kernel + csr_write_kernel per level)",
                    desc="C2 as DCSR: dcsr_add f32 of the C2 operands with empty rows "
                         "dropped"),
+    "c5inner": dict(op="inner_prod", kernel="i and j level unions (csr_partition_kernel + "
+                                          "csr_pair_count_kernel + csr_write_kernel each) + "
+                                          "k level spread intersection + dot_tiles_kernel + "
+                                          "dot_final_kernel",
+                    desc="inner_prod f32 of the C5 CSF3 operands: sum of a*b over the "
+                         "(i, j, k) both hold"),
+    "c5innercoo": dict(op="inner_prod_coo", kernel="coo3_keys_kernel + csr_partition_kernel + "
+                                                   "csr_write_kernel<Intersect> (spread) + "
+                                                   "dot_tiles_kernel + dot_final_kernel",
+                       desc="inner_prod_coo f32 of the C5 operands as COO3"),
+    "c2coocsr": dict(op="coo_csr_add", kernel="coo_row_offsets_kernel + csr_partition_kernel "
+                                             "(with the row pass) + csr_pair_count_kernel + "
+                                             "csr_write_kernel<Union>",
+                     desc="coo_csr_add f32: the C2 operands, A as CSR and B as COO"),
     "c3dcsr": dict(op="dcsr_mul", kernel="two chained level merges + row compaction",
                    desc="C3 as DCSR: dcsr_mul f32 of the C3 operands with empty rows "
                         "dropped"),
@@ -103,8 +121,9 @@ WORKLOADS = {
                                        "device pipeline, host readback gaps excluded)",
                     desc="sssmm f32: A * A masked by A on the C4 operand (R-MAT 2^20); "
                          "GFLOP/s = 3 FLOP (two multiplies, one add) per term"),
-    "c4": dict(op="spgemm", kernel="long_hist_kernel + chunk_kernel (scatter) + dense/bitmap/sort "
-                                 "unit kernels + copy_units_kernel and the sizing kernels "
+    "c4": dict(op="spgemm", kernel="long_hist_kernel + long_runs_kernel (run descriptors) + "
+                                 "dense/bitmap/sort unit kernels + copy_units_kernel and the "
+                                 "sizing kernels "
                                  "(one call's device pipeline, host readback gaps excluded)",
                desc="C4 ESC SpGEMM C=A*A f32, R-MAT 2^20 (a,b,c,d)=(.57,.19,.19,.05), "
                     "8*2^20 draws deduplicated, no vertex permutation, values U[0.5,1.5], "
@@ -557,14 +576,16 @@ def bench_tuple_workload(args, device, workload, prepared=None):
         ops = synth.c2_operands() if workload == "c2dcsr" else synth.c3_operands()
         ops_np = [(dcsr_levels(p, c), v) for p, c, v in ops]
         shape = (len(ops[0][0]) - 1, len(ops[0][0]) - 1)
-    elif workload in ("c2coo", "c3coo"):
-        ops = synth.c2_operands() if workload == "c2coo" else synth.c3_operands()
+    elif workload in ("c2coo", "c3coo", "c2coocsr"):
+        ops = synth.c3_operands() if workload == "c3coo" else synth.c2_operands()
         (pa, ca, va), (pb, cb, vb) = ops
         rows = len(pa) - 1
         ia = np.repeat(np.arange(rows, dtype=np.int32), np.diff(pa))
         ib = np.repeat(np.arange(rows, dtype=np.int32), np.diff(pb))
         ops_np = [((ia, ca), va), ((ib, cb), vb)]
         shape = (rows, rows)
+        if workload == "c2coocsr":  # A keeps its row offsets
+            ops_np[0] = ((pa, ca), va)
     else:
         (ac, av), (bc, bv) = synth.c5_operands()
         ops_np = [(tuple(ac[:, d] for d in range(3)), av), (tuple(bc[:, d] for d in range(3)), bv)]
@@ -573,25 +594,29 @@ def bench_tuple_workload(args, device, workload, prepared=None):
         log(f"generated {workload}: nnzA={len(ops_np[0][1])} nnzB={len(ops_np[1][1])} "
             f"in {time.perf_counter() - t0:.1f}s")
 
-    def upload(crd, val):
+    def upload(crd, val, k):
         t = [torch.from_numpy(np.ascontiguousarray(c, dtype=np.int32)).to(device) for c in crd]
         v = torch.from_numpy(np.ascontiguousarray(val, dtype=np.float32)).to(device)
         dims = torch.tensor(list(shape), dtype=torch.int32)
         if workload in ("c2dcsr", "c3dcsr"):
             return nacho_amd.DCSR_gpu(t[0], t[1], t[2], v, dims)
-        if workload in ("c2coo", "c3coo"):
+        if workload in ("c2coo", "c3coo", "c2coocsr"):
+            if workload == "c2coocsr" and k == 0:  # A: CSR (row offsets, columns)
+                return nacho_amd.CSR_gpu(t[0], t[1], v, dims)
             return nacho_amd.COO_gpu(t[0], t[1], v, dims)
-        if workload == "c5coo":
+        if workload in ("c5coo", "c5innercoo"):
             return nacho_amd.COO3_gpu(t[0], t[1], t[2], v, dims)
         levels = csf3_levels(np.stack(crd, axis=1))
         lv = [torch.from_numpy(np.ascontiguousarray(x, dtype=np.int32)).to(device) for x in levels]
         return nacho_amd.CSF3_gpu(*lv, v, dims)
 
-    copies = [tuple(upload(*o) for o in ops_np) for _ in range(ROTATE)]
+    copies = [tuple(upload(*o, k) for k, o in enumerate(ops_np)) for _ in range(ROTATE)]
     fn = {"c2coo": nacho_amd.gpu_coo_add_f32, "c3coo": nacho_amd.gpu_coo_mul_f32,
           "c5coo": nacho_amd.gpu_coo3d_add_f32,
           "c5": nacho_amd.gpu_csf_add_f32, "c2dcsr": nacho_amd.gpu_dcsr_add_f32,
-          "c3dcsr": nacho_amd.gpu_dcsr_mul_f32}[workload]
+          "c3dcsr": nacho_amd.gpu_dcsr_mul_f32, "c5inner": nacho_amd.gpu_inner_prod_f32,
+          "c5innercoo": nacho_amd.gpu_inner_prod_coo_f32,
+          "c2coocsr": nacho_amd.gpu_coo_csr_add_f32}[workload]
     z = fn(*copies[0])
     torch.cuda.synchronize()
     nnz = [len(ops_np[0][1]), len(ops_np[1][1]), int(z.values.numel())]
@@ -600,6 +625,15 @@ def bench_tuple_workload(args, device, workload, prepared=None):
               z.dim_k_offsets.numel(), z.dim_k_indices.numel()]
         alg_bytes = csf_bytes([csf3_levels(np.stack(o[0], axis=1)) for o in ops_np])
         alg_bytes += 4 * (sum(lz) + lz[4])
+    elif workload == "c5inner":
+        # every array of A and B once, and the one result value
+        alg_bytes = csf_bytes([csf3_levels(np.stack(o[0], axis=1)) for o in ops_np]) + 4
+    elif workload == "c5innercoo":
+        alg_bytes = 16 * (nnz[0] + nnz[1]) + 4
+    elif workload == "c2coocsr":
+        # A: pos, crd, val; B: i, j, val; C: pos, crd, val
+        rows = shape[0]
+        alg_bytes = 8 * (rows + 1) + 8 * nnz[0] + 12 * nnz[1] + 8 * nnz[2]
     elif workload in ("c2dcsr", "c3dcsr"):
         # crd_i, pos_j, crd_j and values of A, B and C
         alg_bytes = sum(4 * (len(o[0][0]) + len(o[0][1]) + 2 * len(o[0][2])) for o in ops_np)
@@ -633,7 +667,7 @@ def bench_tuple_workload(args, device, workload, prepared=None):
 
         cores = host_cores()
         times = []
-        if workload == "c5":
+        if workload in ("c5", "c5inner"):
             levels = [csf3_levels(np.stack(o[0], axis=1)) for o in ops_np]
         begin = time.perf_counter()
         while time.perf_counter() - begin < args.cpu_budget and len(times) < 20:
@@ -645,6 +679,20 @@ def bench_tuple_workload(args, device, workload, prepared=None):
             elif workload == "c5":
                 oracle.port_csf3_union(levels[0], ops_np[0][1], levels[1], ops_np[1][1],
                                        timing=t, nthreads=cores)
+            elif workload == "c5inner":
+                oracle.port_csf3_inner(levels[0], ops_np[0][1], levels[1], ops_np[1][1],
+                                       timing=t, nthreads=cores)
+            elif workload == "c5innercoo":
+                oracle.port_coo3_inner(ops_np[0][0], ops_np[0][1], ops_np[1][0], ops_np[1][1],
+                                       timing=t, nthreads=cores)
+            elif workload == "c2coocsr":
+                # the C restatement of csr_add on the same operands (B's row offsets given)
+                pb = np.zeros(shape[0] + 1, np.int64)
+                np.add.at(pb, np.asarray(ops_np[1][0][0], np.int64) + 1, 1)
+                pb = np.cumsum(pb).astype(np.int32)
+                oracle.port_csr_binary("add", shape[0], ops_np[0][0][0], ops_np[0][0][1],
+                                       ops_np[0][1], pb, ops_np[1][0][1], ops_np[1][1],
+                                       nthreads=cores, timing=t)
             else:
                 oracle.port_coo_binary("mul" if workload == "c3coo" else "add", ops_np[0][0],
                                        ops_np[0][1], ops_np[1][0], ops_np[1][1],
@@ -950,7 +998,8 @@ def run_workload(args, device, workload):
         return bench_spgemm(args, device)
     if workload == "c4sssmm":
         return bench_sssmm(args, device)
-    if workload in ("c5", "c5coo", "c2coo", "c3coo", "c2dcsr", "c3dcsr"):
+    if workload in ("c5", "c5coo", "c2coo", "c3coo", "c2dcsr", "c3dcsr", "c5inner",
+                    "c5innercoo", "c2coocsr"):
         return bench_tuple_workload(args, device, workload)
     return bench_csr(args, device, workload)
 

@@ -1298,22 +1298,30 @@ __device__ __forceinline__ void block_sum_fixed(double *sh) {
     __syncthreads();
 }
 
-// Workgroup t sums the products that tile t of the spread intersection wrote (tile_count[t]
-// of them, at its own start position in the smaller operand's range) in binary64, in a
-// fixed order: partial[t].
+// Workgroups of the two-level sums below: few enough that one workgroup then adds their
+// partials in a handful of loads per thread.
+constexpr int kDotBlocks = 1024;
+
+// Workgroup b sums the products that tiles [b*T/G, (b+1)*T/G) of the spread intersection
+// wrote (tile_count[t] of them each, at the tile's own start position in the smaller
+// operand's range) in binary64, in a fixed order: partial[b].
 __global__ __launch_bounds__(kBlock) void dot_tiles_kernel(
     const int *__restrict__ split_a, const int *__restrict__ split_b, int by_a,
-    const int64_t *__restrict__ tile_count, const float *__restrict__ prod,
+    const int64_t *__restrict__ tile_count, int num_tiles, const float *__restrict__ prod,
     double *__restrict__ partial) {
     __shared__ double sh[kBlock];
-    const int t = blockIdx.x;
-    const int base = by_a ? split_a[t] : split_b[t];
-    const int n = static_cast<int>(tile_count[t]);
+    const long long g = gridDim.x;
+    const int t0 = static_cast<int>(num_tiles * static_cast<long long>(blockIdx.x) / g);
+    const int t1 = static_cast<int>(num_tiles * (static_cast<long long>(blockIdx.x) + 1) / g);
     double acc = 0.0;
-    for (int i = threadIdx.x; i < n; i += kBlock) acc += static_cast<double>(prod[base + i]);
+    for (int t = t0; t < t1; ++t) {
+        const int base = by_a ? split_a[t] : split_b[t];
+        const int n = static_cast<int>(tile_count[t]);
+        for (int i = threadIdx.x; i < n; i += kBlock) acc += static_cast<double>(prod[base + i]);
+    }
     sh[threadIdx.x] = acc;
     block_sum_fixed(sh);
-    if (threadIdx.x == 0) partial[t] = sh[0];
+    if (threadIdx.x == 0) partial[blockIdx.x] = sh[0];
 }
 
 // One workgroup: the sum of the n tile partials in a fixed order, rounded once to *dot.
@@ -1327,15 +1335,14 @@ __global__ __launch_bounds__(kBlock) void dot_final_kernel(const double *__restr
     if (threadIdx.x == 0) *dot = static_cast<float>(sh[0]);
 }
 
-// Workgroup b sums v[b * kSumTile, min(n, (b + 1) * kSumTile)) in binary64, in a fixed
-// order: partial[b].
-constexpr int kSumTile = 16 * kBlock;
+// Workgroup b of G sums v[b*n/G, (b+1)*n/G) in binary64, in a fixed order: partial[b].
 __global__ __launch_bounds__(kBlock) void sum_blocks_kernel(const float *__restrict__ v,
                                                             long long n,
                                                             double *__restrict__ partial) {
     __shared__ double sh[kBlock];
-    const long long lo = static_cast<long long>(blockIdx.x) * kSumTile;
-    const long long hi = min(n, lo + kSumTile);
+    const long long g = gridDim.x;
+    const long long lo = n * static_cast<long long>(blockIdx.x) / g;
+    const long long hi = n * (static_cast<long long>(blockIdx.x) + 1) / g;
     double acc = 0.0;
     for (long long i = lo + threadIdx.x; i < hi; i += kBlock) acc += static_cast<double>(v[i]);
     sh[threadIdx.x] = acc;
@@ -1344,14 +1351,14 @@ __global__ __launch_bounds__(kBlock) void sum_blocks_kernel(const float *__restr
 }
 
 int sum_values(Call &call, const float *v, long long n, float *out) {
-    const long long blocks = std::max<long long>(1, (n + kSumTile - 1) / kSumTile);
-    if (blocks > INT_MAX) return NACHO_ERR_INDEX_OVERFLOW;
+    const int blocks = static_cast<int>(
+        std::max<long long>(1, std::min<long long>(kDotBlocks, (n + kBlock - 1) / kBlock)));
     double *partial = nullptr;
     NACHO_TRY(call.scratch_n(static_cast<size_t>(blocks), &partial));
     const hipStream_t s = call.stream();
-    sum_blocks_kernel<<<static_cast<unsigned>(blocks), kBlock, 0, s>>>(v, n, partial);
+    sum_blocks_kernel<<<blocks, kBlock, 0, s>>>(v, n, partial);
     NACHO_TRY_HIP(hipGetLastError());
-    dot_final_kernel<<<1, kBlock, 0, s>>>(partial, static_cast<int>(blocks), out);
+    dot_final_kernel<<<1, kBlock, 0, s>>>(partial, blocks, out);
     NACHO_TRY_HIP(hipGetLastError());
     return NACHO_OK;
 }
@@ -1407,11 +1414,12 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
         int64_t *len_dev = chunk_total + grid;
         int *pos = Z.pos;
         double *partial = nullptr;
+        const int dot_grid = std::min(num_tiles, kDotBlocks);
         if (Z.dot) {
             // the inner product: the spread write's pos and length go to scratch, and the
             // host does not wait for the length
             NACHO_TRY(call.scratch_n(static_cast<size_t>(rows) + 1, &pos));
-            NACHO_TRY(call.scratch_n(static_cast<size_t>(num_tiles), &partial));
+            NACHO_TRY(call.scratch_n(static_cast<size_t>(dot_grid), &partial));
             length_out = chunk_total + grid + 1;
         }
         NACHO_TRY(call.timer_start(kernel_name));  // the whole device pipeline of this level
@@ -1428,10 +1436,10 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
                                      length_out, nullptr, nullptr, tmp_row, nullptr, 0);
         NACHO_TRY_HIP(hipGetLastError());
         if (Z.dot) {
-            dot_tiles_kernel<<<num_tiles, kBlock, 0, s>>>(split_a, split_b, by_a, tile_count,
-                                                          tmp_val, partial);
+            dot_tiles_kernel<<<dot_grid, kBlock, 0, s>>>(split_a, split_b, by_a, tile_count,
+                                                         num_tiles, tmp_val, partial);
             NACHO_TRY_HIP(hipGetLastError());
-            dot_final_kernel<<<1, kBlock, 0, s>>>(partial, num_tiles, Z.dot);
+            dot_final_kernel<<<1, kBlock, 0, s>>>(partial, dot_grid, Z.dot);
             NACHO_TRY_HIP(hipGetLastError());
             NACHO_TRY(call.timer_stop());
             NACHO_TRY(call.collect_timer());  // (kernel timing only: waits for the stream)

@@ -1656,37 +1656,57 @@ typedef struct {
     double *part;
 } csf_inner_job;
 
-/* Thread t: A's i entries [t*a_ni/nt, (t+1)*a_ni/nt) against the B i entries of equal or
- * larger coordinate, walked as the three-level intersection. */
+/* First index x in [lo, hi] with key[x] >= q (hi + 1 when none), over int32 offsets. */
+static int first_at_least(const int32_t *key, int lo, int hi, long q) {
+    int h = hi + 1;
+    while (lo < h) {
+        const int mid = lo + (h - lo) / 2;
+        if ((long)key[mid] < q) {
+            lo = mid + 1;
+        } else {
+            h = mid;
+        }
+    }
+    return lo;
+}
+
+/* Thread t: A's (i, j) fibres whose k entries start in [t*nk/nt, (t+1)*nk/nt), so threads
+ * hold equal shares of A's entries however skewed the i level is; each fibre is matched
+ * with B's fibre of the same (i, j) and their k lists intersected. */
 static void csf_inner_task(int t, void *arg) {
     csf_inner_job *J = (csf_inner_job *)arg;
-    int ia = (int)((long)J->a_ni * t / J->nt), ia_end = (int)((long)J->a_ni * (t + 1) / J->nt);
+    const int a_nj = J->a_ni > 0 ? J->a_pj[J->a_ni] : 0;
+    const long a_nk = a_nj > 0 ? J->a_pk[a_nj] : 0;
+    const int f0 = first_at_least(J->a_pk, 0, a_nj, a_nk * t / J->nt);
+    const int f1 = t + 1 == J->nt ? a_nj : first_at_least(J->a_pk, 0, a_nj, a_nk * (t + 1) / J->nt);
     double s = 0.0;
-    int ib = ia < ia_end ? lower_bound_i32(J->b_ci, 0, J->b_ni, J->a_ci[ia]) : J->b_ni;
-    while (ia < ia_end && ib < J->b_ni) {
-        if (J->a_ci[ia] < J->b_ci[ib]) {
-            ++ia;
-            continue;
-        }
-        if (J->b_ci[ib] < J->a_ci[ia]) {
-            ++ib;
-            continue;
-        }
-        int ja = J->a_pj[ia], jae = J->a_pj[ia + 1], jb = J->b_pj[ib], jbe = J->b_pj[ib + 1];
-        while (ja < jae && jb < jbe) {
-            if (J->a_cj[ja] < J->b_cj[jb]) {
-                ++ja;
-            } else if (J->b_cj[jb] < J->a_cj[ja]) {
-                ++jb;
-            } else {
-                s += k_intersect(J->a_ck, J->a_v, J->a_pk[ja], J->a_pk[ja + 1], J->b_ck,
-                                 J->b_v, J->b_pk[jb], J->b_pk[jb + 1]);
-                ++ja;
-                ++jb;
+    if (f0 < f1) {
+        /* the i entry holding fibre f0: the last ia with a_pj[ia] <= f0 */
+        int ia = first_at_least(J->a_pj, 0, J->a_ni, (long)f0 + 1) - 1;
+        int f = f0;
+        while (f < f1) {
+            const int fend = J->a_pj[ia + 1] < f1 ? J->a_pj[ia + 1] : f1;
+            const int ib = lower_bound_i32(J->b_ci, 0, J->b_ni, J->a_ci[ia]);
+            if (ib < J->b_ni && J->b_ci[ib] == J->a_ci[ia]) {
+                const int jbe = J->b_pj[ib + 1];
+                int jb = lower_bound_i32(J->b_cj, J->b_pj[ib], jbe, J->a_cj[f]);
+                int fa = f;
+                while (fa < fend && jb < jbe) {
+                    if (J->a_cj[fa] < J->b_cj[jb]) {
+                        ++fa;
+                    } else if (J->b_cj[jb] < J->a_cj[fa]) {
+                        ++jb;
+                    } else {
+                        s += k_intersect(J->a_ck, J->a_v, J->a_pk[fa], J->a_pk[fa + 1], J->b_ck,
+                                         J->b_v, J->b_pk[jb], J->b_pk[jb + 1]);
+                        ++fa;
+                        ++jb;
+                    }
+                }
             }
+            f = fend;
+            ++ia;
         }
-        ++ia;
-        ++ib;
     }
     J->part[t] = s;
 }
