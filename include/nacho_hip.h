@@ -185,6 +185,16 @@ int nacho_free(void *ptr, void *stream);
  * stream-ordered).  This returns every cached, unused buffer to the driver. */
 int nacho_release_cached_memory(void);
 
+/* Cap on the bytes the default allocator keeps cached (unused buffers held for reuse);
+ * SIZE_MAX, the default, keeps every released buffer.  A release that takes the cache past
+ * the cap synchronises the device and returns the oldest buffers of the largest sizes to
+ * the driver until it fits; setting a cap trims at once.  No counterpart in the reference
+ * (cudaMallocAsync's pool, stitch_and_generate_gpu.cpp:187-196). */
+int nacho_set_cache_limit(size_t bytes);
+
+/* Bytes the default allocator holds cached (released, unused) now. */
+size_t nacho_cached_bytes(void);
+
 /* Note that work queued on `stream` uses the buffer `ptr` (a buffer the default allocator
  * returned, not yet released).  When the buffer is released on its own stream, an event is
  * also recorded on `stream`, and the buffer is reused only by work ordered after it: a

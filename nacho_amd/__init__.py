@@ -9,6 +9,7 @@ except the file readers (host C++ in the same library).
 
 from .convert import to_coo, to_coo3, to_csf3, to_csr, to_dcsr  # noqa: F401
 from .ops import (  # noqa: F401
+    cached_bytes,
     gpu_coo3d_add_f32,
     gpu_coo_add_f32,
     gpu_coo_csr_add_f32,
@@ -27,6 +28,7 @@ from .ops import (  # noqa: F401
     gpu_spgemm_f32,
     last_kernel_ms,
     release_cached_memory,
+    set_cache_limit,
     set_kernel_timing,
     set_validation,
     validate_csr,

@@ -228,6 +228,10 @@ def load() -> ctypes.CDLL:
     lib.nacho_free.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
     lib.nacho_release_cached_memory.restype = ctypes.c_int
     lib.nacho_release_cached_memory.argtypes = []
+    lib.nacho_set_cache_limit.restype = ctypes.c_int
+    lib.nacho_set_cache_limit.argtypes = [ctypes.c_size_t]
+    lib.nacho_cached_bytes.restype = ctypes.c_size_t
+    lib.nacho_cached_bytes.argtypes = []
     lib.nacho_error_string.restype = ctypes.c_char_p
     lib.nacho_error_string.argtypes = [ctypes.c_int]
     lib.nacho_version.restype = ctypes.c_char_p

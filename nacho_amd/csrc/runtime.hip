@@ -3,6 +3,7 @@
 #include "runtime.hpp"
 
 #include <atomic>
+#include <climits>
 #include <cstdint>
 #include <cstring>
 #include <map>
@@ -28,6 +29,12 @@ namespace {
 // outside the cache lock).  The host never blocks on a stream for reuse, and the common case
 // (one stream) records no event at all.  When the driver runs out of memory the cache is
 // emptied (after a device synchronise) and the allocation retried.
+//
+// Size.  By default every released block stays cached (a C4 SpGEMM leaves about 100 GB
+// there, which other allocators in the process cannot use until nacho_release_cached_memory).
+// nacho_set_cache_limit caps the cached bytes: a release that takes them past the cap
+// synchronises the device and returns the oldest blocks of the largest size classes to the
+// driver until they fit.
 
 // A pooled event, possibly shared by several blocks.
 struct SharedEvent {
@@ -49,6 +56,8 @@ std::mutex g_cache_mutex;
 std::unordered_map<void *, Block> g_live;              // allocated blocks by pointer
 std::map<std::pair<int, size_t>, std::vector<Block>> g_free;  // (device, size) -> free
 std::vector<hipEvent_t> g_event_pool;  // idle events (created with timing disabled)
+size_t g_free_bytes = 0;               // bytes in g_free
+std::atomic<size_t> g_cache_limit{SIZE_MAX};
 
 // An idle event, or a new one (nullptr if creation fails).  Caller holds g_cache_mutex.
 hipEvent_t take_event_locked() {
@@ -104,8 +113,29 @@ void release_cached_blocks_locked() {
         }
     }
     g_free.clear();
+    g_free_bytes = 0;
     for (hipEvent_t e : g_event_pool) (void)hipEventDestroy(e);
     g_event_pool.clear();
+}
+
+// Return cached blocks to the driver until at most `limit` bytes stay cached: the largest
+// size classes first, the oldest block of a class first.  The device is synchronised first
+// (a cached block's last use may still be queued).  Caller holds g_cache_mutex.
+void trim_cache_locked(size_t limit) {
+    if (g_free_bytes <= limit) return;
+    (void)hipDeviceSynchronize();
+    for (auto it = g_free.rbegin(); it != g_free.rend() && g_free_bytes > limit; ++it) {
+        std::vector<Block> &bin = it->second;
+        size_t drop = 0;
+        while (drop < bin.size() && g_free_bytes > limit) {
+            Block &b = bin[drop++];
+            for (SharedEvent *e : b.pending) drop_shared_locked(e);
+            b.pending.clear();
+            (void)hipFree(b.ptr);
+            g_free_bytes -= b.size;
+        }
+        bin.erase(bin.begin(), bin.begin() + static_cast<std::ptrdiff_t>(drop));
+    }
 }
 
 // Make `stream` wait for the events a reused block carries (outside the cache lock), then
@@ -143,6 +173,7 @@ void *default_allocate(size_t bytes, hipStream_t stream) {
                 if (bin[i].stream != stream) continue;
                 Block b = std::move(bin[i]);
                 bin.erase(bin.begin() + static_cast<std::ptrdiff_t>(i));
+                g_free_bytes -= b.size;
                 pending.swap(b.pending);
                 b.used_on.clear();
                 reused = b.ptr;
@@ -196,8 +227,10 @@ void release_batch(void *const *ptrs, size_t n, hipStream_t stream) {
             }
         }
         b.used_on.clear();
+        g_free_bytes += b.size;
         g_free[{b.device, b.size}].push_back(std::move(b));
     }
+    trim_cache_locked(g_cache_limit.load(std::memory_order_relaxed));
 }
 
 void default_release(void *ptr, hipStream_t stream) { release_batch(&ptr, 1, stream); }
@@ -436,6 +469,18 @@ int nacho_release_cached_memory(void) {
     std::lock_guard<std::mutex> lock(nacho::g_cache_mutex);
     nacho::release_cached_blocks_locked();
     return NACHO_OK;
+}
+
+int nacho_set_cache_limit(size_t bytes) {
+    std::lock_guard<std::mutex> lock(nacho::g_cache_mutex);
+    nacho::g_cache_limit.store(bytes, std::memory_order_relaxed);
+    nacho::trim_cache_locked(bytes);
+    return NACHO_OK;
+}
+
+size_t nacho_cached_bytes(void) {
+    std::lock_guard<std::mutex> lock(nacho::g_cache_mutex);
+    return nacho::g_free_bytes;
 }
 
 const char *nacho_error_string(int code) {

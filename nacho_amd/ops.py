@@ -353,6 +353,21 @@ def release_cached_memory() -> None:
     _lib.check(_lib.load().nacho_release_cached_memory(), "nacho_release_cached_memory")
 
 
+def set_cache_limit(nbytes: int | None) -> None:
+    """Cap the bytes the library's caching allocator keeps for reuse (None: no cap, the
+    default).  Past the cap, released buffers go back to the driver (after a device
+    synchronise), so that torch's allocator in the same process can use that memory."""
+    limit = ctypes.c_size_t(-1).value if nbytes is None else int(nbytes)
+    if limit < 0:
+        raise ValueError("cache limit must be >= 0")
+    _lib.check(_lib.load().nacho_set_cache_limit(limit), "nacho_set_cache_limit")
+
+
+def cached_bytes() -> int:
+    """Bytes the library's caching allocator holds for reuse now."""
+    return int(_lib.load().nacho_cached_bytes())
+
+
 def set_kernel_timing(enable: bool) -> None:
     _lib.load().nacho_set_kernel_timing(1 if enable else 0)
 

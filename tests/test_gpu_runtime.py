@@ -113,3 +113,42 @@ def test_record_stream_orders_reuse_after_a_side_stream(gpu):
         assert torch.equal(seen, expected)
         assert torch.equal(z2.values, -expected)
         del z2
+
+
+def test_cache_limit_returns_memory_to_the_driver(gpu):
+    """With a cap of 0 nothing released stays cached; without a cap the call's released
+    buffers stay for reuse until nacho_release_cached_memory; results stay correct."""
+    import nacho_amd
+    from oracle import oracle
+    from tests.helpers import assert_csr_equal
+    from tests.test_gpu_csr import from_gpu
+
+    rng = np.random.default_rng(21)
+    rows, cols = 20000, 20000
+    a, b = random_csr(rng, rows, cols, 0.002), random_csr(rng, rows, cols, 0.002)
+    want = oracle.closed_csr_binary("add", rows, cols, *a, *b)
+    ga, gb = to_gpu(a, rows, cols, gpu), to_gpu(b, rows, cols, gpu)
+    try:
+        print("[gpu] cache limit 0", flush=True)
+        nacho_amd.set_cache_limit(0)
+        assert nacho_amd.cached_bytes() == 0
+        for _ in range(3):
+            z = nacho_amd.gpu_csr_add_f32(ga, gb)
+            assert_csr_equal(from_gpu(z), want, "limit 0")
+            del z
+            torch.cuda.synchronize()
+            assert nacho_amd.cached_bytes() == 0
+        print("[gpu] cache unlimited", flush=True)
+        nacho_amd.set_cache_limit(None)
+        z = nacho_amd.gpu_csr_add_f32(ga, gb)
+        assert_csr_equal(from_gpu(z), want, "unlimited")
+        del z
+        torch.cuda.synchronize()
+        assert nacho_amd.cached_bytes() > 0
+        held = nacho_amd.cached_bytes()
+        nacho_amd.set_cache_limit(held // 2)  # trims at once
+        assert nacho_amd.cached_bytes() <= held // 2
+    finally:
+        nacho_amd.set_cache_limit(None)
+    nacho_amd.release_cached_memory()
+    assert nacho_amd.cached_bytes() == 0
