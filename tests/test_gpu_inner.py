@@ -143,3 +143,19 @@ def test_c5_full_size(gpu, kind):
     got = gpu_inner(kind, synth.C5_SHAPE, ac, av, ac, av, gpu)
     want = float(np.sum((av * av).astype(np.float64)))
     assert_close(got, want, ac, av, ac, av, f"{kind} C5 self")
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("smaller", ["a", "b"])
+def test_subset_operand(gpu, kind, smaller):
+    """One operand a subset of the other's coordinates: the products are spread over the
+    smaller operand's positions, whichever side that is."""
+    rng = np.random.default_rng(15)
+    shape = (300, 400, 500)
+    big, bigv = random_coords(rng, shape, 200000)
+    keep = rng.random(len(big)) < 0.3
+    small = big[keep]
+    smallv = rng.uniform(-1, 1, len(small)).astype(np.float32)
+    ac, av, bc, bv = (small, smallv, big, bigv) if smaller == "a" else (big, bigv, small, smallv)
+    got = gpu_inner(kind, shape, ac, av, bc, bv, gpu)
+    assert_close(got, want_inner(kind, ac, av, bc, bv), ac, av, bc, bv, f"{kind} {smaller}")
