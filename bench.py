@@ -100,10 +100,9 @@ WORKLOADS = {
                                         "csr_pair_count_kernel + csr_write_kernel per level)",
                    desc="C2 as DCSR: dcsr_add f32 of the C2 operands with empty rows "
                         "dropped"),
-    "c5inner": dict(op="inner_prod", kernel="i and j level unions (csr_partition_kernel + "
-                                          "csr_pair_count_kernel + csr_write_kernel each) + "
-                                          "k level spread intersection + dot_tiles_kernel + "
-                                          "dot_final_kernel",
+    "c5inner": dict(op="inner_prod", kernel="csf_row_offsets_kernel + csf_keys_kernel + "
+                                          "csr_partition_kernel + csr_write_kernel<Intersect> "
+                                          "(spread) + dot_tiles_kernel + dot_final_kernel",
                     desc="inner_prod f32 of the C5 CSF3 operands: sum of a*b over the "
                          "(i, j, k) both hold"),
     "c5innercoo": dict(op="inner_prod_coo", kernel="coo3_keys_kernel + csr_partition_kernel + "

@@ -14,8 +14,13 @@
 //            copy) and the result's k offsets.
 // Every coordinate of each level's union is emitted; for operands without empty fibres (what
 // to_csf3 builds) no output fibre is empty.
+//
+// The inner product (inner_prod, compiler.cpp:141) reduces the intersection of the two trees
+// to one value: through rows i of (j, k) column keys built from the levels when the keys fit
+// 31 bits, otherwise through the i and j unions above and a k level intersection.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <climits>
 #include <cstdint>
 
@@ -146,7 +151,112 @@ int csf_add(const nacho_csf3 *a, const nacho_csf3 *b, nacho_csf3 *z, int32_t num
     return NACHO_OK;
 }
 
-// Inner product of two CSF3 tensors: Σ a·b over the (i, j, k) both hold.  The i and j
+// ---- inner product through row offsets and (j, k) column keys -----------------------------
+//
+// A CSF3 tensor is a matrix with rows i and columns (j, k) in lexicographic order: its k
+// entries in storage order are the row-major entries of that matrix.  When the j and k
+// extents fit 31 bits together (key j << kbits | k below INT_MAX), the inner product is the
+// level intersection of those two matrices, with no union of the i and j levels first.
+
+struct CsfKeysJob {
+    const int *ci, *pj, *cj, *pk, *ck;
+    int ni, nj;
+    int *pos;  // rows + 1 row offsets (into the k entries)
+    int *key;  // nk column keys
+};
+
+// Row offsets of both operands: work item p in [0, ni] of an operand gives the rows in
+// (ci[p - 1], ci[p]] (ci[-1] = -1, ci[ni] = rows) the k offset of i entry p's first fibre,
+// pk[pj[p]] (nk for p = ni).  Items [0, na] are A's, the rest B's.
+__global__ void csf_row_offsets_kernel(CsfKeysJob ja, CsfKeysJob jb, int rows) {
+    const long long na = static_cast<long long>(ja.ni) + 1;
+    const long long nb = static_cast<long long>(jb.ni) + 1;
+    for (long long g = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+         g < na + nb; g += static_cast<long long>(gridDim.x) * blockDim.x) {
+        const bool first = g < na;
+        const int *__restrict__ ci = first ? ja.ci : jb.ci;
+        const int *__restrict__ pj = first ? ja.pj : jb.pj;
+        const int *__restrict__ pk = first ? ja.pk : jb.pk;
+        int *__restrict__ pos = first ? ja.pos : jb.pos;
+        const int ni = first ? ja.ni : jb.ni;
+        const int p = static_cast<int>(first ? g : g - na);
+        const int lo = p == 0 ? -1 : min(max(ci[p - 1], -1), rows);
+        const int hi = p == ni ? rows : min(max(ci[p], -1), rows);
+        const int at = pk[pj[p]];
+        for (int r = lo + 1; r <= hi; ++r) pos[r] = at;
+    }
+}
+
+// Column keys of both operands: cj[f] << kbits | ck[e] for every k entry e of fibre f.  One
+// wavefront per group of 64 consecutive fibres (groups [0, ga) are A's, the rest B's): lane l
+// holds fibre f0 + l's offset and j bits, and the wave strides over the group's k entries
+// with consecutive lanes on consecutive entries, each finding its fibre among the 64 offsets
+// by a six-step search over the lanes (ds_bpermute, every lane active).
+//
+// Measured alternatives at C5 (19.8M entries in 7.75M fibres per operand): one fibre per
+// thread, 515 us; 256 fibres per wave staged in LDS, 164 us; one wave per 1024 entries
+// (fibres of a Zipf-heavy i hold about 60 entries) with 1025 staged fibres, 232 us; this
+// form, 148 us.
+__global__ __launch_bounds__(256) void csf_keys_kernel(CsfKeysJob ja, CsfKeysJob jb, int ga,
+                                                       int gb, int kbits) {
+    constexpr int W = 64;
+    const int lane = static_cast<int>(threadIdx.x) % W;
+    const long long g = static_cast<long long>(blockIdx.x) * (blockDim.x / W) + threadIdx.x / W;
+    if (g >= static_cast<long long>(ga) + gb) return;  // whole waves
+    const bool first = g < ga;
+    // the operand's fields as plain values (no addressable copy of either job)
+    const int *__restrict__ pk = first ? ja.pk : jb.pk;
+    const int *__restrict__ cj = first ? ja.cj : jb.cj;
+    const int *__restrict__ ck = first ? ja.ck : jb.ck;
+    int *__restrict__ key = first ? ja.key : jb.key;
+    const int nj = first ? ja.nj : jb.nj;
+    const int f0 = static_cast<int>((first ? g : g - ga) * W);
+    const int nf = min(W, nj - f0);
+    const int f = f0 + min(lane, nf - 1);
+    const int start = pk[f];     // lane's fibre start (clamped)
+    const int e1 = pk[f0 + nf];  // end of the group's entries
+    const int jhi = cj[f] << kbits;
+    const int e0 = __shfl(start, 0, W);
+    constexpr int U = 4;  // entries per lane whose loads are issued together
+    for (int base = e0; base < e1; base += U * W) {  // uniform: every lane shuffles
+        int kv[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) kv[u] = ck[min(base + u * W + lane, e1 - 1)];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int e = base + u * W + lane;
+            // the last lane l < nf with start(l) <= e, in six steps
+            int lo = 0;
+#pragma unroll
+            for (int step = W / 2; step > 0; step >>= 1) {
+                const int cand = lo + step;
+                const int v = __shfl(start, min(cand, nf - 1), W);
+                if (cand < nf && v <= e) lo = cand;
+            }
+            const int hi_bits = __shfl(jhi, lo, W);
+            if (e < e1) key[e] = hi_bits | kv[u];
+        }
+    }
+}
+
+// Bits of coordinates below `extent`.
+static int extent_bits(int extent) {
+    unsigned m = extent > 1 ? static_cast<unsigned>(extent - 1) : 0u;
+    int bits = 0;
+    while (m) {
+        ++bits;
+        m >>= 1;
+    }
+    return bits;
+}
+
+// Rows at most this many times the entries take the key path (its row offsets cost one
+// write per row).
+constexpr long long kKeyPathRowsPerEntry = 4;
+
+// Inner product of two CSF3 tensors: Σ a·b over the (i, j, k) both hold.  When the (j, k)
+// keys fit, both operands become rows i of column keys and one level intersection sums the
+// products (csf_inner_by_keys).  Otherwise the i and j
 // levels are merged as in csf_add (unions carrying child pointers, into scratch), so every
 // (i, j) fibre of either operand becomes a row whose A and B ranges are its k entries (empty
 // on the side that lacks it); the k level is the intersection of each row's ranges, whose
@@ -172,6 +282,53 @@ int csf_inner_prod(const nacho_csf3 *a, const nacho_csf3 *b, nacho_scalar *z, in
     const hipStream_t s = call.stream();
     float *value = nullptr;
     NACHO_TRY(call.result_n(1, &value));
+
+    const int kbits = extent_bits(a->dim_k_size);
+    const bool keys_fit = a->dim_j_size >= 1 && a->dim_k_size >= 1 &&
+                          extent_bits(a->dim_j_size) + kbits <= 31 &&
+                          ((static_cast<long long>(a->dim_j_size - 1) << kbits) |
+                           (a->dim_k_size - 1)) < INT_MAX;
+    const long long entries = static_cast<long long>(a->dim_k_length) + b->dim_k_length;
+    if (keys_fit && a->dim_i_size <= kKeyPathRowsPerEntry * entries + (1 << 20) &&
+        entries + a->dim_i_size <= static_cast<long long>(INT_MAX) - 2 * csr::kLevelTileSlack) {
+        const int rows = a->dim_i_size;
+        int *pa = nullptr, *pb = nullptr, *ka = nullptr, *kb = nullptr;
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(rows) + 1, &pa));
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(rows) + 1, &pb));
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(std::max(a->dim_k_length, 1)), &ka));
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(std::max(b->dim_k_length, 1)), &kb));
+        const CsfKeysJob ja{a->dim_i_indices, a->dim_j_offsets, a->dim_j_indices,
+                            a->dim_k_offsets, a->dim_k_indices, a->dim_i_length,
+                            a->dim_j_length, pa, ka};
+        const CsfKeysJob jb{b->dim_i_indices, b->dim_j_offsets, b->dim_j_indices,
+                            b->dim_k_offsets, b->dim_k_indices, b->dim_i_length,
+                            b->dim_j_length, pb, kb};
+        NACHO_TRY(call.timer_start("inner_prod (row offsets + (j, k) keys)"));
+        const long long row_items = static_cast<long long>(a->dim_i_length) + b->dim_i_length + 2;
+        csf_row_offsets_kernel<<<static_cast<unsigned>(std::min<long long>(
+                                     4096, (row_items + 255) / 256)),
+                                 256, 0, s>>>(ja, jb, rows);
+        NACHO_TRY_HIP(hipGetLastError());
+        const int ga = (a->dim_j_length + 63) / 64, gb = (b->dim_j_length + 63) / 64;
+        if (ga + gb > 0) {
+            csf_keys_kernel<<<static_cast<unsigned>((ga + gb + 3) / 4), 256, 0, s>>>(
+                ja, jb, ga, gb, kbits);
+            NACHO_TRY_HIP(hipGetLastError());
+        }
+        NACHO_TRY(call.timer_stop());
+        NACHO_TRY(call.collect_timer());  // (kernel timing only) before the merge's interval
+        const csr::LevelOperand A{pa, ka, a->values, a->dim_k_length, nullptr};
+        const csr::LevelOperand B{pb, kb, b->values, b->dim_k_length, nullptr};
+        csr::LevelResult Z{nullptr, nullptr, nullptr, nullptr, nullptr};
+        Z.dot = value;
+        long long unused = 0;
+        NACHO_TRY(csr::merge_level(call, true, true, false, rows, A, B, Z, &unused,
+                                   "inner_prod"));
+        z->values = value;
+        z->nnz = 1;
+        call.commit();
+        return NACHO_OK;
+    }
 
     // i level: union of the root rows, child pointers into the j offsets
     int *root = nullptr, *root_out = nullptr, *ci_a = nullptr, *ci_b = nullptr, *crd_i = nullptr;

@@ -107,17 +107,30 @@ def test_self_product(gpu, kind):
     assert_close(got, want, ac, av, ac, av, "self")
 
 
-def test_coo_wide_keys(gpu):
-    """COO3 whose (j, k) keys do not fit 31 bits: the packed-tuple intersection path, then
-    the sum of its products."""
+@pytest.mark.parametrize("kind", KINDS)
+def test_wide_keys(gpu, kind):
+    """(j, k) keys that do not fit 31 bits: COO3 takes the packed-tuple intersection and sums
+    its products, CSF3 the i and j level unions and the k level intersection."""
     rng = np.random.default_rng(14)
     shape = (50, 1 << 20, 1 << 20)
     ac, av = random_coords(rng, shape, 100000)
     keep = rng.random(len(ac)) < 0.5
     bc = ac[keep]
     bv = rng.uniform(-1, 1, len(bc)).astype(np.float32)
-    got = gpu_inner("coo", shape, ac, av, bc, bv, gpu)
-    assert_close(got, want_inner("coo", ac, av, bc, bv), ac, av, bc, bv, "wide keys")
+    got = gpu_inner(kind, shape, ac, av, bc, bv, gpu)
+    assert_close(got, want_inner(kind, ac, av, bc, bv), ac, av, bc, bv, f"{kind} wide keys")
+
+
+@pytest.mark.parametrize("kind", KINDS)
+def test_sparse_rows(gpu, kind):
+    """Few i coordinates spread over many rows (row offsets with long empty gaps), j and k
+    extents of one (keys of no bits)."""
+    rng = np.random.default_rng(16)
+    shape = (1 << 20, 1, 1)
+    ac, av = random_coords(rng, shape, 3000)
+    bc, bv = random_coords(rng, shape, 3000)
+    got = gpu_inner(kind, shape, ac, av, bc, bv, gpu)
+    assert_close(got, want_inner(kind, ac, av, bc, bv), ac, av, bc, bv, f"{kind} sparse rows")
 
 
 def test_c5_reduced(gpu):
@@ -159,3 +172,45 @@ def test_subset_operand(gpu, kind, smaller):
     ac, av, bc, bv = (small, smallv, big, bigv) if smaller == "a" else (big, bigv, small, smallv)
     got = gpu_inner(kind, shape, ac, av, bc, bv, gpu)
     assert_close(got, want_inner(kind, ac, av, bc, bv), ac, av, bc, bv, f"{kind} {smaller}")
+
+
+def test_csf_empty_fibres(gpu):
+    """CSF3 operands with many empty (i, j) fibres (legal for the C ABI, never built by
+    to_csf3): runs of fibres with no k entries between the ones that have them, so that a
+    range of k entries spans more fibres than the key kernel stages."""
+    import nacho_amd
+
+    shape = (4, 60000, 50)
+
+    def levels_with_gaps(seed):
+        r = np.random.default_rng(seed)
+        ci = np.array([0, 2, 3], np.int32)
+        pj, cj, pk, ck, val = [0], [], [0], [], []
+        for _ in ci:
+            js = np.sort(r.choice(shape[1], 20000, replace=False))
+            for n, j in enumerate(js):
+                cj.append(j)
+                if n % 10 == 0:  # one fibre in ten holds entries
+                    ks = np.sort(r.choice(shape[2], int(r.integers(1, 4)), replace=False))
+                    ck.extend(ks)
+                    val.extend(r.uniform(-1, 1, len(ks)))
+                pk.append(len(ck))
+            pj.append(len(cj))
+        return ((ci, np.array(pj, np.int32), np.array(cj, np.int32), np.array(pk, np.int32),
+                 np.array(ck, np.int32)), np.array(val, np.float32))
+
+    (la, va), (lb, vb) = levels_with_gaps(1), levels_with_gaps(2)
+    lb = (lb[0], lb[1], la[2], lb[3], lb[4])  # the same j coordinates, so fibres pair
+    # (B keeps its own k offsets: its entries sit under every tenth fibre as well)
+
+    def gpu_csf(levels, val):
+        bufs = [torch.from_numpy(np.asarray(x, np.int32)).to(gpu) for x in levels]
+        return nacho_amd.CSF3_gpu(*bufs, torch.from_numpy(val).to(gpu),
+                                  torch.tensor(list(shape), dtype=torch.int32))
+
+    print(f"[gpu] inner_prod csf empty fibres nnz=({len(va)},{len(vb)})", flush=True)
+    z = nacho_amd.gpu_inner_prod_f32(gpu_csf(la, va), gpu_csf(lb, vb))
+    got = float(z.values.cpu().numpy()[0])
+    want = oracle.port_csf3_inner(la, va, lb, vb, nthreads=4)
+    scale = float(np.abs(va).max() * np.abs(vb).max()) * min(len(va), len(vb))
+    assert abs(got - want) <= 1.2e-7 * abs(want) + 1e-12 * scale, (got, want)
