@@ -87,6 +87,20 @@ def _csf3_desc(t: CSF3_gpu) -> _lib.Csf3Desc:
                          _p(t.values), nk)
 
 
+def _cached_desc(t, desc_fn):
+    """The operand's C descriptor, rebuilt only when a buffer's address or length changed
+    since it was last built for this object (its fields are read-only, but a buffer could
+    be resized in place): repeated calls on the same operands skip the size checks and the
+    ctypes construction."""
+    key = tuple((b.data_ptr(), b.numel()) for b in (getattr(t, "_" + n) for n, _ in t._fields))
+    cached = t.__dict__.get("_cdesc")
+    if cached is not None and cached[0] is desc_fn and cached[1] == key:
+        return cached[2]
+    d = desc_fn(t)
+    object.__setattr__(t, "_cdesc", (desc_fn, key, d))
+    return d
+
+
 # ---- result adoption -----------------------------------------------------------------
 
 def _adopt_csr(z: _lib.CsrDesc, device, stream) -> CSR_gpu:
@@ -184,6 +198,20 @@ def _maybe_validate(*operands):
 
 # ---- generic call --------------------------------------------------------------------
 
+_ENTRIES: dict = {}
+
+
+def _entry(name):
+    """The library's entry point `name` (looked up once)."""
+    fn = _ENTRIES.get(name)
+    if fn is None:
+        fn = getattr(_lib.load(), name, None)
+        if fn is None:
+            raise RuntimeError(f"{name} is not exported by {_lib.LIBRARY_PATH.name}")
+        _ENTRIES[name] = fn
+    return fn
+
+
 def _call(entry, a, b, cls, desc_fn, result_desc, adopt_fn, num_blocks, threads_per_block,
           cls_b=None, desc_fn_b=None):
     """One two-operand entry point: a (class `cls`) and b (class `cls_b`, default `cls`)."""
@@ -195,11 +223,8 @@ def _call(entry, a, b, cls, desc_fn, result_desc, adopt_fn, num_blocks, threads_
                             f"got {type(t).__name__}")
     _maybe_validate(a, b)
     device = _same_device(a, b)
-    lib = _lib.load()
-    fn = getattr(lib, entry, None)
-    if fn is None:
-        raise RuntimeError(f"{entry} is not exported by {_lib.LIBRARY_PATH.name}")
-    da, db = desc_fn(a), desc_fn_b(b)
+    fn = _entry(entry)
+    da, db = _cached_desc(a, desc_fn), _cached_desc(b, desc_fn_b)
     z = result_desc()
     with _device.on_device(device):
         stream = _device.current_stream(device)
@@ -222,11 +247,8 @@ def _call3(entry, a, b, c, num_blocks, threads_per_block) -> CSR_gpu:
             raise TypeError(f"{entry}: operand {name} must be CSR_gpu, got {type(t).__name__}")
     _maybe_validate(a, b, c)
     device = _same_device(a, b, c)
-    lib = _lib.load()
-    fn = getattr(lib, entry, None)
-    if fn is None:
-        raise RuntimeError(f"{entry} is not exported by {_lib.LIBRARY_PATH.name}")
-    da, db, dc = _csr_desc(a), _csr_desc(b), _csr_desc(c)
+    fn = _entry(entry)
+    da, db, dc = (_cached_desc(t, _csr_desc) for t in (a, b, c))
     z = _lib.CsrDesc()
     with _device.on_device(device):
         stream = _device.current_stream(device)
