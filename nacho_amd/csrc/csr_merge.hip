@@ -105,6 +105,7 @@ struct RowPairs {
     // (px: the offsets of the operand with fewer entries, whose entries in b's rows bound
     // b's records), whichever needs less scratch.
     int4 *rec;
+    int *rec_row;  // the row of each record (same index as rec)
     const int *px;
     int *blk_base;   // region start per workgroup
     int *blk_elems;  // entries to search per workgroup
@@ -127,7 +128,6 @@ __device__ __forceinline__ void row_pass_block(const int *__restrict__ pa,
     const long long per_block = static_cast<long long>(kPartBlock) * rpt;
     const long long row0 = block * per_block;  // < rows (or 0)
     const int region = rp.px ? rp.px[row0] : static_cast<int>(row0);
-    int4 *out = rp.rec + region;
     int e_base = 0, r_base = 0;  // entries to search and records of the rows before
     // Step j covers rows row0 + j*64 .. +63, one per lane (coalesced), so the records come out
     // in row order from one wave scan per step; kRowUnroll steps' loads are issued together.
@@ -152,9 +152,10 @@ __device__ __forceinline__ void row_pass_block(const int *__restrict__ pa,
             const int r_incl = dev::wave_inclusive_sum(static_cast<int>(rec));
             if (rec) {
                 const bool a_small = la <= lb;
-                out[r_base + r_incl - 1] =
-                    make_int4(e_base + e_incl - e, a_small ? a0[u] : b0[u],
-                              a_small ? b0[u] : a0[u], a_small ? lb : (la | INT_MIN));
+                const int at = region + r_base + r_incl - 1;
+                rp.rec[at] = make_int4(e_base + e_incl - e, a_small ? a0[u] : b0[u],
+                                       a_small ? b0[u] : a0[u], a_small ? lb : (la | INT_MIN));
+                rp.rec_row[at] = static_cast<int>(r);
             }
             e_base += __builtin_amdgcn_readlane(e_incl, dev::kWave - 1);
             r_base += __builtin_amdgcn_readlane(r_incl, dev::kWave - 1);
@@ -881,12 +882,11 @@ __device__ __forceinline__ int stage_row_pass(PairShared &sh, const RowPairs &rp
 // lies in row-pass workgroup b (staged offsets), record k of b (binary search of the
 // records' first entries), and is the smaller side's entry rec.y + (e - first); a lower
 // bound in the larger side tells whether its column is there.  A pair's write chunk is the
-// chunk whose A range holds its A entry (the partition keeps pairs inside one tile).
+// chunk of the tile holding its A entry, merged item a + b + row (the partition keeps pairs
+// inside one tile), so no search over the tile splits is needed.
 __device__ __forceinline__ void pair_search(PairShared &sh, const int *__restrict__ ca,
                                             const int *__restrict__ cb, const RowPairs &rp,
-                                            const int *__restrict__ split_a, int num_tiles,
-                                            int write_chunk, int write_grid,
-                                            unsigned *__restrict__ pair_count,
+                                            int write_chunk, unsigned *__restrict__ pair_count,
                                             unsigned long long *__restrict__ done,
                                             int64_t *__restrict__ length_out, long long items) {
     const int tid = threadIdx.x;
@@ -937,17 +937,12 @@ __device__ __forceinline__ void pair_search(PairShared &sh, const int *__restric
                 }
             }
             if (p < rc.z + l_len && large[p] == x) {
-                const int a_idx = b_small ? p : s_idx;
-                int wlo = 0, whi = write_grid - 1;
-                while (wlo < whi) {
-                    const int mid = (wlo + whi + 1) >> 1;
-                    if (split_a[min(mid * write_chunk, num_tiles)] <= a_idx) {
-                        wlo = mid;
-                    } else {
-                        whi = mid - 1;
-                    }
-                }
-                chunk_id = wlo;
+                // The pair's A entry is merged item a + b + row (A, B and row-end items
+                // before it; ties put A first), and the partition keeps the pair in the
+                // tile holding that item.
+                const int a_idx = b_small ? p : s_idx, b_idx = b_small ? s_idx : p;
+                const int row = rp.rec_row[s_base[lo] + klo];
+                chunk_id = (a_idx + b_idx + row) / kTile / write_chunk;
             }
         }
         // one atomic per distinct write chunk among the wave's pairs
@@ -994,8 +989,7 @@ __global__ __launch_bounds__(kBlock) void csr_pair_count_kernel(
     const int tid = threadIdx.x;
     if (!STARTS && rp.blk_elems != nullptr) {  // after a row pass
         if (stage_row_pass(sh, rp, items) == kModeSearch) {  // uniform
-            pair_search(sh, ca, cb, rp, split_a, num_tiles, write_chunk, write_grid,
-                        chunk_count, done, length_out, items);
+            pair_search(sh, ca, cb, rp, write_chunk, chunk_count, done, length_out, items);
             return;
         }
     }
@@ -1487,9 +1481,10 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
         const long long by_rows = static_cast<long long>(row_grid) * per_block;
         const long long by_entries = std::min<long long>(A.len, B.len);
         rp.px = by_entries < by_rows ? (A.len <= B.len ? A.pos : B.pos) : nullptr;
-        NACHO_TRY(call.scratch_n(static_cast<size_t>(std::max<long long>(
-                                     1, std::min(by_rows, by_entries))),
-                                 &rp.rec));
+        const size_t n_rec =
+            static_cast<size_t>(std::max<long long>(1, std::min(by_rows, by_entries)));
+        NACHO_TRY(call.scratch_n(n_rec, &rp.rec));
+        NACHO_TRY(call.scratch_n(n_rec, &rp.rec_row));
         int *words = nullptr;
         NACHO_TRY(call.scratch_n(3 * static_cast<size_t>(row_grid) + 1, &words));
         rp.blk_base = words;
