@@ -860,9 +860,11 @@ def bench_files(args, device):
 
     mtx: consecutive pairs of the given Matrix Market files (a single file is paired with
     itself), each clipped to a common shape as the reference's matrix sweep does
-    (benchmarks/csr_add.py:57-65), then csr_add and csr_mul.
+    (benchmarks/csr_add.py:57-65), then csr_add, csr_mul and coo_csr_add (the second
+    matrix as COO).
     tns: each FROSTT file as A (sorted, repeats summed) and its shifted copy as B
-    (benchmarks/frostt_tensors_add.py:62-64), then csf_add (CSF3) and coo3d_add (COO3)."""
+    (benchmarks/frostt_tensors_add.py:62-64), then csf_add (CSF3), coo3d_add (COO3),
+    inner_prod (CSF3) and inner_prod_coo (COO3)."""
     import numpy as np
 
     from nacho_amd import io
@@ -893,6 +895,15 @@ def bench_files(args, device):
                 data = f"local Matrix Market files: {names}"
                 lines.append(bench_csr(args, device, "mtx",
                                        prepared=(spec, (a, b), (rows, cols), data)))
+            # the same pair with the right operand as COO (benchmarks/coo_csr_add.py:25-44)
+            spec = dict(WORKLOADS["c2coocsr"])
+            spec["desc"] = (f"coo_csr_add f32 of {names} clipped to {rows}x{cols}, the "
+                            f"second as COO (nnz {len(a[1])} + {len(b[1])})")
+            bi = np.repeat(np.arange(rows, dtype=np.int32), np.diff(np.asarray(b[0])))
+            ops = [((a[0], a[1]), a[2]), ((bi, b[1]), b[2])]
+            lines.append(bench_tuple_workload(args, device, "c2coocsr",
+                                              prepared=(spec, ops, (rows, cols),
+                                                        f"local Matrix Market files: {names}")))
     else:
         for p in paths:
             t0 = time.perf_counter()
@@ -909,7 +920,10 @@ def bench_files(args, device):
                 f"in {time.perf_counter() - t0:.1f}s")
             ops = [(tuple(np.ascontiguousarray(c[0][:, d]) for d in range(3)), c[1])
                    for c in (a, b)]
-            for w, kernel in (("c5", "csf_add"), ("c5coo", "coo3d_add")):
+            # csf_add and coo3d_add (benchmarks/frostt_tensors_add.py), inner_prod and
+            # inner_prod_coo (benchmarks/inner_prod.py) on the same shifted pair
+            for w, kernel in (("c5", "csf_add"), ("c5coo", "coo3d_add"),
+                              ("c5inner", "inner_prod"), ("c5innercoo", "inner_prod_coo")):
                 spec = dict(WORKLOADS[w])
                 spec["desc"] = (f"{kernel} f32 of {p.name} (shape {dims}, nnz {len(a[1])}) "
                                 f"and its copy shifted by one along every mode")
