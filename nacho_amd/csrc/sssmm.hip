@@ -35,6 +35,7 @@
 // one float32 rounding; the structure is exact.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <climits>
 #include <cstdint>
 
@@ -118,11 +119,33 @@ __global__ void zero_int_kernel(int *__restrict__ p, int64_t n) {
     }
 }
 
-__global__ void count_cols_kernel(const int *__restrict__ crd, int64_t n,
-                                  unsigned long long *__restrict__ count) {
-    for (int64_t e = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; e < n;
-         e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        atomicAdd(&count[crd[e]], 1ull);
+// Workgroup b counts the columns of entries [b*kSpan, (b+1)*kSpan): columns below kHotCols in
+// an LDS histogram flushed with one global atomic per nonzero bin (power-law operands put
+// most entries in a few low-numbered hub columns, whose global counters would serialise
+// every entry's atomic), the others with a global atomic each.
+constexpr int kHotCols = 8192;
+constexpr int kSpan = 16 * kBlock;  // entries per workgroup of the two kernels below
+
+__global__ __launch_bounds__(kBlock) void count_cols_kernel(const int *__restrict__ crd,
+                                                            int64_t n, int cols,
+                                                            unsigned long long *__restrict__ count) {
+    __shared__ unsigned hist[kHotCols];
+    const int hot = min(cols, kHotCols);
+    for (int i = threadIdx.x; i < hot; i += kBlock) hist[i] = 0u;
+    __syncthreads();
+    const int64_t lo = static_cast<int64_t>(blockIdx.x) * kSpan;
+    const int64_t hi = min(n, lo + kSpan);
+    for (int64_t e = lo + threadIdx.x; e < hi; e += kBlock) {
+        const int k = crd[e];
+        if (k < hot) {
+            atomicAdd(&hist[k], 1u);
+        } else {
+            atomicAdd(&count[k], 1ull);
+        }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < hot; i += kBlock) {
+        if (hist[i]) atomicAdd(&count[i], static_cast<unsigned long long>(hist[i]));
     }
 }
 
@@ -144,16 +167,37 @@ __global__ void table_sizes_kernel(const int *__restrict__ pos, const int64_t *_
     }
 }
 
+// Workgroup b takes entries [lo, hi) = [b*kSpan, (b+1)*kSpan) of a list split by the offsets
+// p (n + 1 entries); [r_lo, r_hi] holds the rows of its first and last entry and so bounds
+// every entry's row search.  False (for the whole workgroup) when the span is empty.
+__device__ __forceinline__ bool span_rows(const int *__restrict__ p, int n, int64_t nnz,
+                                          int64_t &lo, int64_t &hi, int &r_lo, int &r_hi) {
+    __shared__ int s_rows[2];
+    lo = static_cast<int64_t>(blockIdx.x) * kSpan;
+    hi = min(nnz, lo + kSpan);
+    if (lo >= hi) return false;
+    if (threadIdx.x == 0) {
+        const int first = static_cast<int>(last_le(p, 0, n - 1, lo));
+        s_rows[0] = first;
+        s_rows[1] = static_cast<int>(last_le(p, first, n - 1, hi - 1));
+    }
+    __syncthreads();
+    r_lo = s_rows[0];
+    r_hi = s_rows[1];
+    return true;
+}
+
 // B's entries into columns (CSC) and into the per-column tables keyed by row id.
-__global__ void transpose_kernel(const int *__restrict__ pb, int inner,
-                                 const int *__restrict__ cb, const float *__restrict__ vb,
-                                 int64_t nnz_b, const int64_t *__restrict__ col_off,
-                                 unsigned long long *__restrict__ col_fill,
-                                 const int64_t *__restrict__ tab_off, int *__restrict__ csc_row,
-                                 float *__restrict__ csc_val, uint64_t *__restrict__ tab_b) {
-    for (int64_t e = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; e < nnz_b;
-         e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        const int j = static_cast<int>(last_le(pb, 0, inner - 1, e));
+__global__ __launch_bounds__(kBlock) void transpose_kernel(
+    const int *__restrict__ pb, int inner, const int *__restrict__ cb,
+    const float *__restrict__ vb, int64_t nnz_b, const int64_t *__restrict__ col_off,
+    unsigned long long *__restrict__ col_fill, const int64_t *__restrict__ tab_off,
+    int *__restrict__ csc_row, float *__restrict__ csc_val, uint64_t *__restrict__ tab_b) {
+    int64_t lo, hi;
+    int r_lo, r_hi;
+    if (!span_rows(pb, inner, nnz_b, lo, hi, r_lo, r_hi)) return;
+    for (int64_t e = lo + threadIdx.x; e < hi; e += kBlock) {
+        const int j = static_cast<int>(last_le(pb, r_lo, r_hi, e));
         const int k = cb[e];
         const float v = vb[e];
         const int64_t slot = col_off[k] + static_cast<int64_t>(atomicAdd(&col_fill[k], 1ull));
@@ -166,13 +210,15 @@ __global__ void transpose_kernel(const int *__restrict__ pb, int inner,
 }
 
 // A's entries into the per-row tables keyed by column id.
-__global__ void rows_table_kernel(const int *__restrict__ pa, int rows,
-                                  const int *__restrict__ ca, const float *__restrict__ va,
-                                  int64_t nnz_a, const int64_t *__restrict__ tab_off,
-                                  uint64_t *__restrict__ tab_a) {
-    for (int64_t e = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; e < nnz_a;
-         e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        const int i = static_cast<int>(last_le(pa, 0, rows - 1, e));
+__global__ __launch_bounds__(kBlock) void rows_table_kernel(
+    const int *__restrict__ pa, int rows, const int *__restrict__ ca,
+    const float *__restrict__ va, int64_t nnz_a, const int64_t *__restrict__ tab_off,
+    uint64_t *__restrict__ tab_a) {
+    int64_t lo, hi;
+    int r_lo, r_hi;
+    if (!span_rows(pa, rows, nnz_a, lo, hi, r_lo, r_hi)) return;
+    for (int64_t e = lo + threadIdx.x; e < hi; e += kBlock) {
+        const int i = static_cast<int>(last_le(pa, r_lo, r_hi, e));
         const int64_t size = tab_off[i + 1] - tab_off[i];
         table_insert(tab_a, tab_off[i], static_cast<uint32_t>(size - 1),
                      static_cast<uint32_t>(ca[e]), va[e]);
@@ -394,8 +440,10 @@ int multiply(const nacho_csr *a, const nacho_csr *b, const nacho_csr *c, nacho_c
     NACHO_TRY(call.scratch_n(static_cast<size_t>(rows) + 1, &toff_a));
     zero_kernel<<<grid_for(cols), kBlock, 0, st>>>(col_count, cols);
     zero_kernel<<<grid_for(cols), kBlock, 0, st>>>(col_fill, cols);
-    count_cols_kernel<<<grid_for(nnz_b), kBlock, 0, st>>>(
-        b->dim_j_indices, nnz_b, reinterpret_cast<unsigned long long *>(col_count));
+    const unsigned span_grid =
+        static_cast<unsigned>(std::max<int64_t>(1, (nnz_b + kSpan - 1) / kSpan));
+    count_cols_kernel<<<span_grid, kBlock, 0, st>>>(
+        b->dim_j_indices, nnz_b, cols, reinterpret_cast<unsigned long long *>(col_count));
     NACHO_TRY_HIP(hipGetLastError());
     NACHO_TRY(scan::exclusive_scan_i64(call, col_count, cols, col_off));
     table_sizes_kernel<<<grid_for(cols), kBlock, 0, st>>>(nullptr, col_count, cols, tsize_b);
@@ -427,12 +475,12 @@ int multiply(const nacho_csr *a, const nacho_csr *b, const nacho_csr *c, nacho_c
     NACHO_TRY(call.scratch_n(static_cast<size_t>(nnz_b), &csc_val));
     fill_kernel<<<grid_for(sizes[0]), kBlock, 0, st>>>(tab_b, sizes[0], kEmptySlot);
     fill_kernel<<<grid_for(sizes[1]), kBlock, 0, st>>>(tab_a, sizes[1], kEmptySlot);
-    transpose_kernel<<<grid_for(nnz_b), kBlock, 0, st>>>(
+    transpose_kernel<<<span_grid, kBlock, 0, st>>>(
         b->dim_j_offsets, inner, b->dim_j_indices, b->values, nnz_b, col_off,
         reinterpret_cast<unsigned long long *>(col_fill), toff_b, csc_row, csc_val, tab_b);
-    rows_table_kernel<<<grid_for(nnz_a), kBlock, 0, st>>>(a->dim_j_offsets, rows,
-                                                          a->dim_j_indices, a->values, nnz_a,
-                                                          toff_a, tab_a);
+    rows_table_kernel<<<static_cast<unsigned>(std::max<int64_t>(1, (nnz_a + kSpan - 1) / kSpan)),
+                        kBlock, 0, st>>>(a->dim_j_offsets, rows, a->dim_j_indices, a->values,
+                                         nnz_a, toff_a, tab_a);
     NACHO_TRY_HIP(hipGetLastError());
 
     // probes per mask entry
