@@ -1359,7 +1359,9 @@ int sum_values(Call &call, const float *v, long long n, float *out) {
 
 int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
                 const LevelOperand &A, const LevelOperand &B, const LevelResult &Z,
-                long long *out_len, const char *kernel_name, UnionCount count_plan) {
+                long long *out_len, const char *kernel_name, UnionCount count_plan,
+                bool *length_pending) {
+    if (length_pending) *length_pending = false;
     const long long total = static_cast<long long>(A.len) + B.len + rows;
     if (total > static_cast<long long>(INT_MAX) - 2 * kTile) return NACHO_ERR_INDEX_OVERFLOW;
     const int num_tiles = total > 0 ? static_cast<int>((total + kTile - 1) / kTile) : 1;
@@ -1446,6 +1448,10 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
             tmp_crd, tmp_val, Z.pos, Z.crd, Z.val, len_dev, tmp_row, Z.row);
         NACHO_TRY_HIP(hipGetLastError());
         NACHO_TRY(call.timer_stop());
+        if (length_pending) {
+            *length_pending = true;
+            return NACHO_OK;
+        }
         int64_t len = 0;
         NACHO_TRY(call.wait_length(&len));
         *out_len = len;

@@ -63,10 +63,15 @@ constexpr long long kLevelTileSlack = 4096;
 // (a+b / a*b / copies) when `values`, or with child pointers when `child`.  Writes Z.pos for
 // every row and returns the result length in *out_len.  The call's kernel timer (if enabled)
 // brackets all of the level's kernels under `kernel_name`.
+//
+// With `length_pending` (intersection value levels), the host does not wait for the length:
+// *length_pending is set, *out_len is left alone, and the caller, having queued what it has
+// to on the stream, reads the length with call.wait_length before any other level merge of
+// the call (and collects the level's timer with call.collect_timer before starting another).
 int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
                 const LevelOperand &A, const LevelOperand &B, const LevelResult &Z,
                 long long *out_len, const char *kernel_name,
-                UnionCount count = UnionCount::kAuto);
+                UnionCount count = UnionCount::kAuto, bool *length_pending = nullptr);
 
 // Σ v[0, n) summed in binary64 in a fixed order and rounded once to the device float *out
 // (kernels queued on the call's stream; v may be null when n is 0).

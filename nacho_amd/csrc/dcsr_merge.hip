@@ -77,6 +77,11 @@ __global__ void compact_rows_kernel(const int64_t *__restrict__ keep_off,
     }
 }
 
+// *dst = *src (a count computed on the device, into the call's side word).
+__global__ void store_count_kernel(const int64_t *__restrict__ src, int64_t *__restrict__ dst) {
+    if (threadIdx.x == 0 && blockIdx.x == 0) *dst = *src;
+}
+
 static unsigned grid_for(long long n) {
     return static_cast<unsigned>((n + kBlock - 1) / kBlock > 0 ? (n + kBlock - 1) / kBlock : 1);
 }
@@ -135,18 +140,32 @@ int dcsr_binary(bool intersect, const nacho_dcsr *a, const nacho_dcsr *b, nacho_
     }
     if (nu > cap_i) return NACHO_ERR_MALFORMED_INPUT;
 
-    // j-level row offsets over the union rows
+    // j-level row offsets over the union rows; for a multiply, also the rows kept (present in
+    // both operands), whose count goes to the side word while the j level runs
     const int *ja = ci_a, *jb = ci_b;
+    int64_t *keep_off = nullptr;
     if (intersect) {
         int *ra = nullptr, *rb = nullptr;
+        int64_t *keep = nullptr, *kept_dev = nullptr;
         NACHO_TRY(call.scratch_n(static_cast<size_t>(nu) + 1, &ra));
         NACHO_TRY(call.scratch_n(static_cast<size_t>(nu) + 1, &rb));
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(nu) + 1, &keep));
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(nu) + 1, &keep_off));
+        NACHO_TRY(call.side_word(&kept_dev));
         NACHO_TRY(call.timer_start(name));
         row_offsets_kernel<<<grid_for(nu + 1), kBlock, 0, s>>>(
             ci_a, ci_b, a->dim_j_offsets, b->dim_j_offsets, static_cast<int>(nu), ra, rb);
         NACHO_TRY_HIP(hipGetLastError());
+        if (nu > 0) {
+            both_present_kernel<<<grid_for(nu), kBlock, 0, s>>>(ci_a, ci_b, static_cast<int>(nu),
+                                                                 keep);
+            NACHO_TRY_HIP(hipGetLastError());
+        }
+        NACHO_TRY(scan::exclusive_scan_i64(call, keep, nu, keep_off));
+        store_count_kernel<<<1, 64, 0, s>>>(keep_off + nu, kept_dev);
+        NACHO_TRY_HIP(hipGetLastError());
         NACHO_TRY(call.timer_stop());
-        NACHO_TRY(call.collect_timer());
+        NACHO_TRY(call.collect_timer());  // (kernel timing only) before the j level's interval
         ja = ra;
         jb = rb;
     }
@@ -162,44 +181,43 @@ int dcsr_binary(bool intersect, const nacho_dcsr *a, const nacho_dcsr *b, nacho_
     NACHO_TRY(call.result_n(static_cast<size_t>(cap_j), &crd_j));
     NACHO_TRY(call.result_n(static_cast<size_t>(cap_j), &val));
     long long nj = 0;
+    bool nj_pending = false;  // multiply: the length is read after the rows are queued
     {
         const csr::LevelOperand A{ja, a->dim_j_indices, a->values, a->dim_j_length, nullptr};
         const csr::LevelOperand B{jb, b->dim_j_indices, b->values, b->dim_j_length, nullptr};
         const csr::LevelResult Z{pos_u, crd_j, val, nullptr, nullptr};
         NACHO_TRY(csr::merge_level(call, intersect, true, false, static_cast<int>(nu), A, B, Z,
-                                   &nj, name));
+                                   &nj, name, csr::UnionCount::kAuto,
+                                   intersect ? &nj_pending : nullptr));
     }
-    if (nj > cap_j) return NACHO_ERR_MALFORMED_INPUT;
 
     // rows of the result
     int *crd_i = crd_u, *pos_j = pos_u;
     long long ni = nu;
     if (intersect) {
-        int64_t *keep = nullptr, *keep_off = nullptr;
-        NACHO_TRY(call.scratch_n(static_cast<size_t>(nu) + 1, &keep));
-        NACHO_TRY(call.scratch_n(static_cast<size_t>(nu) + 1, &keep_off));
-        NACHO_TRY(call.timer_start(name));
-        if (nu > 0) {
-            both_present_kernel<<<grid_for(nu), kBlock, 0, s>>>(ci_a, ci_b, static_cast<int>(nu),
-                                                                 keep);
-            NACHO_TRY_HIP(hipGetLastError());
-        }
-        NACHO_TRY(scan::exclusive_scan_i64(call, keep, nu, keep_off));
-        // The kept rows are compacted into arrays sized for all nu rows, so the compaction
-        // follows the scan on the stream without a host round trip; the count is read once,
-        // at the end.
+        // The kept rows are compacted into arrays sized for all nu rows, so nothing waits for
+        // their count; it and the j level's length are read once the j level's write pass has
+        // ended, while its compaction and this one may still run (stream-ordered).
+        NACHO_TRY(call.collect_timer());  // (kernel timing only) the j level's interval
         NACHO_TRY(call.result_n(static_cast<size_t>(nu), &crd_i));
         NACHO_TRY(call.result_n(static_cast<size_t>(nu) + 1, &pos_j));
+        NACHO_TRY(call.timer_start(name));
         compact_rows_kernel<<<grid_for(nu + 1), kBlock, 0, s>>>(keep_off, crd_u, pos_u,
                                                                 static_cast<int>(nu), crd_i,
                                                                 pos_j);
         NACHO_TRY_HIP(hipGetLastError());
         NACHO_TRY(call.timer_stop());
+        if (nj_pending) {
+            int64_t len = 0;
+            NACHO_TRY(call.wait_length(&len));
+            nj = len;
+        }
         int64_t kept = 0;
-        NACHO_TRY(call.read_back(&kept, keep_off + nu, sizeof(kept)));
+        NACHO_TRY(call.side_value(&kept));
         ni = kept;
         NACHO_TRY(call.collect_timer());
     }
+    if (nj > cap_j || ni > nu) return NACHO_ERR_MALFORMED_INPUT;
     if (ni == 0 && crd_i) {
         call.drop_result(crd_i);
         crd_i = nullptr;

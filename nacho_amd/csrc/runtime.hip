@@ -358,12 +358,8 @@ int Call::read_back(void *host, const void *device, size_t bytes) {
     return collect_timer();
 }
 
-int Call::length_word(int64_t **dev) {
-    if (arena_) {  // the kernel that totals the length stores it in the arena
-        NACHO_TRY(scratch_n(1, &arena_len_));
-        *dev = arena_len_;
-        return NACHO_OK;
-    }
+namespace {
+int ensure_len_words() {
     if (!t_len_host) {
         void *h = nullptr;
         NACHO_TRY_HIP(hipHostMalloc(&h, 64, hipHostMallocMapped | hipHostMallocCoherent |
@@ -377,9 +373,42 @@ int Call::length_word(int64_t **dev) {
         t_len_host = static_cast<volatile int64_t *>(h);
         t_len_dev = static_cast<int64_t *>(d);
     }
+    return NACHO_OK;
+}
+}  // namespace
+
+int Call::length_word(int64_t **dev) {
+    if (arena_) {  // the kernel that totals the length stores it in the arena
+        NACHO_TRY(scratch_n(1, &arena_len_));
+        *dev = arena_len_;
+        return NACHO_OK;
+    }
+    NACHO_TRY(ensure_len_words());
     *t_len_host = -1;  // a kernel that did not store would show as an impossible length
     *dev = t_len_dev;
     return NACHO_OK;
+}
+
+int Call::side_word(int64_t **dev) {
+    if (arena_) {
+        NACHO_TRY(scratch_n(1, &arena_side_));
+        *dev = arena_side_;
+        return NACHO_OK;
+    }
+    NACHO_TRY(ensure_len_words());
+    t_len_host[1] = -1;
+    *dev = t_len_dev + 1;
+    return NACHO_OK;
+}
+
+int Call::side_value(int64_t *v) {
+    if (arena_) {
+        if (!arena_side_) return NACHO_ERR_INTERNAL;
+        NACHO_TRY(read_back(v, arena_side_, sizeof(*v)));
+    } else {
+        *v = t_len_host[1];
+    }
+    return *v < 0 ? NACHO_ERR_INTERNAL : NACHO_OK;
 }
 
 int Call::mark_length() {

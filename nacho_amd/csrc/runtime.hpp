@@ -83,6 +83,11 @@ class Call {
     int length_word(int64_t **dev);
     int mark_length();
     int wait_length(int64_t *len);
+    // A second word beside the length, for a count whose kernel runs before the one that
+    // stores the length: read it with side_value once wait_length has returned (the stream
+    // has then passed the store).
+    int side_word(int64_t **dev);
+    int side_value(int64_t *v);
 
     // Kernel timing hook (see nacho_set_kernel_timing): intervals between timer_start and
     // timer_stop are summed over the call and reported when the call ends.  An interval is
@@ -107,6 +112,7 @@ class Call {
     size_t arena_size_ = 0;
     size_t arena_used_ = 0;
     int64_t *arena_len_ = nullptr;
+    int64_t *arena_side_ = nullptr;
     bool timed_ = false;
     float timed_ms_ = 0.0f;  // sum of this call's bracketed intervals
 };
