@@ -250,48 +250,74 @@ __device__ __forceinline__ TileSplit lds_split(const int *s_split, int i) {
                      s_split[3 * i + 3], s_split[3 * i + 4], s_split[3 * i + 5]};
 }
 
-// One lane's share of a tile's inputs, loaded one tile ahead.  Loads are issued
-// unconditionally (lanes past the end re-read the last element) and nothing is computed from
-// them until they are stored to LDS, so a whole tile's loads are in flight at once.
-template <int LOADS>
-struct Staged {
-    int crd[LOADS];
-    int val[LOADS];  // float bits
-    int pa[LOADS];
-    int pb[LOADS];
+// A staged tile in LDS is one word array `s_cr` of n + 1 words, n = na + nb + (r1 - r0)
+// (at most kTile + 1: the pair rule adds one B entry to a tile): A's coordinates at
+// [0, na), B's at [na, na + nb), then the tile's row words s_row = s_cr + na + nb, where
+// s_row[k] = (max(posA[r0+k], a0) - a0) | (max(posB[r0+k], b0) - b0) << 16 for k < nr =
+// r1 - r0 + 1 (s_row[0] is 0: a0 and b0 lie in row r0).  Values, when the level has them, are
+// in s_val at the coordinates' indices.  Entries and rows share the array because a tile's
+// items are its entries plus its row ends: a tile of many short rows holds few entries.
+//
+// Slot k of the n staged words (k >= 1 for rows) is loaded into two registers: A's (or B's)
+// coordinate and value bits, or row r0 + 1 + (k - na - nb)'s two offsets.  Lane `tid` loads
+// slots tid + j * kBlock, j < kSlots, one tile ahead; slot kSlots * kBlock (a tile of
+// kTile + 1 words) is loaded when the tile is staged.
+constexpr int kSlots = kTile / kBlock;
+constexpr int kCap = kTile + 2;  // n + 1 words
+static_assert(kSlots * kBlock == kTile, "a tile is a whole number of slot rounds");
+
+struct Slots {
+    int x[kSlots];  // coordinate, or posA of a row
+    int y[kSlots];  // value bits, or posB of a row
 };
 
-template <bool VALUES, int LOADS>
-__device__ __forceinline__ void fetch_tile(Staged<LOADS> &st, const TileSplit &sp,
-                                           const int *__restrict__ pa, const int *__restrict__ ca,
-                                           const float *__restrict__ va,
-                                           const int *__restrict__ pb, const int *__restrict__ cb,
-                                           const float *__restrict__ vb, int tid) {
-    const int na = sp.a1 - sp.a0, nab = na + (sp.b1 - sp.b0), nr = sp.r1 - sp.r0 + 1;
-    const int *vai = reinterpret_cast<const int *>(va);
-    const int *vbi = reinterpret_cast<const int *>(vb);
-    if (nab > 0) {  // uniform
-#pragma unroll
-        for (int j = 0; j < LOADS; ++j) {
-            const int k = min(tid + j * kBlock, nab - 1);
-            const bool in_a = k < na;
-            const int off = in_a ? sp.a0 + k : sp.b0 + (k - na);
-            st.crd[j] = (in_a ? ca : cb)[off];
-            if (VALUES) st.val[j] = (in_a ? vai : vbi)[off];
-        }
-    }
-#pragma unroll
-    for (int j = 0; j < LOADS; ++j) {
-        const int kr = sp.r0 + min(tid + j * kBlock, nr - 1);
-        st.pa[j] = pa[kr];
-        st.pb[j] = pb[kr];
+// Global addresses of slot k (0 <= k < n) of the tile `sp`: x from px[off], y from py[off].
+__device__ __forceinline__ void slot_source(int k, const TileSplit &sp, int na, int nab,
+                                            const int *__restrict__ pa,
+                                            const int *__restrict__ ca, const int *__restrict__ va,
+                                            const int *__restrict__ pb,
+                                            const int *__restrict__ cb, const int *__restrict__ vb,
+                                            const int *&px, const int *&py, int &off) {
+    if (k < na) {
+        px = ca;
+        py = va;
+        off = sp.a0 + k;
+    } else if (k < nab) {
+        px = cb;
+        py = vb;
+        off = sp.b0 + (k - na);
+    } else {
+        px = pa;
+        py = pb;
+        off = sp.r0 + 1 + (k - nab);
     }
 }
 
-// LDS layout of a staged tile: s_crd = A's crd range then B's; s_val likewise; s_row[k] =
-// (max(posA[r0+k], a0) - a0) | (max(posB[r0+k], b0) - b0) << 16.
-//
-// Row-start bins (when s_bin is given): row k >= 1 of the tile starts at item
+// Loads are issued unconditionally (lanes past the end re-read the last slot) and nothing is
+// computed from them until they are stored to LDS, so a whole tile's loads are in flight at
+// once.  Levels without values load y for row slots only.
+template <bool VALUES>
+__device__ __forceinline__ void fetch_slots(Slots &st, const TileSplit &sp,
+                                            const int *__restrict__ pa, const int *__restrict__ ca,
+                                            const float *__restrict__ va,
+                                            const int *__restrict__ pb, const int *__restrict__ cb,
+                                            const float *__restrict__ vb, int tid) {
+    const int na = sp.a1 - sp.a0, nab = na + (sp.b1 - sp.b0), n = nab + (sp.r1 - sp.r0);
+    if (n == 0) return;  // uniform
+    const int *vai = reinterpret_cast<const int *>(va);
+    const int *vbi = reinterpret_cast<const int *>(vb);
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+        const int k = min(tid + j * kBlock, n - 1);
+        const int *px, *py;
+        int off;
+        slot_source(k, sp, na, nab, pa, ca, vai, pb, cb, vbi, px, py, off);
+        st.x[j] = px[off];
+        if (VALUES || k >= nab) st.y[j] = py[off];
+    }
+}
+
+// Row-start bins (when IPT > 0): row k >= 1 of the tile starts at item
 // x_k = (a0 + b0 + r0 - tile_lo) + ra_k + rb_k + k counted from the tile's lane grid
 // tile_lo = tile * kBlock * IPT, so it is the row of every lane L >= ceil(x_k / IPT) until a
 // later row starts.  It is recorded as atomicMax(s_bin[L], tag << 16 | k) for that first L
@@ -299,34 +325,59 @@ __device__ __forceinline__ void fetch_tile(Staged<LOADS> &st, const TileSplit &s
 // with one workgroup max-scan, replacing a per-lane binary search over the tile's rows.  The
 // tag (distinct per staged tile of a workgroup, increasing) makes stale entries of earlier
 // tiles lose every max and read as "no row", so the bins are never cleared.
-template <bool VALUES, int LOADS, int IPT = 0>
-__device__ __forceinline__ void stage_tile(const Staged<LOADS> &st, const TileSplit &sp,
-                                           int *s_crd, float *s_val, unsigned *s_row, int tid,
-                                           unsigned *s_bin = nullptr, unsigned tag = 0,
-                                           int tile_lo = 0) {
-    const int nab = (sp.a1 - sp.a0) + (sp.b1 - sp.b0), nr = sp.r1 - sp.r0 + 1;
-#pragma unroll
-    for (int j = 0; j < LOADS; ++j) {
-        const int k = tid + j * kBlock;
-        if (k < nab) {
-            s_crd[k] = st.crd[j];
-            if (VALUES) s_val[k] = __int_as_float(st.val[j]);
+template <int IPT>
+__device__ __forceinline__ void stage_slot(int k, int x, int y, const TileSplit &sp, int nab,
+                                           int *s_cr, float *s_val, unsigned *s_bin,
+                                           unsigned tag, int tile_lo) {
+    if (k < nab) {
+        s_cr[k] = x;
+        if (s_val) s_val[k] = __int_as_float(y);
+    } else {
+        const int kr = k - nab + 1;  // tile row
+        const unsigned ra = static_cast<unsigned>(max(x, sp.a0) - sp.a0);
+        const unsigned rb = static_cast<unsigned>(max(y, sp.b0) - sp.b0);
+        s_cr[nab + kr] = static_cast<int>(ra | (rb << 16));
+        if (IPT > 0) {
+            const int xi = (sp.a0 + sp.b0 + sp.r0 - tile_lo) + static_cast<int>(ra + rb) + kr;
+            const int lane = max(1, (xi + IPT - 1) / IPT);
+            if (lane < kBlock) atomicMax(&s_bin[lane], (tag << 16) | static_cast<unsigned>(kr));
         }
-        if (k < nr) {
-            const unsigned ra = static_cast<unsigned>(max(st.pa[j], sp.a0) - sp.a0);
-            const unsigned rb = static_cast<unsigned>(max(st.pb[j], sp.b0) - sp.b0);
-            s_row[k] = ra | (rb << 16);
-            if (IPT > 0 && k > 0) {
-                const int x = (sp.a0 + sp.b0 + sp.r0 - tile_lo) + static_cast<int>(ra + rb) + k;
-                const int lane = max(1, (x + IPT - 1) / IPT);
-                if (lane < kBlock) atomicMax(&s_bin[lane], (tag << 16) | static_cast<unsigned>(k));
-            }
+    }
+}
+
+template <bool VALUES, int IPT = 0>
+__device__ __forceinline__ void stage_slots(const Slots &st, const TileSplit &sp, int *s_cr,
+                                            float *s_val, int tid,
+                                            const int *__restrict__ pa, const int *__restrict__ ca,
+                                            const float *__restrict__ va,
+                                            const int *__restrict__ pb, const int *__restrict__ cb,
+                                            const float *__restrict__ vb,
+                                            unsigned *s_bin = nullptr, unsigned tag = 0,
+                                            int tile_lo = 0) {
+    const int na = sp.a1 - sp.a0, nab = na + (sp.b1 - sp.b0), n = nab + (sp.r1 - sp.r0);
+    float *sv = VALUES ? s_val : nullptr;
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+        const int k = tid + j * kBlock;
+        if (k < n) stage_slot<IPT>(k, st.x[j], st.y[j], sp, nab, s_cr, sv, s_bin, tag, tile_lo);
+    }
+    if (tid == 0) {
+        s_cr[nab] = 0;  // row 0's word
+        if (n > kSlots * kBlock) {  // the tile's last slot (rare): loaded now
+            const int k = kSlots * kBlock;
+            const int *px, *py;
+            int off;
+            slot_source(k, sp, na, nab, pa, ca, reinterpret_cast<const int *>(va), pb, cb,
+                        reinterpret_cast<const int *>(vb), px, py, off);
+            const int x = px[off];
+            const int y = (VALUES || k >= nab) ? py[off] : 0;
+            stage_slot<IPT>(k, x, y, sp, nab, s_cr, sv, s_bin, tag, tile_lo);
         }
     }
 }
 
 // This lane's first row (tile-local) from the row-start bins of the tile staged with `tag`
-// (see stage_tile): the largest row recorded at or before this lane.  Call after the barrier
+// (see stage_slot): the largest row recorded at or before this lane.  Call after the barrier
 // that ends the staging.  No barrier: each wave reads the earlier waves' bins itself (at most
 // three per lane) and takes their maximum along with its own running maximum.
 __device__ __forceinline__ int lane_first_row(const unsigned *s_bin, unsigned tag, int tid) {
@@ -1049,7 +1100,10 @@ __global__ __launch_bounds__(kBlock) void csr_pair_count_kernel(
 // row-start bins and a search inside its row, as the spread intersection does, instead of
 // loading it from `starts`.  When `mode` is non-null and holds kModeSearch, chunk_count
 // holds each chunk's pairs instead of its output count.
-template <Op OP, int IPT, bool VALUES, bool CHILD, bool SPREAD, bool SEARCH = false>
+//
+// ROWS (value levels): rc receives each output's row, staged in LDS beside the outputs.
+template <Op OP, int IPT, bool VALUES, bool CHILD, bool SPREAD, bool SEARCH = false,
+          bool ROWS = false>
 __global__ __launch_bounds__(kBlock) void csr_write_kernel(
     const int *__restrict__ pa, const int *__restrict__ ca, const float *__restrict__ va,
     const int *__restrict__ pb, const int *__restrict__ cb, const float *__restrict__ vb,
@@ -1063,20 +1117,21 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
     int64_t *__restrict__ length_out, const uint2 *__restrict__ starts,
     const int *__restrict__ mode, int *__restrict__ rc, int *__restrict__ ck, int kbits) {
     static_assert(!(VALUES && CHILD), "a level carries values or child pointers, not both");
-    // rc (value levels, optional): each output's row, staged in s_row once the walk is done;
+    static_assert(!(ROWS && !VALUES), "output rows: value levels");
+    static_assert(IPT == kItemsPerLane, "the staged tile is kTile items");
     // ck (value levels, optional): outputs stored split, c >> kbits to cc and the low kbits
     // to ck
     static_assert(!SPREAD || (OP == Op::Intersect && !CHILD), "spread output: intersection");
-    constexpr int kCap = kBlock * IPT + 2;
-    constexpr int kLoads = (kCap + kBlock - 1) / kBlock;
     constexpr int kSteps = IPT + 1;
-    __shared__ int s_crd[kCap];
-    __shared__ float s_val[kCap];
-    __shared__ unsigned s_row[kCap];
+    constexpr int kLoads = (kCap + kBlock - 1) / kBlock;  // outputs per lane in the stores
+    constexpr bool kAux = CHILD || ROWS;  // a third array: outputs' child positions or rows
+    __shared__ int s_cr[kCap];  // coordinates then row words (see slot staging)
+    __shared__ float s_val[VALUES ? kCap : 1];
+    __shared__ unsigned s_aux[kAux ? kCap : 1];
     __shared__ int s_wave[kBlock / dev::kWave];
     __shared__ int s_split[3 * (kMaxChunk + 1)];
     constexpr bool kOwn = SPREAD || SEARCH;  // lanes find their own starts
-    __shared__ unsigned s_bin[kOwn ? kBlock : 1];  // row-start bins (see stage_tile)
+    __shared__ unsigned s_bin[kOwn ? kBlock : 1];  // row-start bins (see stage_slot)
 
     const int tid = threadIdx.x;
     int t0, t1;
@@ -1112,16 +1167,16 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
     if (blockIdx.x == 0 && tid == 0) pc[0] = 0;
 
     TileSplit sp = lds_split(s_split, 0);  // (the exclusive sum above ended with a barrier)
-    Staged<kLoads> st;
-    fetch_tile<VALUES, kLoads>(st, sp, pa, ca, va, pb, cb, vb, tid);
+    Slots st;
+    fetch_slots<VALUES>(st, sp, pa, ca, va, pb, cb, vb, tid);
     // A union's lane starts come from its count kernel (loaded one tile ahead); the spread
     // intersection has no count pass, and the SEARCH union has no stored starts: their lanes
     // take their row from the row-start bins and search only inside it.
     constexpr bool kGiven = !kOwn;
     constexpr Start kMode = kOwn ? Start::RowGiven : Start::Given;
-    constexpr int kBinIpt = kOwn ? IPT : 0;  // stage_tile fills the bins only then
-    stage_tile<VALUES, kLoads, kBinIpt>(st, sp, s_crd, s_val, s_row, tid, s_bin, 1u,
-                                        t0 * kBlock * IPT);
+    constexpr int kBinIpt = kOwn ? IPT : 0;  // stage_slots fills the bins only then
+    stage_slots<VALUES, kBinIpt>(st, sp, s_cr, s_val, tid, pa, ca, va, pb, cb, vb, s_bin, 1u,
+                                 t0 * kBlock * IPT);
     __syncthreads();
     TileSplit nsp = lds_split(s_split, t0 + 1 < t1 ? 1 : 0);
     int64_t spread_sum = 0;
@@ -1133,14 +1188,16 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
         cur = LaneStart{static_cast<unsigned>(lane_first_row(s_bin, 1u, tid)), 0u};
     }
     for (int t = t0; t < t1; ++t) {
-        fetch_tile<VALUES, kLoads>(st, nsp, pa, ca, va, pb, cb, vb, tid);
+        fetch_slots<VALUES>(st, nsp, pa, ca, va, pb, cb, vb, tid);
         if (kGiven && t + 1 < t1) {
             const uint2 v = starts[static_cast<size_t>(t + 1) * kBlock + tid];
             nxt = LaneStart{v.x, v.y};
         }
         const TileSplit nsp2 = lds_split(s_split, t + 2 < t1 ? t + 2 - t0 : t + 1 < t1 ? t + 1 - t0 : t - t0);
         LaneOut<kSteps> lo;
-        walk_lane<OP, VALUES, CHILD, IPT, kMode>(lo, sp, t, s_crd, s_val, s_row, tid, cur);
+        const unsigned *s_row =
+            reinterpret_cast<const unsigned *>(s_cr) + (sp.a1 - sp.a0) + (sp.b1 - sp.b0);
+        walk_lane<OP, VALUES, CHILD, IPT, kMode>(lo, sp, t, s_cr, s_val, s_row, tid, cur);
         if (kGiven) cur = nxt;
         if (SPREAD) base = spread_by_a ? sp.a0 : sp.b0;
 
@@ -1158,25 +1215,25 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
                 ++r;
             }
             if (lo.valid & (1u << s)) {
-                s_crd[o] = lo.crd[s];
+                s_cr[o] = lo.crd[s];
                 if (VALUES) s_val[o] = lo.val[s];
-                if (VALUES && rc) s_row[o] = static_cast<unsigned>(r);
+                if (ROWS) s_aux[o] = static_cast<unsigned>(r);
                 // child pointers: the A / B positions before the output, tile-local, packed;
                 // the pointers themselves are gathered by the coalesced store below
-                if (CHILD) s_row[o] = lo.pos[s];
+                if (CHILD) s_aux[o] = lo.pos[s];
                 ++o;
             }
         }
         __syncthreads();
         // child pointers of this lane's outputs, all gathered before any is stored (lanes past
         // the tile's end repeat its last output; a tile of only empty rows gathers nothing,
-        // since s_row then holds no positions of this tile)
+        // since s_aux then holds no positions of this tile)
         int ga[CHILD ? kLoads : 1], gb[CHILD ? kLoads : 1];
         if (CHILD && tile_total > 0) {
 #pragma unroll
             for (int j = 0; j < kLoads; ++j) {
                 const int q = min(tid + j * kBlock, tile_total - 1);
-                const unsigned pq = s_row[q];
+                const unsigned pq = s_aux[q];
                 const int pa_q = sp.a0 + static_cast<int>(pq & 0xffffu);
                 const int pb_q = sp.b0 + static_cast<int>(pq >> 16);
                 ga[j] = next_a ? next_a[pa_q] : pa_q;
@@ -1188,14 +1245,14 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
             const int q = tid + j * kBlock;
             if (q < tile_total) {
                 if (VALUES && ck) {
-                    const int c = s_crd[q];
+                    const int c = s_cr[q];
                     cc[base + q] = c >> kbits;
                     ck[base + q] = c & ((1 << kbits) - 1);
                 } else {
-                    cc[base + q] = s_crd[q];
+                    cc[base + q] = s_cr[q];
                 }
                 if (VALUES) vc[base + q] = s_val[q];
-                if (VALUES && rc) rc[base + q] = static_cast<int>(s_row[q]);
+                if (ROWS) rc[base + q] = static_cast<int>(s_aux[q]);
                 if (CHILD) {
                     child_a[base + q] = ga[j];
                     child_b[base + q] = gb[j];
@@ -1218,8 +1275,8 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
         __syncthreads();  // staged outputs consumed
         if (t + 1 < t1) {
             const unsigned tag = static_cast<unsigned>(t + 2 - t0);
-            stage_tile<VALUES, kLoads, kBinIpt>(st, nsp, s_crd, s_val, s_row, tid, s_bin, tag,
-                                                (t + 1) * kBlock * IPT);
+            stage_slots<VALUES, kBinIpt>(st, nsp, s_cr, s_val, tid, pa, ca, va, pb, cb, vb,
+                                         s_bin, tag, (t + 1) * kBlock * IPT);
             __syncthreads();
             if (!kGiven) {
                 cur = LaneStart{static_cast<unsigned>(lane_first_row(s_bin, tag, tid)),
@@ -1357,6 +1414,12 @@ int sum_values(Call &call, const float *v, long long n, float *out) {
     return NACHO_OK;
 }
 
+template <Op OP, bool VALUES, bool CHILD, bool SPREAD, bool SEARCH, bool ROWS>
+const void *write_kernel_of() {
+    return reinterpret_cast<const void *>(
+        csr_write_kernel<OP, kItemsPerLane, VALUES, CHILD, SPREAD, SEARCH, ROWS>);
+}
+
 int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
                 const LevelOperand &A, const LevelOperand &B, const LevelResult &Z,
                 long long *out_len, const char *kernel_name, UnionCount count_plan,
@@ -1371,14 +1434,29 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
     NACHO_TRY(call.scratch_n(3 * (static_cast<size_t>(num_tiles) + 1), &splits));
     int *split_r = splits, *split_a = splits + num_tiles + 1, *split_b = splits + 2 * (num_tiles + 1);
 
-    // Grid: as many workgroups as stay resident, each owning a contiguous chunk of tiles.
+    // How a union level counts (see UnionCount): the row pass and the pair search where
+    // rows are long enough, else the tile walk, storing lane starts where the write pass
+    // does not search for them.
+    const long long items = static_cast<long long>(A.len) + B.len;
+    const bool row_pass = !intersect && values && count_plan == UnionCount::kAuto &&
+                          static_cast<long long>(rows) * kRowPassMinEntriesPerRow <= items;
+    const bool keep_starts =
+        !intersect && (!values || (count_plan == UnionCount::kAuto && !row_pass));
+    const bool out_rows = values && Z.row != nullptr;
+    // The write kernel this level launches.
+    const void *write_kernel =
+        intersect ? (out_rows ? write_kernel_of<Op::Intersect, true, false, true, false, true>()
+                              : write_kernel_of<Op::Intersect, true, false, true, false, false>())
+        : !values ? (child ? write_kernel_of<Op::Union, false, true, false, false, false>()
+                           : write_kernel_of<Op::Union, false, false, false, false, false>())
+        : keep_starts ? (out_rows ? write_kernel_of<Op::Union, true, false, false, false, true>()
+                                  : write_kernel_of<Op::Union, true, false, false, false, false>())
+                      : (out_rows ? write_kernel_of<Op::Union, true, false, false, true, true>()
+                                  : write_kernel_of<Op::Union, true, false, false, true, false>());
+    // Grid: as many workgroups of the write kernel as stay resident, each owning a
+    // contiguous chunk of tiles.
     int resident = 0;
-    const void *probe =
-        values ? reinterpret_cast<const void *>(
-                     csr_write_kernel<Op::Union, kItemsPerLane, true, false, false>)
-               : reinterpret_cast<const void *>(
-                     csr_write_kernel<Op::Union, kItemsPerLane, false, true, false>);
-    NACHO_TRY(resident_grid(probe, kBlock, &resident));
+    NACHO_TRY(resident_grid(write_kernel, kBlock, &resident));
     int chunk = (num_tiles + resident - 1) / resident;
     if (chunk > kMaxChunk) chunk = kMaxChunk;  // more workgroups than resident: still correct
     const int grid = (num_tiles + chunk - 1) / chunk;
@@ -1424,12 +1502,19 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
             A.pos, A.crd, B.pos, B.crd, rows, static_cast<int>(total), num_tiles, split_r,
             split_a, split_b, done, nullptr, 0, part_blocks, RowPairs{});
         NACHO_TRY_HIP(hipGetLastError());
-        csr_write_kernel<Op::Intersect, kItemsPerLane, true, false, true>
-            <<<grid, kBlock, 0, s>>>(A.pos, A.crd, A.val, B.pos, B.crd, B.val, A.len, B.len,
-                                     num_tiles, chunk, split_r, split_a, split_b, nullptr, rows,
-                                     pos, tmp_crd, tmp_val, nullptr, nullptr, nullptr,
-                                     nullptr, nullptr, by_a, tile_count, chunk_total, done,
-                                     length_out, nullptr, nullptr, tmp_row, nullptr, 0);
+#define NACHO_SPREAD_LAUNCH(ROWS)                                                             \
+    csr_write_kernel<Op::Intersect, kItemsPerLane, true, false, true, false, ROWS>           \
+        <<<grid, kBlock, 0, s>>>(A.pos, A.crd, A.val, B.pos, B.crd, B.val, A.len, B.len,     \
+                                 num_tiles, chunk, split_r, split_a, split_b, nullptr, rows, \
+                                 pos, tmp_crd, tmp_val, nullptr, nullptr, nullptr, nullptr, \
+                                 nullptr, by_a, tile_count, chunk_total, done, length_out,   \
+                                 nullptr, nullptr, tmp_row, nullptr, 0)
+        if (tmp_row) {
+            NACHO_SPREAD_LAUNCH(true);
+        } else {
+            NACHO_SPREAD_LAUNCH(false);
+        }
+#undef NACHO_SPREAD_LAUNCH
         NACHO_TRY_HIP(hipGetLastError());
         if (Z.dot) {
             dot_tiles_kernel<<<dot_grid, kBlock, 0, s>>>(split_a, split_b, by_a, tile_count,
@@ -1465,11 +1550,6 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
     NACHO_TRY(misalign(A.pos, &mis.pa));
     NACHO_TRY(misalign(B.pos, &mis.pb));
     if (!values && count_plan != UnionCount::kAuto) return NACHO_ERR_INVALID_ARGUMENT;
-    const long long items = static_cast<long long>(A.len) + B.len;
-    const bool row_pass = values && count_plan == UnionCount::kAuto &&
-                          static_cast<long long>(rows) * kRowPassMinEntriesPerRow <= items;
-    // stored lane starts: levels without values, and value levels that skip the row pass
-    const bool keep_starts = !values || (count_plan == UnionCount::kAuto && !row_pass);
     uint2 *starts = nullptr;
     if (keep_starts) NACHO_TRY(call.scratch_n(static_cast<size_t>(num_tiles) * kBlock, &starts));
     RowPairs rp{};
@@ -1525,8 +1605,8 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
     }
     NACHO_TRY_HIP(hipGetLastError());
     NACHO_TRY(call.mark_length());
-#define NACHO_WRITE_LAUNCH(OPV, VAL, CHD, SRCH)                                                  \
-    csr_write_kernel<OPV, kItemsPerLane, VAL, CHD, false, SRCH><<<grid, kBlock, 0, s>>>(         \
+#define NACHO_WRITE_LAUNCH(OPV, VAL, CHD, SRCH, ROWS)                                            \
+    csr_write_kernel<OPV, kItemsPerLane, VAL, CHD, false, SRCH, ROWS><<<grid, kBlock, 0, s>>>(   \
         A.pos, A.crd, A.val, B.pos, B.crd, B.val, A.len, B.len, num_tiles, chunk, split_r,      \
         split_a, split_b, counts, rows, Z.pos, Z.crd, Z.val, A.next, B.next, Z.child_a,         \
         Z.child_b, length, 0, nullptr, nullptr, nullptr, nullptr, starts, rp.mode,             \
@@ -1534,14 +1614,20 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
     if (values) {
         if (child) return NACHO_ERR_INVALID_ARGUMENT;
         if (keep_starts) {
-            NACHO_WRITE_LAUNCH(Op::Union, true, false, false);
+            if (Z.row) {
+                NACHO_WRITE_LAUNCH(Op::Union, true, false, false, true);
+            } else {
+                NACHO_WRITE_LAUNCH(Op::Union, true, false, false, false);
+            }
+        } else if (Z.row) {
+            NACHO_WRITE_LAUNCH(Op::Union, true, false, true, true);
         } else {
-            NACHO_WRITE_LAUNCH(Op::Union, true, false, true);
+            NACHO_WRITE_LAUNCH(Op::Union, true, false, true, false);
         }
     } else if (child) {
-        NACHO_WRITE_LAUNCH(Op::Union, false, true, false);
+        NACHO_WRITE_LAUNCH(Op::Union, false, true, false, false);
     } else {
-        NACHO_WRITE_LAUNCH(Op::Union, false, false, false);
+        NACHO_WRITE_LAUNCH(Op::Union, false, false, false, false);
     }
 #undef NACHO_WRITE_LAUNCH
     NACHO_TRY_HIP(hipGetLastError());
