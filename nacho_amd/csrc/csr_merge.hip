@@ -46,6 +46,7 @@
 #include <climits>
 #include <cstdint>
 #include <mutex>
+#include <type_traits>
 
 #include "csr_merge.hpp"
 #include "device_utils.hpp"
@@ -245,9 +246,10 @@ __device__ __forceinline__ void stage_splits(int *s_split, const int *__restrict
     }
 }
 
+// Every lane reads the same words, so the split is moved to scalar registers.
 __device__ __forceinline__ TileSplit lds_split(const int *s_split, int i) {
-    return TileSplit{s_split[3 * i], s_split[3 * i + 1], s_split[3 * i + 2],
-                     s_split[3 * i + 3], s_split[3 * i + 4], s_split[3 * i + 5]};
+    auto u = [&](int k) { return __builtin_amdgcn_readfirstlane(s_split[3 * i + k]); };
+    return TileSplit{u(0), u(1), u(2), u(3), u(4), u(5)};
 }
 
 // A staged tile in LDS is one word array `s_cr` of n + 1 words, n = na + nb + (r1 - r0)
@@ -1124,10 +1126,13 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
     static_assert(!SPREAD || (OP == Op::Intersect && !CHILD), "spread output: intersection");
     constexpr int kSteps = IPT + 1;
     constexpr int kLoads = (kCap + kBlock - 1) / kBlock;  // outputs per lane in the stores
-    constexpr bool kAux = CHILD || ROWS;  // a third array: outputs' child positions or rows
+    // A third array: the outputs' packed child positions, or their tile-local rows (a tile
+    // stages fewer than 2^16 rows).
+    constexpr bool kAux = CHILD || ROWS;
+    using Aux = typename std::conditional<CHILD, unsigned, unsigned short>::type;
     __shared__ int s_cr[kCap];  // coordinates then row words (see slot staging)
     __shared__ float s_val[VALUES ? kCap : 1];
-    __shared__ unsigned s_aux[kAux ? kCap : 1];
+    __shared__ Aux s_aux[kAux ? kCap : 1];
     __shared__ int s_wave[kBlock / dev::kWave];
     __shared__ int s_split[3 * (kMaxChunk + 1)];
     constexpr bool kOwn = SPREAD || SEARCH;  // lanes find their own starts
@@ -1217,7 +1222,7 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
             if (lo.valid & (1u << s)) {
                 s_cr[o] = lo.crd[s];
                 if (VALUES) s_val[o] = lo.val[s];
-                if (ROWS) s_aux[o] = static_cast<unsigned>(r);
+                if (ROWS) s_aux[o] = static_cast<Aux>(r - sp.r0);
                 // child pointers: the A / B positions before the output, tile-local, packed;
                 // the pointers themselves are gathered by the coalesced store below
                 if (CHILD) s_aux[o] = lo.pos[s];
@@ -1225,37 +1230,44 @@ __global__ __launch_bounds__(kBlock) void csr_write_kernel(
             }
         }
         __syncthreads();
-        // child pointers of this lane's outputs, all gathered before any is stored (lanes past
-        // the tile's end repeat its last output; a tile of only empty rows gathers nothing,
-        // since s_aux then holds no positions of this tile)
-        int ga[CHILD ? kLoads : 1], gb[CHILD ? kLoads : 1];
-        if (CHILD && tile_total > 0) {
+        // Coalesced stores of the staged outputs, in passes of kPass outputs per lane.  Child
+        // pointers of a pass's outputs are all gathered before any is stored (lanes past the
+        // tile's end repeat its last output); a pass of 8 keeps the gathered pointers in 16
+        // registers.
+        constexpr int kPass = CHILD ? 8 : kLoads;
+        const unsigned low_mask = (1u << kbits) - 1u;  // kbits <= 31
 #pragma unroll
-            for (int j = 0; j < kLoads; ++j) {
-                const int q = min(tid + j * kBlock, tile_total - 1);
-                const unsigned pq = s_aux[q];
-                const int pa_q = sp.a0 + static_cast<int>(pq & 0xffffu);
-                const int pb_q = sp.b0 + static_cast<int>(pq >> 16);
-                ga[j] = next_a ? next_a[pa_q] : pa_q;
-                gb[j] = next_b ? next_b[pb_q] : pb_q;
-            }
-        }
+        for (int j0 = 0; j0 < kLoads; j0 += kPass) {
+            if (j0 * kBlock >= tile_total) break;  // uniform
+            int ga[CHILD ? kPass : 1], gb[CHILD ? kPass : 1];
+            if (CHILD) {
 #pragma unroll
-        for (int j = 0; j < kLoads; ++j) {
-            const int q = tid + j * kBlock;
-            if (q < tile_total) {
-                if (VALUES && ck) {
-                    const int c = s_cr[q];
-                    cc[base + q] = c >> kbits;
-                    ck[base + q] = c & ((1 << kbits) - 1);
-                } else {
-                    cc[base + q] = s_cr[q];
+                for (int j = 0; j < kPass; ++j) {
+                    const int q = min(tid + (j0 + j) * kBlock, tile_total - 1);
+                    const unsigned pq = s_aux[q];
+                    const int pa_q = sp.a0 + static_cast<int>(pq & 0xffffu);
+                    const int pb_q = sp.b0 + static_cast<int>(pq >> 16);
+                    ga[j] = next_a ? next_a[pa_q] : pa_q;
+                    gb[j] = next_b ? next_b[pb_q] : pb_q;
                 }
-                if (VALUES) vc[base + q] = s_val[q];
-                if (ROWS) rc[base + q] = static_cast<int>(s_aux[q]);
-                if (CHILD) {
-                    child_a[base + q] = ga[j];
-                    child_b[base + q] = gb[j];
+            }
+#pragma unroll
+            for (int j = 0; j < kPass; ++j) {
+                const int q = tid + (j0 + j) * kBlock;
+                if (q < tile_total) {
+                    if (VALUES && ck) {
+                        const int c = s_cr[q];
+                        cc[base + q] = c >> kbits;
+                        ck[base + q] = static_cast<int>(static_cast<unsigned>(c) & low_mask);
+                    } else {
+                        cc[base + q] = s_cr[q];
+                    }
+                    if (VALUES) vc[base + q] = s_val[q];
+                    if (ROWS) rc[base + q] = sp.r0 + static_cast<int>(s_aux[q]);
+                    if (CHILD) {
+                        child_a[base + q] = ga[j];
+                        child_b[base + q] = gb[j];
+                    }
                 }
             }
         }
