@@ -900,11 +900,13 @@ int coo_csr_add(const nacho_csr *a, const nacho_coo *b, nacho_csr *z, int32_t nb
     return NACHO_OK;
 }
 
-// Releases a buffer that an entry point returned to the caller, on `stream`.
+// Releases a buffer that an entry point returned to the caller, on `stream`, by the rule the
+// call that allocated it followed: an allocator without `allocate` means the library's own
+// allocator, and an allocator without `release` keeps its buffers.
 static void release_result(void *ptr, void *stream, const nacho_allocator *alloc) {
     if (!ptr) return;
-    if (alloc) {
-        alloc->release(alloc->ctx, ptr, stream);
+    if (alloc && alloc->allocate) {
+        if (alloc->release) alloc->release(alloc->ctx, ptr, stream);
     } else {
         (void)nacho_free(ptr, stream);
     }

@@ -406,6 +406,10 @@ int Call::side_value(int64_t *v) {
         if (!arena_side_) return NACHO_ERR_INTERNAL;
         NACHO_TRY(read_back(v, arena_side_, sizeof(*v)));
     } else {
+        // The side word is stored before the kernel that the length event follows, so the
+        // event (this call's, never an earlier call's) orders the read.
+        if (!len_marked_) return NACHO_ERR_INTERNAL;
+        NACHO_TRY_HIP(hipEventSynchronize(t_ev_len));
         *v = t_len_host[1];
     }
     return *v < 0 ? NACHO_ERR_INTERNAL : NACHO_OK;
@@ -415,6 +419,7 @@ int Call::mark_length() {
     if (arena_) return NACHO_OK;  // wait_length synchronises the stream instead
     if (!t_ev_len) NACHO_TRY_HIP(hipEventCreateWithFlags(&t_ev_len, hipEventDisableTiming));
     NACHO_TRY_HIP(hipEventRecord(t_ev_len, stream_));
+    len_marked_ = true;
     return NACHO_OK;
 }
 

@@ -84,8 +84,8 @@ class Call {
     int mark_length();
     int wait_length(int64_t *len);
     // A second word beside the length, for a count whose kernel runs before the one that
-    // stores the length: read it with side_value once wait_length has returned (the stream
-    // has then passed the store).
+    // stores the length: side_value waits for this call's length event (mark_length) and
+    // reads it; without that event it returns NACHO_ERR_INTERNAL.
     int side_word(int64_t **dev);
     int side_value(int64_t *v);
 
@@ -114,6 +114,7 @@ class Call {
     int64_t *arena_len_ = nullptr;
     int64_t *arena_side_ = nullptr;
     bool timed_ = false;
+    bool len_marked_ = false;  // mark_length recorded the length event for this call
     float timed_ms_ = 0.0f;  // sum of this call's bracketed intervals
 };
 

@@ -64,11 +64,13 @@ def test_coo3_random(gpu, seed):
 
 
 @pytest.mark.parametrize("shape", [(7, 2**16, 2**15), (7, 2**16, 2**15 - 1),
-                                   (7, 2**16 + 1, 2**15), (3, 1000, 1), (2**23, 50, 50)])
+                                   (7, 2**16 + 1, 2**15), (3, 1000, 1), (2**23, 50, 50),
+                                   (7, 1, 2**31 - 1), (7, 1, 2**30 + 3)])
 def test_coo3_column_key_bounds(gpu, shape):
     """(j, k) keys of 31 bits whose largest is INT_MAX (the merge's sentinel: packed path)
-    and of 32 bits (packed path), a k extent of one (no k bits: row-offset path), and far
-    more rows than entries (packed path)."""
+    and of 32 bits (packed path), a k extent of one (no k bits: row-offset path), far more
+    rows than entries (packed path), and a j extent of one with k keys of 31 bits (row-offset
+    path; the result's k is the key's low 31 bits)."""
     rng = np.random.default_rng(sum(shape))
     n = 30000
     coords = np.unique(np.stack([rng.integers(0, e, size=n) for e in shape], axis=1), axis=0)

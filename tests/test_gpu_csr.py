@@ -126,6 +126,39 @@ def test_zipf_medium(gpu, op):
     assert_csr_equal(got, oracle.closed_csr_binary(op, rows, rows, *a, *b), "zipf 2^15")
 
 
+@pytest.mark.parametrize("dense_rows", [1024, 96])
+def test_add_sparse_overlap_with_a_dense_block(gpu, dense_rows):
+    """Union whose overlap is sparse overall (the count searches the smaller side of each row
+    present in both operands) except for a block of rows where both operands hold the same
+    64 columns: 1024 such rows (a whole row-pass workgroup dense in pairs) or 96.
+    Bit-exact against the oracle."""
+    from nacho_amd import synth
+
+    rows, cols = 200_000, 1 << 20
+    a = synth.zipf_csr(rows, 21, cols=cols)
+    b = synth.zipf_csr(rows, 22, cols=cols)
+    rng = np.random.default_rng(23)
+
+    def with_dense(t, seed_cols):
+        pos, crd, val = t
+        lengths = np.diff(pos.astype(np.int64))
+        row_cols = [crd[pos[r]:pos[r + 1]] for r in range(rows)]
+        for r in range(4096, 4096 + dense_rows):
+            row_cols[r] = seed_cols
+            lengths[r] = len(seed_cols)
+        new_pos = np.zeros(rows + 1, np.int64)
+        np.cumsum(lengths, out=new_pos[1:])
+        new_crd = np.concatenate(row_cols).astype(np.int32)
+        new_val = rng.uniform(-1, 1, len(new_crd)).astype(np.float32)
+        return new_pos.astype(np.int32), new_crd, new_val
+
+    shared = np.sort(rng.choice(cols, 64, replace=False)).astype(np.int32)
+    a, b = with_dense(a, shared), with_dense(b, shared)
+    got = gpu_op("add", a, b, rows, cols, gpu)
+    assert_csr_equal(got, oracle.closed_csr_binary("add", rows, cols, *a, *b),
+                     f"dense block of {dense_rows} rows")
+
+
 def test_c2_full_size_add(gpu):
     """BASELINE C2 at full size: bit-exact against the oracle, plus invariants."""
     from nacho_amd import synth

@@ -214,3 +214,62 @@ def test_csf_empty_fibres(gpu):
     want = oracle.port_csf3_inner(la, va, lb, vb, nthreads=4)
     scale = float(np.abs(va).max() * np.abs(vb).max()) * min(len(va), len(vb))
     assert abs(got - want) <= 1.2e-7 * abs(want) + 1e-12 * scale, (got, want)
+
+
+@pytest.mark.parametrize("with_release", [True, False])
+def test_wide_keys_coo_through_a_caller_allocator(gpu, with_release):
+    """inner_prod_coo with (j, k) keys wider than 31 bits (the packed-tuple intersection,
+    whose result buffers the entry point frees itself) through the C ABI with a caller
+    allocator: every buffer but the result goes back through `release`, and an allocator
+    without `release` keeps its buffers."""
+    import ctypes
+
+    from nacho_amd import _lib
+
+    lib = _lib.load()
+    rng = np.random.default_rng(15)
+    shape = (50, 1 << 20, 1 << 20)
+    ac, av = random_coords(rng, shape, 20000)
+    bc = ac[rng.random(len(ac)) < 0.5]
+    bv = rng.uniform(-1, 1, len(bc)).astype(np.float32)
+    keep, handed, released = {}, [], []
+
+    @ctypes.CFUNCTYPE(ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p)
+    def allocate(ctx, nbytes, stream):
+        t = torch.empty(int(nbytes), dtype=torch.uint8, device=gpu)
+        keep[t.data_ptr()] = t
+        handed.append(t.data_ptr())
+        return t.data_ptr()
+
+    @ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p)
+    def release(ctx, ptr, stream):
+        released.append(ptr)
+
+    alloc = _lib.Allocator(None, allocate, release) if with_release else \
+        _lib.Allocator(None, allocate, ctypes.cast(None, _lib.Allocator._fields_[2][1]))
+
+    def desc(c, v):
+        cols = [torch.from_numpy(np.ascontiguousarray(c[:, d])).to(gpu) for d in range(3)]
+        vals = torch.from_numpy(v).to(gpu)
+        keep[id(cols[0])] = (cols, vals)
+        n = len(v)
+        return _lib.Coo3Desc(shape[0], shape[1], shape[2], n, cols[0].data_ptr(), n,
+                             cols[1].data_ptr(), n, cols[2].data_ptr(), vals.data_ptr(), n)
+
+    da, db = desc(ac, av), desc(bc, bv)
+    z = _lib.ScalarDesc()
+    stream = torch.cuda.current_stream(gpu).cuda_stream
+    print(f"[gpu] inner_prod_coo wide keys, caller allocator, release={with_release}",
+          flush=True)
+    rc = lib.nacho_gpu_inner_prod_coo_f32(ctypes.byref(da), ctypes.byref(db), ctypes.byref(z),
+                                          256, 256, ctypes.c_void_p(stream),
+                                          ctypes.byref(alloc))
+    assert rc == 0, _lib.error_string(rc)
+    torch.cuda.synchronize()
+    assert z.nnz == 1 and z.values in keep
+    got = float(keep[z.values].view(torch.float32)[:1].cpu().numpy()[0])
+    assert_close(got, want_inner("coo", ac, av, bc, bv), ac, av, bc, bv, "caller allocator")
+    if with_release:
+        assert sorted(released) == sorted(p for p in handed if p != z.values)
+    else:
+        assert not released
