@@ -737,26 +737,35 @@ Kernel &Kernel::recursive_partitioning(bool enabled) {
     return *this;
 }
 
+Emitted emit_declaration(const Declaration &declaration, bool bindings,
+                         const std::string &output_dir) {
+    std::filesystem::create_directories(output_dir);
+    Emitted e = emit_gpu(declaration, output_dir);
+    if (!bindings) {
+        std::filesystem::remove(e.wrapper);
+        e.wrapper.clear();
+    }
+    session().emitted.push_back(e);
+    return e;
+}
+
+void refuse(const std::string &kernel, const std::string &reason) {
+    session().refused.emplace_back(kernel, reason);
+    if (kernel_is_named(kernel)) throw UnsupportedForm(reason);
+}
+
 void Kernel::emit() {
     if (!kernel_is_selected(name_)) return;
     if (std::find(targets_.begin(), targets_.end(), Target::GPU) == targets_.end()) return;
-    Session &s = session();
     try {
         Declaration d = analyse(name_, expr_);
         if (!ordering_.empty()) d.ordering = ordering_;
         d.result_name = result_name_;
         d.python_name = gpu_python_name_;
         d.recursive_partitioning = recursive_partitioning_;
-        std::filesystem::create_directories(s.output_dir);
-        Emitted e = emit_gpu(d, s.output_dir);
-        if (!bindings_) {
-            std::filesystem::remove(e.wrapper);
-            e.wrapper.clear();
-        }
-        s.emitted.push_back(e);
+        emit_declaration(d, bindings_, session().output_dir);
     } catch (const UnsupportedForm &err) {
-        s.refused.emplace_back(name_, err.what());
-        if (kernel_is_named(name_)) throw;
+        refuse(name_, err.what());
     }
 }
 

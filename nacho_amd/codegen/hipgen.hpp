@@ -168,6 +168,15 @@ Emitted emit_gpu(const Declaration &declaration, const std::string &output_dir);
 // Forgets the Python classes recorded by earlier emit_gpu calls.
 void reset_classes();
 
+// emit_gpu into `output_dir` (created if missing), without the wrapper unless `bindings`,
+// recorded in emitted().
+Emitted emit_declaration(const Declaration &declaration, bool bindings,
+                         const std::string &output_dir);
+
+// Records `kernel` as not generated, with `reason`, in refused(); throws UnsupportedForm when
+// the kernel was named by --kernels (a default run lists it and goes on).
+void refuse(const std::string &kernel, const std::string &reason);
+
 // ---- the reference's Kernel builder ------------------------------------------------------
 
 enum class Target { CPU, GPU };
