@@ -272,6 +272,15 @@ __global__ __launch_bounds__(kBlock) void long_hist_kernel(
     }
 }
 
+// B's columns and value bits as one array of pairs, read by the reduce units' gathers.
+__global__ void interleave_kernel(const int *__restrict__ crd_b, const float *__restrict__ val_b,
+                                  int64_t nnz_b, int2 *__restrict__ cv_b) {
+    for (int64_t p = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; p < nnz_b;
+         p += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        cv_b[p] = make_int2(crd_b[p], __float_as_int(val_b[p]));
+    }
+}
+
 // ---- 3b: run descriptors -----------------------------------------------------------------
 
 // A run of products: B entries [x, x + y) times the A value with bits z (w unused).
@@ -380,7 +389,9 @@ __global__ void short_runs_kernel(const int *__restrict__ pos_a, const int *__re
 }
 
 // A unit's products, expanded from its runs desc[r0, r0 + R) (in segment order): run r
-// contributes (crd_b[q], a_r * val_b[q]) for q in [first_r, first_r + length_r), and the unit's
+// contributes (cv_b[q].x, a_r * cv_b[q].y) for q in [first_r, first_r + length_r) (cv_b: B's
+// columns and value bits interleaved, so a lane's consecutive products are one contiguous
+// span of 8-byte pairs), and the unit's
 // products [0, n) are the runs' products concatenated.  Lane t of the BLOCK-thread workgroup
 // receives positions [t * PER, (t + 1) * PER) in kk / vv (positions >= n repeat position
 // n - 1), BLOCK * PER == kTile.  Every run has at least one product, so R <= n <= kTile.
@@ -389,8 +400,7 @@ __global__ void short_runs_kernel(const int *__restrict__ pos_a, const int *__re
 // a_ij * b_jk.
 template <int BLOCK, int PER>
 __device__ __forceinline__ void expand_runs(const int4 *__restrict__ desc, int64_t r0, int R,
-                                            int n, const int *__restrict__ crd_b,
-                                            const float *__restrict__ val_b, int *s_bs,
+                                            int n, const int2 *__restrict__ cv_b, int *s_bs,
                                             float *s_a, int *s_mark, int *s_wave,
                                             int (&kk)[PER], float (&vv)[PER]) {
     static_assert(BLOCK * PER == kTile, "a unit's products are PER per lane");
@@ -436,8 +446,9 @@ __device__ __forceinline__ void expand_runs(const int4 *__restrict__ desc, int64
     if (n > 0) {
 #pragma unroll
         for (int j = 0; j < kPer; ++j) {
-            kk[j] = crd_b[qv[j]];
-            vv[j] = val_b[qv[j]];
+            const int2 e = cv_b[qv[j]];
+            kk[j] = e.x;
+            vv[j] = __int_as_float(e.y);
         }
 #pragma unroll
         for (int j = 0; j < kPer; ++j) vv[j] = av[j] * vv[j];
@@ -721,7 +732,7 @@ __global__ __launch_bounds__(kBlock) void sort_unit_kernel(
     int64_t n_seg, const int64_t *__restrict__ seg_len, const int64_t *__restrict__ seg_off,
     const int *__restrict__ seg_row, const int64_t *__restrict__ row_off, int col_shift,
     const int4 *__restrict__ desc, const int64_t *__restrict__ seg_roff,
-    const int *__restrict__ crd_b, const float *__restrict__ val_b, int *__restrict__ ukey,
+    const int2 *__restrict__ cv_b, int *__restrict__ ukey,
     float *__restrict__ uval, int64_t *__restrict__ unit_nnz, int *__restrict__ row_unit,
     int *__restrict__ row_local) {
     static_assert(sizeof(K) >= sizeof(int), "run starts are staged in s_key");
@@ -742,7 +753,7 @@ __global__ __launch_bounds__(kBlock) void sort_unit_kernel(
         float vv[kPer];
         const int64_t r0 = seg_roff[s0];
         const int R = static_cast<int>(seg_roff[s_end] - r0);
-        expand_runs<kBlock, kPer>(desc, r0, R, n, crd_b, val_b, reinterpret_cast<int *>(s_key),
+        expand_runs<kBlock, kPer>(desc, r0, R, n, cv_b, reinterpret_cast<int *>(s_key),
                                   s_val, s_mark, s_wave, kk, vv);
         const int lo = threadIdx.x * kPer;
 #pragma unroll
@@ -895,8 +906,8 @@ __global__ __launch_bounds__(kBitmapBlock) void bitmap_unit_kernel(
     const int64_t *__restrict__ seg_len, const int64_t *__restrict__ seg_off,
     const int64_t *__restrict__ seg_prefix, const int *__restrict__ seg_row,
     const int64_t *__restrict__ row_off, int shift, const int4 *__restrict__ desc,
-    const int64_t *__restrict__ seg_roff, const int *__restrict__ crd_b,
-    const float *__restrict__ val_b, int *__restrict__ ukey, float *__restrict__ uval,
+    const int64_t *__restrict__ seg_roff, const int2 *__restrict__ cv_b,
+    int *__restrict__ ukey, float *__restrict__ uval,
     int64_t *__restrict__ unit_nnz, int *__restrict__ row_unit, int *__restrict__ row_local) {
     constexpr int kWaves = kBitmapBlock / dev::kWave;
     constexpr int kPerB = kTile / kBitmapBlock;
@@ -934,7 +945,7 @@ __global__ __launch_bounds__(kBitmapBlock) void bitmap_unit_kernel(
         float vv[kPerB];
         const int64_t r0 = seg_roff[s0];
         const int R = static_cast<int>(seg_roff[s1] - r0);
-        expand_runs<kBitmapBlock, kPerB>(desc, r0, R, n, crd_b, val_b, reinterpret_cast<int *>(s_acc),
+        expand_runs<kBitmapBlock, kPerB>(desc, r0, R, n, cv_b, reinterpret_cast<int *>(s_acc),
                     reinterpret_cast<float *>(s_acc) + kTile, reinterpret_cast<int *>(s_pv),
                     s_wave, kk, vv);
         const int lo = threadIdx.x * kPerB;
@@ -1051,7 +1062,7 @@ __global__ __launch_bounds__(kDenseBlock) void dense_unit_kernel(
     const int64_t *__restrict__ seg_len, const int64_t *__restrict__ seg_prefix,
     const int *__restrict__ seg_row, const int64_t *__restrict__ row_off, int shift, int cols,
     const int4 *__restrict__ desc, const int64_t *__restrict__ seg_roff,
-    const int *__restrict__ crd_b, const float *__restrict__ val_b, int *__restrict__ ukey,
+    const int2 *__restrict__ cv_b, int *__restrict__ ukey,
     float *__restrict__ uval, int64_t *__restrict__ unit_nnz, int *__restrict__ row_unit,
     int *__restrict__ row_local) {
     __shared__ double s_acc[kDenseCols];
@@ -1115,8 +1126,9 @@ __global__ __launch_bounds__(kDenseBlock) void dense_unit_kernel(
                 float vv[kDensePer];
 #pragma unroll
                 for (int q = 0; q < kDensePer; ++q) {
-                    kk[q] = crd_b[qv[q]];
-                    vv[q] = val_b[qv[q]];
+                    const int2 e = cv_b[qv[q]];
+                    kk[q] = e.x;
+                    vv[q] = __int_as_float(e.y);
                 }
 #pragma unroll
                 for (int q = 0; q < kDensePer; ++q) {
@@ -1301,6 +1313,11 @@ int multiply(Call &call, const nacho_csr *a, const nacho_csr *b, Product *z) {
         NACHO_TRY_HIP(hipGetLastError());
         run_lengths_kernel<<<grid_for(nnz_b, 256), 256, 0, st>>>(run_idx, nnz_b, run_start, run);
         NACHO_TRY_HIP(hipGetLastError());
+        int2 *cv_b = nullptr;
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(nnz_b), &cv_b));
+        interleave_kernel<<<grid_for(nnz_b, 256), 256, 0, st>>>(b->dim_j_indices, b->values,
+                                                                nnz_b, cv_b);
+        NACHO_TRY_HIP(hipGetLastError());
         int64_t *nblk = nullptr, *blk_off = nullptr;
         int *blk_row = nullptr;
         NACHO_TRY(call.scratch_n(static_cast<size_t>(rows) + 1, &nblk));
@@ -1387,27 +1404,24 @@ int multiply(Call &call, const nacho_csr *a, const nacho_csr *b, Product *z) {
         if (n_kind[1] > 0 && cb + kOrdBits <= 32) {
             sort_unit_kernel<uint32_t><<<static_cast<unsigned>(n_kind[1]), kBlock, 0, st>>>(
                 sort_list, unit_seg, unit_start, n_units, n_seg, seg_len, seg_off, seg_row,
-                row_off, cb, desc, seg_roff, b->dim_j_indices, b->values, ukey, uval, unit_nnz,
-                row_unit, row_local);
+                row_off, cb, desc, seg_roff, cv_b, ukey, uval, unit_nnz, row_unit, row_local);
         } else if (n_kind[1] > 0) {
             sort_unit_kernel<uint64_t><<<static_cast<unsigned>(n_kind[1]), kBlock, 0, st>>>(
                 sort_list, unit_seg, unit_start, n_units, n_seg, seg_len, seg_off, seg_row,
-                row_off, 32, desc, seg_roff, b->dim_j_indices, b->values, ukey, uval, unit_nnz,
-                row_unit, row_local);
+                row_off, 32, desc, seg_roff, cv_b, ukey, uval, unit_nnz, row_unit, row_local);
         }
         NACHO_TRY_HIP(hipGetLastError());
         if (n_kind[2] > 0) {
             bitmap_unit_kernel<<<static_cast<unsigned>(n_kind[2]), kBitmapBlock, 0, st>>>(
                 bitmap_list, unit_seg, unit_start, n_units, n_seg, seg_len, seg_off, seg_prefix,
-                seg_row, row_off, shift, desc, seg_roff, b->dim_j_indices, b->values, ukey,
-                uval, unit_nnz, row_unit, row_local);
+                seg_row, row_off, shift, desc, seg_roff, cv_b, ukey, uval, unit_nnz, row_unit,
+                row_local);
             NACHO_TRY_HIP(hipGetLastError());
         }
         if (n_kind[0] > 0) {
             dense_unit_kernel<<<static_cast<unsigned>(n_kind[0]), kDenseBlock, 0, st>>>(
                 dense_list, unit_seg, unit_start, seg_len, seg_prefix, seg_row, row_off, shift,
-                cols, desc, seg_roff, b->dim_j_indices, b->values, ukey, uval, unit_nnz,
-                row_unit, row_local);
+                cols, desc, seg_roff, cv_b, ukey, uval, unit_nnz, row_unit, row_local);
             NACHO_TRY_HIP(hipGetLastError());
         }
         NACHO_TRY(scan::exclusive_scan_i64(call, unit_nnz, n_units, unit_out));
