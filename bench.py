@@ -53,6 +53,7 @@ counts A and C as CSR and B as COO.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -211,14 +212,83 @@ def make_operands(workload):
 
 
 def traffic_from_profiles(workload, family="csr_merge"):
-    """Measured HBM bytes per launch of the dominant kernel, if profiled (else None)."""
+    """(measured HBM bytes per call of the device pipeline, the commit the counters were
+    taken on) from profiles/, or (None, None) when that workload was not profiled."""
     path = REPO / "profiles" / f"{family}_{workload}_traffic.json"
-    if not path.exists():
-        return None
+    if workload is None or not path.exists():
+        return None, None
     try:
-        return json.loads(path.read_text()).get("hbm_bytes_per_launch")
+        rec = json.loads(path.read_text())
     except (OSError, ValueError):
-        return None
+        return None, None
+    return rec.get("hbm_bytes_per_launch"), rec.get("commit")
+
+
+_COPY_CEILING = {}
+
+
+def copy_ceiling(device):
+    """Device-copy rates on this GPU, measured once per run: the library's streaming copy
+    kernel (nacho_device_copy) and torch's copy_, each moving 1 GiB in and 1 GiB out,
+    10 timed copies after 3 warm-up ones, HIP events on the stream the copies run on."""
+    if _COPY_CEILING:
+        return _COPY_CEILING
+    import torch
+
+    from nacho_amd import _lib
+
+    lib = _lib.load()
+    n = 1 << 28  # 1 GiB of float32
+    src = torch.ones(n, dtype=torch.float32, device=device)
+    dst = torch.empty_like(src)
+    stream = torch.cuda.current_stream(device)
+
+    def rate(copy):
+        for _ in range(3):
+            copy()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(10):
+            copy()
+        stop.record(stream)
+        stop.synchronize()
+        return 10 * 2 * 4 * n / (start.elapsed_time(stop) * 1e-3) / 1e9
+
+    def kernel_copy():
+        rc = lib.nacho_device_copy(ctypes.c_void_p(dst.data_ptr()),
+                                   ctypes.c_void_p(src.data_ptr()), 4 * n,
+                                   ctypes.c_void_p(stream.cuda_stream))
+        if rc != 0:
+            raise RuntimeError(_lib.error_string(rc))
+
+    _COPY_CEILING["kernel_gbs"] = round(rate(kernel_copy), 1)
+    _COPY_CEILING["torch_copy_gbs"] = round(rate(lambda: dst.copy_(src)), 1)
+    del src, dst
+    torch.cuda.empty_cache()
+    log(f"copy ceiling: nacho_device_copy {_COPY_CEILING['kernel_gbs']} GB/s, torch copy_ "
+        f"{_COPY_CEILING['torch_copy_gbs']} GB/s (1 GiB read + 1 GiB written)")
+    return _COPY_CEILING
+
+
+def roofline(device, kernel, achieved, kernel_avg_ms, traffic_key, family):
+    """The line's roofline object: HBM-bound, against the MI355X peak, with the measured
+    copy ceilings and the counter-measured traffic (and its commit) of the workload."""
+    traffic, commit = traffic_from_profiles(traffic_key, family)
+    ceiling = copy_ceiling(device)
+    return {
+        "bound": "hbm",
+        "kernel": kernel,
+        "achieved": round(achieved, 2),
+        "peak": PEAK_HBM_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / PEAK_HBM_GBS, 4),
+        "traffic": traffic,
+        "traffic_commit": commit,
+        "kernel_avg_us": round(kernel_avg_ms * 1e3, 2),
+        "copy_ceiling_gbs": ceiling["kernel_gbs"],
+        "torch_copy_gbs": ceiling["torch_copy_gbs"],
+        "frac_of_copy_ceiling": round(achieved / ceiling["kernel_gbs"], 4),
+    }
 
 
 def cpu_baseline(workload, op, operands, rows, bytes_per_call, budget_s):
@@ -380,16 +450,8 @@ def bench_spgemm(args, device):
             "compulsory_bytes_per_step": compulsory,
             "parallelism": "single GPU",
         },
-        "roofline": {
-            "bound": "hbm",
-            "kernel": spec["kernel"],
-            "achieved": round(achieved, 2),
-            "peak": PEAK_HBM_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": traffic_from_profiles("c4", "spgemm"),
-            "kernel_avg_us": round(kernel_avg_ms * 1e3, 2),
-        },
+        "roofline": roofline(device, spec["kernel"], achieved, kernel_avg_ms, "c4",
+                             "spgemm"),
         "cpu_baseline": cpu,
         "gpu_over_cpu": round(value / cpu["value"], 1) if cpu else None,
     }
@@ -517,16 +579,8 @@ def bench_sssmm(args, device):
             "algorithmic_bytes_per_step": alg_bytes,
             "parallelism": "single GPU",
         },
-        "roofline": {
-            "bound": "hbm",
-            "kernel": spec["kernel"],
-            "achieved": round(achieved, 2),
-            "peak": PEAK_HBM_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": traffic_from_profiles("c4sssmm", "sssmm"),
-            "kernel_avg_us": round(kernel_avg_ms * 1e3, 2),
-        },
+        "roofline": roofline(device, spec["kernel"], achieved, kernel_avg_ms, "c4sssmm",
+                             "sssmm"),
         "cpu_baseline": cpu,
         "gpu_over_cpu": round(value / cpu["value"], 1) if cpu else None,
     }
@@ -732,17 +786,8 @@ def bench_tuple_workload(args, device, workload, prepared=None):
             "percent_of_peak_hbm": round(100.0 * value / PEAK_HBM_GBS, 2),
             "parallelism": "single GPU",
         },
-        "roofline": {
-            "bound": "hbm",
-            "kernel": spec["kernel"],
-            "achieved": round(achieved, 2),
-            "peak": PEAK_HBM_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": traffic_from_profiles(traffic_key, "tuple_merge") if traffic_key
-                       else None,
-            "kernel_avg_us": round(kernel_avg_ms * 1e3, 2),
-        },
+        "roofline": roofline(device, spec["kernel"], achieved, kernel_avg_ms, traffic_key,
+                             "tuple_merge"),
         "cpu_baseline": cpu,
     }
 
@@ -839,16 +884,8 @@ def bench_csr(args, device, workload, prepared=None):
             "percent_of_peak_hbm": round(100.0 * value / PEAK_HBM_GBS, 2),
             "parallelism": "single GPU",
         },
-        "roofline": {
-            "bound": "hbm",
-            "kernel": spec["kernel"],
-            "achieved": round(achieved, 2),
-            "peak": PEAK_HBM_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": traffic_from_profiles(workload),
-            "kernel_avg_us": round(kernel_avg_ms * 1e3, 2),
-        },
+        "roofline": roofline(device, spec["kernel"], achieved, kernel_avg_ms, workload,
+                             "csr_merge"),
         "cpu_baseline": cpu,
     }
     return line
@@ -971,14 +1008,26 @@ def main():
     device = torch.device("cuda:0")
 
     if args.calibrate_copy:
+        # 5 launches of torch's copy_, then 5 of the library's copy kernel, each 1 GiB in and
+        # 1 GiB out: what FETCH_SIZE / WRITE_SIZE read for known bytes
+        from nacho_amd import _lib
+
+        lib = _lib.load()
         n = 1 << 28  # 1 GiB of float32
         src = torch.ones(n, dtype=torch.float32, device=device)
         dst = torch.empty_like(src)
         for _ in range(5):
             dst.copy_(src)
+        stream = torch.cuda.current_stream(device).cuda_stream
+        for _ in range(5):
+            rc = lib.nacho_device_copy(ctypes.c_void_p(dst.data_ptr()),
+                                       ctypes.c_void_p(src.data_ptr()), 4 * n,
+                                       ctypes.c_void_p(stream))
+            if rc != 0:
+                raise RuntimeError(_lib.error_string(rc))
         torch.cuda.synchronize()
         print(json.dumps({"calibration": "copy", "bytes_read": 4 * n, "bytes_written": 4 * n,
-                          "launches": 5}))
+                          "launches": {"torch copy_": 5, "nacho_device_copy": 5}}))
         return
 
     if args.workload in ("mtx", "tns"):

@@ -398,6 +398,12 @@ void nacho_host_free(void *p);
 /* Static string naming an error code (HIP codes use hipGetErrorString). */
 const char *nacho_error_string(int code);
 
+/* Copy `bytes` (a multiple of 16, both pointers 16-byte aligned) from device memory `src`
+ * to `dst` on `stream` with the library's own streaming copy kernel: the bandwidth reference
+ * a roofline measurement states beside the peak.  Returns NACHO_ERR_INVALID_ARGUMENT for
+ * misaligned or null buffers.  No counterpart in the reference. */
+int nacho_device_copy(void *dst, const void *src, size_t bytes, void *stream);
+
 /* Library version string. */
 const char *nacho_version(void);
 

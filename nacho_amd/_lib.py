@@ -234,6 +234,9 @@ def load() -> ctypes.CDLL:
     lib.nacho_cached_bytes.argtypes = []
     lib.nacho_error_string.restype = ctypes.c_char_p
     lib.nacho_error_string.argtypes = [ctypes.c_int]
+    lib.nacho_device_copy.restype = ctypes.c_int
+    lib.nacho_device_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                                      ctypes.c_void_p]
     lib.nacho_version.restype = ctypes.c_char_p
     lib.nacho_version.argtypes = []
     lib.nacho_set_kernel_timing.restype = None

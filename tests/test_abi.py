@@ -93,6 +93,16 @@ def test_invalid_arguments_rejected_without_a_device(lib):
     assert z.dim_j_offsets is None and z.nnz == 0
 
 
+def test_device_copy_rejects_misaligned_buffers_without_a_device(lib):
+    v = ctypes.c_void_p
+    assert lib.nacho_device_copy(v(0x1000), v(0x2000), 0, None) == 0  # nothing to copy
+    assert lib.nacho_device_copy(None, v(0x2000), 32, None) == -1
+    assert lib.nacho_device_copy(v(0x1000), None, 32, None) == -1
+    assert lib.nacho_device_copy(v(0x1004), v(0x2000), 32, None) == -1  # dst misaligned
+    assert lib.nacho_device_copy(v(0x1000), v(0x2008), 32, None) == -1  # src misaligned
+    assert lib.nacho_device_copy(v(0x1000), v(0x2000), 24, None) == -1  # not 16-byte units
+
+
 def test_csr_add_3_arguments_rejected_without_a_device(lib):
     """The fused three-way union checks its third operand like the other two, and refuses
     a total item count past int32 before any allocation."""

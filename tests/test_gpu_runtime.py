@@ -158,3 +158,24 @@ def test_cache_limit_returns_memory_to_the_driver(gpu):
         nacho_amd.set_cache_limit(None)
     nacho_amd.release_cached_memory()
     assert nacho_amd.cached_bytes() == 0
+
+
+@pytest.mark.parametrize("nbytes", [16, 4096 * 16 + 48, (1 << 24) + 16 * 1000])
+def test_device_copy_is_exact(gpu, nbytes):
+    """nacho_device_copy (the bandwidth reference of the roofline) copies every byte and
+    nothing past the end, whole passes and a partial last pass alike."""
+    import ctypes
+
+    from nacho_amd import _lib
+
+    lib = _lib.load()
+    src = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device=gpu)
+    dst = torch.zeros(nbytes + 64, dtype=torch.uint8, device=gpu)
+    stream = torch.cuda.current_stream(gpu).cuda_stream
+    print(f"[gpu] device copy {nbytes} bytes", flush=True)
+    rc = lib.nacho_device_copy(ctypes.c_void_p(dst.data_ptr()), ctypes.c_void_p(src.data_ptr()),
+                               nbytes, ctypes.c_void_p(stream))
+    assert rc == 0, _lib.error_string(rc)
+    torch.cuda.synchronize()
+    assert torch.equal(dst[:nbytes], src)
+    assert not dst[nbytes:].any()
