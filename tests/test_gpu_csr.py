@@ -115,15 +115,21 @@ def test_c1_config(gpu):
     assert_csr_equal(got, oracle.port_csr_binary("add", 4096, *a, *b), "C1")
 
 
-@pytest.mark.parametrize("op", ["add", "mul"])
-def test_zipf_medium(gpu, op):
+@pytest.mark.parametrize("op,partner", [("add", "independent"), ("mul", "overlap"),
+                                        ("add", "overlap")])
+def test_zipf_medium(gpu, op, partner):
+    """Zipf rows (2^15): a union of independent operands (sparse overlap: the count searches
+    the pairs), an intersection, and a union of operands sharing half their entries (dense
+    overlap: the count walks the tiles, each counting workgroup finding its own splits)."""
     from nacho_amd import synth
 
     rows = 1 << 15
     a = synth.zipf_csr(rows, 11)
-    b = synth.zipf_csr(rows, 12) if op == "add" else synth.overlap_partner(a, rows, 13)
+    b = synth.zipf_csr(rows, 12) if partner == "independent" else \
+        synth.overlap_partner(a, rows, 13)
     got = gpu_op(op, a, b, rows, rows, gpu)
-    assert_csr_equal(got, oracle.closed_csr_binary(op, rows, rows, *a, *b), "zipf 2^15")
+    assert_csr_equal(got, oracle.closed_csr_binary(op, rows, rows, *a, *b),
+                     f"zipf 2^15 {op} {partner}")
 
 
 @pytest.mark.parametrize("dense_rows", [1024, 96])
