@@ -120,7 +120,7 @@ __global__ __launch_bounds__(kPartBlock) void coo_partition_kernel(Codec codec, 
                                                             unsigned long long *__restrict__ done) {
     const int t = blockIdx.x * blockDim.x + threadIdx.x;
     if (t > num_tiles) return;
-    if (t == 0) *done = 0ull;  // accumulator of the kernel that totals the length
+    if (t == 0) dev::zero_total(done);  // accumulator of the kernel that totals the length
     const int total = nnz_a + nnz_b;
     const long long d64 = static_cast<long long>(t) * kTile;
     const int diag = d64 > total ? total : static_cast<int>(d64);
@@ -488,7 +488,7 @@ int coo_binary(int arity, const int32_t extents[3], Coords ca, const float *va, 
         int chunk = (num_tiles + resident - 1) / resident;
         if (chunk > kMaxChunk) chunk = kMaxChunk;
         const int grid = (num_tiles + chunk - 1) / chunk;
-        NACHO_TRY(call.scratch_n(static_cast<size_t>(grid) + 6, &counts));
+        NACHO_TRY(call.scratch_n(static_cast<size_t>(grid) + 4 + 2 * dev::kTotalWords, &counts));
         // 64-bit accumulator of the length total (an 8-byte aligned slot after the counts).
     unsigned long long *done =
         reinterpret_cast<unsigned long long *>(counts + ((grid + 2) & ~1));

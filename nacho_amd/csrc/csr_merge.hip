@@ -186,7 +186,7 @@ __global__ __launch_bounds__(kPartBlock) void csr_partition_kernel(
                   kPartLanes;
     if (t > num_tiles) return;  // whole lane groups
     const bool lead = threadIdx.x % kPartLanes == 0;
-    if (lead && t == 0) *done = 0ull;  // accumulator of the kernel that totals the length
+    if (lead && t == 0) dev::zero_total(done);  // accumulator of the kernel that totals the length
     if (lead && t < n_counts) zero_counts[t] = 0u;  // chunk counts the count kernel adds into
     const long long d64 = static_cast<long long>(t) * kTile;
     const int diag = d64 > total ? total : static_cast<int>(d64);
@@ -692,6 +692,28 @@ struct PairShared {
     unsigned wsum[kBlock / dev::kWave];
 };
 
+// LDS of the count kernel's search mode (overlays PairShared).  The M entries to search are
+// cut into slices of kBlock entries inside one row-pass workgroup's entries; a slice's
+// records (at most kBlock: each holds at least one entry) are staged from `rec` before its
+// lanes look up their records.
+constexpr int kStageRecs = 2 * kBlock;
+struct PairSearchLds {
+    int start[kRowPassMaxBlocks + 1];  // entries to search before row-pass workgroup b; [nb] = M
+    int recs[kRowPassMaxBlocks];       // records of workgroup b
+    int base[kRowPassMaxBlocks];       // region start of workgroup b in rec / rec_row
+    int work[kRowPassMaxBlocks + 1];   // slices before workgroup b; [nb] = all slices
+    int4 rec[kStageRecs];              // records k0 .. k0 + kStageRecs - 1 of the slice's workgroup
+    int rec_row[kStageRecs];
+    int last[kBlock / dev::kWave];     // narrowing rounds: last probe <= the slice's first entry
+    int wave[kBlock / dev::kWave];
+    unsigned wsum[kBlock / dev::kWave];
+};
+union PairLds {
+    PairShared walk;
+    PairSearchLds search;
+};
+static_assert(sizeof(PairSearchLds) <= sizeof(PairShared), "search mode fits the walk's LDS");
+
 // Running totals of a pair-count workgroup.
 struct PairTotals {
     unsigned found;    // this lane's pairs since the last flush
@@ -892,38 +914,44 @@ __device__ __forceinline__ void pair_tile(
     __syncthreads();  // every lane is done with this tile's LDS
 }
 
-// The row pass's totals staged in LDS by every count workgroup: s_start[b] = entries to
-// search before workgroup b, s_start[nb] = M.  Returns the mode (the same in every
-// workgroup); workgroup 0 stores it for the write kernel.  Ends synchronised.
-__device__ __forceinline__ int stage_row_pass(PairShared &sh, const RowPairs &rp,
+// The row pass's totals staged in LDS by every count workgroup: sh.start[b] = entries to
+// search before workgroup b (sh.start[nb] = M), its records and region start, and
+// sh.work[b] = slices of kBlock entries before workgroup b.  Returns the mode (the same in
+// every workgroup); workgroup 0 stores it for the write kernel.  Ends synchronised.
+__device__ __forceinline__ int stage_row_pass(PairSearchLds &sh, const RowPairs &rp,
                                               long long items) {
-    static_assert(3 * kRowPassMaxBlocks + 1 <= kGrainCap, "row-pass totals fit the LDS");
     constexpr int kPer = kRowPassMaxBlocks / kBlock;
     const int tid = threadIdx.x;
     const int nb = rp.nb;
-    int *s_start = sh.crd;                            // nb + 1 entries
-    int *s_recs = sh.crd + kRowPassMaxBlocks + 1;      // nb entries
-    int *s_base = sh.crd + 2 * kRowPassMaxBlocks + 1;  // nb entries
-    int v[kPer], sum = 0;
+    int v[kPer], sum = 0, slices = 0;
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
         const int i = tid * kPer + k;
         v[k] = i < nb ? rp.blk_elems[i] : 0;
         sum += v[k];
+        slices += (v[k] + kBlock - 1) / kBlock;
         if (i < nb) {
-            s_recs[i] = rp.blk_recs[i];
-            s_base[i] = rp.blk_base[i];
+            sh.recs[i] = rp.blk_recs[i];
+            sh.base[i] = rp.blk_base[i];
         }
     }
-    int total = 0;
+    int total = 0, all_slices = 0;
     int off = dev::block_exclusive_sum<kBlock>(sum, sh.wave, total);
+    int woff = dev::block_exclusive_sum<kBlock>(slices, sh.wave, all_slices);
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
         const int i = tid * kPer + k;
-        if (i < nb) s_start[i] = off;
+        if (i < nb) {
+            sh.start[i] = off;
+            sh.work[i] = woff;
+        }
         off += v[k];
+        woff += (v[k] + kBlock - 1) / kBlock;
     }
-    if (tid == 0) s_start[nb] = total;
+    if (tid == 0) {
+        sh.start[nb] = total;
+        sh.work[nb] = all_slices;
+    }
     const int mode =
         static_cast<long long>(total) * kSearchRatio <= items ? kModeSearch : kModeCount;
     if (blockIdx.x == 0 && tid == 0) *rp.mode = mode;
@@ -931,50 +959,87 @@ __device__ __forceinline__ int stage_row_pass(PairShared &sh, const RowPairs &rp
     return mode;
 }
 
-// Search mode of the count kernel: a grid-stride loop over the M entries to search.  Entry e
-// lies in row-pass workgroup b (staged offsets), record k of b (binary search of the
-// records' first entries), and is the smaller side's entry rec.y + (e - first); a lower
-// bound in the larger side tells whether its column is there.  A pair's write chunk is the
-// chunk of the tile holding its A entry, merged item a + b + row (the partition keeps pairs
-// inside one tile), so no search over the tile splits is needed.
-__device__ __forceinline__ void pair_search(PairShared &sh, const int *__restrict__ ca,
+// First staged record of a slice whose first entry (within its row-pass workgroup) is
+// `first`, among the workgroup's `n` records at `rec`: a record k0 with the record holding
+// `first` in [k0, k0 + kBlock).  Each round probes kBlock evenly spaced records at once and
+// keeps the span after the last probe at or before `first` (records' first entries
+// increase, and record 0's is 0).  Uniform in the workgroup; ends synchronised.
+__device__ __forceinline__ int first_staged_record(PairSearchLds &sh, const int4 *rec, int n,
+                                                   int first) {
+    const int tid = threadIdx.x;
+    int lo = 0;
+    while (n > kBlock) {  // uniform
+        const int stride = (n + kBlock - 1) / kBlock;
+        const int k = lo + tid * stride;
+        const bool le = k < lo + n && rec[k].x <= first;
+        const unsigned long long m = __ballot(le);
+        if (dev::lane() == 0) sh.last[tid / dev::kWave] = m ? 63 - __clzll(m) + (tid & ~63) : -1;
+        __syncthreads();
+        int t = -1;
+#pragma unroll
+        for (int w = 0; w < kBlock / dev::kWave; ++w) t = max(t, sh.last[w]);
+        __syncthreads();
+        lo += t * stride;  // t >= 0: probe 0 is record lo, at or before `first`
+        n = min(stride, n - t * stride);
+    }
+    return lo;
+}
+
+// Search mode of the count kernel.  Slice w (a grid-stride loop over sh.work[nb] slices) is
+// slice j of row-pass workgroup b: its entries j * kBlock + tid.  The slice's records are
+// staged in LDS; a lane finds its record there (a binary search over the records' first
+// entries), reads its smaller-side entry rec.y + (local - rec.x), and a lower bound in the
+// larger side tells whether its column is there.  A pair's write chunk is the chunk of the
+// tile holding its A entry, merged item a + b + row (the partition keeps pairs inside one
+// tile), so no search over the tile splits is needed.
+__device__ __forceinline__ void pair_search(PairSearchLds &sh, const int *__restrict__ ca,
                                             const int *__restrict__ cb, const RowPairs &rp,
                                             int write_chunk, unsigned *__restrict__ pair_count,
                                             unsigned long long *__restrict__ done,
                                             int64_t *__restrict__ length_out, long long items) {
     const int tid = threadIdx.x;
     const int nb = rp.nb;
-    const int *s_start = sh.crd;  // staged by stage_row_pass
-    const int *s_recs = sh.crd + kRowPassMaxBlocks + 1;
-    const int *s_base = sh.crd + 2 * kRowPassMaxBlocks + 1;
-    const int m_total = s_start[nb];
+    const int slices = sh.work[nb];
     unsigned found = 0;  // pairs seen by this wave (uniform in the wave)
-    for (long long base = static_cast<long long>(blockIdx.x) * kBlock; base < m_total;
-         base += static_cast<long long>(gridDim.x) * kBlock) {
-        const long long e = base + tid;
-        int chunk_id = -1;
-        if (e < m_total) {
-            int lo = 0, hi = nb - 1;
-            while (lo < hi) {
-                const int mid = (lo + hi + 1) >> 1;
-                if (s_start[mid] <= e) {
-                    lo = mid;
-                } else {
-                    hi = mid - 1;
-                }
+    for (int w = blockIdx.x; w < slices; w += gridDim.x) {  // uniform
+        int b = 0, hi = nb - 1;
+        while (b < hi) {
+            const int mid = (b + hi + 1) >> 1;
+            if (sh.work[mid] <= w) {
+                b = mid;
+            } else {
+                hi = mid - 1;
             }
-            const int local = static_cast<int>(e - s_start[lo]);
-            const int4 *recs = rp.rec + s_base[lo];
-            int klo = 0, khi = s_recs[lo] - 1;
+        }
+        const int first = (w - sh.work[b]) * kBlock;
+        const int elems = sh.start[b + 1] - sh.start[b];
+        const int n_rec = sh.recs[b];
+        const int4 *rec = rp.rec + sh.base[b];
+        const int *rec_row = rp.rec_row + sh.base[b];
+        const int k0 = first_staged_record(sh, rec, n_rec, first);
+        const int n_staged = min(kStageRecs, n_rec - k0);
+#pragma unroll
+        for (int i = 0; i < kStageRecs / kBlock; ++i) {
+            const int k = i * kBlock + tid;
+            if (k < n_staged) {
+                sh.rec[k] = rec[k0 + k];
+                sh.rec_row[k] = rec_row[k0 + k];
+            }
+        }
+        __syncthreads();
+        const int local = first + tid;
+        int chunk_id = -1;
+        if (local < elems) {
+            int klo = 0, khi = n_staged - 1;
             while (klo < khi) {
                 const int mid = (klo + khi + 1) >> 1;
-                if (recs[mid].x <= local) {
+                if (sh.rec[mid].x <= local) {
                     klo = mid;
                 } else {
                     khi = mid - 1;
                 }
             }
-            const int4 rc = recs[klo];
+            const int4 rc = sh.rec[klo];
             const bool b_small = rc.w < 0;
             const int l_len = rc.w & INT_MAX;
             const int s_idx = rc.y + (local - rc.x);
@@ -994,8 +1059,7 @@ __device__ __forceinline__ void pair_search(PairShared &sh, const int *__restric
                 // before it; ties put A first), and the partition keeps the pair in the
                 // tile holding that item.
                 const int a_idx = b_small ? p : s_idx, b_idx = b_small ? s_idx : p;
-                const int row = rp.rec_row[s_base[lo] + klo];
-                chunk_id = (a_idx + b_idx + row) / kTile / write_chunk;
+                chunk_id = (a_idx + b_idx + sh.rec_row[klo]) / kTile / write_chunk;
             }
         }
         // one atomic per distinct write chunk among the wave's pairs
@@ -1008,6 +1072,7 @@ __device__ __forceinline__ void pair_search(PairShared &sh, const int *__restric
             if (dev::lane() == leader) atomicAdd(&pair_count[c], static_cast<unsigned>(__popcll(same)));
             pending &= ~same;
         }
+        __syncthreads();  // the staged records are rewritten by the next slice
     }
     if (dev::lane() == 0) sh.wsum[tid / dev::kWave] = found;
     __syncthreads();
@@ -1036,13 +1101,15 @@ __global__ __launch_bounds__(kBlock) void csr_pair_count_kernel(
     const int *__restrict__ split_b, unsigned *__restrict__ chunk_count,
     unsigned long long *__restrict__ done, int64_t *__restrict__ length_out,
     uint2 *__restrict__ starts, RowPairs rp, int write_grid, long long items) {
-    __shared__ PairShared sh;
+    __shared__ PairLds lds;
     __shared__ int s_split[3 * (kMaxChunk + 1)];
+    PairShared &sh = lds.walk;
 
     const int tid = threadIdx.x;
     if (!STARTS && rp.blk_elems != nullptr) {  // after a row pass
-        if (stage_row_pass(sh, rp, items) == kModeSearch) {  // uniform
-            pair_search(sh, ca, cb, rp, write_chunk, chunk_count, done, length_out, items);
+        if (stage_row_pass(lds.search, rp, items) == kModeSearch) {  // uniform
+            pair_search(lds.search, ca, cb, rp, write_chunk, chunk_count, done, length_out,
+                        items);
             return;
         }
     }
@@ -1472,9 +1539,9 @@ int merge_level(Call &call, bool intersect, bool values, bool child, int rows,
     int chunk = (num_tiles + resident - 1) / resident;
     if (chunk > kMaxChunk) chunk = kMaxChunk;  // more workgroups than resident: still correct
     const int grid = (num_tiles + chunk - 1) / chunk;
-    NACHO_TRY(call.scratch_n(static_cast<size_t>(grid) + 6, &counts));
+    NACHO_TRY(call.scratch_n(static_cast<size_t>(grid) + 4 + 2 * dev::kTotalWords, &counts));
     unsigned *length = counts + grid;
-    // 64-bit accumulator of the length total (an 8-byte aligned slot after the counts).
+    // 64-bit accumulator of the length total (8-byte aligned words after the counts).
     unsigned long long *done =
         reinterpret_cast<unsigned long long *>(counts + ((grid + 2) & ~1));
     // The result length goes straight to a pinned host word as soon as the kernel that

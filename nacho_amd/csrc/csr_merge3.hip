@@ -220,7 +220,7 @@ __global__ __launch_bounds__(kPartBlock) void csr3_partition_kernel(
     if (t > num_tiles) return;  // whole lane groups
     const bool lead = threadIdx.x % kPartLanes == 0;
     if (lead && t < n_counts) zero_counts[t] = 0u;
-    if (lead && t == 0) *done = 0ull;
+    if (lead && t == 0) dev::zero_total(done);
     const long long d64 = static_cast<long long>(t) * kTile;
     const int diag = d64 > total ? total : static_cast<int>(d64);
     // largest row r with S(r) <= diag (S(0) = 0)
@@ -842,7 +842,7 @@ int csr_add3_fused(const nacho_csr *a, const nacho_csr *b, const nacho_csr *c, n
     if (chunk > kMaxChunk) chunk = kMaxChunk;
     const int grid = (num_tiles + chunk - 1) / chunk;
     unsigned *counts = nullptr;
-    NACHO_TRY(call.scratch_n(static_cast<size_t>(grid) + 6, &counts));
+    NACHO_TRY(call.scratch_n(static_cast<size_t>(grid) + 4 + 2 * dev::kTotalWords, &counts));
     unsigned long long *done =
         reinterpret_cast<unsigned long long *>(counts + ((grid + 2) & ~1));
     // every lane's start in every tile, from the count kernel's tile walk (count mode)

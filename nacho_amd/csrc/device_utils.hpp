@@ -163,27 +163,53 @@ __device__ __forceinline__ int block_exclusive_max(int v, int *s_wave) {
 
 // ---- device-wide total without a second kernel -------------------------------------
 // Called by thread 0 of every workgroup of a grid with the workgroup's own part (< 2^32).
-// One 64-bit atomic add per workgroup puts a ticket in the high half of `*acc` (zeroed by
-// an earlier kernel on the stream) and the part in the low half; the workgroup whose ticket
-// is the last one sees every other part already added (one address, so the adds are totally
-// ordered) and stores the total to `*out`.  Nothing waits and no fence is needed.  The
+// A 64-bit atomic add puts a ticket in the high half of a counter and the part in the low
+// half; the workgroup whose ticket is the last one on a counter sees every other part on it
+// already added (one address, so the adds are totally ordered).  Atomics on one address are
+// serialised where they are executed (about 13 ns each measured on MI355X: 13.5 us for a
+// launch of 1000 workgroups that only add their part), so the workgroups first add into one
+// of kTotalGroups group counters (workgroup b into group b % kTotalGroups), each in its own
+// 256-byte line, and the last of each group adds the group's sum into the top counter,
+// whose last adder stores the total to `*out`.  Nothing waits and no fence is needed.  The
 // caller guarantees that the total stays below 2^32 (it is a result length < 2^31).
+//
+// The accumulator holds kTotalWords 64-bit words, zeroed by zero_total in an earlier kernel
+// on the stream.
+constexpr int kTotalGroups = 32;
+constexpr int kTotalStride = 32;  // 64-bit words between counters: 256 bytes
+constexpr int kTotalWords = (kTotalGroups + 1) * kTotalStride;
+
+// Zeroes the counters of a total's accumulator (one thread).
+__device__ __forceinline__ void zero_total(unsigned long long *acc) {
+#pragma unroll
+    for (int g = 0; g <= kTotalGroups; ++g) acc[g * kTotalStride] = 0ull;
+}
+
+// The grid's total of `part`, or -1 in every workgroup but the last to add.
+__device__ __forceinline__ int64_t two_level_total(uint32_t part, unsigned long long *acc) {
+    const unsigned groups = gridDim.x < kTotalGroups ? gridDim.x : kTotalGroups;
+    const unsigned g = blockIdx.x % kTotalGroups;
+    const unsigned members = (gridDim.x - g + kTotalGroups - 1) / kTotalGroups;
+    const unsigned long long prev = atomicAdd(&acc[(g + 1) * kTotalStride], (1ull << 32) | part);
+    if ((prev >> 32) != members - 1) return -1;
+    const uint32_t group_sum = static_cast<uint32_t>((prev + part) & 0xffffffffull);
+    const unsigned long long top = atomicAdd(&acc[0], (1ull << 32) | group_sum);
+    if ((top >> 32) != groups - 1) return -1;
+    return static_cast<int64_t>((top + group_sum) & 0xffffffffull);
+}
+
 __device__ __forceinline__ void add_to_total(uint32_t part, unsigned long long *acc,
                                              int64_t *out) {
-    const unsigned long long prev = atomicAdd(acc, (1ull << 32) | part);
-    if ((prev >> 32) == gridDim.x - 1) {
-        *out = static_cast<int64_t>((prev + part) & 0xffffffffull);
-    }
+    const int64_t total = two_level_total(part, acc);
+    if (total >= 0) *out = total;
 }
 
 // The same, storing `from` minus the total (a result length counted as the operands'
 // entries less the pairs that merge).
 __device__ __forceinline__ void subtract_total(uint32_t part, unsigned long long *acc,
                                                int64_t from, int64_t *out) {
-    const unsigned long long prev = atomicAdd(acc, (1ull << 32) | part);
-    if ((prev >> 32) == gridDim.x - 1) {
-        *out = from - static_cast<int64_t>((prev + part) & 0xffffffffull);
-    }
+    const int64_t total = two_level_total(part, acc);
+    if (total >= 0) *out = from - total;
 }
 
 }  // namespace dev

@@ -165,6 +165,32 @@ def test_add_sparse_overlap_with_a_dense_block(gpu, dense_rows):
                      f"dense block of {dense_rows} rows")
 
 
+@pytest.mark.parametrize("rows", [1 << 16, 3 * 1024 + 77])
+def test_add_one_entry_against_twenty(gpu, rows):
+    """Union where every row of A holds one entry and every row of B twenty, half of them
+    holding A's column: the count searches one entry per row, so every row-pass workgroup
+    holds a record per row (1024, more than one slice's worth), and each slice's records
+    are found by narrowing rounds before they are staged.  Bit-exact against the oracle."""
+    rng = np.random.default_rng(31)
+    cols = 1 << 20
+    a_crd = rng.integers(0, cols, rows).astype(np.int32)
+    b_rows = []
+    for r in range(rows):
+        others = rng.choice(cols, 24, replace=False)
+        others = others[others != a_crd[r]][:19 if r % 2 == 0 else 20]
+        row = np.concatenate([others, [a_crd[r]]]) if r % 2 == 0 else others
+        b_rows.append(np.sort(row).astype(np.int32))
+    a = (np.arange(rows + 1, dtype=np.int32), a_crd,
+         rng.uniform(-1, 1, rows).astype(np.float32))
+    b_pos = np.zeros(rows + 1, np.int64)
+    np.cumsum([len(x) for x in b_rows], out=b_pos[1:])
+    b_crd = np.concatenate(b_rows)
+    b = (b_pos.astype(np.int32), b_crd, rng.uniform(-1, 1, len(b_crd)).astype(np.float32))
+    got = gpu_op("add", a, b, rows, cols, gpu)
+    assert_csr_equal(got, oracle.closed_csr_binary("add", rows, cols, *a, *b),
+                     f"one entry against twenty, {rows} rows")
+
+
 def test_c2_full_size_add(gpu):
     """BASELINE C2 at full size: bit-exact against the oracle, plus invariants."""
     from nacho_amd import synth
