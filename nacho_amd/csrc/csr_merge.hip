@@ -86,6 +86,8 @@ constexpr int kPartLanes = 8;
 constexpr int kModeCount = 0;
 constexpr int kModeSearch = 1;
 constexpr int kSearchRatio = 16;
+// Ways of the search mode's lower bounds in the larger side (probes per round + 1).
+constexpr int kSearchWays = 8;
 // Tile mode of the pair count: a tile whose rows need at least this many searches counts its
 // pairs by walking each lane's items instead (about 16 dependent LDS steps per lane against
 // about 14 per search); lower when the lane's start is searched anyway (STARTS).
@@ -1045,14 +1047,23 @@ __device__ __forceinline__ void pair_search(PairSearchLds &sh, const int *__rest
             const int s_idx = rc.y + (local - rc.x);
             const int x = b_small ? cb[s_idx] : ca[s_idx];
             const int *large = b_small ? ca : cb;
+            // Lower bound of x in large[rc.z, rc.z + l_len), kSearchWays - 1 probes per
+            // round: the probes of a round are independent loads (the first round's are
+            // issued with x's), so a row of n entries costs about log_8(n) load latencies
+            // instead of log_2(n).  The answer stays in [p, q].
             int p = rc.z, q = rc.z + l_len;
             while (p < q) {
-                const int mid = (p + q) >> 1;
-                if (large[mid] < x) {
-                    p = mid + 1;
-                } else {
-                    q = mid;
+                const int step = (q - p + kSearchWays - 1) / kSearchWays;
+                int below = 0;  // probes p + j * step - 1 (j >= 1) inside the range with large < x
+#pragma unroll
+                for (int j = 1; j < kSearchWays; ++j) {
+                    const int at = p + j * step - 1;
+                    const int v = large[min(at, q - 1)];
+                    below += (at < q && v < x) ? 1 : 0;
                 }
+                const int np = p + below * step;
+                q = below == kSearchWays - 1 ? q : min(p + (below + 1) * step - 1, q);
+                p = np;
             }
             if (p < rc.z + l_len && large[p] == x) {
                 // The pair's A entry is merged item a + b + row (A, B and row-end items
