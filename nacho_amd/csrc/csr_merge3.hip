@@ -126,6 +126,8 @@ __device__ __forceinline__ void split3(RA A, RB B, RC C, int aS, int aE, int bS,
 constexpr int kModeCount = 0;
 constexpr int kModeSearch = 1;
 constexpr int kSearchRatio = 16;
+// Ways of the search mode's lower bounds (probes per round + 1).
+constexpr int kSearchWays = 8;
 constexpr int kRowPassMaxBlocks = 1024;  // workgroups of the row pass (a multiple of kBlock)
 constexpr int kRowUnroll = 8;  // row steps of the row pass whose loads are issued together
 constexpr int kRowPassMinEntriesPerRow = 8;
@@ -508,18 +510,42 @@ __device__ __forceinline__ int stage_rows3(int *s_start, int *s_recs, int *s_bas
     return mode;
 }
 
-// Whether x is among c[lo, lo + n) (ascending).
+// One round of a lower bound of x in c[p, q) (ascending) with kSearchWays - 1 independent
+// probes: narrows [p, q] (the answer's range) to under a kSearchWays-th of its length.
+__device__ __forceinline__ void lower_bound_round(const int *__restrict__ c, int x, int &p,
+                                                  int &q) {
+    const int step = (q - p + kSearchWays - 1) / kSearchWays;
+    int below = 0;  // probes p + j * step - 1 (j >= 1) inside the range holding less than x
+#pragma unroll
+    for (int j = 1; j < kSearchWays; ++j) {
+        const int at = p + j * step - 1;
+        const int v = c[min(at, q - 1)];
+        below += (at < q && v < x) ? 1 : 0;
+    }
+    const int np = p + below * step;
+    q = below == kSearchWays - 1 ? q : min(p + (below + 1) * step - 1, q);
+    p = np;
+}
+
+// Whether x is among c[lo, lo + n) (ascending), with rounds of independent probes, so that
+// n entries cost about log_8(n) load latencies.
 __device__ __forceinline__ bool holds(const int *__restrict__ c, int lo, int n, int x) {
     int p = lo, q = lo + n;
-    while (p < q) {
-        const int mid = (p + q) >> 1;
-        if (c[mid] < x) {
-            p = mid + 1;
-        } else {
-            q = mid;
-        }
-    }
+    while (p < q) lower_bound_round(c, x, p, q);
     return p < lo + n && c[p] == x;
+}
+
+// holds(c1, lo1, n1, x) and holds(c2, lo2, n2, x), the two searches' rounds issued together.
+__device__ __forceinline__ void holds_both(const int *__restrict__ c1, int lo1, int n1,
+                                           const int *__restrict__ c2, int lo2, int n2, int x,
+                                           bool &in1, bool &in2) {
+    int p1 = lo1, q1 = lo1 + n1, p2 = lo2, q2 = lo2 + n2;
+    while (p1 < q1 || p2 < q2) {
+        if (p1 < q1) lower_bound_round(c1, x, p1, q1);
+        if (p2 < q2) lower_bound_round(c2, x, p2, q2);
+    }
+    in1 = p1 < lo1 + n1 && c1[p1] == x;
+    in2 = p2 < lo2 + n2 && c2[p2] == x;
 }
 
 // Search mode of the count kernel: a grid-stride loop over the M searches.  Search e lies in
@@ -566,14 +592,20 @@ __device__ __forceinline__ void dup_search(const int *s_start, const int *s_recs
             }
             const int local = static_cast<int>(e - s_start[lo]);
             const int4 *recs = rp.rec + 2 * static_cast<long long>(s_base[lo]);
+            // last record whose first search is at or before `local` (record 0's is 0), with
+            // rounds of kSearchWays - 1 independent probes
             int klo = 0, khi = s_recs[lo] - 1;
             while (klo < khi) {
-                const int mid = (klo + khi + 1) >> 1;
-                if (recs[2 * mid].x <= local) {
-                    klo = mid;
-                } else {
-                    khi = mid - 1;
+                const int step = (khi - klo + kSearchWays) / kSearchWays;
+                int at_or_before = 0;
+#pragma unroll
+                for (int j = 1; j < kSearchWays; ++j) {
+                    const int at = klo + j * step;
+                    const int v = recs[2 * min(at, khi)].x;
+                    at_or_before += (at <= khi && v <= local) ? 1 : 0;
                 }
+                khi = min(klo + (at_or_before + 1) * step - 1, khi);
+                klo += at_or_before * step;
             }
             const int4 r0 = recs[2 * klo], r1 = recs[2 * klo + 1];
             const int a0 = r0.y, b0 = r0.z, c0 = r0.w, la = r1.x, lb = r1.y, lc = r1.z;
@@ -596,7 +628,9 @@ __device__ __forceinline__ void dup_search(const int *s_start, const int *s_recs
                 op = 3;
                 pos = c0 + jc;
                 const int x = cc[pos];
-                dup = holds(ca, a0, la, x) || holds(cb, b0, lb, x);
+                bool in_a, in_b;
+                holds_both(ca, a0, la, cb, b0, lb, x, in_a, in_b);
+                dup = in_a || in_b;
             } else if (jc < la) {  // ... by A's entries
                 op = 1;
                 pos = a0 + jc;
@@ -605,7 +639,9 @@ __device__ __forceinline__ void dup_search(const int *s_start, const int *s_recs
                 op = 2;
                 pos = b0 + (jc - la);
                 const int x = cb[pos];
-                dup = holds(cc, c0, lc, x) && !holds(ca, a0, la, x);
+                bool in_c, in_a;
+                holds_both(cc, c0, lc, ca, a0, la, x, in_c, in_a);
+                dup = in_c && !in_a;
             }
             if (dup) {
                 // the write chunk holding it: last w whose first split is at or before pos
