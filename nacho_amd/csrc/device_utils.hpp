@@ -161,6 +161,25 @@ __device__ __forceinline__ int block_exclusive_max(int v, int *s_wave) {
     return excl;
 }
 
+// ---- XCD-aware workgroup order -------------------------------------------------------
+// The dispatcher sends workgroup b to XCD b % kXcds, and each XCD has its own L2.  Kernels
+// whose neighbouring work items share data (a row's units reading adjacent ranges of the
+// same B rows, a mask row's probes into one table) take logical index xcd_block<G>()
+// instead of blockIdx.x: in every run of kXcds * G workgroups, those of one XCD take G
+// consecutive items, so the lines those items share are fetched into one L2, while each
+// XCD still draws its items from every part of the launch.  A bijection on
+// [0, gridDim.x) (a last partial run keeps its order).
+constexpr unsigned kXcds = 8;
+
+template <unsigned G>
+__device__ __forceinline__ unsigned xcd_block() {
+    constexpr unsigned kRun = kXcds * G;
+    const unsigned b = blockIdx.x;
+    const unsigned run = b / kRun, w = b % kRun;
+    if (run >= gridDim.x / kRun) return b;
+    return run * kRun + (w % kXcds) * G + w / kXcds;
+}
+
 // ---- device-wide total without a second kernel -------------------------------------
 // Called by thread 0 of every workgroup of a grid with the workgroup's own part (< 2^32).
 // A 64-bit atomic add puts a ticket in the high half of a counter and the part in the low

@@ -296,9 +296,12 @@ __global__ __launch_bounds__(kBlock) void probe_kernel(
     double *__restrict__ acc, int *__restrict__ hit) {
     __shared__ int s_e[kPadded];
     __shared__ int s_wave[kBlock / dev::kWave];
-    const int64_t c0 = static_cast<int64_t>(blockIdx.x) * kChunk;
+    // neighbouring chunks (a mask row's probes into one table) on one XCD, 64 at a time:
+    // probe_kernel fetched 11% less at C4
+    const int64_t chunk = dev::xcd_block<64>();
+    const int64_t c0 = chunk * kChunk;
     const int n = static_cast<int>(min(static_cast<int64_t>(kChunk), total - c0));
-    const int64_t e_lo = bounds[2 * blockIdx.x], e_hi = bounds[2 * blockIdx.x + 1];
+    const int64_t e_lo = bounds[2 * chunk], e_hi = bounds[2 * chunk + 1];
     // decode: s_e[x] = (mask entry of probe c0 + x) - e_lo
     for (int x = threadIdx.x; x < kChunk; x += kBlock) s_e[pad(x)] = 0;
     __syncthreads();
