@@ -587,10 +587,12 @@ int coo_binary(int arity, const int32_t extents[3], Coords ca, const float *va, 
 // pos[r] = the first entry whose row is >= r, r in [0, rows].  Entry p writes the rows after
 // the previous entry's row up to its own, and the position nnz closes the last rows (row
 // indices clamped to [0, rows]; coordinates must be sorted and in range, as for every
-// operand).  Each thread takes kRowOffsetsPer consecutive entries, read with two 16-byte loads
-// when the array is 16-byte aligned.  (A merge of the row markers with the entries, balanced
-// whatever the gaps between nonempty rows, reloaded one entry per step and was 18x slower.)
-constexpr int kRowOffsetsPer = 8;
+// operand).  Each thread takes kRowOffsetsPer consecutive entries, read with one 16-byte load
+// when the array is 16-byte aligned, so a wavefront's loads cover 1 KB contiguously (eight
+// entries per thread in two 16-byte loads took 49.3 us for the C2 operands as COO, four
+// 44.0 us).  (A merge of the row markers with the entries, balanced whatever the gaps
+// between nonempty rows, reloaded one entry per step and was 18x slower.)
+constexpr int kRowOffsetsPer = 4;
 
 struct RowOffsetsJob {
     const int *ci;
@@ -614,9 +616,7 @@ __global__ void coo_row_offsets_kernel(RowOffsetsJob ja, RowOffsetsJob jb, int b
         int v[kRowOffsetsPer];
         if (aligned && p0 + kRowOffsetsPer <= nnz) {
             const int4 x0 = *reinterpret_cast<const int4 *>(ci + p0);
-            const int4 x1 = *reinterpret_cast<const int4 *>(ci + p0 + 4);
             v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
-            v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
         } else {
 #pragma unroll
             for (int u = 0; u < kRowOffsetsPer; ++u) {
@@ -724,26 +724,19 @@ __global__ void coo3_keys_kernel(KeysJob ja, KeysJob jb, int blocks_a, int rows,
     const bool aligned = ((reinterpret_cast<uintptr_t>(ci) | reinterpret_cast<uintptr_t>(cj) |
                            reinterpret_cast<uintptr_t>(ck) | reinterpret_cast<uintptr_t>(key)) &
                           15u) == 0;
-    static_assert(kRowOffsetsPer == 8, "two 16-byte groups per thread");
+    static_assert(kRowOffsetsPer == 4, "one 16-byte group per thread");
     for (int64_t g = block * blockDim.x + threadIdx.x; g < n_groups; g += blocks * blockDim.x) {
         const int64_t p0 = g * kRowOffsetsPer;
         int v[kRowOffsetsPer], kv[kRowOffsetsPer];
         const int before = p0 == 0 ? -1 : ci[p0 - 1];
         if (aligned && p0 + kRowOffsetsPer <= nnz) {
             const int4 i0 = *reinterpret_cast<const int4 *>(ci + p0);
-            const int4 i1 = *reinterpret_cast<const int4 *>(ci + p0 + 4);
             const int4 j0 = *reinterpret_cast<const int4 *>(cj + p0);
-            const int4 j1 = *reinterpret_cast<const int4 *>(cj + p0 + 4);
             const int4 k0 = *reinterpret_cast<const int4 *>(ck + p0);
-            const int4 k1 = *reinterpret_cast<const int4 *>(ck + p0 + 4);
             v[0] = i0.x; v[1] = i0.y; v[2] = i0.z; v[3] = i0.w;
-            v[4] = i1.x; v[5] = i1.y; v[6] = i1.z; v[7] = i1.w;
             kv[0] = j0.x << kbits | k0.x; kv[1] = j0.y << kbits | k0.y;
             kv[2] = j0.z << kbits | k0.z; kv[3] = j0.w << kbits | k0.w;
-            kv[4] = j1.x << kbits | k1.x; kv[5] = j1.y << kbits | k1.y;
-            kv[6] = j1.z << kbits | k1.z; kv[7] = j1.w << kbits | k1.w;
             *reinterpret_cast<int4 *>(key + p0) = make_int4(kv[0], kv[1], kv[2], kv[3]);
-            *reinterpret_cast<int4 *>(key + p0 + 4) = make_int4(kv[4], kv[5], kv[6], kv[7]);
         } else {
 #pragma unroll
             for (int u = 0; u < kRowOffsetsPer; ++u) {
