@@ -23,6 +23,7 @@
 #include <cstdint>
 
 #include "csr_merge.hpp"
+#include "device_utils.hpp"
 #include "runtime.hpp"
 #include "scan.hpp"
 
@@ -77,9 +78,10 @@ __global__ void compact_rows_kernel(const int64_t *__restrict__ keep_off,
     }
 }
 
-// *dst = *src (a count computed on the device, into the call's side word).
+// *dst = *src (a count computed on the device, into the call's side word, which the host
+// reads from pinned memory while the stream runs on).
 __global__ void store_count_kernel(const int64_t *__restrict__ src, int64_t *__restrict__ dst) {
-    if (threadIdx.x == 0 && blockIdx.x == 0) *dst = *src;
+    if (threadIdx.x == 0 && blockIdx.x == 0) dev::store_system(dst, *src);
 }
 
 static unsigned grid_for(long long n) {

@@ -217,10 +217,16 @@ __device__ __forceinline__ int64_t two_level_total(uint32_t part, unsigned long 
     return static_cast<int64_t>((top + group_sum) & 0xffffffffull);
 }
 
+// Stores a result length with a system-scope release: the host reads it from pinned memory
+// while later kernels of the stream still run.
+__device__ __forceinline__ void store_system(int64_t *out, int64_t v) {
+    __hip_atomic_store(out, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 __device__ __forceinline__ void add_to_total(uint32_t part, unsigned long long *acc,
                                              int64_t *out) {
     const int64_t total = two_level_total(part, acc);
-    if (total >= 0) *out = total;
+    if (total >= 0) store_system(out, total);
 }
 
 // The same, storing `from` minus the total (a result length counted as the operands'
@@ -228,7 +234,7 @@ __device__ __forceinline__ void add_to_total(uint32_t part, unsigned long long *
 __device__ __forceinline__ void subtract_total(uint32_t part, unsigned long long *acc,
                                                int64_t from, int64_t *out) {
     const int64_t total = two_level_total(part, acc);
-    if (total >= 0) *out = from - total;
+    if (total >= 0) store_system(out, from - total);
 }
 
 }  // namespace dev

@@ -3,6 +3,7 @@
 #include "runtime.hpp"
 
 #include <atomic>
+#include <chrono>
 #include <climits>
 #include <cstdint>
 #include <cstring>
@@ -260,11 +261,10 @@ thread_local const char *t_last_name = "";
 // Pinned host word for length readbacks, one per host thread.
 thread_local void *t_pinned = nullptr;
 
-// Coherent pinned word that kernels store a length into (early readback), its device
-// address, and the event marking the kernel that stores it; one of each per host thread.
+// Coherent pinned words that kernels store a length and a side count into (early readback)
+// and their device address; one pair per host thread.
 thread_local volatile int64_t *t_len_host = nullptr;
 thread_local int64_t *t_len_dev = nullptr;
-thread_local hipEvent_t t_ev_len = nullptr;
 
 }  // namespace
 
@@ -401,25 +401,57 @@ int Call::side_word(int64_t **dev) {
     return NACHO_OK;
 }
 
+namespace {
+// Waits until the device has stored a value >= 0 into the pinned word `w` (set to -1 before
+// the launch; kernels store it with a system-scope release).  Nothing is enqueued on the
+// stream for the wait: an event recorded after the kernel that stores the word, or a
+// stream query while the pipeline runs, each held the next dispatch back by about 6 us on
+// MI355X.  Only after kStreamCheckAfter of waiting is the stream checked now and then, so
+// that a stream that failed, or that finished without storing the word, ends the wait.
+constexpr auto kStreamCheckAfter = std::chrono::milliseconds(20);
+
+int spin_for_word(volatile int64_t *w, hipStream_t stream, int64_t *out) {
+    const auto begin = std::chrono::steady_clock::now();
+    bool check = false;
+    for (unsigned i = 1;; ++i) {
+        const int64_t v = *w;
+        if (v >= 0) {
+            std::atomic_thread_fence(std::memory_order_acquire);
+            *out = v;
+            return NACHO_OK;
+        }
+        if ((i & 4095u) != 0) continue;
+        if (!check) {
+            check = std::chrono::steady_clock::now() - begin >= kStreamCheckAfter;
+        } else {
+            const hipError_t e = hipStreamQuery(stream);
+            if (e == hipSuccess) {  // every kernel of the stream ended: the word is final
+                const int64_t last = *w;
+                if (last < 0) return NACHO_ERR_INTERNAL;
+                *out = last;
+                return NACHO_OK;
+            }
+            if (e != hipErrorNotReady) return static_cast<int>(e);
+        }
+    }
+}
+}  // namespace
+
 int Call::side_value(int64_t *v) {
     if (arena_) {
         if (!arena_side_) return NACHO_ERR_INTERNAL;
         NACHO_TRY(read_back(v, arena_side_, sizeof(*v)));
     } else {
-        // The side word is stored before the kernel that the length event follows, so the
-        // event (this call's, never an earlier call's) orders the read.
+        // The side word is stored (system scope) by a kernel of this call before the one
+        // that stores the length; it is waited for in the same way.
         if (!len_marked_) return NACHO_ERR_INTERNAL;
-        NACHO_TRY_HIP(hipEventSynchronize(t_ev_len));
-        *v = t_len_host[1];
+        NACHO_TRY(spin_for_word(t_len_host + 1, stream_, v));
     }
     return *v < 0 ? NACHO_ERR_INTERNAL : NACHO_OK;
 }
 
 int Call::mark_length() {
-    if (arena_) return NACHO_OK;  // wait_length synchronises the stream instead
-    if (!t_ev_len) NACHO_TRY_HIP(hipEventCreateWithFlags(&t_ev_len, hipEventDisableTiming));
-    NACHO_TRY_HIP(hipEventRecord(t_ev_len, stream_));
-    len_marked_ = true;
+    len_marked_ = true;  // wait_length spins on the pinned word (or synchronises, arena)
     return NACHO_OK;
 }
 
@@ -432,9 +464,8 @@ int Call::wait_length(int64_t *len) {
         *len = v;
         return NACHO_OK;
     }
-    NACHO_TRY_HIP(hipEventSynchronize(t_ev_len));
-    *len = *t_len_host;
-    if (*len < 0) return NACHO_ERR_INTERNAL;
+    if (!len_marked_) return NACHO_ERR_INTERNAL;
+    NACHO_TRY(spin_for_word(t_len_host, stream_, len));
     return collect_timer();
 }
 

@@ -74,18 +74,19 @@ class Call {
     // Copy `bytes` from device to a host variable and wait for the stream.
     int read_back(void *host, const void *device, size_t bytes);
 
-    // Early length readback.  A kernel stores a result length straight into this host
-    // thread's pinned, device-visible word (`*dev` receives its device address); the host
-    // records an event right after that kernel (mark_length), keeps launching the rest of
-    // the pipeline, and wait_length waits only for the event, so the call returns while
-    // the remaining kernels still run, stream-ordered, like the reference's generated entry
-    // point, which returns after launching its write pass.
+    // Early length readback.  A kernel stores a result length (system scope) straight into
+    // this host thread's pinned, device-visible word (`*dev` receives its device address;
+    // the word reads -1 until then); the host marks that the kernel is launched
+    // (mark_length), keeps launching the rest of the pipeline, and wait_length waits only
+    // for the word, so the call returns while the remaining kernels still run,
+    // stream-ordered, like the reference's generated entry point, which returns after
+    // launching its write pass.
     int length_word(int64_t **dev);
     int mark_length();
     int wait_length(int64_t *len);
     // A second word beside the length, for a count whose kernel runs before the one that
-    // stores the length: side_value waits for this call's length event (mark_length) and
-    // reads it; without that event it returns NACHO_ERR_INTERNAL.
+    // stores the length: side_value waits for it in the same way, after mark_length;
+    // without mark_length it returns NACHO_ERR_INTERNAL.
     int side_word(int64_t **dev);
     int side_value(int64_t *v);
 
@@ -114,7 +115,7 @@ class Call {
     int64_t *arena_len_ = nullptr;
     int64_t *arena_side_ = nullptr;
     bool timed_ = false;
-    bool len_marked_ = false;  // mark_length recorded the length event for this call
+    bool len_marked_ = false;  // mark_length: this call launched the kernel storing its length
     float timed_ms_ = 0.0f;  // sum of this call's bracketed intervals
 };
 
