@@ -94,7 +94,7 @@ constexpr int kSearchWays = 8;
 constexpr int kWalkMin = 2 * kBlock;
 constexpr int kWalkMinStarts = kBlock;
 constexpr int kRowPassMaxBlocks = 1024;  // workgroups of the row pass (a multiple of kBlock)
-constexpr int kRowUnroll = 8;  // row steps of the row pass whose loads are issued together
+constexpr int kRowUnroll = 16;  // row steps of the row pass whose loads are issued together
 // The row pass reads two offsets per row, so it runs only where rows hold this many entries
 // on average: with about one entry per row (a CSF3 k level) its reads cost as much as the
 // tile walk it may save, and the few entries per row make the walk's lane starts cheap.
