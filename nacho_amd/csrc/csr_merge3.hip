@@ -341,6 +341,78 @@ __device__ __forceinline__ void stage3(const Staged3 &st, const Split3 &sp, int 
     }
 }
 
+// Write-kernel staging in one word sequence per array: slot k < n is entry k (A's, then
+// B's, then C's: coordinate in s_crd, value in s_val), slot n + k is row r0 + k (s_crd: A's
+// and B's tile-local starts packed A | B << 16; s_val, as int bits: C's tile-local start).
+// A tile's entries and row ends are at most kTile + 2 items, so n + nr <= kCap.  Lane tid
+// loads slots tid + j * kBlock (clamped to the last, consumed only when staged), three
+// registers a slot: the rows' third offset is loaded only where a wave holds rows.
+struct Slots3 {
+    int x[kLoads];  // coordinate, or posA of a row
+    int y[kLoads];  // value bits, or posB of a row
+    int z[kLoads];  // posC of a row
+};
+
+__device__ __forceinline__ void fetch_slots3(Slots3 &st, const Split3 &sp,
+                                             const int *__restrict__ pa,
+                                             const int *__restrict__ ca,
+                                             const float *__restrict__ va,
+                                             const int *__restrict__ pb,
+                                             const int *__restrict__ cb,
+                                             const float *__restrict__ vb,
+                                             const int *__restrict__ pc,
+                                             const int *__restrict__ cc,
+                                             const float *__restrict__ vc, int tid) {
+    const int na = sp.a1 - sp.a0, nab = na + (sp.b1 - sp.b0);
+    const int n = nab + (sp.c1 - sp.c0), total = n + (sp.r1 - sp.r0 + 1);
+#pragma unroll
+    for (int j = 0; j < kLoads; ++j) {
+        const int k = min(tid + j * kBlock, total - 1);
+        const int *px;
+        const int *py;
+        int off;
+        if (k < na) {
+            px = ca;
+            py = reinterpret_cast<const int *>(va);
+            off = sp.a0 + k;
+        } else if (k < nab) {
+            px = cb;
+            py = reinterpret_cast<const int *>(vb);
+            off = sp.b0 + (k - na);
+        } else if (k < n) {
+            px = cc;
+            py = reinterpret_cast<const int *>(vc);
+            off = sp.c0 + (k - nab);
+        } else {
+            px = pa;
+            py = pb;
+            off = sp.r0 + (k - n);
+        }
+        st.x[j] = px[off];
+        st.y[j] = py[off];
+        st.z[j] = k >= n ? pc[off] : 0;
+    }
+}
+
+__device__ __forceinline__ void stage_slots3(const Slots3 &st, const Split3 &sp, int *s_crd,
+                                             float *s_val, int tid) {
+    const int n = (sp.a1 - sp.a0) + (sp.b1 - sp.b0) + (sp.c1 - sp.c0);
+    const int total = n + (sp.r1 - sp.r0 + 1);
+#pragma unroll
+    for (int j = 0; j < kLoads; ++j) {
+        const int k = tid + j * kBlock;
+        if (k < n) {
+            s_crd[k] = st.x[j];
+            s_val[k] = __int_as_float(st.y[j]);
+        } else if (k < total) {
+            const unsigned ra = static_cast<unsigned>(max(st.x[j], sp.a0) - sp.a0);
+            const unsigned rb = static_cast<unsigned>(max(st.y[j], sp.b0) - sp.b0);
+            s_crd[k] = static_cast<int>(ra | (rb << 16));
+            s_val[k] = __int_as_float(max(st.z[j], sp.c0) - sp.c0);
+        }
+    }
+}
+
 // ---- one lane's walk ----------------------------------------------------------------------
 
 struct Lane3Out {
@@ -765,13 +837,20 @@ __global__ __launch_bounds__(kBlock) void csr3_write_kernel(
     const int *__restrict__ mode) {
     __shared__ int s_crd[kCap];
     __shared__ float s_val[kCap];
-    __shared__ unsigned s_row[kCap];
-    __shared__ int s_rowc[kCap];
     __shared__ int s_wave[kBlock / dev::kWave];
     __shared__ int s_split[4 * (kMaxChunk + 1)];
     const int tid = threadIdx.x;
     const int t0 = blockIdx.x * chunk, t1 = min(t0 + chunk, num_tiles);
     if (t0 >= t1) return;
+    // the staged rows follow the staged entries (stage_slots3)
+    auto rows_a = [&](const Split3 &q) {
+        const int n = (q.a1 - q.a0) + (q.b1 - q.b0) + (q.c1 - q.c0);
+        return reinterpret_cast<const unsigned *>(s_crd + n);
+    };
+    auto rows_c = [&](const Split3 &q) {
+        const int n = (q.a1 - q.a0) + (q.b1 - q.b0) + (q.c1 - q.c0);
+        return reinterpret_cast<const int *>(s_val + n);
+    };
     // search mode (see dup_search): chunk_count holds duplicates, and lanes search their starts
     const bool search = mode != nullptr && *mode == kModeSearch;
     stage_splits3(s_split, split, t0, t1);
@@ -783,20 +862,20 @@ __global__ __launch_bounds__(kBlock) void csr3_write_kernel(
     if (search) base = s_split[1] + s_split[2] + s_split[3] - base;
     if (blockIdx.x == 0 && tid == 0) pz[0] = 0;
     Split3 sp = lds_split3(s_split, 0);
-    Staged3 st;
+    Slots3 st;
     uint2 start = search ? make_uint2(0u, 0u) : starts[static_cast<size_t>(t0) * kBlock + tid];
-    fetch3<true>(st, sp, pa, ca, va, pb, cb, vb, pc, cc, vc, tid);
-    stage3<true>(st, sp, s_crd, s_val, s_row, s_rowc, tid);
+    fetch_slots3(st, sp, pa, ca, va, pb, cb, vb, pc, cc, vc, tid);
+    stage_slots3(st, sp, s_crd, s_val, tid);
     __syncthreads();
     for (int t = t0; t < t1; ++t) {
         const Split3 nsp = lds_split3(s_split, t + 1 < t1 ? t + 1 - t0 : t - t0);
         uint2 next_start = start;
         if (t + 1 < t1) {
-            fetch3<true>(st, nsp, pa, ca, va, pb, cb, vb, pc, cc, vc, tid);
+            fetch_slots3(st, nsp, pa, ca, va, pb, cb, vb, pc, cc, vc, tid);
             if (!search) next_start = starts[static_cast<size_t>(t + 1) * kBlock + tid];
         }
         Lane3Out lo;
-        walk3<true, false>(lo, sp, t, s_crd, s_val, s_row, s_rowc, tid, start, !search);
+        walk3<true, false>(lo, sp, t, s_crd, s_val, rows_a(sp), rows_c(sp), tid, start, !search);
         int tile_total = 0;
         const int offset = dev::block_exclusive_sum<kBlock>(lo.count, s_wave, tile_total);
         // (the scan's barriers also mean every lane is done reading this tile's inputs)
@@ -826,7 +905,7 @@ __global__ __launch_bounds__(kBlock) void csr3_write_kernel(
         base += tile_total;
         __syncthreads();  // staged outputs consumed
         if (t + 1 < t1) {
-            stage3<true>(st, nsp, s_crd, s_val, s_row, s_rowc, tid);
+            stage_slots3(st, nsp, s_crd, s_val, tid);
             __syncthreads();
         }
         sp = nsp;
