@@ -228,9 +228,12 @@ int nacho_gpu_csr_add_f32(const nacho_csr *a, const nacho_csr *b, nacho_csr *z,
  *   - Scratch is a static device array of 8 MiB per GPU (held until the process ends),
  *     enough for a->dim_j_length + b->dim_j_length + dim_i_size <= NACHO_NOALLOC_MAX_ITEMS;
  *     larger inputs fail with NACHO_ERR_SCRATCH_TOO_SMALL before any device work.
- *   - Every call on a GPU shares that GPU's scratch: calls that overlap on one GPU (other
- *     host threads, or other streams still running) race and must be serialised by the
- *     caller.
+ *   - Every call on a GPU shares that GPU's scratch, so calls on one GPU take turns: a
+ *     call holds a per-GPU lock from its first launch until its kernels have finished
+ *     (it synchronises `stream` before returning, also on failure), so calls from other
+ *     host threads wait, and no kernel of a returned call still reads the scratch when
+ *     the next call, on any stream, starts.  The scratch keeps the last call's contents;
+ *     each call clears what must start at zero.
  *   - The call synchronises `stream` to read the result length back. */
 #define NACHO_NOALLOC_MAX_ITEMS 250000000LL
 int nacho_gpu_csr_add_f32_noalloc(const nacho_csr *a, const nacho_csr *b, nacho_csr *z,

@@ -1802,23 +1802,37 @@ static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
 constexpr int kMaxDevices = 64;
 
-// Device address of `scratch` on the current device, looked up on the first call there.
-int scratch_address(void **out) {
-    static std::mutex mutex;
-    static void *address[kMaxDevices] = {};
+// One GPU's `scratch`: its device address (looked up on the first call there) and the lock
+// that one call holds from its first launch until its last kernel has finished.
+struct ScratchSlot {
+    std::mutex busy;
+    void *address = nullptr;
+};
+
+int scratch_slot(ScratchSlot **out) {
+    static std::mutex lookup;
+    static ScratchSlot slots[kMaxDevices];
     int device = 0;
     NACHO_TRY_HIP(hipGetDevice(&device));
     if (device < 0 || device >= kMaxDevices) return NACHO_ERR_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lock(mutex);
-    if (!address[device]) {
+    std::lock_guard<std::mutex> lock(lookup);
+    ScratchSlot &slot = slots[device];
+    if (!slot.address) {
         void *p = nullptr;
         NACHO_TRY_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
         if (!p) return NACHO_ERR_INTERNAL;
-        address[device] = p;
+        slot.address = p;
     }
-    *out = address[device];
+    *out = &slot;
     return NACHO_OK;
 }
+
+// Waits for the stream when the call leaves, on every exit path, so that no kernel of the
+// call still reads `scratch` once the slot's lock is released.
+struct StreamDrain {
+    hipStream_t stream;
+    ~StreamDrain() { (void)hipStreamSynchronize(stream); }
+};
 
 int csr_add_noalloc(const nacho_csr *a, const nacho_csr *b, nacho_csr *z, int32_t num_blocks,
                     int32_t threads_per_block, void *stream) {
@@ -1842,9 +1856,13 @@ int csr_add_noalloc(const nacho_csr *a, const nacho_csr *b, nacho_csr *z, int32_
     }
     if (items > NACHO_NOALLOC_MAX_ITEMS) return NACHO_ERR_SCRATCH_TOO_SMALL;
     if (merge_level_arena_bytes(items) > kNoAllocScratchBytes) return NACHO_ERR_INTERNAL;
-    void *arena = nullptr;
-    NACHO_TRY(scratch_address(&arena));
-    Call call(stream, arena, kNoAllocScratchBytes);
+    ScratchSlot *slot = nullptr;
+    NACHO_TRY(scratch_slot(&slot));
+    // Calls on one GPU take turns: the lock is held until the call's kernels have drained
+    // (StreamDrain runs after Call's destructor, before the lock is released).
+    std::lock_guard<std::mutex> hold(slot->busy);
+    StreamDrain drain{static_cast<hipStream_t>(stream)};
+    Call call(stream, slot->address, kNoAllocScratchBytes);
     const LevelOperand A{a->dim_j_offsets, a->dim_j_indices, a->values, a->dim_j_length, nullptr};
     const LevelOperand B{b->dim_j_offsets, b->dim_j_indices, b->values, b->dim_j_length, nullptr};
     const LevelResult Z{pc, cc, vc, nullptr, nullptr};

@@ -86,6 +86,56 @@ def test_noalloc_matches_csr_add_twice_second_smaller(gpu):
                          f"noalloc vs oracle rows={rows}")
 
 
+@pytest.mark.gpu
+def test_noalloc_calls_from_two_threads_on_two_streams_take_turns(gpu):
+    """Two host threads, each on its own stream, call the entry point at the same time
+    (ctypes releases the GIL during the call).  Both share the GPU's scratch; the per-GPU
+    lock and the drain before return keep every result equal to the allocating entry
+    point's."""
+    import threading
+
+    from nacho_amd import _device, _lib, synth
+
+    lib = _lib.load()
+    rows = cols = 1 << 16
+    ops = [(synth.zipf_csr(rows, 31), synth.zipf_csr(rows, 32)),
+           (synth.zipf_csr(rows, 33), synth.zipf_csr(rows, 34))]
+    descs, wants = [], []
+    main = _device.current_stream(gpu)
+    for a, b in ops:
+        ga = [torch.from_numpy(x).to(gpu) for x in a]
+        gb = [torch.from_numpy(x).to(gpu) for x in b]
+        da, db = _desc(_lib, rows, cols, *ga), _desc(_lib, rows, cols, *gb)
+        descs.append((da, db, ga, gb, len(a[1]) + len(b[1])))
+        wants.append(_with_alloc(lib, _lib, da, db, rows, gpu, main))
+    streams = [torch.cuda.Stream(gpu) for _ in ops]
+    torch.cuda.synchronize()
+    results, errors = [[] for _ in ops], []
+
+    def worker(t):
+        try:
+            da, db, _, _, cap = descs[t]
+            # the result buffers are filled on the same stream the call runs on
+            with torch.cuda.device(gpu), torch.cuda.stream(streams[t]):
+                for _ in range(4):
+                    results[t].append(_noalloc(lib, _lib, da, db, rows, cols, cap, gpu,
+                                               streams[t].cuda_stream))
+        except Exception as e:  # noqa: BLE001 - reported by the main thread
+            errors.append(e)
+
+    print(f"[gpu] noalloc two threads rows={rows}", flush=True)
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(len(ops))]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    assert not errors, errors
+    for t, want in enumerate(wants):
+        assert len(results[t]) == 4
+        for i, got in enumerate(results[t]):
+            assert_csr_equal(got, want, f"thread {t} call {i}")
+
+
 def test_noalloc_refuses_short_capacity_and_oversized_inputs():
     """Checks that run before any device work (fake device addresses, nothing launched)."""
     from nacho_amd import _lib
