@@ -122,7 +122,7 @@ WORKLOADS = {
                     desc="sssmm f32: A * A masked by A on the C4 operand (R-MAT 2^20); "
                          "GFLOP/s = 3 FLOP (two multiplies, one add) per term"),
     "c4": dict(op="spgemm", kernel="long_hist_kernel + long_runs_kernel (run descriptors) + "
-                                 "dense/bitmap/sort unit kernels + copy_units_kernel and the "
+                                 "dense/bitmap/sort unit kernels + copy_units_kernel (staged output) and the "
                                  "sizing kernels "
                                  "(one call's device pipeline, host readback gaps excluded)",
                desc="C4 ESC SpGEMM C=A*A f32, R-MAT 2^20 (a,b,c,d)=(.57,.19,.19,.05), "

@@ -34,9 +34,14 @@
 //      compacts the touched columns in order.  All write the distinct (k, sum rounded once to
 //      float32) at the unit's product offset in an output staging buffer and record the
 //      unit's count and the local offset of every row starting in it.
-//   6. output: scan of unit counts -> result offsets; copy each unit's entries; row offsets
-//      from the unit offsets.  Every distinct column is kept (structural result, as the
-//      reference).
+//   6. output, sized one of two ways (output_mode).  Staged: the units write at their product
+//      offsets in a staging buffer; a scan of unit counts gives result offsets, each unit's
+//      entries are copied, row offsets come from the unit offsets.  Symbolic (columns below
+//      2^20): before the runs, a symbolic pass counts every segment's distinct columns from
+//      A and B (long rows in an LDS bitmap of the row's columns, short rows in a per-wave LDS
+//      hash table); their scan gives segment and row offsets, the result is allocated at its
+//      exact size and the units write straight into it.  Every distinct column is kept
+//      (structural result, as the reference).
 // Summation order inside a segment follows the runs' order and LDS atomics, so values are
 // reproducible to within one float32 rounding of the float64 sum (the reference's own order
 // is not deterministic either).
@@ -45,6 +50,8 @@
 #include <algorithm>
 #include <climits>
 #include <cstdint>
+#include <cstdlib>
+#include <cstring>
 
 #include "device_utils.hpp"
 #include "runtime.hpp"
@@ -741,7 +748,7 @@ __global__ __launch_bounds__(kBlock) void sort_unit_kernel(
     const int4 *__restrict__ desc, const int64_t *__restrict__ seg_roff,
     const int2 *__restrict__ cv_b, int *__restrict__ ukey,
     float *__restrict__ uval, int64_t *__restrict__ unit_nnz, int *__restrict__ row_unit,
-    int *__restrict__ row_local) {
+    int *__restrict__ row_local, const int64_t *__restrict__ seg_out) {
     static_assert(sizeof(K) >= sizeof(int), "run starts are staged in s_key");
     __shared__ K s_key[kPadded];
     __shared__ float s_val[kPadded];
@@ -864,9 +871,10 @@ __global__ __launch_bounds__(kBlock) void sort_unit_kernel(
         }
     }
     __syncthreads();
+    const int64_t out = seg_out ? seg_out[s0] : start;
     for (int j = threadIdx.x; j < runs; j += kBlock) {
-        ukey[start + j] = s_ok[pad(j)];
-        uval[start + j] = s_val[pad(j)];
+        ukey[out + j] = s_ok[pad(j)];
+        uval[out + j] = s_val[pad(j)];
     }
     if (threadIdx.x == 0) unit_nnz[u] = runs;
 }
@@ -915,7 +923,8 @@ __global__ __launch_bounds__(kBitmapBlock) void bitmap_unit_kernel(
     const int64_t *__restrict__ row_off, int shift, const int4 *__restrict__ desc,
     const int64_t *__restrict__ seg_roff, const int2 *__restrict__ cv_b,
     int *__restrict__ ukey, float *__restrict__ uval,
-    int64_t *__restrict__ unit_nnz, int *__restrict__ row_unit, int *__restrict__ row_local) {
+    int64_t *__restrict__ unit_nnz, int *__restrict__ row_unit, int *__restrict__ row_local,
+    const int64_t *__restrict__ seg_out) {
     constexpr int kWaves = kBitmapBlock / dev::kWave;
     constexpr int kPerB = kTile / kBitmapBlock;
     __shared__ double s_acc[kTile];
@@ -1035,11 +1044,12 @@ __global__ __launch_bounds__(kBitmapBlock) void bitmap_unit_kernel(
     // the unit's entries, consecutive lanes on consecutive outputs: output i belongs to the
     // last bucket whose offset is at most i (a lane's outputs only move forward)
     int o = 0;
+    const int64_t out = seg_out ? seg_out[s0] : start;
     for (int i = threadIdx.x; i < total; i += kBitmapBlock) {
         while (o + 1 < n_buckets && s_out[o + 1] <= i) ++o;
         const int x = s_x0[o] + (i - s_out[o]);
-        ukey[start + i] = s_base[o] + s_col[x];
-        uval[start + i] = static_cast<float>(s_acc[x]);
+        ukey[out + i] = s_base[o] + s_col[x];
+        uval[out + i] = static_cast<float>(s_acc[x]);
     }
     // rows starting in this unit, and the unit's count
     if (static_cast<int>(threadIdx.x) < n_buckets) {
@@ -1071,7 +1081,7 @@ __global__ __launch_bounds__(kDenseBlock) void dense_unit_kernel(
     const int4 *__restrict__ desc, const int64_t *__restrict__ seg_roff,
     const int2 *__restrict__ cv_b, int *__restrict__ ukey,
     float *__restrict__ uval, int64_t *__restrict__ unit_nnz, int *__restrict__ row_unit,
-    int *__restrict__ row_local) {
+    int *__restrict__ row_local, const int64_t *__restrict__ seg_out) {
     __shared__ double s_acc[kDenseCols];
     __shared__ unsigned s_bits[kDenseCols / 32];
     __shared__ int s_wave[kDenseBlock / dev::kWave];
@@ -1091,7 +1101,8 @@ __global__ __launch_bounds__(kDenseBlock) void dense_unit_kernel(
         row_unit[row] = static_cast<int>(u);
         row_local[row] = 0;
     }
-    int64_t written = 0;
+    int64_t written = seg_out ? seg_out[s] : start;
+    const int64_t out0 = written;
     for (int64_t w0 = c_lo; w0 < c_hi; w0 += kDenseCols) {
         for (int i = threadIdx.x; i < kDenseCols; i += kDenseBlock) s_acc[i] = 0.0;
         if (threadIdx.x < kDenseCols / 32) s_bits[threadIdx.x] = 0u;
@@ -1157,14 +1168,325 @@ __global__ __launch_bounds__(kDenseBlock) void dense_unit_kernel(
             const int bit = __ffs(m) - 1;
             m &= m - 1;
             const int c = threadIdx.x * 16 + bit;
-            ukey[start + written + rank] = static_cast<int>(w0 + c);
-            uval[start + written + rank] = static_cast<float>(s_acc[c]);
+            ukey[written + rank] = static_cast<int>(w0 + c);
+            uval[written + rank] = static_cast<float>(s_acc[c]);
             ++rank;
         }
         written += total;
         __syncthreads();
     }
-    if (threadIdx.x == 0) unit_nnz[u] = written;
+    if (threadIdx.x == 0) unit_nnz[u] = written - out0;
+}
+
+// ---- symbolic pass: the result's size before the reduce ----------------------------------
+//
+// When every column index fits kSymColBits bits, the distinct columns of every segment are
+// counted before any unit reduces, from A and B directly (no run descriptors): seg_nnz[s].
+// Their exclusive scan gives every segment's result offset, the result is allocated at its
+// exact size, and the reduce units write straight into it (a unit's entries are its
+// segments' distinct entries in segment order, so the unit starts at its first segment's
+// offset).  A row starts at its first segment's offset.  The reference sizes its result the
+// same way before reducing into it, from the head flags of its sorted products
+// (stitch_and_generate_gpu.cpp:96-126).
+//
+// Long rows: one workgroup per row (rows from a work counter, the heaviest first) ORs each
+// product's column into a bitmap of the row's columns in LDS (2^20 bits, 128 KB), then counts
+// each bucket's bits (a bucket is 8192 columns, 256 words, or the whole row when nb = 1) and
+// clears the words it read.  The row's A entries are staged kSymChunk at a time (their B
+// rows' starts and product offsets; empty B rows dropped); each wavefront takes an equal
+// share of the chunk's products in windows of 64 consecutive products, lane x on product x
+// of the window, so that a window's loads are consecutive entries of a few B rows.  The
+// entry of lane x's product is the window's first entry plus the number of entries starting
+// inside the window at or before x, counted in a 64-bit mask of those starts (an OR over the
+// wavefront).  The first entries of kSymBatch windows are searched at once, one lane each,
+// and the windows' loads are all issued before their ORs.
+// Short rows (at most kShort products): one wavefront per row inserts the columns into an
+// open-addressing table of its own in LDS (kSymSlots 32-bit slots, at most half full) and
+// counts the keys it added; then it refills the table with the empty key.
+constexpr int kSymColBits = 20;
+constexpr int kSymBlock = 1024;
+constexpr int kSymWords = 1 << (kSymColBits - 5);
+constexpr int kSymChunk = kSymBlock;
+constexpr int kSymBatch = 16;
+constexpr int64_t kSymHeavy = int64_t{1} << 18;  // long rows with more products go first
+constexpr int kSymShortBlock = 512;
+constexpr int kSymSlots = 4096;
+constexpr unsigned kSymEmpty = 0xffffffffu;  // above every column index (< 2^kSymColBits)
+static_assert(kSymWords == 32 * kSymBlock, "a thread counts 32 words of the bitmap");
+static_assert(kDenseCols / 32 == 8 * 32, "a bucket of 8192 columns is 8 threads' words");
+static_assert(kSymSlots >= 2 * kShort, "a short row's table stays at most half full");
+
+// OR of v over the 64 lanes, returned to every lane (DPP inclusive OR scan, then lane 63).
+// Every lane must be active.
+__device__ __forceinline__ unsigned wave_or(unsigned v) {
+    int x = static_cast<int>(v);
+    x |= __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
+    x |= __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
+    x |= __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
+    x |= __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
+    x |= __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15
+    x |= __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31
+    return static_cast<unsigned>(__builtin_amdgcn_readlane(x, dev::kWave - 1));
+}
+
+// Entry of lane l's product in a window of 64 products starting at wb, given e0, the entry
+// holding product wb: entries e0 + 1 + l (l < 63) may start inside the window (off: their
+// first products, ne entries in all, nonempty, so their starts are distinct and > wb).
+// Uniform control flow.
+__device__ __forceinline__ int window_entry(const int *off, int ne, int e0, int wb, int l) {
+    const int e = e0 + 1 + l;
+    const int d = e < ne ? off[e] - wb : dev::kWave;
+    const bool in = d < dev::kWave;
+    const unsigned mlo = wave_or(in && d < 32 ? 1u << d : 0u);
+    const unsigned mhi = wave_or(in && d >= 32 ? 1u << (d - 32) : 0u);
+    const int cnt = l < 32 ? __popc(mlo & ((2u << l) - 1u))
+                           : __popc(mlo) + __popc(mhi & ((2u << (l - 32)) - 1u));
+    return e0 + cnt;
+}
+
+// Work lists of the symbolic pass.  key1[i] = 2^32 for a long row with more than kSymHeavy
+// products, 1 for another long row; key2[i] = 1 for a short row with products.  An empty
+// row's segment count is 0.  Zeroes the two work counters.
+__global__ void sym_flags_kernel(const int64_t *__restrict__ row_off, int rows,
+                                 const int64_t *__restrict__ seg_prefix,
+                                 int64_t *__restrict__ key1, int64_t *__restrict__ key2,
+                                 int64_t *__restrict__ seg_nnz, int *__restrict__ work) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < rows; i += gridDim.x * blockDim.x) {
+        const int64_t prod = row_off[i + 1] - row_off[i];
+        key1[i] = prod > kShort ? (prod > kSymHeavy ? (int64_t{1} << 32) : 1) : 0;
+        key2[i] = prod > 0 && prod <= kShort ? 1 : 0;
+        if (prod == 0) seg_nnz[seg_prefix[i]] = 0;
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        work[0] = 0;
+        work[1] = 0;
+    }
+}
+
+// long_list: the heavy long rows, then the others (each group in row order); short_list:
+// the short rows with products.  counts[0] / counts[1]: their lengths.  rank1 / rank2 are
+// the exclusive scans of key1 / key2 (rank1 packs both groups' ranks, heavy in the high half).
+__global__ void sym_lists_kernel(const int64_t *__restrict__ row_off, int rows,
+                                 const int64_t *__restrict__ rank1,
+                                 const int64_t *__restrict__ rank2, int *__restrict__ long_list,
+                                 int *__restrict__ short_list, int64_t *__restrict__ counts) {
+    const int64_t t1 = rank1[rows];
+    const int64_t n_heavy = t1 >> 32;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < rows; i += gridDim.x * blockDim.x) {
+        const int64_t prod = row_off[i + 1] - row_off[i];
+        if (prod > kShort) {
+            const int64_t r = rank1[i];
+            long_list[prod > kSymHeavy ? (r >> 32) : n_heavy + (r & 0xffffffffll)] = i;
+        } else if (prod > 0) {
+            short_list[rank2[i]] = i;
+        }
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        counts[0] = n_heavy + (t1 & 0xffffffffll);
+        counts[1] = rank2[rows];
+    }
+}
+
+// Distinct columns of every bucket of the long rows (see above).  One resident workgroup
+// per CU; rows from work[0].
+__global__ __launch_bounds__(kSymBlock) void sym_long_kernel(
+    const int *__restrict__ pos_a, const int *__restrict__ crd_a,
+    const int *__restrict__ pos_b, const int *__restrict__ crd_b,
+    const int *__restrict__ long_list, const int64_t *__restrict__ counts,
+    int *__restrict__ work, const int64_t *__restrict__ seg_prefix, int nb, int cols,
+    int64_t *__restrict__ seg_nnz) {
+    constexpr int kWaves = kSymBlock / dev::kWave;
+    __shared__ uint4 s_bm4[kSymWords / 4];
+    __shared__ int s_off[kSymChunk + 1];
+    __shared__ int s_bs[kSymChunk];
+    __shared__ int64_t s_wave[kWaves];
+    __shared__ int s_sum[kWaves];
+    __shared__ int s_item;
+    unsigned *s_bm = reinterpret_cast<unsigned *>(s_bm4);
+    const int tid = threadIdx.x, w = tid / dev::kWave, l = dev::lane();
+    const int64_t n_long = counts[0];
+    const int words = (cols + 31) >> 5;  // <= kSymWords
+    for (int i = tid; i < kSymWords / 4; i += kSymBlock) s_bm4[i] = make_uint4(0u, 0u, 0u, 0u);
+    for (;;) {
+        if (tid == 0) s_item = atomicAdd(work, 1);
+        __syncthreads();  // (also: the bitmap is clear)
+        const int64_t x = s_item;
+        if (x >= n_long) break;  // uniform
+        const int row = long_list[x];
+        const int p_end = pos_a[row + 1];
+        for (int p0 = pos_a[row]; p0 < p_end; p0 += kSymChunk) {
+            const int p = p0 + tid;
+            int bs = 0, len = 0;
+            if (p < p_end) {
+                const int k = crd_a[p];
+                bs = pos_b[k];
+                len = pos_b[k + 1] - bs;
+            }
+            // one scan for both the nonempty entries' ranks (high half) and product offsets
+            // (low half: a chunk's products are at most nnz(B), its B rows being distinct)
+            int64_t tot = 0;
+            const int64_t ex = dev::block_exclusive_sum<kSymBlock, int64_t>(
+                (static_cast<int64_t>(len > 0) << 32) | static_cast<int64_t>(len), s_wave, tot);
+            const int ne = static_cast<int>(tot >> 32);
+            const int T = static_cast<int>(tot & 0xffffffffll);
+            if (len > 0) {
+                const int e = static_cast<int>(ex >> 32);
+                const int off = static_cast<int>(ex & 0xffffffffll);
+                s_off[e] = off;
+                s_bs[e] = bs - off;  // product x of entry e is B entry s_bs[e] + x
+            }
+            if (tid == 0) s_off[ne] = T;
+            __syncthreads();
+            const int share = (T + kWaves - 1) / kWaves;
+            const int lo = min(T, w * share), hi = min(T, lo + share);
+            for (int x0 = lo; x0 < hi; x0 += dev::kWave * kSymBatch) {  // uniform per wave
+                int first = 0;  // lane j < kSymBatch: the entry of window j's first product
+                {
+                    const int q = x0 + l * dev::kWave;
+                    if (l < kSymBatch && q < hi) {
+                        first = static_cast<int>(dev::last_le(s_off, 0, ne - 1, q));
+                    }
+                }
+                int c[kSymBatch];
+#pragma unroll
+                for (int j = 0; j < kSymBatch; ++j) {
+                    const int wb = x0 + j * dev::kWave;
+                    c[j] = -1;
+                    if (wb < hi) {  // uniform
+                        const int e0 = __builtin_amdgcn_readlane(first, j);
+                        const int e = window_entry(s_off, ne, e0, wb, l);
+                        if (wb + l < hi) c[j] = crd_b[s_bs[e] + wb + l];
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < kSymBatch; ++j) {
+                    if (c[j] >= 0) atomicOr(&s_bm[c[j] >> 5], 1u << (c[j] & 31));
+                }
+            }
+            __syncthreads();  // the chunk's tables are read; the ORs are done
+        }
+        // count and clear: thread t holds words [32t, 32t + 32)
+        int bits = 0;
+        if (32 * tid < words) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint4 v = s_bm4[8 * tid + i];
+                bits += __popc(v.x) + __popc(v.y) + __popc(v.z) + __popc(v.w);
+                s_bm4[8 * tid + i] = make_uint4(0u, 0u, 0u, 0u);
+            }
+        }
+        const int64_t s0 = seg_prefix[row];
+        if (nb == 1) {
+            int total = 0;
+            (void)dev::block_exclusive_sum<kSymBlock>(bits, s_sum, total);
+            if (tid == 0) seg_nnz[s0] = total;
+        } else {  // buckets of 8192 columns: 8 consecutive threads each
+            bits += __shfl_xor(bits, 1, dev::kWave);
+            bits += __shfl_xor(bits, 2, dev::kWave);
+            bits += __shfl_xor(bits, 4, dev::kWave);
+            if ((tid & 7) == 0 && (tid >> 3) < nb) seg_nnz[s0 + (tid >> 3)] = bits;
+        }
+    }
+}
+
+// Distinct columns of every short row (see above): one wavefront per row, rows from work[1].
+__global__ __launch_bounds__(kSymShortBlock) void sym_short_kernel(
+    const int *__restrict__ pos_a, const int *__restrict__ crd_a,
+    const int *__restrict__ pos_b, const int *__restrict__ crd_b,
+    const int *__restrict__ short_list, const int64_t *__restrict__ counts,
+    int *__restrict__ work, const int64_t *__restrict__ seg_prefix,
+    int64_t *__restrict__ seg_nnz) {
+    constexpr int kWaves = kSymShortBlock / dev::kWave;
+    __shared__ uint4 s_tab4[kWaves][kSymSlots / 4];
+    __shared__ int s_off[kWaves][dev::kWave + 1];
+    __shared__ int s_bs[kWaves][dev::kWave];
+    const int w = threadIdx.x / dev::kWave, l = dev::lane();
+    unsigned *tab = reinterpret_cast<unsigned *>(s_tab4[w]);
+    int *off = s_off[w];
+    int *bsw = s_bs[w];
+    const uint4 empty4 = make_uint4(kSymEmpty, kSymEmpty, kSymEmpty, kSymEmpty);
+    const int64_t n_short = counts[1];
+    for (int i = l; i < kSymSlots / 4; i += dev::kWave) s_tab4[w][i] = empty4;
+    for (;;) {
+        int x = 0;
+        if (l == 0) x = atomicAdd(work + 1, 1);
+        x = __builtin_amdgcn_readfirstlane(x);
+        if (x >= n_short) break;  // uniform
+        const int row = short_list[x];
+        const int p_end = pos_a[row + 1];
+        int fresh = 0;
+        for (int p0 = pos_a[row]; p0 < p_end; p0 += dev::kWave) {  // 64 A entries at a time
+            const int p = p0 + l;
+            int bs = 0, len = 0;
+            if (p < p_end) {
+                const int k = crd_a[p];
+                bs = pos_b[k];
+                len = pos_b[k + 1] - bs;
+            }
+            const unsigned long long nz = __ballot(len > 0);
+            const int e = static_cast<int>(__popcll(nz & ((1ull << l) - 1ull)));
+            const int ne = static_cast<int>(__popcll(nz));
+            const int incl = dev::wave_inclusive_sum_dpp(len);
+            const int T = __builtin_amdgcn_readlane(incl, dev::kWave - 1);
+            if (len > 0) {
+                off[e] = incl - len;
+                bsw[e] = bs - (incl - len);
+            }
+            if (l == 0) off[ne] = T;
+            wave_sync();
+            for (int x0 = 0; x0 < T; x0 += dev::kWave * kSymBatch) {  // uniform
+                int first = 0;
+                {
+                    const int q = x0 + l * dev::kWave;
+                    if (l < kSymBatch && q < T) {
+                        first = static_cast<int>(dev::last_le(off, 0, ne - 1, q));
+                    }
+                }
+                int c[kSymBatch];
+#pragma unroll
+                for (int j = 0; j < kSymBatch; ++j) {
+                    const int wb = x0 + j * dev::kWave;
+                    c[j] = -1;
+                    if (wb < T) {  // uniform
+                        const int e0 = __builtin_amdgcn_readlane(first, j);
+                        const int ee = window_entry(off, ne, e0, wb, l);
+                        if (wb + l < T) c[j] = crd_b[bsw[ee] + wb + l];
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < kSymBatch; ++j) {
+                    if (c[j] >= 0) {
+                        const unsigned key = static_cast<unsigned>(c[j]);
+                        unsigned h = (key * 0x9e3779b1u) >> (32 - 12);
+                        for (;;) {
+                            const unsigned old = atomicCAS(&tab[h], kSymEmpty, key);
+                            if (old == kSymEmpty) {
+                                ++fresh;
+                                break;
+                            }
+                            if (old == key) break;
+                            h = (h + 1u) & (kSymSlots - 1);
+                        }
+                    }
+                }
+            }
+            wave_sync();  // off / bsw are read before the next 64 entries replace them
+        }
+        const int total = dev::wave_sum(fresh);
+        if (l == 0) seg_nnz[seg_prefix[row]] = total;
+        for (int i = l; i < kSymSlots / 4; i += dev::kWave) s_tab4[w][i] = empty4;
+        wave_sync();
+    }
+}
+
+// Row offsets from the segment offsets: row i starts at its first segment's offset
+// (seg_prefix[rows] = n_seg, whose offset is nnz).
+template <typename PosT>
+__global__ void seg_pos_kernel(const int64_t *__restrict__ seg_prefix, int rows,
+                               const int64_t *__restrict__ seg_out, PosT *__restrict__ pos) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i <= rows; i += gridDim.x * blockDim.x) {
+        pos[i] = static_cast<PosT>(seg_out[seg_prefix[i]]);
+    }
 }
 
 // ---- 6: output -------------------------------------------------------------------------
@@ -1221,6 +1543,29 @@ int col_bits(int cols) {
     return b;
 }
 
+// How the result is sized.  Staged: the reduce units write their distinct entries at their
+// units' product offsets in a staging buffer of 8 bytes per product, and a copy moves them
+// into the result once every unit's count is known.  Symbolic: the symbolic pass counts
+// every segment's distinct columns first, and the units write straight into the result
+// (no staging buffer; possible when every column fits the pass's 2^kSymColBits-bit row
+// bitmap).  At C4 the copy costs 11.0 ms and the symbolic pass 20.6 ms (its long-row kernel
+// is bound by the per-row chain of one workgroup per CU), so the staged path is taken
+// while its buffer fits in half of the device memory that is free or cached by the
+// library, the symbolic one otherwise.  NACHO_SPGEMM_OUTPUT=staged or =symbolic chooses
+// one (symbolic only where it applies).
+enum class Output { Staged, Symbolic };
+
+Output output_mode(int64_t products, bool symbolic_fits) {
+    const char *v = std::getenv("NACHO_SPGEMM_OUTPUT");
+    if (v != nullptr && std::strcmp(v, "staged") == 0) return Output::Staged;
+    if (!symbolic_fits) return Output::Staged;
+    if (v != nullptr && std::strcmp(v, "symbolic") == 0) return Output::Symbolic;
+    size_t free_bytes = 0, total_bytes = 0;
+    if (hipMemGetInfo(&free_bytes, &total_bytes) != hipSuccess) return Output::Symbolic;
+    const double room = (static_cast<double>(free_bytes) + static_cast<double>(nacho_cached_bytes())) / 2;
+    return 8.0 * static_cast<double>(products) <= room ? Output::Staged : Output::Symbolic;
+}
+
 struct Product {
     int rows = 0, cols = 0;
     int64_t nnz = 0;
@@ -1242,7 +1587,7 @@ int multiply(Call &call, const nacho_csr *a, const nacho_csr *b, Product *z) {
     const int shift = std::max(std::min(kDenseBits, cb), cb - kMaxBucketBits);
     const int nb = cols > 0 ? ((cols - 1) >> shift) + 1 : 1;
     const int dense_min = shift <= kDenseBits ? kDenseMin : kShort;
-    const char *name = "spgemm: runs+reduce+copy";
+    const char *name = "spgemm: runs+reduce+output";
     NACHO_TRY(call.timer_start(name));
 
     // 1-2. products per A entry, per row; segments per row
@@ -1269,8 +1614,13 @@ int multiply(Call &call, const nacho_csr *a, const nacho_csr *b, Product *z) {
     NACHO_TRY(call.read_back(&n_seg, seg_prefix + rows, sizeof(n_seg)));
     NACHO_TRY(call.timer_start(name));
     if (n_seg >= INT_MAX) return NACHO_ERR_INDEX_OVERFLOW;  // segment ids are int32
+    const bool symbolic =
+        P > 0 && output_mode(P, cb <= kSymColBits &&
+                                    b->dim_j_length <= static_cast<int64_t>(INT_MAX) -
+                                                           4 * kSymChunk) == Output::Symbolic;
 
     int64_t n_units = 0;
+    int64_t *seg_out = nullptr;  // symbolic pass: result offset of every segment
     int64_t *unit_start = nullptr, *unit_nnz = nullptr, *unit_out = nullptr;
     int *row_unit = nullptr, *row_local = nullptr;
     NACHO_TRY(call.scratch_n(static_cast<size_t>(rows) + 1, &row_unit));
@@ -1291,11 +1641,50 @@ int multiply(Call &call, const nacho_csr *a, const nacho_csr *b, Product *z) {
                                                             seg_len, seg_runs, seg_fill);
         NACHO_TRY_HIP(hipGetLastError());
 
+        // symbolic pass: distinct columns per segment, scanned into result offsets
+        if (symbolic) {
+            int64_t *seg_nnz = nullptr, *keys = nullptr, *ranks = nullptr, *counts = nullptr;
+            int *lists = nullptr, *work = nullptr;
+            NACHO_TRY(call.scratch_n(static_cast<size_t>(n_seg) + 1, &seg_nnz));
+            NACHO_TRY(call.scratch_n(static_cast<size_t>(n_seg) + 1, &seg_out));
+            NACHO_TRY(call.scratch_n(2 * (static_cast<size_t>(rows) + 1), &keys));
+            NACHO_TRY(call.scratch_n(2 * (static_cast<size_t>(rows) + 1), &ranks));
+            NACHO_TRY(call.scratch_n(2 * static_cast<size_t>(rows) + 2, &lists));
+            NACHO_TRY(call.scratch_n(2, &counts));
+            NACHO_TRY(call.scratch_n(2, &work));
+            int64_t *key2 = keys + (rows + 1), *rank2 = ranks + (rows + 1);
+            int *long_list = lists, *short_list = lists + (rows + 1);
+            sym_flags_kernel<<<grid_for(rows, 256), 256, 0, st>>>(row_off, rows, seg_prefix,
+                                                                 keys, key2, seg_nnz, work);
+            NACHO_TRY_HIP(hipGetLastError());
+            NACHO_TRY(scan::exclusive_scan_i64(call, keys, rows, ranks));
+            NACHO_TRY(scan::exclusive_scan_i64(call, key2, rows, rank2));
+            sym_lists_kernel<<<grid_for(rows, 256), 256, 0, st>>>(row_off, rows, ranks, rank2,
+                                                                 long_list, short_list, counts);
+            NACHO_TRY_HIP(hipGetLastError());
+            int g_long = 0, g_short = 0;
+            NACHO_TRY(resident_grid(reinterpret_cast<const void *>(sym_long_kernel), kSymBlock,
+                                    &g_long));
+            NACHO_TRY(resident_grid(reinterpret_cast<const void *>(sym_short_kernel),
+                                    kSymShortBlock, &g_short));
+            sym_long_kernel<<<static_cast<unsigned>(g_long), kSymBlock, 0, st>>>(
+                a->dim_j_offsets, a->dim_j_indices, b->dim_j_offsets, b->dim_j_indices,
+                long_list, counts, work, seg_prefix, nb, cols, seg_nnz);
+            NACHO_TRY_HIP(hipGetLastError());
+            sym_short_kernel<<<static_cast<unsigned>(g_short), kSymShortBlock, 0, st>>>(
+                a->dim_j_offsets, a->dim_j_indices, b->dim_j_offsets, b->dim_j_indices,
+                short_list, counts, work, seg_prefix, seg_nnz);
+            NACHO_TRY_HIP(hipGetLastError());
+            NACHO_TRY(scan::exclusive_scan_i64(call, seg_nnz, n_seg, seg_out));
+        }
+
         // 3. histogram, segment offsets, runs
-        int *ukey = nullptr;
+        int *ukey = nullptr;  // the units' output: staged at product offsets, or the result
         float *uval = nullptr;
-        NACHO_TRY(call.scratch_n(static_cast<size_t>(P), &ukey));
-        NACHO_TRY(call.scratch_n(static_cast<size_t>(P), &uval));
+        if (!symbolic) {
+            NACHO_TRY(call.scratch_n(static_cast<size_t>(P), &ukey));
+            NACHO_TRY(call.scratch_n(static_cast<size_t>(P), &uval));
+        }
         // long rows' bucket counts from B's runs (P > 0, so B has entries)
         const int64_t nnz_b = b->dim_j_length;
         const int rows_b = b->dim_i_size;
@@ -1344,9 +1733,19 @@ int multiply(Call &call, const nacho_csr *a, const nacho_csr *b, Product *z) {
         NACHO_TRY_HIP(hipGetLastError());
         NACHO_TRY(scan::exclusive_scan_i64(call, seg_len, n_seg, seg_off));
         NACHO_TRY(scan::exclusive_scan_i64(call, seg_runs, n_seg, seg_roff));
-        int64_t n_runs = 0;
+        int64_t n_runs = 0, nnz_sym = 0;
         NACHO_TRY(call.timer_stop());
         NACHO_TRY(call.read_back(&n_runs, seg_roff + n_seg, sizeof(n_runs)));
+        if (symbolic) {
+            NACHO_TRY(call.read_back(&nnz_sym, seg_out + n_seg, sizeof(nnz_sym)));
+            if (sizeof(PosT) == sizeof(int32_t) && nnz_sym > INT_MAX) {
+                return NACHO_ERR_INDEX_OVERFLOW;
+            }
+            NACHO_TRY(call.result_n(static_cast<size_t>(nnz_sym), &z->crd));
+            NACHO_TRY(call.result_n(static_cast<size_t>(nnz_sym), &z->val));
+            ukey = z->crd;
+            uval = z->val;
+        }
         NACHO_TRY(call.timer_start(name));
         int4 *desc = nullptr;
         NACHO_TRY(call.scratch_n(static_cast<size_t>(std::max<int64_t>(n_runs, 1)), &desc));
@@ -1411,48 +1810,58 @@ int multiply(Call &call, const nacho_csr *a, const nacho_csr *b, Product *z) {
         if (n_kind[1] > 0 && cb + kOrdBits <= 32) {
             sort_unit_kernel<uint32_t><<<static_cast<unsigned>(n_kind[1]), kBlock, 0, st>>>(
                 sort_list, unit_seg, unit_start, n_units, n_seg, seg_len, seg_off, seg_row,
-                row_off, cb, desc, seg_roff, cv_b, ukey, uval, unit_nnz, row_unit, row_local);
+                row_off, cb, desc, seg_roff, cv_b, ukey, uval, unit_nnz, row_unit, row_local,
+                seg_out);
         } else if (n_kind[1] > 0) {
             sort_unit_kernel<uint64_t><<<static_cast<unsigned>(n_kind[1]), kBlock, 0, st>>>(
                 sort_list, unit_seg, unit_start, n_units, n_seg, seg_len, seg_off, seg_row,
-                row_off, 32, desc, seg_roff, cv_b, ukey, uval, unit_nnz, row_unit, row_local);
+                row_off, 32, desc, seg_roff, cv_b, ukey, uval, unit_nnz, row_unit, row_local,
+                seg_out);
         }
         NACHO_TRY_HIP(hipGetLastError());
         if (n_kind[2] > 0) {
             bitmap_unit_kernel<<<static_cast<unsigned>(n_kind[2]), kBitmapBlock, 0, st>>>(
                 bitmap_list, unit_seg, unit_start, n_units, n_seg, seg_len, seg_off, seg_prefix,
                 seg_row, row_off, shift, desc, seg_roff, cv_b, ukey, uval, unit_nnz, row_unit,
-                row_local);
+                row_local, seg_out);
             NACHO_TRY_HIP(hipGetLastError());
         }
         if (n_kind[0] > 0) {
             dense_unit_kernel<<<static_cast<unsigned>(n_kind[0]), kDenseBlock, 0, st>>>(
                 dense_list, unit_seg, unit_start, seg_len, seg_prefix, seg_row, row_off, shift,
-                cols, desc, seg_roff, cv_b, ukey, uval, unit_nnz, row_unit, row_local);
+                cols, desc, seg_roff, cv_b, ukey, uval, unit_nnz, row_unit, row_local, seg_out);
             NACHO_TRY_HIP(hipGetLastError());
         }
-        NACHO_TRY(scan::exclusive_scan_i64(call, unit_nnz, n_units, unit_out));
+        if (symbolic) {
+            z->nnz = nnz_sym;  // the units wrote straight into the result
+        } else {
+            NACHO_TRY(scan::exclusive_scan_i64(call, unit_nnz, n_units, unit_out));
+            int64_t nnz = 0;
+            NACHO_TRY(call.timer_stop());
+            NACHO_TRY(call.read_back(&nnz, unit_out + n_units, sizeof(nnz)));
+            if (sizeof(PosT) == sizeof(int32_t) && nnz > INT_MAX) return NACHO_ERR_INDEX_OVERFLOW;
+            NACHO_TRY(call.timer_start(name));
 
-        int64_t nnz = 0;
-        NACHO_TRY(call.timer_stop());
-        NACHO_TRY(call.read_back(&nnz, unit_out + n_units, sizeof(nnz)));
-        if (sizeof(PosT) == sizeof(int32_t) && nnz > INT_MAX) return NACHO_ERR_INDEX_OVERFLOW;
-        NACHO_TRY(call.timer_start(name));
-
-        // 6. output
-        NACHO_TRY(call.result_n(static_cast<size_t>(nnz), &z->crd));
-        NACHO_TRY(call.result_n(static_cast<size_t>(nnz), &z->val));
-        if (nnz > 0) {
-            copy_units_kernel<<<ug, kBlock, 0, st>>>(unit_start, unit_nnz, unit_out, ukey,
-                                                     uval, z->crd, z->val);
-            NACHO_TRY_HIP(hipGetLastError());
+            // 6. output
+            NACHO_TRY(call.result_n(static_cast<size_t>(nnz), &z->crd));
+            NACHO_TRY(call.result_n(static_cast<size_t>(nnz), &z->val));
+            if (nnz > 0) {
+                copy_units_kernel<<<ug, kBlock, 0, st>>>(unit_start, unit_nnz, unit_out, ukey,
+                                                         uval, z->crd, z->val);
+                NACHO_TRY_HIP(hipGetLastError());
+            }
+            z->nnz = nnz;
         }
-        z->nnz = nnz;
     }
     PosT *pos = nullptr;
     NACHO_TRY(call.result_n(static_cast<size_t>(rows) + 1, &pos));
-    row_pos_kernel<PosT><<<grid_for(static_cast<int64_t>(rows) + 1, 256), 256, 0, st>>>(
-        row_off, rows, P, z->nnz, row_unit, row_local, unit_out, pos);
+    if (seg_out) {
+        seg_pos_kernel<PosT><<<grid_for(static_cast<int64_t>(rows) + 1, 256), 256, 0, st>>>(
+            seg_prefix, rows, seg_out, pos);
+    } else {
+        row_pos_kernel<PosT><<<grid_for(static_cast<int64_t>(rows) + 1, 256), 256, 0, st>>>(
+            row_off, rows, P, z->nnz, row_unit, row_local, unit_out, pos);
+    }
     NACHO_TRY_HIP(hipGetLastError());
     NACHO_TRY(call.timer_stop());
     NACHO_TRY(call.collect_timer());

@@ -130,6 +130,68 @@ def test_long_runs_cross_tiles(gpu):
     assert pos.tolist() == [0, 2, 4] and crd.tolist() == [5, 7, 5, 7]
 
 
+def _hub_operands(rng, cols):
+    """A with a heavy row (3000 A entries, every third B row empty, about 3.5e5 products:
+    several staged chunks, above the heavy-row threshold), a row of 1025 entries, rows with
+    products just around the short-row limit, and empty rows; B's rows have 0-400 distinct
+    columns in [0, cols)."""
+    inner = 4000
+    lens_b = rng.integers(1, 400, inner)
+    lens_b[::3] = 0
+    rows_b = [np.sort(rng.choice(cols, size=int(L), replace=False)).tolist() for L in lens_b]
+    nnz_b = int(lens_b.sum())
+    b = csr_from_rows(inner, cols, rows_b, rng.uniform(-1, 1, nnz_b).astype(np.float32))
+    rows_a = [sorted(rng.choice(inner, size=3000, replace=False).tolist()), [],
+              sorted(rng.choice(inner, size=1025, replace=False).tolist()),
+              [1, 2], [0, 3, 6], []]
+    # a short row of exactly kShort (2048) products and a long one of kShort + 1
+    for target in (2048, 2049):
+        row, total = [], 0
+        for j in rng.permutation(inner):
+            if lens_b[j] > 0 and total + lens_b[j] <= target:
+                row.append(int(j))
+                total += int(lens_b[j])
+            if total == target:
+                break
+        rows_a.append(sorted(row))
+    rows = len(rows_a)
+    nnz_a = sum(len(r) for r in rows_a)
+    a = csr_from_rows(rows, inner, rows_a, rng.uniform(0.5, 1.5, nnz_a).astype(np.float32))
+    return rows, inner, a, b
+
+
+@pytest.mark.parametrize("cols", [1 << 20, (1 << 20) - 5, 8192, 8193])
+def test_symbolic_pass_hub_rows(gpu, cols, monkeypatch):
+    """The symbolic pass sizes the result (columns fit its 2^20-bit row bitmap): long rows
+    staged in several chunks with empty B rows among their A entries, a row above the
+    heavy-row threshold, short rows at the short-row limit; one bucket (cols <= 8192) and
+    8192-column buckets with a partial last one."""
+    monkeypatch.setenv("NACHO_SPGEMM_OUTPUT", "symbolic")
+    rng = np.random.default_rng(cols % 997)
+    rows, inner, a, b = _hub_operands(rng, cols)
+    run_and_check(gpu, rows, inner, cols, a, b, f"symbolic hub rows cols={cols}")
+
+
+def test_staged_and_symbolic_outputs_agree(gpu, monkeypatch):
+    """NACHO_SPGEMM_OUTPUT=staged runs the units into a staging buffer at their product
+    offsets and copies them to the result; =symbolic sizes the result first with the
+    symbolic pass.  Both match the oracle and each other's structure exactly."""
+    from nacho_amd import synth
+
+    n = 1 << 14
+    t = synth.rmat_csr(14, seed=6)
+    rng = np.random.default_rng(11)
+    rows, inner, a, b = _hub_operands(rng, 1 << 20)
+    for what, args in (("rmat14", (n, n, n, t, t)), ("hub rows", (rows, inner, 1 << 20, a, b))):
+        z = {}
+        for mode in ("staged", "symbolic"):
+            monkeypatch.setenv("NACHO_SPGEMM_OUTPUT", mode)
+            z[mode] = run_and_check(gpu, *args, f"{what} {mode}")
+        np.testing.assert_array_equal(z["staged"][0], z["symbolic"][0])
+        np.testing.assert_array_equal(z["staged"][1], z["symbolic"][1])
+        np.testing.assert_allclose(z["staged"][2], z["symbolic"][2], rtol=RTOL, atol=ATOL)
+
+
 def test_wide_columns_use_64bit_keys(gpu):
     """cols > 2^20 leaves fewer than 12 free key bits, so the 64-bit sort key path runs."""
     rng = np.random.default_rng(10)
@@ -316,5 +378,38 @@ def test_c4_full_size(gpu):
         with pytest.raises(RuntimeError, match="exceeds int32"):
             nacho_amd.gpu_spgemm_f32(a_gpu, a_gpu)
     finally:
+        torch.cuda.synchronize()
+        nacho_amd.release_cached_memory()
+
+
+def test_c4_symbolic_matches_staged(gpu, monkeypatch):
+    """The C4 square with the symbolic pass sizing the result (the path taken when the
+    staging buffer would not fit) equals the staged path's result, which
+    test_c4_full_size checks row by row against the oracle: offsets and columns exactly,
+    values within the tolerance (the two runs' float64 sums may differ in order)."""
+    import nacho_amd
+    from nacho_amd import synth
+
+    n = 1 << 20
+    pos, crd, val = synth.c4_operand()
+    a_gpu = to_gpu((pos, crd, val), n, n, gpu)
+    z = {}
+    for mode in ("staged", "symbolic"):
+        monkeypatch.setenv("NACHO_SPGEMM_OUTPUT", mode)
+        print(f"[gpu] spgemm64 C4 {mode}", flush=True)
+        z[mode] = nacho_amd.gpu_spgemm64_f32(a_gpu, a_gpu)
+        torch.cuda.synchronize()
+    staged, symbolic = z.pop("staged"), z.pop("symbolic")
+    try:
+        assert torch.equal(staged.dim_j_offsets, symbolic.dim_j_offsets)
+        assert torch.equal(staged.dim_j_indices, symbolic.dim_j_indices)
+        nnz = staged.values.numel()
+        step = 1 << 28
+        for i in range(0, nnz, step):
+            x = staged.values[i:i + step].to(torch.float64)
+            y = symbolic.values[i:i + step].to(torch.float64)
+            assert bool(((x - y).abs() <= ATOL + RTOL * y.abs()).all()), f"values [{i}, +{step})"
+    finally:
+        del staged, symbolic
         torch.cuda.synchronize()
         nacho_amd.release_cached_memory()
