@@ -1189,7 +1189,7 @@ __global__ __launch_bounds__(kDenseBlock) void dense_unit_kernel(
 // same way before reducing into it, from the head flags of its sorted products
 // (stitch_and_generate_gpu.cpp:96-126).
 //
-// Long rows: one workgroup per row (rows from a work counter, the heaviest first) ORs each
+// Long rows: one workgroup per row (rows claimed from a list, the heaviest first) ORs each
 // product's column into a bitmap of the row's columns in LDS (2^20 bits, 128 KB), then counts
 // each bucket's bits (a bucket is 8192 columns, 256 words, or the whole row when nb = 1) and
 // clears the words it read.  The row's A entries are staged kSymChunk at a time (their B
@@ -1246,7 +1246,7 @@ __device__ __forceinline__ int window_entry(const int *off, int ne, int e0, int 
 
 // Work lists of the symbolic pass.  key1[i] = 2^32 for a long row with more than kSymHeavy
 // products, 1 for another long row; key2[i] = 1 for a short row with products.  An empty
-// row's segment count is 0.  Zeroes the two work counters.
+// row's segment count is 0.  Zeroes the long-row work counter.
 __global__ void sym_flags_kernel(const int64_t *__restrict__ row_off, int rows,
                                  const int64_t *__restrict__ seg_prefix,
                                  int64_t *__restrict__ key1, int64_t *__restrict__ key2,
@@ -1257,10 +1257,7 @@ __global__ void sym_flags_kernel(const int64_t *__restrict__ row_off, int rows,
         key2[i] = prod > 0 && prod <= kShort ? 1 : 0;
         if (prod == 0) seg_nnz[seg_prefix[i]] = 0;
     }
-    if (blockIdx.x == 0 && threadIdx.x == 0) {
-        work[0] = 0;
-        work[1] = 0;
-    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) *work = 0;
 }
 
 // long_list: the heavy long rows, then the others (each group in row order); short_list:
@@ -1288,7 +1285,10 @@ __global__ void sym_lists_kernel(const int64_t *__restrict__ row_off, int rows,
 }
 
 // Distinct columns of every bucket of the long rows (see above).  One resident workgroup
-// per CU; rows from work[0].
+// per CU; workgroup g starts with long-list item g and claims its next item from `work`
+// (zeroed) when it starts a row, so the next chunk of A entries (the rest of this row's, or
+// the claimed item's first) is known in advance: its column loads are issued before this
+// chunk's batches and its B row starts after them, off the chunk-to-chunk path.
 __global__ __launch_bounds__(kSymBlock) void sym_long_kernel(
     const int *__restrict__ pos_a, const int *__restrict__ crd_a,
     const int *__restrict__ pos_b, const int *__restrict__ crd_b,
@@ -1301,101 +1301,133 @@ __global__ __launch_bounds__(kSymBlock) void sym_long_kernel(
     __shared__ int s_bs[kSymChunk];
     __shared__ int64_t s_wave[kWaves];
     __shared__ int s_sum[kWaves];
-    __shared__ int s_item;
+    __shared__ int64_t s_next;  // the item claimed for after the current row
     unsigned *s_bm = reinterpret_cast<unsigned *>(s_bm4);
     const int tid = threadIdx.x, w = tid / dev::kWave, l = dev::lane();
     const int64_t n_long = counts[0];
+    int64_t item = blockIdx.x;
+    if (item >= n_long) return;  // uniform
     const int words = (cols + 31) >> 5;  // <= kSymWords
     for (int i = tid; i < kSymWords / 4; i += kSymBlock) s_bm4[i] = make_uint4(0u, 0u, 0u, 0u);
+    int row = long_list[item];
+    int p0 = pos_a[row], p_end = pos_a[row + 1];
+    bool row_start = true;
+    int bs = 0, len = 0;  // this thread's A entry of the current chunk: its B row
+    if (p0 + tid < p_end) {
+        const int k = crd_a[p0 + tid];
+        bs = pos_b[k];
+        len = pos_b[k + 1] - bs;
+    }
     for (;;) {
-        if (tid == 0) s_item = atomicAdd(work, 1);
-        __syncthreads();  // (also: the bitmap is clear)
-        const int64_t x = s_item;
-        if (x >= n_long) break;  // uniform
-        const int row = long_list[x];
-        const int p_end = pos_a[row + 1];
-        for (int p0 = pos_a[row]; p0 < p_end; p0 += kSymChunk) {
-            const int p = p0 + tid;
-            int bs = 0, len = 0;
-            if (p < p_end) {
-                const int k = crd_a[p];
-                bs = pos_b[k];
-                len = pos_b[k + 1] - bs;
-            }
-            // one scan for both the nonempty entries' ranks (high half) and product offsets
-            // (low half: a chunk's products are at most nnz(B), its B rows being distinct)
-            int64_t tot = 0;
-            const int64_t ex = dev::block_exclusive_sum<kSymBlock, int64_t>(
-                (static_cast<int64_t>(len > 0) << 32) | static_cast<int64_t>(len), s_wave, tot);
-            const int ne = static_cast<int>(tot >> 32);
-            const int T = static_cast<int>(tot & 0xffffffffll);
-            if (len > 0) {
-                const int e = static_cast<int>(ex >> 32);
-                const int off = static_cast<int>(ex & 0xffffffffll);
-                s_off[e] = off;
-                s_bs[e] = bs - off;  // product x of entry e is B entry s_bs[e] + x
-            }
-            if (tid == 0) s_off[ne] = T;
-            __syncthreads();
-            const int share = (T + kWaves - 1) / kWaves;
-            const int lo = min(T, w * share), hi = min(T, lo + share);
-            for (int x0 = lo; x0 < hi; x0 += dev::kWave * kSymBatch) {  // uniform per wave
-                int first = 0;  // lane j < kSymBatch: the entry of window j's first product
-                {
-                    const int q = x0 + l * dev::kWave;
-                    if (l < kSymBatch && q < hi) {
-                        first = static_cast<int>(dev::last_le(s_off, 0, ne - 1, q));
-                    }
-                }
-                int c[kSymBatch];
-#pragma unroll
-                for (int j = 0; j < kSymBatch; ++j) {
-                    const int wb = x0 + j * dev::kWave;
-                    c[j] = -1;
-                    if (wb < hi) {  // uniform
-                        const int e0 = __builtin_amdgcn_readlane(first, j);
-                        const int e = window_entry(s_off, ne, e0, wb, l);
-                        if (wb + l < hi) c[j] = crd_b[s_bs[e] + wb + l];
-                    }
-                }
-#pragma unroll
-                for (int j = 0; j < kSymBatch; ++j) {
-                    if (c[j] >= 0) atomicOr(&s_bm[c[j] >> 5], 1u << (c[j] & 31));
-                }
-            }
-            __syncthreads();  // the chunk's tables are read; the ORs are done
-        }
-        // count and clear: thread t holds words [32t, 32t + 32)
-        int bits = 0;
-        if (32 * tid < words) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const uint4 v = s_bm4[8 * tid + i];
-                bits += __popc(v.x) + __popc(v.y) + __popc(v.z) + __popc(v.w);
-                s_bm4[8 * tid + i] = make_uint4(0u, 0u, 0u, 0u);
+        // (every thread read the previous claim before the last chunk's final barrier; this
+        // one is read after this chunk's barriers)
+        if (row_start && tid == 0) s_next = static_cast<int64_t>(gridDim.x) + atomicAdd(work, 1);
+        // the next chunk, and its column loads (in flight during this chunk)
+        int64_t n_item = item;
+        int n_row = row, n_p0 = p0 + kSymChunk, n_end = p_end;
+        const bool row_done = n_p0 >= p_end;
+        if (row_done) {
+            __syncthreads();  // the claim
+            n_item = s_next;
+            if (n_item < n_long) {
+                n_row = long_list[n_item];
+                n_p0 = pos_a[n_row];
+                n_end = pos_a[n_row + 1];
             }
         }
-        const int64_t s0 = seg_prefix[row];
-        if (nb == 1) {
-            int total = 0;
-            (void)dev::block_exclusive_sum<kSymBlock>(bits, s_sum, total);
-            if (tid == 0) seg_nnz[s0] = total;
-        } else {  // buckets of 8192 columns: 8 consecutive threads each
-            bits += __shfl_xor(bits, 1, dev::kWave);
-            bits += __shfl_xor(bits, 2, dev::kWave);
-            bits += __shfl_xor(bits, 4, dev::kWave);
-            if ((tid & 7) == 0 && (tid >> 3) < nb) seg_nnz[s0 + (tid >> 3)] = bits;
+        const bool more = n_item < n_long;
+        const int n_k = more && n_p0 + tid < n_end ? crd_a[n_p0 + tid] : -1;
+        // one scan for both the nonempty entries' ranks (high half) and product offsets
+        // (low half: a chunk's products are at most nnz(B), its B rows being distinct)
+        int64_t tot = 0;
+        const int64_t ex = dev::block_exclusive_sum<kSymBlock, int64_t>(
+            (static_cast<int64_t>(len > 0) << 32) | static_cast<int64_t>(len), s_wave, tot);
+        const int ne = static_cast<int>(tot >> 32);
+        const int T = static_cast<int>(tot & 0xffffffffll);
+        if (len > 0) {
+            const int e = static_cast<int>(ex >> 32);
+            const int off = static_cast<int>(ex & 0xffffffffll);
+            s_off[e] = off;
+            s_bs[e] = bs - off;  // product x of entry e is B entry s_bs[e] + x
         }
+        if (tid == 0) s_off[ne] = T;
+        __syncthreads();
+        const int share = (T + kWaves - 1) / kWaves;
+        const int lo = min(T, w * share), hi = min(T, lo + share);
+        for (int x0 = lo; x0 < hi; x0 += dev::kWave * kSymBatch) {  // uniform per wave
+            int first = 0;  // lane j < kSymBatch: the entry of window j's first product
+            {
+                const int q = x0 + l * dev::kWave;
+                if (l < kSymBatch && q < hi) {
+                    first = static_cast<int>(dev::last_le(s_off, 0, ne - 1, q));
+                }
+            }
+            int c[kSymBatch];
+#pragma unroll
+            for (int j = 0; j < kSymBatch; ++j) {
+                const int wb = x0 + j * dev::kWave;
+                c[j] = -1;
+                if (wb < hi) {  // uniform
+                    const int e0 = __builtin_amdgcn_readlane(first, j);
+                    const int e = window_entry(s_off, ne, e0, wb, l);
+                    if (wb + l < hi) c[j] = crd_b[s_bs[e] + wb + l];
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < kSymBatch; ++j) {
+                if (c[j] >= 0) atomicOr(&s_bm[c[j] >> 5], 1u << (c[j] & 31));
+            }
+        }
+        // the next chunk's B rows (in flight during the barrier and the bucket counts)
+        int n_bs = 0, n_len = 0;
+        if (n_k >= 0) {
+            n_bs = pos_b[n_k];
+            n_len = pos_b[n_k + 1] - n_bs;
+        }
+        __syncthreads();  // the chunk's tables are read; the ORs are done
+        if (row_done) {
+            // count and clear: thread t holds words [32t, 32t + 32).  The next chunk's scan
+            // barrier orders the clears before its ORs.
+            int bits = 0;
+            if (32 * tid < words) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const uint4 v = s_bm4[8 * tid + i];
+                    bits += __popc(v.x) + __popc(v.y) + __popc(v.z) + __popc(v.w);
+                    s_bm4[8 * tid + i] = make_uint4(0u, 0u, 0u, 0u);
+                }
+            }
+            const int64_t s0 = seg_prefix[row];
+            if (nb == 1) {
+                int total = 0;
+                (void)dev::block_exclusive_sum<kSymBlock>(bits, s_sum, total);
+                if (tid == 0) seg_nnz[s0] = total;
+            } else {  // buckets of 8192 columns: 8 consecutive threads each
+                bits += __shfl_xor(bits, 1, dev::kWave);
+                bits += __shfl_xor(bits, 2, dev::kWave);
+                bits += __shfl_xor(bits, 4, dev::kWave);
+                if ((tid & 7) == 0 && (tid >> 3) < nb) seg_nnz[s0 + (tid >> 3)] = bits;
+            }
+        }
+        if (!more) break;  // uniform
+        row_start = row_done;
+        item = n_item;
+        row = n_row;
+        p0 = n_p0;
+        p_end = n_end;
+        bs = n_bs;
+        len = n_len;
     }
 }
 
-// Distinct columns of every short row (see above): one wavefront per row, rows from work[1].
+// Distinct columns of every short row (see above): one wavefront per row; wave v of the
+// grid takes short-list items v, v + V, v + 2V, ... (V waves), and loads the next item's
+// row and offsets while it counts the current one.
 __global__ __launch_bounds__(kSymShortBlock) void sym_short_kernel(
     const int *__restrict__ pos_a, const int *__restrict__ crd_a,
     const int *__restrict__ pos_b, const int *__restrict__ crd_b,
     const int *__restrict__ short_list, const int64_t *__restrict__ counts,
-    int *__restrict__ work, const int64_t *__restrict__ seg_prefix,
-    int64_t *__restrict__ seg_nnz) {
+    const int64_t *__restrict__ seg_prefix, int64_t *__restrict__ seg_nnz) {
     constexpr int kWaves = kSymShortBlock / dev::kWave;
     __shared__ uint4 s_tab4[kWaves][kSymSlots / 4];
     __shared__ int s_off[kWaves][dev::kWave + 1];
@@ -1406,16 +1438,23 @@ __global__ __launch_bounds__(kSymShortBlock) void sym_short_kernel(
     int *bsw = s_bs[w];
     const uint4 empty4 = make_uint4(kSymEmpty, kSymEmpty, kSymEmpty, kSymEmpty);
     const int64_t n_short = counts[1];
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kWaves;
+    int64_t item = static_cast<int64_t>(blockIdx.x) * kWaves + w;
     for (int i = l; i < kSymSlots / 4; i += dev::kWave) s_tab4[w][i] = empty4;
+    if (item >= n_short) return;  // uniform per wave (no barriers below)
+    int row = short_list[item];
+    int p_lo = pos_a[row], p_end = pos_a[row + 1];
     for (;;) {
-        int x = 0;
-        if (l == 0) x = atomicAdd(work + 1, 1);
-        x = __builtin_amdgcn_readfirstlane(x);
-        if (x >= n_short) break;  // uniform
-        const int row = short_list[x];
-        const int p_end = pos_a[row + 1];
+        const int64_t n_item = item + stride;
+        const bool more = n_item < n_short;
+        int n_row = 0, n_lo = 0, n_end = 0;
+        if (more) {  // next item's row and offsets, in flight during this row
+            n_row = short_list[n_item];
+            n_lo = pos_a[n_row];
+            n_end = pos_a[n_row + 1];
+        }
         int fresh = 0;
-        for (int p0 = pos_a[row]; p0 < p_end; p0 += dev::kWave) {  // 64 A entries at a time
+        for (int p0 = p_lo; p0 < p_end; p0 += dev::kWave) {  // 64 A entries at a time
             const int p = p0 + l;
             int bs = 0, len = 0;
             if (p < p_end) {
@@ -1476,6 +1515,11 @@ __global__ __launch_bounds__(kSymShortBlock) void sym_short_kernel(
         if (l == 0) seg_nnz[seg_prefix[row]] = total;
         for (int i = l; i < kSymSlots / 4; i += dev::kWave) s_tab4[w][i] = empty4;
         wave_sync();
+        if (!more) break;
+        item = n_item;
+        row = n_row;
+        p_lo = n_lo;
+        p_end = n_end;
     }
 }
 
@@ -1651,7 +1695,7 @@ int multiply(Call &call, const nacho_csr *a, const nacho_csr *b, Product *z) {
             NACHO_TRY(call.scratch_n(2 * (static_cast<size_t>(rows) + 1), &ranks));
             NACHO_TRY(call.scratch_n(2 * static_cast<size_t>(rows) + 2, &lists));
             NACHO_TRY(call.scratch_n(2, &counts));
-            NACHO_TRY(call.scratch_n(2, &work));
+            NACHO_TRY(call.scratch_n(1, &work));
             int64_t *key2 = keys + (rows + 1), *rank2 = ranks + (rows + 1);
             int *long_list = lists, *short_list = lists + (rows + 1);
             sym_flags_kernel<<<grid_for(rows, 256), 256, 0, st>>>(row_off, rows, seg_prefix,
@@ -1673,7 +1717,7 @@ int multiply(Call &call, const nacho_csr *a, const nacho_csr *b, Product *z) {
             NACHO_TRY_HIP(hipGetLastError());
             sym_short_kernel<<<static_cast<unsigned>(g_short), kSymShortBlock, 0, st>>>(
                 a->dim_j_offsets, a->dim_j_indices, b->dim_j_offsets, b->dim_j_indices,
-                short_list, counts, work, seg_prefix, seg_nnz);
+                short_list, counts, seg_prefix, seg_nnz);
             NACHO_TRY_HIP(hipGetLastError());
             NACHO_TRY(scan::exclusive_scan_i64(call, seg_nnz, n_seg, seg_out));
         }
