@@ -49,6 +49,7 @@ namespace sssmm {
 constexpr int kBlock = 256;
 constexpr int kChunk = 4096;       // probes per workgroup
 constexpr int kPer = kChunk / kBlock;
+constexpr int kBatch = 4;  // probe rounds whose loads are issued together
 constexpr uint32_t kEmptyKey = 0xffffffffu;
 constexpr uint64_t kEmptySlot = 0x00000000ffffffffull;  // value bits 0, key empty
 constexpr uint32_t kWalkB = 0x80000000u;  // entry flag: walk B's column, probe A's row table
@@ -321,41 +322,84 @@ __global__ __launch_bounds__(kBlock) void probe_kernel(
         s_e[pad(base + u)] = run;
     }
     __syncthreads();
-    // probes, kBlock consecutive ones per round so a wavefront holds 64 consecutive probes
-    for (int x = threadIdx.x; x < kChunk; x += kBlock) {
-        const bool live = x < n;
-        const int64_t e = e_lo + (live ? s_e[pad(x)] : 0);
-        double v = 0.0;
-        int h = 0;
-        if (live) {
-            const int64_t t = c0 + x - woff[e];
-            const uint32_t pm = probe_mask[e];
-            const int64_t wb = walk_base[e] + t;
-            const uint32_t mask = pm & ~kWalkB;
-            float a, b;
-            bool found;
-            if (pm & kWalkB) {
-                b = csc_val[wb];
-                found = table_find(tab_a, probe_base[e], mask, static_cast<uint32_t>(csc_row[wb]),
-                                   &a);
-            } else {
-                a = va[wb];
-                found = table_find(tab_b, probe_base[e], mask, static_cast<uint32_t>(ca[wb]), &b);
-            }
-            if (found) {
-                const float ab = a * b;
-                v = static_cast<double>(ab * vc[e]);
-                h = 1;
+    // probes, kBlock consecutive ones per round so a wavefront holds 64 consecutive probes.
+    // kBatch rounds at a time: each step of a probe's chain of dependent loads (the entry's
+    // fields, the walked entry, the table slot) is issued for all of them before the next,
+    // so that kBatch chains are in flight per lane.
+    static_assert(kPer % kBatch == 0, "rounds come in whole batches");
+    for (int r0 = 0; r0 < kPer; r0 += kBatch) {
+        bool live[kBatch];
+        int64_t e[kBatch], wb[kBatch], tb[kBatch];
+        uint32_t pm[kBatch];
+#pragma unroll
+        for (int g = 0; g < kBatch; ++g) {
+            const int x = threadIdx.x + (r0 + g) * kBlock;
+            live[g] = x < n;
+            e[g] = e_lo + (live[g] ? s_e[pad(x)] : 0);
+        }
+#pragma unroll
+        for (int g = 0; g < kBatch; ++g) {
+            const int x = threadIdx.x + (r0 + g) * kBlock;
+            pm[g] = probe_mask[e[g]];
+            wb[g] = walk_base[e[g]] + (c0 + x - woff[e[g]]);
+            tb[g] = probe_base[e[g]];
+        }
+        uint32_t key[kBatch];
+        float own[kBatch];  // the walked entry's value
+#pragma unroll
+        for (int g = 0; g < kBatch; ++g) {
+            key[g] = 0;
+            own[g] = 0.0f;
+            if (live[g]) {
+                const bool walk_b = (pm[g] & kWalkB) != 0;
+                key[g] = static_cast<uint32_t>(walk_b ? csc_row[wb[g]] : ca[wb[g]]);
+                own[g] = walk_b ? csc_val[wb[g]] : va[wb[g]];
             }
         }
-        const int seg = live ? static_cast<int>(e - e_lo) : -1;
-        wave_segmented_sum(seg, v, h);
-        const int l = dev::lane();
-        const int next_seg = __shfl_down(seg, 1, dev::kWave);
-        const bool tail = live && (l == dev::kWave - 1 || next_seg != seg);
-        if (tail && h > 0) {
-            atomicAdd(&acc[e], v);
-            hit[e] = 1;
+        uint32_t slot[kBatch];
+        uint64_t w[kBatch];
+#pragma unroll
+        for (int g = 0; g < kBatch; ++g) {  // first probe of every table
+            const uint32_t mask = pm[g] & ~kWalkB;
+            slot[g] = mix(key[g]) & mask;
+            w[g] = kEmptySlot;
+            if (live[g]) w[g] = ((pm[g] & kWalkB) ? tab_a : tab_b)[tb[g] + slot[g]];
+        }
+        float cv[kBatch];
+#pragma unroll
+        for (int g = 0; g < kBatch; ++g) cv[g] = live[g] ? vc[e[g]] : 0.0f;
+#pragma unroll
+        for (int g = 0; g < kBatch; ++g) {
+            double v = 0.0;
+            int h = 0;
+            if (live[g]) {
+                const uint32_t mask = pm[g] & ~kWalkB;
+                const uint64_t *tab = (pm[g] & kWalkB) ? tab_a : tab_b;
+                uint64_t ww = w[g];
+                uint32_t hh = slot[g];
+                // collisions: the next slots, one at a time
+                while (static_cast<uint32_t>(ww) != key[g] &&
+                       static_cast<uint32_t>(ww) != kEmptyKey) {
+                    hh = (hh + 1) & mask;
+                    ww = tab[tb[g] + hh];
+                }
+                if (static_cast<uint32_t>(ww) == key[g]) {
+                    const float other = __uint_as_float(static_cast<uint32_t>(ww >> 32));
+                    // a * b with a from A and b from B, as the reference writes it
+                    const float ab = (pm[g] & kWalkB) ? other * own[g] : own[g] * other;
+                    v = static_cast<double>(ab * cv[g]);
+                    h = 1;
+                }
+            }
+            const int seg = live[g] ? static_cast<int>(e[g] - e_lo) : -1;
+            wave_segmented_sum(seg, v, h);
+            const int l = dev::lane();
+            const int next_seg = __shfl_down(seg, 1, dev::kWave);
+            const bool tail = live[g] && (l == dev::kWave - 1 || next_seg != seg);
+            if (tail && h > 0) {
+                atomicAdd(&acc[e[g]], v);
+                hit[e[g]] = 1;
+            }
         }
     }
 }
