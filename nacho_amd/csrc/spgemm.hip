@@ -69,7 +69,10 @@ constexpr int kDenseBits = 13;          // dense accumulation window: 8192 colum
 constexpr int kDenseCols = 1 << kDenseBits;
 constexpr int kMaxBucketBits = 10;      // at most 1024 column buckets per long row
 constexpr int kMaxBuckets = 1 << kMaxBucketBits;
-constexpr int kDenseMin = kShort;       // a long row's bucket above this is accumulated densely
+// A long row's bucket with more products than this is accumulated densely (its 8192-column
+// window in LDS) rather than by a bitmap or sort unit.  At C4, 1536 / 2048 (one box, two
+// rounds): 95.46 / 95.45 against 96.66 / 95.98 ms; 1024 and 1280 lose.
+constexpr int kDenseMin = 1536;
 constexpr int kMaxBitmapSegs = 256;     // segments (empty ones included) of a bitmap unit
 constexpr int kMaxBitmapBuckets = 32;   // nonempty buckets of a bitmap unit (larger buckets)
 constexpr int kBitmapWords = 8192 / 32; // one bit per column of an 8192-column bucket
@@ -79,8 +82,9 @@ constexpr int kHistGrid = 8192;         // workgroups of the long-row histogram
 // neighbouring buckets gather adjacent ranges of the same B rows, which then share one L2.
 // At C4 the unit kernels fetched 124 -> 105 GB per call (96.97 -> 95.58 ms) with groups of
 // 64; one contiguous range per XCD fetched as little but took 102.2 ms (the XCDs' loads no
-// longer matched).
-constexpr unsigned kXcdGroup = 64;
+// longer matched).  Groups of 128 / 256 against 64, one box, two rounds each: 96.10 / 95.88,
+// 95.67 / 95.54 against 96.66 / 95.98 ms.
+constexpr unsigned kXcdGroup = 256;
 
 static_assert(kTile == 1 << kOrdBits, "segment ordinals must fit kOrdBits");
 static_assert(kTile == kBlock * kPer, "a unit's products are kPer per lane");
