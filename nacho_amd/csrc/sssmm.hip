@@ -49,7 +49,7 @@ namespace sssmm {
 constexpr int kBlock = 256;
 constexpr int kChunk = 4096;       // probes per workgroup
 constexpr int kPer = kChunk / kBlock;
-constexpr int kBatch = 4;  // probe rounds whose loads are issued together
+constexpr int kBatch = 2;  // probe rounds whose loads are issued together
 constexpr uint32_t kEmptyKey = 0xffffffffu;
 constexpr uint64_t kEmptySlot = 0x00000000ffffffffull;  // value bits 0, key empty
 constexpr uint32_t kWalkB = 0x80000000u;  // entry flag: walk B's column, probe A's row table
