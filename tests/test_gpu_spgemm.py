@@ -46,6 +46,14 @@ def spgemm(a, b, rows, inner, cols, device, wide=True):
             z.values.cpu().numpy())
 
 
+@pytest.fixture(params=["staged", "symbolic"])
+def output_mode(request, monkeypatch):
+    """Both ways of sizing the result: staged output and copy, or the symbolic pass first
+    (NACHO_SPGEMM_OUTPUT; by default the library picks by free memory)."""
+    monkeypatch.setenv("NACHO_SPGEMM_OUTPUT", request.param)
+    return request.param
+
+
 def check(rows, inner, cols, a, b, z, what):
     pos, crd, val = z
     check_csr_invariants(pos, crd, rows, cols)
@@ -62,7 +70,7 @@ def run_and_check(gpu, rows, inner, cols, a, b, what, wide=True):
 
 
 @pytest.mark.parametrize("wide", [True, False])
-def test_reference_smoke_case(gpu, wide):
+def test_reference_smoke_case(gpu, wide, output_mode):
     rng = np.random.default_rng(0)
     a = random_csr(rng, 200, 180, 0.05)
     b = random_csr(rng, 180, 200, 0.05)
@@ -75,7 +83,7 @@ def test_reference_smoke_case(gpu, wide):
                                                 ((64, 5000, 64), 0.3, 3),
                                                 ((1, 300, 20000), 0.5, 4),
                                                 ((20000, 50, 1), 0.2, 5)])
-def test_random_shapes(gpu, shape, density, seed):
+def test_random_shapes(gpu, shape, density, seed, output_mode):
     rows, inner, cols = shape
     rng = np.random.default_rng(seed)
     a = random_csr(rng, rows, inner, density)
@@ -95,7 +103,7 @@ def product_rows(lengths, cols, rng):
     return a, b
 
 
-def test_tile_boundaries(gpu):
+def test_tile_boundaries(gpu, output_mode):
     """Rows of exactly 1, kShort, kShort+1, one tile, one tile + 1 and several tiles of
     products, with empty rows between (tiles: 4096 products; short rows: <= 2048)."""
     rng = np.random.default_rng(7)
@@ -106,7 +114,7 @@ def test_tile_boundaries(gpu):
     run_and_check(gpu, n, n, 50000, a, b, "tile boundaries")
 
 
-def test_many_short_rows_share_tiles(gpu):
+def test_many_short_rows_share_tiles(gpu, output_mode):
     rng = np.random.default_rng(8)
     lengths = rng.integers(0, 40, 30000)
     lengths[rng.random(30000) < 0.3] = 0
@@ -205,7 +213,7 @@ def test_wide_columns_use_64bit_keys(gpu):
     run_and_check(gpu, rows, inner, cols, a, (pb, cb.astype(np.int32), vb), "wide cols")
 
 
-def test_cancellation_keeps_entry(gpu):
+def test_cancellation_keeps_entry(gpu, output_mode):
     a = csr_from_rows(1, 2, [[0, 1]], np.array([1.0, -1.0], np.float32))
     b = csr_from_rows(2, 5, [[3], [3]], np.array([2.5, 2.5], np.float32))
     pos, crd, val = spgemm(a, b, 1, 2, 5, gpu)
@@ -213,7 +221,7 @@ def test_cancellation_keeps_entry(gpu):
 
 
 @pytest.mark.parametrize("wide", [True, False])
-def test_empty_operands(gpu, wide):
+def test_empty_operands(gpu, wide, output_mode):
     a = csr_from_rows(3, 4, [[], [], []])
     b = csr_from_rows(4, 5, [[1], [], [2], []])
     pos, crd, val = spgemm(a, b, 3, 4, 5, gpu, wide)
@@ -228,7 +236,7 @@ def test_empty_operands(gpu, wide):
     assert pos.tolist() == [0]
 
 
-def test_identity_exact(gpu):
+def test_identity_exact(gpu, output_mode):
     rng = np.random.default_rng(11)
     n = 5000
     a = random_csr(rng, n, n, 0.002)
@@ -248,7 +256,7 @@ def test_dimension_mismatch_raises(gpu):
         nacho_amd.gpu_spgemm64_f32(to_gpu(a, 2, 3, gpu), to_gpu(b, 4, 3, gpu))
 
 
-def test_rmat_medium(gpu):
+def test_rmat_medium(gpu, output_mode):
     from nacho_amd import synth
 
     n = 1 << 15
@@ -257,7 +265,7 @@ def test_rmat_medium(gpu):
     run_and_check(gpu, n, n, n, t, t, "rmat15")
 
 
-def test_repeatable(gpu):
+def test_repeatable(gpu, output_mode):
     """Structure is identical run to run; values agree to within one float32 rounding of the
     float64 sums (their summation order follows the scatter's arrival order)."""
     from nacho_amd import synth
