@@ -105,3 +105,28 @@ def test_c2_rows_as_dcsr(gpu, op):
     mats = [dcsr_of(sp.csr_matrix((val, crd, pos), shape=(rows, cols)))
             for pos, crd, val in ops]
     assert_dcsr_equal(run(op, (rows, cols), *mats, gpu), want(op, *mats), f"C2 dcsr {op}")
+
+
+def _hypersparse(rng, rows, cols, n_rows, shared=None):
+    """DCSR levels with n_rows stored rows scattered over [0, rows) (plus the rows in
+    `shared`), 1-5 entries each."""
+    ids = set(rng.choice(rows, size=n_rows, replace=False).tolist())
+    if shared is not None:
+        ids |= set(shared)
+    ci = np.array(sorted(ids), np.int32)
+    lens = rng.integers(1, 6, len(ci))
+    pj = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    cj = np.concatenate([np.sort(rng.choice(cols, size=int(k), replace=False)) for k in lens])
+    return (ci, pj, cj.astype(np.int32)), rng.uniform(-1, 1, len(cj)).astype(np.float32)
+
+
+@pytest.mark.parametrize("op", ["add", "mul"])
+def test_hypersparse_rows(gpu, op):
+    """A row extent of 2^30 with a few thousand stored rows per operand (half of them shared,
+    some with an empty column intersection): nothing may scale with the row extent."""
+    rng = np.random.default_rng(31)
+    rows, cols = 1 << 30, 64
+    shared = rng.choice(rows, size=1500, replace=False).tolist()
+    a = _hypersparse(rng, rows, cols, 1500, shared)
+    b = _hypersparse(rng, rows, cols, 1500, shared)
+    assert_dcsr_equal(run(op, (rows, cols), a, b, gpu), want(op, a, b), f"hypersparse {op}")
