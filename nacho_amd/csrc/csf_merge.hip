@@ -25,6 +25,7 @@
 #include <cstdint>
 
 #include "csr_merge.hpp"
+#include "device_utils.hpp"
 #include "runtime.hpp"
 
 namespace nacho {
@@ -200,7 +201,9 @@ __global__ void csf_row_offsets_kernel(CsfKeysJob ja, CsfKeysJob jb, int rows) {
 __global__ __launch_bounds__(256) void csf_keys_kernel(CsfKeysJob ja, CsfKeysJob jb, int ga,
                                                        int gb, int kbits) {
     constexpr int W = 64;
+    __shared__ int s_mark[256 / W][W];  // per wave: the last fibre starting at each window slot
     const int lane = static_cast<int>(threadIdx.x) % W;
+    int *mark = s_mark[threadIdx.x / W];
     const long long g = static_cast<long long>(blockIdx.x) * (blockDim.x / W) + threadIdx.x / W;
     if (g >= static_cast<long long>(ga) + gb) return;  // whole waves
     const bool first = g < ga;
@@ -217,24 +220,33 @@ __global__ __launch_bounds__(256) void csf_keys_kernel(CsfKeysJob ja, CsfKeysJob
     const int e1 = pk[f0 + nf];  // end of the group's entries
     const int jhi = cj[f] << kbits;
     const int e0 = __shfl(start, 0, W);
-    constexpr int U = 4;  // entries per lane whose loads are issued together
-    for (int base = e0; base < e1; base += U * W) {  // uniform: every lane shuffles
+    const bool mine = lane < nf;
+    mark[lane] = 0;
+    dev::wave_sync();
+    constexpr int U = 4;  // windows of W entries whose loads are issued together
+    for (int base = e0; base < e1; base += U * W) {  // uniform
         int kv[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) kv[u] = ck[min(base + u * W + lane, e1 - 1)];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int e = base + u * W + lane;
-            // the last lane l < nf with start(l) <= e, in six steps
-            int lo = 0;
-#pragma unroll
-            for (int step = W / 2; step > 0; step >>= 1) {
-                const int cand = lo + step;
-                const int v = __shfl(start, min(cand, nf - 1), W);
-                if (cand < nf && v <= e) lo = cand;
-            }
-            const int hi_bits = __shfl(jhi, lo, W);
+            // The fibre of entry wb + x is the last fibre starting at or before it: the
+            // fibres starting at or before wb (a ballot), then the last one starting inside
+            // the window up to x (marks by start slot, the largest fibre winning where
+            // empty fibres share a start, and a running maximum over the lanes).
+            const int wb = base + u * W;
+            const int before = __popcll(__ballot(mine && start <= wb));
+            const int d = start - wb;
+            if (mine && d > 0 && d < W) atomicMax(&mark[d], lane + 1);
+            dev::wave_sync();
+            const int m = mark[lane];
+            mark[lane] = 0;
+            const int run = dev::wave_inclusive_max_dpp(m);
+            const int fib = run > 0 ? run - 1 : before - 1;
+            const int hi_bits = __shfl(jhi, fib, W);
+            const int e = wb + lane;
             if (e < e1) key[e] = hi_bits | kv[u];
+            dev::wave_sync();  // the marks are cleared before the next window's
         }
     }
 }

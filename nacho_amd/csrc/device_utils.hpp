@@ -60,6 +60,14 @@ __device__ __forceinline__ T wave_inclusive_sum(T v) {
     }
 }
 
+// Orders one wavefront's LDS accesses across its lanes.  The LDS processes a wavefront's
+// instructions in order, so only the compiler must not move accesses across this point; a
+// workgroup-scope fence would also wait for the wavefront's outstanding global stores.
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+
 // Sum over the 64 lanes, result in every lane.
 template <typename T>
 __device__ __forceinline__ T wave_sum(T v) {

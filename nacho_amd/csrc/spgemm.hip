@@ -885,13 +885,7 @@ __global__ __launch_bounds__(kBlock) void sort_unit_kernel(
 
 // ---- 5b: bitmap units ------------------------------------------------------------------
 
-// Orders one wavefront's LDS accesses across its lanes.  The LDS processes a wavefront's
-// instructions in order, so only the compiler must not move accesses across this point; a
-// workgroup-scope fence would also wait for the wavefront's outstanding global stores.
-__device__ __forceinline__ void wave_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-}
+using dev::wave_sync;
 
 // Marks the columns of a bucket (window offsets s_col[x0, x1)) in bm.
 __device__ __forceinline__ void mark_bucket(unsigned *bm, const unsigned short *s_col, int x0,
