@@ -191,6 +191,67 @@ def test_add_one_entry_against_twenty(gpu, rows):
                      f"one entry against twenty, {rows} rows")
 
 
+def _rows_of(pos):
+    return np.repeat(np.arange(len(pos) - 1), np.diff(pos.astype(np.int64)))
+
+
+def _csr_from_coo(rows, r, c, v):
+    order = np.lexsort((c, r))
+    pos = np.zeros(rows + 1, np.int64)
+    np.cumsum(np.bincount(r, minlength=rows), out=pos[1:])
+    return pos.astype(np.int32), c[order].astype(np.int32), v[order].astype(np.float32)
+
+
+def _pair_free_operands(case, rows=1 << 16):
+    """Union operands whose write chunks hold no pairs, or only some of them.  A's columns
+    are even and B's odd (Zipf rows of C2's generator, column range doubled); 45% of the rows
+    keep only A's entries and 45% only B's.  'disjoint': that alone (no pair; the count
+    searches the rows holding both sides and finds none); 'planted': plus one shared column
+    in every 31st row holding both sides (some chunks with pairs); 'half_equal': B's rows below
+    rows / 2 are A's columns (pairs in half the entries, so the count walks the tiles and
+    counts outputs, and the chunks of the upper half have none)."""
+    from nacho_amd import synth
+
+    rng = np.random.default_rng(41)
+    a = synth.zipf_csr(rows, 42)
+    b = synth.zipf_csr(rows, 43)
+    side = rng.choice(3, rows, p=[0.45, 0.45, 0.10])  # 0: A only, 1: B only, 2: both
+    ra, rb = _rows_of(a[0]), _rows_of(b[0])
+    ka, kb = side[ra] != 1, side[rb] != 0
+    ar, ac, av = ra[ka], 2 * a[1][ka].astype(np.int64), a[2][ka]
+    br, bc, bv = rb[kb], 2 * b[1][kb].astype(np.int64) + 1, b[2][kb]
+    if case == "planted":
+        a_first = {}
+        for r_, c_ in zip(ar[::-1], ac[::-1]):
+            a_first[r_] = c_
+        planted = [r_ for r_ in range(0, rows, 31) if side[r_] == 2 and r_ in a_first
+                   and np.any(br == r_)]
+        assert planted
+        br = np.concatenate([br, planted])
+        bc = np.concatenate([bc, [a_first[r_] for r_ in planted]])
+        bv = np.concatenate([bv, rng.uniform(-1, 1, len(planted)).astype(np.float32)])
+    elif case == "half_equal":
+        low_a, low_b = ar < rows // 2, br < rows // 2
+        br = np.concatenate([br[~low_b], ar[low_a]])
+        bc = np.concatenate([bc[~low_b], ac[low_a]])
+        bv = np.concatenate([bv[~low_b], rng.uniform(-1, 1, int(low_a.sum())).astype(np.float32)])
+    return _csr_from_coo(rows, ar, ac, av), _csr_from_coo(rows, br, bc, bv), 2 * rows
+
+
+@pytest.mark.parametrize("case", ["disjoint", "planted", "half_equal"])
+def test_add_chunks_without_pairs(gpu, case):
+    """Unions whose write chunks hold no pairs (all, most, or the upper half's): the count's
+    pair search finding none or a few, and the count walk over tiles half of which merge
+    nothing.  Bit-exact against the numpy closed form."""
+    rows = 1 << 16
+    a, b, cols = _pair_free_operands(case, rows)
+    print(f"[gpu] csr_add chunks without pairs case={case} nnz=({len(a[1])},{len(b[1])})",
+          flush=True)
+    got = gpu_op("add", a, b, rows, cols, gpu)
+    assert_csr_equal(got, oracle.closed_csr_binary("add", rows, cols, *a, *b),
+                     f"chunks without pairs: {case}")
+
+
 def test_c2_full_size_add(gpu):
     """BASELINE C2 at full size: bit-exact against the oracle, plus invariants."""
     from nacho_amd import synth
