@@ -190,14 +190,17 @@ __global__ void csf_row_offsets_kernel(CsfKeysJob ja, CsfKeysJob jb, int rows) {
 
 // Column keys of both operands: cj[f] << kbits | ck[e] for every k entry e of fibre f.  One
 // wavefront per group of 64 consecutive fibres (groups [0, ga) are A's, the rest B's): lane l
-// holds fibre f0 + l's offset and j bits, and the wave strides over the group's k entries
-// with consecutive lanes on consecutive entries, each finding its fibre among the 64 offsets
-// by a six-step search over the lanes (ds_bpermute, every lane active).
+// holds fibre f0 + l's offset and j bits, and the wave strides over the group's k entries in
+// windows of 64, consecutive lanes on consecutive entries.  An entry's fibre is the last one
+// starting at or before it: a ballot counts the fibres starting at or before the window's
+// first entry, and the fibres starting inside the window mark their start slot in LDS, so a
+// running maximum over the lanes gives each entry the last fibre starting up to it.
 //
 // Measured alternatives at C5 (19.8M entries in 7.75M fibres per operand): one fibre per
 // thread, 515 us; 256 fibres per wave staged in LDS, 164 us; one wave per 1024 entries
-// (fibres of a Zipf-heavy i hold about 60 entries) with 1025 staged fibres, 232 us; this
-// form, 148 us.
+// (fibres of a Zipf-heavy i hold about 60 entries) with 1025 staged fibres, 232 us; each
+// entry's fibre by a six-step search over the lanes' offsets (ds_bpermute), 148 us; this
+// form, 103 us.
 __global__ __launch_bounds__(256) void csf_keys_kernel(CsfKeysJob ja, CsfKeysJob jb, int ga,
                                                        int gb, int kbits) {
     constexpr int W = 64;
