@@ -493,43 +493,59 @@ __device__ __forceinline__ void walk3(Lane3Out &out, const Split3 &sp, int tile,
         }
         if (s < steps) {
             if (xa == kMax && xb == kMax && xc == kMax) {  // row end
+                // (reads at indices always inside the staged arrays, then selects: no
+                // nested branches, each waiting for its own read)
                 row_ends |= 1u << s;
                 k = min(k + 1, nr - 1);
-                aE = ea(k);
-                bE = eb(k);
-                cE = ec(k);
+                const int kn = min(k + 1, nr - 1);
+                const unsigned wn = s_row[kn];
+                const int cn = s_rowc[kn];
+                const int ha = at(ia), hb = at(ib), hc = at(ic);
+                const bool last_row = k >= nr - 1;
+                aE = last_row ? na : static_cast<int>(wn & 0xffffu);
+                bE = last_row ? nab : na + static_cast<int>(wn >> 16);
+                cE = last_row ? n : nab + cn;
                 last = INT_MIN;
-                xa = ia < aE ? at(ia) : kMax;
-                xb = ib < bE ? at(ib) : kMax;
-                xc = ic < cE ? at(ic) : kMax;
+                xa = ia < aE ? ha : kMax;
+                xb = ib < bE ? hb : kMax;
+                xc = ic < cE ? hc : kMax;
             } else {
                 const int x = min(xa, min(xb, xc));
-                const int which = xa == x ? 0 : (xb == x ? 1 : 2);  // ties: A, B, C
+                const bool ta = xa == x;  // ties: A, then B, then C
+                const bool tb = !ta && xb == x;
+                const bool tc = !ta && !tb;
                 const bool emit = x != last;
                 if (COUNT_ONLY) {
                     count += emit;
                 } else {
                     out.crd[s] = x;
                     if (VALUES) {
-                        // the group's sum in operand order, from its first item
-                        float v = s_val[min(which == 0 ? ia : (which == 1 ? ib : ic), kCap - 1)];
-                        if (which == 0 && xb == x) v = v + s_val[min(ib, kCap - 1)];
-                        if (which <= 1 && xc == x) v = v + s_val[min(ic, kCap - 1)];
+                        // the group's sum in operand order, from its first item: the three
+                        // reads are independent (indices inside the staged arrays), and the
+                        // additions the group does not hold are discarded
+                        const int own = ta ? ia : (tb ? ib : ic);
+                        const float v0 = s_val[min(own, kCap - 1)];
+                        const float v1 = s_val[min(ib, kCap - 1)];
+                        const float v2 = s_val[min(ic, kCap - 1)];
+                        const float vab = v0 + v1;
+                        float v = (ta && xb == x) ? vab : v0;
+                        const float vabc = v + v2;
+                        v = ((ta || tb) && xc == x) ? vabc : v;
                         out.val[s] = v;
                     }
                     valid |= static_cast<unsigned>(emit) << s;
                 }
                 last = x;
-                if (which == 0) {
-                    ++ia;
-                    xa = ia < aE ? at(ia) : kMax;
-                } else if (which == 1) {
-                    ++ib;
-                    xb = ib < bE ? at(ib) : kMax;
-                } else {
-                    ++ic;
-                    xc = ic < cE ? at(ic) : kMax;
-                }
+                ia += ta;
+                ib += tb;
+                ic += tc;
+                const int np = ta ? ia : (tb ? ib : ic);  // reload the head that advanced
+                const int ne = ta ? aE : (tb ? bE : cE);
+                const int h0 = at(np);
+                const int h = np < ne ? h0 : kMax;
+                xa = ta ? h : xa;
+                xb = tb ? h : xb;
+                xc = tc ? h : xc;
             }
         }
     }
