@@ -875,25 +875,32 @@ __device__ __forceinline__ void pair_tile(
                 int xa = ia < iae ? sh.crd[offA + ia] : kEnd;
                 int xb = ib < ibe ? sh.crd[offB + ib] : kEnd;
                 unsigned pairs = 0;
+                // (reads at indices inside the staged arrays, then selects: no nested
+                // branches, each waiting for its own read)
+                auto crd_at = [&](int x) { return sh.crd[min(x, kGrainCap - 1)]; };
 #pragma unroll
                 for (int st = 0; st < kItemsPerLane + 1; ++st) {
                     if (st < steps) {
                         if (xa == kEnd && xb == kEnd) {  // row end
                             ++r;
-                            iae = end_a(r);
-                            ibe = end_b(r);
-                            xa = ia < iae ? sh.crd[offA + ia] : kEnd;
-                            xb = ib < ibe ? sh.crd[offB + ib] : kEnd;
+                            const int rn = min(r + 1, nr - 1);
+                            const int an = sh.ra[rn], bn = sh.rb[rn];
+                            const int ha = crd_at(offA + ia), hb = crd_at(offB + ib);
+                            const bool last_row = r + 1 >= nr;
+                            iae = last_row ? na : an;
+                            ibe = last_row ? nb : bn;
+                            xa = ia < iae ? ha : kEnd;
+                            xb = ib < ibe ? hb : kEnd;
                         } else {
                             const bool take_a = xa <= xb;
                             pairs += (take_a && xa == xb) ? 1u : 0u;
-                            if (take_a) {
-                                ++ia;
-                                xa = ia < iae ? sh.crd[offA + ia] : kEnd;
-                            } else {
-                                ++ib;
-                                xb = ib < ibe ? sh.crd[offB + ib] : kEnd;
-                            }
+                            ia += take_a;
+                            ib += !take_a;
+                            const bool in = take_a ? ia < iae : ib < ibe;
+                            const int h0 = crd_at(take_a ? offA + ia : offB + ib);
+                            const int h = in ? h0 : kEnd;
+                            xa = take_a ? h : xa;
+                            xb = take_a ? xb : h;
                         }
                     }
                 }
