@@ -685,11 +685,11 @@ __device__ __forceinline__ void merge_sort(K (&k)[kPer], float (&v)[kPer], K *s_
                 v[u] = s_val[pad(src)];
                 a += take_a;
                 b += !take_a;
-                if (take_a) {
-                    ka = s_key[pad(A + min(a, len - 1))];
-                } else {
-                    kb = s_key[pad(B + min(b, len - 1))];
-                }
+                // the head that advanced, read at an index inside its run, then selected:
+                // no branch whose sides wait for their own reads
+                const K kn = s_key[pad(take_a ? A + min(a, len - 1) : B + min(b, len - 1))];
+                ka = take_a ? kn : ka;
+                kb = take_a ? kb : kn;
             }
         }
         __syncthreads();
