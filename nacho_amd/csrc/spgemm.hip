@@ -226,6 +226,43 @@ struct BRuns {
     const int *run_start;
 };
 
+// The runs of a work block's A entries, dealt evenly over the workgroup: an A entry's B row
+// may hold one run or a hundred (a hub), so one lane per entry leaves most lanes of a
+// wavefront waiting for its longest.  Every lane publishes its entry's run count, first run
+// and A value; the block's T runs (entry by entry) are then taken kRunsPer per lane per
+// round, run j by lane j mod kBlock, which finds the entry owning j with a fixed eight-step
+// search of the entries' run offsets in LDS (the kRunsPer searches interleaved).
+constexpr int kRunsPer = 4;
+
+struct BlockRuns {
+    int off[kBlock];      // exclusive scan of the entries' run counts
+    int64_t q0[kBlock];   // first run of the entry's B row in br.run
+    float a[kBlock];      // the entry's A value
+    int wave[kBlock / dev::kWave];
+};
+
+// Publishes this lane's entry (n_runs runs from q0, A value a); returns T.  Ends synchronised.
+__device__ __forceinline__ int publish_runs(BlockRuns &sh, int n_runs, int64_t q0, float a) {
+    int total = 0;
+    const int off = dev::block_exclusive_sum<kBlock>(n_runs, sh.wave, total);
+    sh.off[threadIdx.x] = off;
+    sh.q0[threadIdx.x] = q0;
+    sh.a[threadIdx.x] = a;
+    __syncthreads();
+    return total;
+}
+
+// Run j of the block (j < T): its index in br.run and its entry's A value.
+__device__ __forceinline__ void block_run(const BlockRuns &sh, int j, int64_t &q, float &a) {
+    int lo = 0;  // last entry whose first run is at or before j (off[0] = 0)
+#pragma unroll
+    for (int step = kBlock / 2; step > 0; step >>= 1) {
+        lo += sh.off[lo + step] <= j ? step : 0;
+    }
+    q = sh.q0[lo] + (j - sh.off[lo]);
+    a = sh.a[lo];
+}
+
 // Work blocks strided over the grid (a heavy row's blocks land on different workgroups):
 // every thread takes one A entry of the block and adds, per run of its B row, the run's
 // length and one run to LDS histograms of the row's buckets; nonzero bins are then added to
@@ -238,6 +275,7 @@ __global__ __launch_bounds__(kBlock) void long_hist_kernel(
     int64_t *__restrict__ seg_len, int64_t *__restrict__ seg_runs) {
     __shared__ int s_hist[kMaxBuckets];
     __shared__ int s_runs[kMaxBuckets];
+    __shared__ BlockRuns sh;
     const int64_t n_blk = blk_off[rows];
     for (int64_t blk = blockIdx.x; blk < n_blk; blk += gridDim.x) {
         const int i = blk_row[blk];
@@ -246,27 +284,30 @@ __global__ __launch_bounds__(kBlock) void long_hist_kernel(
             s_hist[b] = 0;
             s_runs[b] = 0;
         }
-        __syncthreads();
         const int p = pos_a[i] + static_cast<int>(blk - first) * kBlock + threadIdx.x;
+        int64_t q0 = 0;
+        int n_runs = 0;
         if (p < pos_a[i + 1]) {
             const int k = crd_a[p];
-            const int64_t q0 = br.run_idx[pos_b[k]];
-            const int n_runs = static_cast<int>(br.run_idx[pos_b[k + 1]] - q0);
-            const int2 *r = br.run + q0;
-            // four runs per iteration, so that four loads are in flight
-            int j = 0;
-            for (; j + 4 <= n_runs; j += 4) {
-                const int2 x0 = r[j], x1 = r[j + 1], x2 = r[j + 2], x3 = r[j + 3];
-                if (x0.x < nb) { atomicAdd(&s_hist[x0.x], x0.y); atomicAdd(&s_runs[x0.x], 1); }
-                if (x1.x < nb) { atomicAdd(&s_hist[x1.x], x1.y); atomicAdd(&s_runs[x1.x], 1); }
-                if (x2.x < nb) { atomicAdd(&s_hist[x2.x], x2.y); atomicAdd(&s_runs[x2.x], 1); }
-                if (x3.x < nb) { atomicAdd(&s_hist[x3.x], x3.y); atomicAdd(&s_runs[x3.x], 1); }
+            q0 = br.run_idx[pos_b[k]];
+            n_runs = static_cast<int>(br.run_idx[pos_b[k + 1]] - q0);
+        }
+        // (its barriers also order the clears above before the adds below)
+        const int T = publish_runs(sh, n_runs, q0, 0.0f);
+        for (int j0 = 0; j0 < T; j0 += kRunsPer * kBlock) {  // uniform
+            int2 x[kRunsPer];
+#pragma unroll
+            for (int u = 0; u < kRunsPer; ++u) {
+                int64_t q;
+                float a;
+                block_run(sh, min(j0 + u * kBlock + static_cast<int>(threadIdx.x), T - 1), q, a);
+                x[u] = br.run[q];
             }
-            for (; j < n_runs; ++j) {
-                const int2 x = r[j];
-                if (x.x < nb) {
-                    atomicAdd(&s_hist[x.x], x.y);
-                    atomicAdd(&s_runs[x.x], 1);
+#pragma unroll
+            for (int u = 0; u < kRunsPer; ++u) {
+                if (j0 + u * kBlock + static_cast<int>(threadIdx.x) < T && x[u].x < nb) {
+                    atomicAdd(&s_hist[x[u].x], x[u].y);
+                    atomicAdd(&s_runs[x[u].x], 1);
                 }
             }
         }
@@ -319,34 +360,38 @@ __global__ __launch_bounds__(kBlock) void long_runs_kernel(
     int4 *__restrict__ desc) {
     __shared__ int s_cnt[kMaxBuckets];
     __shared__ int64_t s_base[kMaxBuckets];
+    __shared__ BlockRuns sh;
     const int64_t n_blk = blk_off[rows];
     for (int64_t blk = blockIdx.x; blk < n_blk; blk += gridDim.x) {
         const int i = blk_row[blk];
         const int64_t first = blk_off[i];
         for (int b = threadIdx.x; b < nb; b += kBlock) s_cnt[b] = 0;
-        __syncthreads();
         const int p = pos_a[i] + static_cast<int>(blk - first) * kBlock + threadIdx.x;
-        const bool mine = p < pos_a[i + 1];
         int64_t q0 = 0;
         int n_runs = 0;
-        float a = 0.0f;
-        if (mine) {
+        float a_mine = 0.0f;
+        if (p < pos_a[i + 1]) {
             const int k = crd_a[p];
-            a = val_a[p];
+            a_mine = val_a[p];
             q0 = br.run_idx[pos_b[k]];
             n_runs = static_cast<int>(br.run_idx[pos_b[k + 1]] - q0);
-            const int2 *rr = br.run + q0;
-            int j = 0;
-            for (; j + 4 <= n_runs; j += 4) {  // four loads in flight
-                const int b0 = rr[j].x, b1 = rr[j + 1].x, b2 = rr[j + 2].x, b3 = rr[j + 3].x;
-                if (b0 < nb) atomicAdd(&s_cnt[b0], 1);
-                if (b1 < nb) atomicAdd(&s_cnt[b1], 1);
-                if (b2 < nb) atomicAdd(&s_cnt[b2], 1);
-                if (b3 < nb) atomicAdd(&s_cnt[b3], 1);
+        }
+        // (its barriers also order the clears above before the counts below)
+        const int T = publish_runs(sh, n_runs, q0, a_mine);
+        for (int j0 = 0; j0 < T; j0 += kRunsPer * kBlock) {  // uniform
+            int2 x[kRunsPer];
+#pragma unroll
+            for (int u = 0; u < kRunsPer; ++u) {
+                int64_t q;
+                float a;
+                block_run(sh, min(j0 + u * kBlock + static_cast<int>(threadIdx.x), T - 1), q, a);
+                x[u] = br.run[q];
             }
-            for (; j < n_runs; ++j) {
-                const int bk = rr[j].x;
-                if (bk < nb) atomicAdd(&s_cnt[bk], 1);
+#pragma unroll
+            for (int u = 0; u < kRunsPer; ++u) {
+                if (j0 + u * kBlock + static_cast<int>(threadIdx.x) < T && x[u].x < nb) {
+                    atomicAdd(&s_cnt[x[u].x], 1);
+                }
             }
         }
         __syncthreads();
@@ -364,24 +409,27 @@ __global__ __launch_bounds__(kBlock) void long_runs_kernel(
             s_cnt[b] = 0;
         }
         __syncthreads();
-        for (int j0 = 0; j0 < n_runs; j0 += 4) {  // four runs' loads in flight
-            int2 x[4];
-            int first_b[4];
+        for (int j0 = 0; j0 < T; j0 += kRunsPer * kBlock) {  // uniform
+            int2 x[kRunsPer];
+            int first_b[kRunsPer];
+            float av[kRunsPer];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int64_t q = q0 + min(j0 + u, n_runs - 1);
+            for (int u = 0; u < kRunsPer; ++u) {
+                int64_t q;
+                block_run(sh, min(j0 + u * kBlock + static_cast<int>(threadIdx.x), T - 1), q,
+                          av[u]);
                 x[u] = br.run[q];
                 first_b[u] = br.run_start[q];
             }
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                if (j0 + u < n_runs && x[u].x < nb) {
+            for (int u = 0; u < kRunsPer; ++u) {
+                if (j0 + u * kBlock + static_cast<int>(threadIdx.x) < T && x[u].x < nb) {
                     const int64_t slot = s_base[x[u].x] + atomicAdd(&s_cnt[x[u].x], 1);
-                    desc[slot] = make_run(first_b[u], x[u].y, a);
+                    desc[slot] = make_run(first_b[u], x[u].y, av[u]);
                 }
             }
         }
-        __syncthreads();  // s_cnt and s_base are read before the next block resets them
+        __syncthreads();  // s_cnt, s_base and sh are read before the next block resets them
     }
 }
 
