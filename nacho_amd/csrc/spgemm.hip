@@ -985,6 +985,7 @@ __global__ __launch_bounds__(kBitmapBlock) void bitmap_unit_kernel(
     __shared__ int s_sid[kMaxBitmapSegs];
     __shared__ int s_out[kMaxBitmapSegs];
     __shared__ int s_wave[kWaves];
+    __shared__ int s_next;  // the next bucket to claim
     const int64_t u = bitmap_list[dev::xcd_block<kXcdGroup>()];
     const int64_t s0 = unit_seg[u];
     const int64_t s1 = u + 1 < n_units ? unit_seg[u + 1] : n_seg;
@@ -1000,7 +1001,10 @@ __global__ __launch_bounds__(kBitmapBlock) void bitmap_unit_kernel(
         s_base[ord] = static_cast<int>((s - seg_prefix[seg_row[s]]) << shift);
         s_sid[ord] = static_cast<int>(s);
     }
-    if (threadIdx.x == 0) s_x0[n_buckets] = n;
+    if (threadIdx.x == 0) {
+        s_x0[n_buckets] = n;
+        s_next = kWaves;  // wavefront w starts with bucket w
+    }
     // the unit's products from its runs: window offsets (bucket = column >> shift, so the
     // offset is the column's low bits) and values, staged once
     const int low = (1 << shift) - 1;
@@ -1029,7 +1033,8 @@ __global__ __launch_bounds__(kBitmapBlock) void bitmap_unit_kernel(
     // accumulate each bucket by rank; its distinct columns (window offsets, in order) and
     // their sums are left in its own product range, s_col / s_acc[x0 + rank]
     constexpr int kWordsPerLane = kBitmapWords / dev::kWave;
-    for (int o = w; o < n_buckets; o += kWaves) {
+    // Buckets differ widely in size: a wavefront that finishes one claims the next.
+    for (int o = w; o < n_buckets;) {  // uniform per wavefront
         const int x0 = s_x0[o], x1 = s_x0[o + 1];
         for (int x = x0 + l; x < x1; x += dev::kWave) s_acc[x] = 0.0;
         mark_bucket(bm, s_col, x0, x1);
@@ -1087,6 +1092,9 @@ __global__ __launch_bounds__(kBitmapBlock) void bitmap_unit_kernel(
         }
         if (l == dev::kWave - 1) s_out[o] = incl;  // the bucket's distinct columns
         wave_sync();
+        int claim = 0;
+        if (l == 0) claim = atomicAdd(&s_next, 1);
+        o = __shfl(claim, 0, dev::kWave);
     }
     __syncthreads();
     // output offset of each bucket inside the unit
