@@ -132,18 +132,42 @@ __global__ void segments_kernel(const int64_t *__restrict__ row_off,
                                 const int *__restrict__ pos_a, const int64_t *__restrict__ len,
                                 int *__restrict__ seg_row, int64_t *__restrict__ seg_len,
                                 int64_t *__restrict__ seg_runs, int64_t *__restrict__ seg_fill) {
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < rows; i += gridDim.x * blockDim.x) {
-        const int64_t s0 = seg_prefix[i], s1 = seg_prefix[i + 1];
-        const int64_t prod = row_off[i + 1] - row_off[i];
-        int64_t runs = 0;
-        if (prod > 0 && prod <= kShort) {
-            for (int p = pos_a[i]; p < pos_a[i + 1]; ++p) runs += len[p] > 0 ? 1 : 0;
+    // One row per lane; a long row's segments (one per column bucket) are then written by
+    // the whole wavefront, 64 consecutive segments per store, instead of by its own lane.
+    const int l = dev::lane();
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i0 = static_cast<int64_t>(blockIdx.x) * blockDim.x + (threadIdx.x - l);
+         i0 < rows; i0 += stride) {  // uniform per wavefront
+        const int i = static_cast<int>(i0) + l;
+        int64_t s0 = 0, s1 = 0, runs = 0, prod = 0;
+        if (i < rows) {
+            s0 = seg_prefix[i];
+            s1 = seg_prefix[i + 1];
+            prod = row_off[i + 1] - row_off[i];
+            if (prod > 0 && prod <= kShort) {
+                for (int p = pos_a[i]; p < pos_a[i + 1]; ++p) runs += len[p] > 0 ? 1 : 0;
+            }
+            if (s1 - s0 == 1) {  // a short row's single segment
+                seg_row[s0] = i;
+                seg_len[s0] = prod > kShort ? 0 : prod;
+                seg_runs[s0] = runs;
+                seg_fill[s0] = 0;
+            }
         }
-        for (int64_t s = s0; s < s1; ++s) {
-            seg_row[s] = i;
-            seg_len[s] = prod > kShort ? 0 : prod;
-            seg_runs[s] = runs;
-            seg_fill[s] = 0;
+        unsigned long long many = __ballot(i < rows && s1 - s0 > 1);
+        while (many) {  // uniform
+            const int src = __ffsll(static_cast<long long>(many)) - 1;
+            many &= many - 1;
+            const int64_t a0 = __shfl(s0, src, dev::kWave), a1 = __shfl(s1, src, dev::kWave);
+            const int row = __shfl(i, src, dev::kWave);
+            const int64_t plen = __shfl(prod, src, dev::kWave);
+            const int64_t prun = __shfl(runs, src, dev::kWave);
+            for (int64_t sg = a0 + l; sg < a1; sg += dev::kWave) {
+                seg_row[sg] = row;
+                seg_len[sg] = plen > kShort ? 0 : plen;
+                seg_runs[sg] = prun;
+                seg_fill[sg] = 0;
+            }
         }
     }
 }
