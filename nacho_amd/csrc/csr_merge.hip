@@ -1402,19 +1402,38 @@ __global__ __launch_bounds__(kBlock) void csr_compact_kernel(
     __shared__ int64_t s_wave[kBlock / dev::kWave];
     const int t = blockIdx.x;
     const int c = t / chunk;
+    // The tile's pairs are loaded first (they do not depend on its offset), so that their
+    // loads are in flight while the offset is summed.  A tile holds at most kTile + 1 items.
+    constexpr int kMove = (kTile + 1 + kBlock - 1) / kBlock;
+    const int from = spread_by_a ? split_a[t] : split_b[t];
+    const int n = static_cast<int>(tile_count[t]);
+    int mc[kMove];
+    float mv[kMove];
+#pragma unroll
+    for (int k = 0; k < kMove; ++k) {
+        const int q = static_cast<int>(threadIdx.x) + k * kBlock;
+        mc[k] = 0;
+        mv[k] = 0.0f;
+        if (q < n) {
+            mc[k] = tmp_crd[from + q];
+            mv[k] = tmp_val[from + q];
+        }
+    }
     int64_t before = 0;
     for (int i = threadIdx.x; i < c; i += kBlock) before += chunk_total[i];
     for (int i = c * chunk + static_cast<int>(threadIdx.x); i < t; i += kBlock) before += tile_count[i];
     int64_t to64 = 0;
     (void)dev::block_exclusive_sum<kBlock>(before, s_wave, to64);
-    const int from = spread_by_a ? split_a[t] : split_b[t];
     const int to = static_cast<int>(to64);
-    const int n = static_cast<int>(tile_count[t]);
     if (t == num_tiles - 1 && threadIdx.x == 0) *length = to64 + n;
-    for (int q = threadIdx.x; q < n; q += kBlock) {
-        cc[to + q] = tmp_crd[from + q];
-        vc[to + q] = tmp_val[from + q];
-        if (rc) rc[to + q] = tmp_row[from + q];
+#pragma unroll
+    for (int k = 0; k < kMove; ++k) {
+        const int q = static_cast<int>(threadIdx.x) + k * kBlock;
+        if (q < n) {
+            cc[to + q] = mc[k];
+            vc[to + q] = mv[k];
+            if (rc) rc[to + q] = tmp_row[from + q];
+        }
     }
     const int r_end = t + 1 < num_tiles ? split_r[t + 1] : rows;
     for (int r = split_r[t] + static_cast<int>(threadIdx.x); r < r_end; r += kBlock) {
