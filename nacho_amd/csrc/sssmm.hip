@@ -377,11 +377,17 @@ __global__ __launch_bounds__(kBlock) void probe_kernel(
                 const uint64_t *tab = (pm[g] & kWalkB) ? tab_a : tab_b;
                 uint64_t ww = w[g];
                 uint32_t hh = slot[g];
-                // collisions: the next slots, one at a time
+                // collisions: the next two slots per step, both loads issued together (a
+                // wavefront waits for its longest chain; the second slot is nearly always in
+                // the same line); the first of them that holds the key or is empty ends it
                 while (static_cast<uint32_t>(ww) != key[g] &&
                        static_cast<uint32_t>(ww) != kEmptyKey) {
-                    hh = (hh + 1) & mask;
-                    ww = tab[tb[g] + hh];
+                    const uint32_t h1 = (hh + 1) & mask, h2 = (hh + 2) & mask;
+                    const uint64_t w1 = tab[tb[g] + h1], w2 = tab[tb[g] + h2];
+                    const bool first = static_cast<uint32_t>(w1) == key[g] ||
+                                       static_cast<uint32_t>(w1) == kEmptyKey;
+                    ww = first ? w1 : w2;
+                    hh = first ? h1 : h2;
                 }
                 if (static_cast<uint32_t>(ww) == key[g]) {
                     const float other = __uint_as_float(static_cast<uint32_t>(ww >> 32));
